@@ -1,0 +1,110 @@
+"""ctypes binding of libasca_hip.so (the C ABI declared in include/asca_hip.h).
+
+This is the Python-side counterpart of the reference's FFI module
+rust/src/cuda/sys.rs: one declaration per exported symbol, and a status check
+that turns a non-zero return into an exception carrying asca_last_error()
+(rust/src/cuda/sys.rs:68-70 does the same with CUresult).
+
+The library is loaded from the package directory only; when it is missing the
+import of any GPU entry point fails loudly (there is no CPU fallback here).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libasca_hip.so")
+
+_i = C.c_int
+_sz = C.c_size_t
+_p = C.c_void_p
+_fp = C.POINTER(C.c_float)
+_u64p = C.POINTER(C.c_uint64)
+
+# name -> (restype, argtypes).  Float tensors travel as void* device pointers.
+SIGNATURES: dict[str, tuple] = {
+    "asca_last_error": (C.c_char_p, []),
+    "asca_init": (_i, [_i]),
+    "asca_device_count": (_i, [C.POINTER(_i)]),
+    "asca_describe": (_i, [C.c_char_p, _i]),
+    "asca_alloc": (_i, [C.POINTER(_p), _sz]),
+    "asca_free": (_i, [_p]),
+    "asca_pool_release": (_i, []),
+    "asca_h2d": (_i, [_p, _p, _sz]),
+    "asca_d2h": (_i, [_p, _p, _sz]),
+    "asca_d2d": (_i, [_p, _p, _sz, _p]),
+    "asca_memset32": (_i, [_p, C.c_uint32, _sz, _p]),
+    "asca_sync": (_i, []),
+    "asca_stream_sync": (_i, [_p]),
+    "asca_stats": (_i, [_u64p, _u64p, _u64p]),
+    "asca_reset_stats": (_i, []),
+    "asca_fail_after": (_i, [C.c_int64]),
+    "asca_stream_create": (_i, [C.POINTER(_p)]),
+    "asca_stream_destroy": (_i, [_p]),
+    "asca_event_create": (_i, [C.POINTER(_p)]),
+    "asca_event_destroy": (_i, [_p]),
+    "asca_event_record": (_i, [_p, _p]),
+    "asca_event_elapsed_ms": (_i, [C.POINTER(C.c_float), _p, _p]),
+    "asca_selftest_wave": (_i, [_p]),
+    "asca_copy_f32": (_i, [_p, _p, _sz, _p]),
+    "asca_rng_seed": (None, [C.c_uint64, _u64p]),
+    "asca_rng_u64": (None, [_u64p, _u64p, _sz]),
+    "asca_rng_normal": (None, [_u64p, _p, _sz, C.c_float, C.c_float]),
+    "asca_delta_ws_bytes": (_i, [_i, _i, _i, _i, C.POINTER(_sz)]),
+    "asca_delta_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "asca_delta_bwd_raw": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "asca_delta_bwd_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "asca_delta_states": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+}
+
+ERRORS = {
+    1: "invalid argument",
+    2: "HIP error",
+    3: "unsupported",
+    4: "not initialised",
+    5: "injected failure",
+    6: "out of device memory",
+    7: "no device",
+}
+
+
+class AscaError(RuntimeError):
+    """A libasca_hip entry point returned a non-zero status."""
+
+    def __init__(self, code: int, func: str, msg: str):
+        super().__init__(f"{func}: {ERRORS.get(code, 'error')} ({code}): {msg}")
+        self.code = code
+        self.func = func
+
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load libasca_hip.so from the package directory and declare its symbols."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -m asca_amd.build` "
+                    "(no CPU fallback exists for the HIP path)"
+                )
+            lib = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+        return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise AscaError on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.asca_last_error().decode(errors="replace")
+        raise AscaError(rc, name, msg)

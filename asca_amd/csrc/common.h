@@ -1,0 +1,70 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of libasca_hip.
+//
+// Wave-level data movement uses DPP (quad_perm / row_half_mirror / row_mirror /
+// row_ror) inside a 16-lane row and the gfx950 v_permlane16_swap /
+// v_permlane32_swap instructions across rows, so reductions never touch LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define ASCA_DEV __device__ __forceinline__
+
+namespace asca {
+
+// DPP control words (GCN3+/CDNA encodings).
+constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_MIRROR = 0x140; // lane i <- 15-i within a 16-lane row
+constexpr int DPP_HALF_MIRROR = 0x141;// lane i <- 7-i within 8 lanes
+constexpr int DPP_ROW_ROR8 = 0x128;   // lane i <- (i+8)&15: xor 8 inside a row
+
+template <int CTRL>
+ASCA_DEV float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// x from lane (lane ^ 32) added to x: every lane receives the pair sum.
+ASCA_DEV float add_xor32(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// x from lane (lane ^ 16) added to x.
+ASCA_DEV float add_xor16(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Transposed pair reduction across lane^32: lanes < 32 return lo(own)+lo(partner),
+// lanes >= 32 return hi(own)+hi(partner).  One swap, one add.
+ASCA_DEV float tsum32(float lo, float hi) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Transposed pair reduction across lane^16: even 16-lane rows return lo sums,
+// odd rows return hi sums.
+ASCA_DEV float tsum16(float lo, float hi) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Butterfly sums over the low log2(N) lane bits (N in 1,2,4,8,16); the result is
+// bitwise identical in every lane of the group.
+template <int N>
+ASCA_DEV float group_sum(float x) {
+    if constexpr (N >= 2) x += dpp<DPP_QUAD_XOR1>(x);
+    if constexpr (N >= 4) x += dpp<DPP_QUAD_XOR2>(x);
+    if constexpr (N >= 8) x += dpp<DPP_HALF_MIRROR>(x);   // valid: quad-uniform
+    if constexpr (N >= 16) x += dpp<DPP_ROW_MIRROR>(x);   // valid: 8-uniform
+    return x;
+}
+
+// Sum over all 64 lanes, result in every lane.
+ASCA_DEV float wave_sum(float x) {
+    x = group_sum<16>(x);
+    x = add_xor16(x);
+    x = add_xor32(x);
+    return x;
+}
+
+ASCA_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+}  // namespace asca

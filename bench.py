@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Headline benchmark: gated delta-rule fwd + BPTT, recurrent form, f32, at
+B=32 T=512 H=8 dh=64 (seed 1) on one MI355X.
+
+A step is one forward (asca_delta_fwd) plus one BPTT with the fused L2-norm and
+sigmoid backward (asca_delta_bwd_fused, the drop-in for Gpu::delta_bwd_dev) over
+one batch of synthetic inputs already resident in HBM.  W untimed warm-up steps,
+then K timed steps on one stream; kernel durations come from HIP events on that
+stream.  Prints one JSON line.
+
+The CPU baseline is the oracle's restatement of the reference CPU path
+(DeltaBlock::scan_cpu + bptt_cpu with its thread decomposition) on the same
+inputs, timed on this host in the same run.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "delta fwd+BPTT tokens/s (B32 T512 H8 dh64 f32) + % of roofline"
+PEAK_F32 = 157.3e12   # MI355X published dense fp32 (matrix) peak, FLOP/s
+PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
+HEADLINE = dict(B=32, T=512, H=8, dh=64, seed=1)
+PMC_FILE = ROOT / "profiles" / "delta_b32t512h8d64_traffic.json"
+
+
+def synth_inputs(B, T, H, dh, seed):
+    """configs[1] inputs drawn from the reference's Rng stream (product
+    restatement in libasca_hip): q, k, v ~ N(0,1); alpha logits 2+N(0,1);
+    beta logits N(0,1); dO ~ N(0,1); then per-head L2 norm of q, k and
+    sigmoid gates."""
+    from asca_amd import _lib
+
+    lib = _lib.load()
+    st = (C.c_uint64 * 2)()
+    lib.asca_rng_seed(seed, st)
+    rows, d = B * T, H * dh
+
+    def normal(n, scale=1.0, offset=0.0):
+        out = np.empty(n, dtype=np.float32)
+        lib.asca_rng_normal(st, out.ctypes.data_as(C.c_void_p), n, scale, offset)
+        return out
+
+    q = normal(rows * d).reshape(rows, d)
+    k = normal(rows * d).reshape(rows, d)
+    v = normal(rows * d).reshape(rows, d)
+    ga = normal(rows * H, 1.0, 2.0).reshape(rows, H)
+    gb = normal(rows * H).reshape(rows, H)
+    d_o = normal(rows * d).reshape(rows, d)
+
+    def l2n(x):
+        x3 = x.reshape(rows, H, dh)
+        n = np.maximum(np.sqrt(np.einsum("rhc,rhc->rh", x3, x3, dtype=np.float32)), np.float32(1e-8))
+        return np.ascontiguousarray((x3 / n[..., None]).reshape(rows, d), dtype=np.float32), n.astype(np.float32)
+
+    q, qn = l2n(q)
+    k, kn = l2n(k)
+    alpha = (1.0 / (1.0 + np.exp(-ga))).astype(np.float32)
+    beta = (1.0 / (1.0 + np.exp(-gb))).astype(np.float32)
+    return dict(q=q, k=k, v=v, alpha=alpha, beta=beta, d_o=d_o, qn=qn, kn=kn)
+
+
+def work_model(B, T, H, dh):
+    """Algorithmic work (rust/src/delta.rs:289-314 forward, :504-564 BPTT):
+    7 dh^2 + 17 dh^2 flops per token-head; compulsory bytes per token-head:
+    fwd reads q,k,v (3 dh) + alpha,beta, writes o (dh); BPTT reads q,k,v,dO
+    (4 dh) + alpha,beta, writes dq,dk,dv (3 dh) + dalpha,dbeta."""
+    th = B * T * H
+    f_fwd, f_bwd = 7 * dh * dh * th, 17 * dh * dh * th
+    b_fwd = (3 * dh * 4 + 8 + dh * 4) * th
+    b_bwd = (4 * dh * 4 + 8 + 3 * dh * 4 + 8) * th
+    return f_fwd, f_bwd, b_fwd, b_bwd
+
+
+def cpu_baseline(x, B, T, H, dh, budget_s=30.0):
+    """The reference CPU path restated in C (oracle), reference threading:
+    one thread per head in the scan, one per (head, sequence) in the BPTT,
+    full state history kept as the reference does.  Median of >= 5 reps after
+    one warm-up (fewer only if one rep exceeds the budget)."""
+    from oracle import pyoracle as orc
+
+    def once():
+        t0 = time.perf_counter()
+        o, st = orc.delta_scan(x["q"], x["k"], x["v"], x["alpha"], x["beta"], B, T, H, dh)
+        raw = orc.delta_bptt_raw(x["q"], x["k"], x["v"], x["alpha"], x["beta"], x["d_o"], st, B, T, H, dh)
+        orc.delta_fuse(x["q"], x["k"], x["qn"], x["kn"], x["alpha"], x["beta"], *raw, H, dh)
+        return time.perf_counter() - t0
+
+    once()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        times.append(once())
+    med = statistics.median(times)
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {
+        "value": round(B * T / med, 1),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"full configs[1] workload (B{B} T{T} H{H} dh{dh}, same inputs), oracle restatement of "
+                   f"scan_cpu + bptt_cpu + norm/sigmoid backward with the reference's threads "
+                   f"({H} scan threads, {H * B} BPTT threads) on {cores} host cores; median of {len(times)} reps "
+                   f"after 1 warm-up, {med:.3f} s each; AVX2={bool(orc.lib().orc_has_avx2())}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run the known-size copy kernel (for counter calibration)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        sys.stderr.write("bench.py: this build runs on exactly one GPU (the delta-rule units are independent "
+                         "per (sequence, head); see DESIGN.md for how the path shards). Use --gpus 1.\n")
+        sys.exit(2)
+
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf
+
+    g = gpu.gpu()
+    if g is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    B, T, H, dh, seed = (HEADLINE[k] for k in ("B", "T", "H", "dh", "seed"))
+    rows, d = B * T, H * dh
+    x = synth_inputs(B, T, H, dh, seed)
+    dev = {k: DevBuf.from_host(v) for k, v in x.items()}
+    wsb = C.c_size_t()
+    _lib.call("asca_delta_ws_bytes", B, T, H, dh, C.byref(wsb))
+    ws = DevBuf(wsb.value)
+    o = DevBuf(rows * d * 4)
+    d_qkv = DevBuf(rows * 3 * d * 4)
+    d_gate = DevBuf(rows * 2 * H * 4)
+    cal_src = cal_dst = None
+    if args.calib:
+        cal_src, cal_dst = DevBuf(256 << 20), DevBuf(256 << 20)
+
+    sp = C.c_void_p()
+    _lib.call("asca_stream_create", C.byref(sp))
+    stream = sp.value
+    V = lambda b: C.c_void_p(b.ptr)  # noqa: E731
+
+    def fwd():
+        _lib.call("asca_delta_fwd", V(dev["q"]), V(dev["k"]), V(dev["v"]), V(dev["alpha"]), V(dev["beta"]), V(o),
+                  V(ws), B, T, H, dh, C.c_void_p(stream))
+
+    def bwd():
+        _lib.call("asca_delta_bwd_fused", V(dev["q"]), V(dev["k"]), V(dev["v"]), V(dev["alpha"]),
+                  V(dev["beta"]), V(dev["qn"]), V(dev["kn"]), V(dev["d_o"]), V(ws), V(d_qkv), V(d_gate),
+                  B, T, H, dh, C.c_void_p(stream))
+
+    def event():
+        e = C.c_void_p()
+        _lib.call("asca_event_create", C.byref(e))
+        return e
+
+    def elapsed(a, b):
+        ms = C.c_float()
+        _lib.call("asca_event_elapsed_ms", C.byref(ms), a, b)
+        return ms.value
+
+    print(f"bench: {gpu.describe()}; B{B} T{T} H{H} dh{dh}; warmup {args.warmup}, steps {args.steps}", flush=True)
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+        if cal_src is not None:
+            _lib.call("asca_copy_f32", V(cal_dst), V(cal_src), C.c_size_t((256 << 20) // 4), C.c_void_p(stream))
+    _lib.call("asca_stream_sync", C.c_void_p(stream))
+
+    K = args.steps
+    ev = [(event(), event(), event()) for _ in range(K)]
+    t0 = time.perf_counter()
+    for i in range(K):
+        _lib.call("asca_event_record", ev[i][0], C.c_void_p(stream))
+        fwd()
+        _lib.call("asca_event_record", ev[i][1], C.c_void_p(stream))
+        bwd()
+        _lib.call("asca_event_record", ev[i][2], C.c_void_p(stream))
+    _lib.call("asca_stream_sync", C.c_void_p(stream))
+    wall = time.perf_counter() - t0
+    fwd_ms = statistics.mean(elapsed(e[0], e[1]) for e in ev)
+    bwd_ms = statistics.mean(elapsed(e[1], e[2]) for e in ev)
+    dev_ms = elapsed(ev[0][0], ev[-1][2]) / K
+    for e in ev:
+        for h in e:
+            _lib.call("asca_event_destroy", h)
+    print(f"bench: fwd {fwd_ms:.4f} ms, bwd {bwd_ms:.4f} ms, device step {dev_ms:.4f} ms, "
+          f"wall step {wall / K * 1e3:.4f} ms", flush=True)
+
+    f_fwd, f_bwd, b_fwd, b_bwd = work_model(B, T, H, dh)
+    step_s = wall / K
+    tokens = B * T
+    dominant = "delta_bwd" if bwd_ms >= fwd_ms else "delta_fwd"
+    dom_ms = max(bwd_ms, fwd_ms)
+    dom_f = f_bwd if dominant == "delta_bwd" else f_fwd
+    dom_b = b_bwd if dominant == "delta_bwd" else b_fwd
+    achieved = dom_f / (dom_ms * 1e-3)
+    traffic = None
+    if PMC_FILE.exists():
+        try:
+            traffic = json.loads(PMC_FILE.read_text()).get(dominant, {}).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    roof_step = max((f_fwd + f_bwd) / PEAK_F32, (b_fwd + b_bwd) / PEAK_HBM)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens / step_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (reference Rng stream, configs[1] distributions, seed 1)",
+        "config": {"workload": "gated delta-rule fwd+BPTT, recurrent form (asca_delta_fwd + asca_delta_bwd_fused)",
+                   "B": B, "T": T, "H": H, "dh": dh, "seed": seed},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved / 1e12, 3),
+            "peak": PEAK_F32 / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_F32, 4),
+            "traffic": traffic,
+            "kernel": dominant,
+            "algorithmic_bytes": dom_b,
+            "algorithmic_flops": dom_f,
+        },
+        "kernels_ms": {"delta_fwd": round(fwd_ms, 4), "delta_bwd": round(bwd_ms, 4)},
+        "step_roofline": {
+            "roofline_us": round(roof_step * 1e6, 2),
+            "measured_us": round(dev_ms * 1e3, 2),
+            "frac": round(roof_step / (dev_ms * 1e-3), 4),
+            "note": "whole fwd+BPTT vs max(24 dh^2 flops / 157.3 TFLOP/s, compulsory bytes / 8 TB/s)",
+        },
+    }
+    if not args.no_cpu:
+        print("bench: timing the CPU baseline ...", flush=True)
+        result["cpu_baseline"] = cpu_baseline(x, B, T, H, dh)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

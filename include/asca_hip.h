@@ -1,0 +1,187 @@
+/*
+ * asca_hip.h -- C ABI of libasca_hip.so, the MI355X (gfx950) backend of the
+ * ASCA gated delta-rule hot path.
+ *
+ * It replaces the reference crate's CUDA FFI module (rust/src/cuda/sys.rs:33-65,
+ * hand-bound CUDA driver API) plus the PTX kernels it launches
+ * (rust/kernels/asca.cu), under the unchanged operator API of
+ * rust/src/cuda/mod.rs (`Gpu::delta_scan`, `Gpu::delta_bwd_dev`, ...).
+ *
+ * Conventions
+ *   - Every function returns an int status: 0 (ASCA_OK) or a positive error
+ *     code; none aborts.  asca_last_error() gives the message of the calling
+ *     thread's last failure (rust/src/cuda/sys.rs:68-70 maps CUresult the same way).
+ *   - Tensor arguments are device pointers to row-major f32 data unless stated.
+ *     The caller owns every buffer it passes.
+ *   - `stream` is an opaque hipStream_t (NULL = the null stream).  Entry points
+ *     that take a stream are asynchronous; synchronise before reading results on
+ *     the host.  The reference synchronises after every op (cuCtxSynchronize).
+ *   - Row layout follows the reference: row r = b*T + t of a (B*T, H*dh) matrix
+ *     holds token t of sequence b, head h in columns h*dh .. h*dh+dh-1
+ *     (rust/kernels/asca.cu:256-263, rust/src/delta.rs:118-120).
+ */
+#ifndef ASCA_HIP_H
+#define ASCA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASCA_API __attribute__((visibility("default")))
+
+enum {
+    ASCA_OK = 0,
+    ASCA_ERR_INVALID = 1,      /* bad argument (shape, null pointer, range)      */
+    ASCA_ERR_HIP = 2,          /* a HIP runtime call failed                       */
+    ASCA_ERR_UNSUPPORTED = 3,  /* shape or device this build does not handle      */
+    ASCA_ERR_NOT_INIT = 4,     /* asca_init has not succeeded                      */
+    ASCA_ERR_INJECTED = 5,     /* failure injected by asca_fail_after             */
+    ASCA_ERR_OOM = 6,          /* device allocation failed                        */
+    ASCA_ERR_NO_DEVICE = 7     /* no HIP device present                           */
+};
+
+/* ------------------------------------------------------------ runtime ---- */
+
+/* Message of the calling thread's last error ("" if none). */
+ASCA_API const char* asca_last_error(void);
+
+/* Replaces cuInit + cuDeviceGet + cuCtxCreate_v2 (sys.rs:34-44) as used by
+ * Gpu::init (rust/src/cuda/mod.rs:177-237).  Fails unless `device` is gfx950. */
+ASCA_API int asca_init(int device);
+
+/* Replaces cuDeviceGetCount-style probing behind cuda::available() (mod.rs:1508). */
+ASCA_API int asca_device_count(int* n);
+
+/* Replaces cuDeviceGetName + cuDeviceGetAttribute(SM count) used by
+ * cuda::describe() (mod.rs:1494-1530): "name (arch, N CUs)". */
+ASCA_API int asca_describe(char* buf, int len);
+
+/* Replaces cuMemAlloc_v2 / cuMemFree_v2 (sys.rs:47-48) behind DevBuf's
+ * size-class pool (mod.rs:100-174): sizes round up to a power of two and
+ * freed blocks are recycled, never returned to HIP until asca_pool_release. */
+ASCA_API int asca_alloc(void** ptr, size_t bytes);
+ASCA_API int asca_free(void* ptr);
+ASCA_API int asca_pool_release(void);
+
+/* Replaces cuMemcpyHtoD_v2 / cuMemcpyDtoH_v2 (sys.rs:49-50) behind
+ * DevBuf::upload/download (mod.rs:126-157).  Synchronous; counted in
+ * asca_stats exactly as H2D_BYTES / D2H_BYTES are (mod.rs:25-27). */
+ASCA_API int asca_h2d(void* dst, const void* src, size_t bytes);
+ASCA_API int asca_d2h(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy on `stream` (no reference counterpart: the reference
+ * never copies on the device). */
+ASCA_API int asca_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* Replaces cuMemsetD32_v2 (sys.rs:51). */
+ASCA_API int asca_memset32(void* dst, uint32_t value, size_t count, void* stream);
+
+/* Replaces cuCtxSynchronize (sys.rs:45). */
+ASCA_API int asca_sync(void);
+ASCA_API int asca_stream_sync(void* stream);
+
+/* Traffic and launch counters: H2D_BYTES, D2H_BYTES, LAUNCHES and
+ * reset_stats() of rust/src/cuda/mod.rs:25-33. */
+ASCA_API int asca_stats(uint64_t* h2d, uint64_t* d2h, uint64_t* launches);
+ASCA_API int asca_reset_stats(void);
+
+/* Fault injection for the CPU-fallback paths (delta.rs:227-240, 640-647): the
+ * n-th kernel launch from now (0 = the next one) fails with ASCA_ERR_INJECTED
+ * without launching; -1 disables.  ASCA_FAIL_LAUNCH=n in the environment sets
+ * it at asca_init.  No reference counterpart. */
+ASCA_API int asca_fail_after(int64_t n);
+
+/* Streams (default priority, non-blocking) and events for timing.  No
+ * reference counterpart: the reference only uses the null stream. */
+ASCA_API int asca_stream_create(void** stream);
+ASCA_API int asca_stream_destroy(void* stream);
+ASCA_API int asca_event_create(void** ev);
+ASCA_API int asca_event_destroy(void* ev);
+ASCA_API int asca_event_record(void* ev, void* stream);
+/* Waits for `stop`, then returns the time between the two events in ms. */
+ASCA_API int asca_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* Diagnostic: runs one wave through the lane-exchange primitives the kernels
+ * use (DPP quad_perm xor1/xor2, row_half_mirror, row_mirror, row_ror:8,
+ * permlane32_swap, permlane16_swap, full-wave sum) on x[lane] = lane and
+ * y[lane] = 100 + lane, and copies 10 x 64 floats to host_out (row c = result
+ * c per lane).  No reference counterpart. */
+ASCA_API int asca_selftest_wave(float* host_out);
+
+/* Plain streaming device copy of n floats (n % 4 == 0, 16-byte aligned
+ * buffers).  The known-size kernel against which HBM traffic counters are
+ * calibrated.  No reference counterpart. */
+ASCA_API int asca_copy_f32(float* dst, const float* src, size_t n, void* stream);
+
+/* ---------------------------------------------------------------- rng --- */
+/* Host-side restatement of the reference's input generator Rng
+ * (rust/src/tensor.rs:299-337): xorshift128+ seeded as Rng::new(seed)
+ * (:307-311), next_u64 (:313-320), Box-Muller normal() in f32 (:328-332).
+ * state[2] carries the stream between calls. */
+ASCA_API void asca_rng_seed(uint64_t seed, uint64_t* state);
+ASCA_API void asca_rng_u64(uint64_t* state, uint64_t* out, size_t n);
+/* out[i] = offset + normal() * scale */
+ASCA_API void asca_rng_normal(uint64_t* state, float* out, size_t n, float scale, float offset);
+
+/* --------------------------------------------------- delta rule (recurrent) */
+
+/* Bytes of the workspace a delta forward leaves for its backward: the per-step
+ * S^T k vector (B*T*H*dh floats) and state checkpoints every C steps
+ * (B*H*ceil(T/C)*dh*dh floats; C depends on dh).  It replaces the full state
+ * history DeltaDev.states of rust/src/cuda/mod.rs:1274-1275,1386-1397
+ * ((T+1)*dh*dh floats per unit).  dh may be 1..128. */
+ASCA_API int asca_delta_ws_bytes(int B, int T, int H, int dh, size_t* bytes);
+
+/* Forward recurrence of the gated delta rule for all (sequence, head) units,
+ * S_0 = 0:  sk_t = S_{t-1}^T k_t;  u_t = beta_t (v_t - alpha_t sk_t);
+ *           S_t = alpha_t S_{t-1} + k_t u_t^T;  o_t = S_t^T q_t.
+ * Replaces Gpu::delta_scan (rust/src/cuda/mod.rs:1253-1321) and kernel
+ * delta_fwd_batch_f32 (rust/kernels/asca.cu:256-317); same math as
+ * DeltaBlock::scan_cpu (rust/src/delta.rs:244-334).
+ *   q, k, v : (B*T, H*dh), q and k already L2-normalised per head
+ *   alpha, beta : (B*T, H)
+ *   o : (B*T, H*dh) output
+ *   ws : asca_delta_ws_bytes(B,T,H,dh) bytes, kept for asca_delta_bwd_*  */
+ASCA_API int asca_delta_fwd(const float* q, const float* k, const float* v,
+                            const float* alpha, const float* beta, float* o, void* ws,
+                            int B, int T, int H, int dh, void* stream);
+
+/* BPTT of the recurrence, raw per-head gradients (no L2-norm or sigmoid
+ * backward): dq, dk, dv (B*T, H*dh) and dalpha, dbeta (B*T, H).  Same math as
+ * the per-(head, sequence) loop of DeltaBlock::bptt_cpu
+ * (rust/src/delta.rs:475-572).  Inputs are those of the matching
+ * asca_delta_fwd plus d_o (B*T, H*dh); ws must be that call's workspace. */
+ASCA_API int asca_delta_bwd_raw(const float* q, const float* k, const float* v,
+                                const float* alpha, const float* beta, const float* d_o,
+                                const void* ws, float* dq, float* dk, float* dv,
+                                float* dalpha, float* dbeta,
+                                int B, int T, int H, int dh, void* stream);
+
+/* BPTT with the L2-norm backward of q, k and the sigmoid backward of the gates
+ * fused in: the drop-in for Gpu::delta_bwd_dev (rust/src/cuda/mod.rs:1328-1382)
+ * and kernel delta_bwd_f32 (rust/kernels/asca.cu:340-485); same results as
+ * DeltaBlock::bptt_cpu including its tail (rust/src/delta.rs:589-612).
+ *   qnorm, knorm : (B*T, H) norms saved by the forward's L2 normalisation
+ *   d_qkv : (B*T, 3*H*dh) = [dq | dk | dv];  d_gate : (B*T, 2*H) = [dalpha | dbeta]
+ *   (logit gradients). */
+ASCA_API int asca_delta_bwd_fused(const float* q, const float* k, const float* v,
+                                  const float* alpha, const float* beta,
+                                  const float* qnorm, const float* knorm, const float* d_o,
+                                  const void* ws, float* d_qkv, float* d_gate,
+                                  int B, int T, int H, int dh, void* stream);
+
+/* Materialise the full state history the reference keeps in DeltaDev.states:
+ * for unit u = h*B + b, (T+1) states of dh*dh floats (S before every step, then
+ * the final state), row-major S[a][i].  Replaces DeltaDev::download_states
+ * (rust/src/cuda/mod.rs:1473-1479), by recomputation.  states is a device
+ * buffer of H*B*(T+1)*dh*dh floats. */
+ASCA_API int asca_delta_states(const float* q, const float* k, const float* v,
+                               const float* alpha, const float* beta, float* states,
+                               int B, int T, int H, int dh, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ASCA_HIP_H */

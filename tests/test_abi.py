@@ -1,0 +1,74 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the header
+declares with the binding's signature table, and its host-only entry points
+(workspace sizing, the reference Rng) behave.  No kernel is launched here."""
+import ctypes as C
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+
+def _header_symbols():
+    text = (ROOT / "include" / "asca_hip.h").read_text()
+    return sorted(set(re.findall(r"ASCA_API\s+[\w\s\*]+?\b(asca_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from asca_amd import _lib
+
+    lib = _lib.load()
+    names = _header_symbols()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} missing from the ctypes signature table"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_workspace_bytes_layout():
+    from asca_amd import _lib
+
+    out = C.c_size_t()
+    _lib.call("asca_delta_ws_bytes", 32, 512, 8, 64, C.byref(out))
+    sk = 32 * 512 * 8 * 64 * 4
+    ckpt = 32 * 8 * (512 // 8) * 64 * 64 * 4
+    assert out.value == sk + ckpt
+    _lib.call("asca_delta_ws_bytes", 4, 128, 4, 32, C.byref(out))
+    assert out.value == 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 32) * 32 * 32 * 4
+    with pytest.raises(_lib.AscaError) as ei:
+        _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))
+    assert ei.value.code == 3
+
+
+def test_product_rng_equals_oracle_rng(orc):
+    from asca_amd import _lib
+
+    lib = _lib.load()
+    st = (C.c_uint64 * 2)()
+    for seed in range(4):
+        lib.asca_rng_seed(seed, st)
+        out = np.zeros(16, dtype=np.uint64)
+        lib.asca_rng_u64(st, out.ctypes.data_as(C.POINTER(C.c_uint64)), 16)
+        np.testing.assert_array_equal(out, orc.rng_u64(seed, 16))
+    lib.asca_rng_seed(1, st)
+    got = np.zeros(1000, dtype=np.float32)
+    lib.asca_rng_normal(st, got.ctypes.data_as(C.c_void_p), 1000, 1.0, 0.0)
+    np.testing.assert_array_equal(got, orc.rng_normal(1, 1000))
+
+
+def test_errors_without_device_are_codes_not_aborts():
+    from asca_amd import _lib
+
+    lib = _lib.load()
+    n = C.c_int(0)
+    if lib.asca_device_count(C.byref(n)) == 0 and n.value > 0:
+        pytest.skip("a GPU is present; this checks the no-device path")
+    rc = lib.asca_init(0)
+    assert rc != 0
+    assert lib.asca_last_error()
+    # entry points fail cleanly before init (no HIP call is reached)
+    fake = C.c_void_p(0x1000)
+    rc = lib.asca_delta_fwd(fake, fake, fake, fake, fake, fake, fake, 1, 4, 1, 16, None)
+    assert rc == 4

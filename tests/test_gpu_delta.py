@@ -1,0 +1,152 @@
+"""GPU parity of the recurrent delta rule (forward + BPTT) against the CPU oracle.
+
+Bars (from the north star): forward <= 2e-5 and every gradient <= 1e-4, both as
+max|gpu - cpu| / max|cpu| per tensor (rust/src/main.rs:1021-1029).  Batch
+isolation is bit-exact, as the reference's gate demands (main.rs:954-981).
+All calls go through the C ABI (asca_amd.gpu -> libasca_hip.so).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 2e-5
+GRAD_TOL = 1e-4
+
+
+def _check_all(orc, g, x, B, T, H, dh, tag):
+    print(f"[delta parity] {tag} B={B} T={T} H={H} dh={dh}", flush=True)
+    o_ref, dq, dk, dv, da, db = orc.delta_fwd_bwd(x.q, x.k, x.v, x.alpha, x.beta, x.d_o, B, T, H, dh)
+    o, dev = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    assert orc.rel_err(o, o_ref) <= FWD_TOL, ("o", orc.rel_err(o, o_ref))
+    raw = g.delta_bwd_raw(dev, x.d_o)
+    for name, got, ref in zip(("dq", "dk", "dv", "dalpha", "dbeta"), raw, (dq, dk, dv, da, db)):
+        e = orc.rel_err(got, ref)
+        assert e <= GRAD_TOL, (name, e)
+    d_qkv_ref, d_gate_ref = orc.delta_fuse(x.q, x.k, x.qn, x.kn, x.alpha, x.beta, dq, dk, dv, da, db, H, dh)
+    d_qkv, d_gate = g.delta_bwd_dev(dev, x.d_o, x.qn, x.kn)
+    assert orc.rel_err(d_qkv, d_qkv_ref) <= GRAD_TOL, ("d_qkv", orc.rel_err(d_qkv, d_qkv_ref))
+    assert orc.rel_err(d_gate, d_gate_ref) <= GRAD_TOL, ("d_gate", orc.rel_err(d_gate, d_gate_ref))
+    return dev
+
+
+def test_wave_primitives_lane_semantics(g):
+    import ctypes as C
+    from asca_amd import _lib
+
+    out = np.zeros((10, 64), dtype=np.float32)
+    _lib.call("asca_selftest_wave", out.ctypes.data_as(C.c_void_p))
+    lane = np.arange(64)
+    np.testing.assert_array_equal(out[0], lane ^ 1)
+    np.testing.assert_array_equal(out[1], lane ^ 2)
+    np.testing.assert_array_equal(out[2], (lane & ~7) | (7 - (lane & 7)))
+    np.testing.assert_array_equal(out[3], (lane & ~15) | (15 - (lane & 15)))
+    np.testing.assert_array_equal(out[4], lane ^ 8)
+    # permlane32_swap(x, y): vdst keeps its low half and takes y's low half up top;
+    # vsrc takes x's high half in its low half and keeps its own high half.
+    np.testing.assert_array_equal(out[5], np.where(lane < 32, lane, 100 + lane - 32))
+    np.testing.assert_array_equal(out[6], np.where(lane < 32, lane + 32, 100 + lane))
+    # permlane16_swap: the same between even and odd 16-lane rows
+    odd = (lane >> 4) & 1
+    np.testing.assert_array_equal(out[7], np.where(odd == 0, lane, 100 + lane - 16))
+    np.testing.assert_array_equal(out[8], np.where(odd == 0, lane + 16, 100 + lane))
+    np.testing.assert_array_equal(out[9], np.full(64, 2016.0))
+
+
+def test_config0_b4_t128_h4_dh32(orc, g):
+    B, T, H, dh = 4, 128, 4, 32
+    _check_all(orc, g, orc.DeltaInputs(0, B, T, H, dh), B, T, H, dh, "configs[0] seed 0")
+
+
+def test_config1_b32_t512_h8_dh64(orc, g):
+    B, T, H, dh = 32, 512, 8, 64
+    _check_all(orc, g, orc.DeltaInputs(1, B, T, H, dh), B, T, H, dh, "configs[1] seed 1")
+
+
+@pytest.mark.parametrize("B,T,H,dh", [
+    (1, 1, 1, 64),      # single step
+    (2, 7, 3, 8),       # dh of rust/tests/gradcheck.rs, ragged T
+    (3, 24, 4, 16),     # the reference's delta_scan gate shape (main.rs:854)
+    (2, 33, 2, 24),     # masked dh, T not a multiple of the checkpoint interval
+    (2, 70, 2, 48),
+    (1, 45, 2, 128),
+    (2, 17, 6, 32),     # dh of the reference's delta-grad gate (main.rs:1106), ragged T
+    (5, 64, 1, 64),
+    (1, 9, 2, 5),       # odd dh
+])
+def test_edge_shapes(orc, g, B, T, H, dh):
+    _check_all(orc, g, orc.DeltaInputs(100 + B * T + dh, B, T, H, dh), B, T, H, dh, "edge")
+
+
+def test_states_download_matches_cpu_history(orc, g):
+    # rust/src/main.rs:854-953: B=3 seq=24 H=4 dh=16, full state history compared
+    B, T, H, dh = 3, 24, 4, 16
+    rng = np.random.default_rng(5)
+    q, _ = orc.l2norm_heads(rng.standard_normal((B * T, H * dh)).astype(np.float32), H, dh)
+    k, _ = orc.l2norm_heads(rng.standard_normal((B * T, H * dh)).astype(np.float32), H, dh)
+    v = (0.5 * rng.standard_normal((B * T, H * dh))).astype(np.float32)
+    alpha = (0.85 + 0.1 * rng.random((B * T, H))).astype(np.float32)
+    beta = (0.7 + 0.2 * rng.random((B * T, H))).astype(np.float32)
+    o_ref, st_ref = orc.delta_scan(q, k, v, alpha, beta, B, T, H, dh)
+    o, dev = g.delta_scan(q, k, v, alpha, beta, B, T, H, dh)
+    assert orc.rel_err(o, o_ref) <= FWD_TOL
+    st = np.stack(dev.download_states())
+    assert st.shape == st_ref.shape
+    assert orc.rel_err(st, st_ref) <= FWD_TOL
+
+
+def test_batch_isolation_bit_exact_on_gpu(orc, g):
+    B, T, H, dh = 3, 40, 2, 64
+    x = orc.DeltaInputs(21, B, T, H, dh)
+    o, dev = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    d_qkv, d_gate = g.delta_bwd_dev(dev, x.d_o, x.qn, x.kn)
+    for b in range(B):
+        rs = slice(b * T, (b + 1) * T)
+        sub = [np.ascontiguousarray(a[rs]) for a in (x.q, x.k, x.v, x.alpha, x.beta)]
+        o1, dev1 = g.delta_scan(*sub, 1, T, H, dh)
+        q1, g1 = g.delta_bwd_dev(dev1, np.ascontiguousarray(x.d_o[rs]), np.ascontiguousarray(x.qn[rs]),
+                                 np.ascontiguousarray(x.kn[rs]))
+        np.testing.assert_array_equal(o1, o[rs])
+        np.testing.assert_array_equal(q1, d_qkv[rs])
+        np.testing.assert_array_equal(g1, d_gate[rs])
+
+
+def test_deterministic_rerun(orc, g):
+    B, T, H, dh = 4, 100, 2, 64
+    x = orc.DeltaInputs(8, B, T, H, dh)
+    o1, dev1 = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    o2, dev2 = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    np.testing.assert_array_equal(o1, o2)
+    a = g.delta_bwd_dev(dev1, x.d_o, x.qn, x.kn)
+    b = g.delta_bwd_dev(dev2, x.d_o, x.qn, x.kn)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+
+
+def test_injected_failure_is_an_error_then_recovers(orc, g):
+    from asca_amd import gpu
+    from asca_amd._lib import AscaError
+
+    B, T, H, dh = 2, 16, 2, 32
+    x = orc.DeltaInputs(2, B, T, H, dh)
+    gpu.fail_after(0)
+    with pytest.raises(AscaError) as ei:
+        g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    assert ei.value.code == 5
+    o, _ = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    o_ref, _ = orc.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    assert orc.rel_err(o, o_ref) <= FWD_TOL
+
+
+def test_empty_and_invalid_shapes(g):
+    from asca_amd._lib import AscaError
+
+    z = np.zeros((0, 64), dtype=np.float32)
+    zg = np.zeros((0, 1), dtype=np.float32)
+    o, _ = g.delta_scan(z, z, z, zg, zg, 0, 5, 1, 64)
+    assert o.shape == (0, 64)
+    x = np.zeros((4, 129 * 1), dtype=np.float32)
+    xg = np.zeros((4, 1), dtype=np.float32)
+    with pytest.raises(AscaError) as ei:
+        g.delta_scan(x, x, x, xg, xg, 1, 4, 1, 129)
+    assert ei.value.code == 3
