@@ -10,19 +10,23 @@
 //    so the forward splits each (sequence, head) unit into dh/16 independent
 //    waves of 16 value columns.  Inside a wave, lane = 4*column + part; a lane
 //    keeps dh/4 rows of its column in VGPRs and S^T k, S^T q are 4-lane DPP
-//    butterflies.  No LDS, no barrier in the forward.  The step loop is
-//    straight-line (unrolled per checkpoint chunk): inputs are prefetched PF
-//    steps ahead into registers, the gates of a chunk arrive as one lane-
-//    distributed load and are broadcast with v_readlane, and masked lanes store
-//    into a trash buffer instead of branching, so every wait is exact.
+//    butterflies.  The k, q rows and v columns of each C-step chunk are staged
+//    once per unit in LDS (double-buffered, loaded one chunk ahead, one barrier
+//    per chunk) because per-lane global loads of the replicated rows saturate
+//    the texture-address path; the step loop is straight-line (unrolled per
+//    chunk), the gates of a chunk arrive as one lane-distributed load and are
+//    broadcast with v_readlane, outputs of 4 steps leave in one store per lane,
+//    and masked lanes store into a trash buffer instead of branching.
 //  * The forward stores S every C steps ("checkpoints", C = 8 at dh = 64, laid
 //    out as S^T so each lane writes 16-byte vectors) and the per-step sk vector,
 //    instead of the reference's full (T+1) dh^2 history (2.15 GB at B32 T512 H8
 //    dh64).
-//  * The backward walks C-step segments in reverse.  Each segment's inputs are
-//    staged in LDS (loaded one segment ahead), the segment is recomputed from its
-//    checkpoint into an LDS stash, then processed backwards.  A lane owns a
-//    (dh/16) x 4 tile: du = dS^T k is a 16-lane DPP butterfly inside a row,
+//  * The backward walks C-step segments in reverse on dh/8 waves per unit (two
+//    per SIMD at dh = 64, so one wave's LDS/scalar work issues beside the
+//    other's VALU work).  Each segment's inputs are staged in LDS (loaded one
+//    segment ahead, double-buffered), the segment is recomputed from its
+//    checkpoint into registers, then processed backwards.  A lane owns a
+//    (dh/16) x 2 tile: du = dS^T k is a 16-lane DPP butterfly inside a row,
 //    the column sums of dq and dk are transposed permlane32/permlane16 swaps
 //    plus a per-segment cross-wave sum through LDS, where the L2-norm and
 //    sigmoid backward of the drop-in variant also run.
@@ -36,19 +40,8 @@ struct DS {
     static constexpr int W = DH / 16;        // waves per unit, 16 value columns each
     static constexpr int THREADS = 64 * W;
     static constexpr int R = DH / 4;         // forward: rows per lane (4 lanes / column)
-    static constexpr int M = DH / 16;        // backward: rows per lane (16 row groups)
-    // Checkpoint interval: C states of the backward's LDS stash stay <= 128 KB.
+    // Checkpoint interval C (forward chunk = backward segment).
     static constexpr int CK = (DH <= 32) ? 16 : (DH == 64) ? 8 : 2;
-    static constexpr int PF = (DH == 128) ? 2 : 4;   // forward prefetch depth (steps)
-    // backward LDS layout (floats unless noted)
-    static constexpr int STASH_F4 = CK * W * M * 64;  // float4
-    static constexpr int RED_F = CK * W * DH;         // dq / dk column sums per wave
-    static constexpr int RAB_F = CK * W * 2;          // dalpha / dbeta per wave
-    static constexpr int STQK_F = CK * DH;            // staged q (and k) rows
-    static constexpr int STW_F = W * CK * 48;         // staged dO, v, sk per wave
-    static constexpr int STAB_F = 2 * CK;             // staged alpha, beta
-    static constexpr size_t LDS_BWD =
-        (size_t)STASH_F4 * 16 + (size_t)(2 * RED_F + RAB_F + 2 * STQK_F + STW_F + STAB_F) * 4;
 };
 
 // Sink for the stores of masked-off lanes, so stores never need a branch.
@@ -79,32 +72,88 @@ ASCA_DEV float4 ld4m(const float* __restrict__ p, int col, int dh) {
 
 // ------------------------------------------------------------------ forward
 
+// LDS of the forward: two chunk buffers, each holding the k and q rows of CK
+// steps (shared by the unit's waves) and every wave's 16 v columns.
+template <int DH>
+struct FwdL {
+    static constexpr int CK = DS<DH>::CK, W = DS<DH>::W, NT = DS<DH>::THREADS;
+    static constexpr int KQ_F = CK * DH;                      // floats of k (or q) per chunk
+    static constexpr int V_F = W * CK * 16;                   // floats of v per chunk
+    static constexpr int BUF_F = 2 * KQ_F + V_F;              // one chunk buffer
+    static constexpr int NKQ = (2 * KQ_F / 4 + NT - 1) / NT;  // staged k/q float4 per thread
+    static constexpr int NV = (CK * 4 + 63) / 64;             // staged v float4 per lane
+};
+
+template <int DH>
+struct FwdStage {
+    float4 kq[FwdL<DH>::NKQ];
+    float4 v[FwdL<DH>::NV];
+};
+
+// Global -> registers for chunk c (steps c*CK .. c*CK+CK-1, clamped to T-1).
 template <int DH, bool EXACT>
-ASCA_DEV void fwd_load(float (&kk)[DH / 4], float (&qq)[DH / 4], float& vv, const float* __restrict__ kt,
-                       const float* __restrict__ qt, const float* __restrict__ vt, int row0, int col, int dh) {
-    constexpr int R = DH / 4;
-    if constexpr (EXACT) {
+ASCA_DEV void fwd_stage_load(FwdStage<DH>& st, int c, const float* __restrict__ q, const float* __restrict__ k,
+                             const float* __restrict__ v, long ubase, long d, int T, int dh, int w, int lane) {
+    using L = FwdL<DH>;
+    constexpr int CK = L::CK;
+    const int t0 = c * CK;
 #pragma unroll
-        for (int j = 0; j < R; j += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(kt + row0 + j);
-            const float4 c = *reinterpret_cast<const float4*>(qt + row0 + j);
-            kk[j] = a.x; kk[j + 1] = a.y; kk[j + 2] = a.z; kk[j + 3] = a.w;
-            qq[j] = c.x; qq[j + 1] = c.y; qq[j + 2] = c.z; qq[j + 3] = c.w;
-        }
-        vv = vt[col];
-    } else {
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const bool ok = row0 + j < dh;
-            const float a = kt[ok ? row0 + j : 0];
-            const float c = qt[ok ? row0 + j : 0];
-            kk[j] = ok ? a : 0.0f;
-            qq[j] = ok ? c : 0.0f;
-        }
-        const bool okc = col < dh;
-        const float x = vt[okc ? col : 0];
-        vv = okc ? x : 0.0f;
+    for (int i = 0; i < L::NKQ; ++i) {
+        const int f0 = (int)threadIdx.x + i * L::NT;
+        const int f = f0 < L::KQ_F / 2 ? f0 : 0;
+        const int tsr = f >= L::KQ_F / 4;
+        const int fl = f - tsr * (L::KQ_F / 4);
+        const int j = fl / (DH / 4), c4 = fl % (DH / 4);
+        const long t = min(t0 + j, T - 1);
+        st.kq[i] = ld4m<EXACT>((tsr ? q : k) + ubase + t * d, 4 * c4, dh);
     }
+#pragma unroll
+    for (int i = 0; i < L::NV; ++i) {
+        const int f0 = lane + 64 * i;
+        const int f = f0 < CK * 4 ? f0 : 0;
+        const int j = f / 4, part = f % 4;
+        const long t = min(t0 + j, T - 1);
+        st.v[i] = ld4m<EXACT>(v + ubase + t * d, w * 16 + part * 4, dh);
+    }
+}
+
+template <int DH>
+ASCA_DEV void fwd_stage_store(const FwdStage<DH>& st, float* __restrict__ buf, int w, int lane) {
+    using L = FwdL<DH>;
+    constexpr int CK = L::CK;
+#pragma unroll
+    for (int i = 0; i < L::NKQ; ++i) {
+        const int f = (int)threadIdx.x + i * L::NT;
+        if (f < L::KQ_F / 2) {
+            const int tsr = f >= L::KQ_F / 4;
+            const int fl = f - tsr * (L::KQ_F / 4);
+            const int j = fl / (DH / 4), c4 = fl % (DH / 4);
+            *reinterpret_cast<float4*>(buf + tsr * L::KQ_F + j * DH + 4 * c4) = st.kq[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < L::NV; ++i) {
+        const int f = lane + 64 * i;
+        if (f < CK * 4) {
+            const int j = f / 4, part = f % 4;
+            *reinterpret_cast<float4*>(buf + 2 * L::KQ_F + (w * CK + j) * 16 + part * 4) = st.v[i];
+        }
+    }
+}
+
+// LDS -> registers: the k, q rows and the v value one lane needs for step jj.
+template <int DH>
+ASCA_DEV void fwd_rd(float (&kk)[DH / 4], float (&qq)[DH / 4], float& vv, const float* __restrict__ buf, int jj,
+                     int w, int row0, int c) {
+    using L = FwdL<DH>;
+#pragma unroll
+    for (int j = 0; j < DH / 4; j += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(buf + jj * DH + row0 + j);
+        const float4 e = *reinterpret_cast<const float4*>(buf + L::KQ_F + jj * DH + row0 + j);
+        kk[j] = a.x; kk[j + 1] = a.y; kk[j + 2] = a.z; kk[j + 3] = a.w;
+        qq[j] = e.x; qq[j + 1] = e.y; qq[j + 2] = e.z; qq[j + 3] = e.w;
+    }
+    vv = buf[2 * L::KQ_F + (w * L::CK + jj) * 16 + c];
 }
 
 // One block per (sequence, head) unit, unit = h*B + b (the reference's s_pre
@@ -116,8 +165,12 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
     const float* __restrict__ alpha, const float* __restrict__ beta, float* __restrict__ o,
     float* __restrict__ sk_out, float* __restrict__ ckpt, int B, int T, int H, int dh, int nslots) {
     using S = DS<DH>;
-    constexpr int R = S::R, CK = S::CK, PF = S::PF;
-    static_assert(CK % PF == 0 && 2 * CK <= 64, "chunk layout");
+    using L = FwdL<DH>;
+    constexpr int R = S::R, CK = S::CK, G = CK < 4 ? CK : 4;
+    static_assert(2 * CK <= 64 && CK % G == 0, "chunk layout");
+    __shared__ float4 lds4[2 * L::BUF_F / 4];
+    float* const lds = reinterpret_cast<float*>(lds4);
+
     const int unit = blockIdx.x;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -127,17 +180,15 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
     const long d = (long)H * dh;
     const long dh2 = (long)dh * dh;
     const long ubase = (long)b * T * d + (long)h * dh;
-    const float* qb = q + ubase;
-    const float* kb = k + ubase;
-    const float* vb = v + ubase;
     float* ob = o + ubase;
     float* skb = sk_out + ubase;
     const long gbase = (long)b * T * H + h;
     float* ckb = ckpt + (long)unit * nslots * dh2;
     const bool col_ok = EXACT || col < dh;
     float* const tr = trash_f(threadIdx.x);
+    const int nchunk = (T + CK - 1) / CK;
 
-    // gates of chunk t0: lane l < CK holds alpha of step t0+l, CK <= l < 2CK beta of t0+l-CK
+    // gates of a chunk: lane l < CK holds alpha of step t0+l, CK <= l < 2CK beta of t0+l-CK
     const int gl = lane & (2 * CK - 1);
     const float* gsrc = (gl < CK ? alpha : beta) + gbase;
     const int gstep = gl % CK;
@@ -146,19 +197,20 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
 #pragma unroll
     for (int j = 0; j < R; ++j) s[j] = 0.0f;
 
-    float kk[PF][R], qq[PF][R], vv[PF];
-#pragma unroll
-    for (int i = 0; i < PF - 1; ++i) {
-        const long t = min(i, T - 1);
-        fwd_load<DH, EXACT>(kk[i], qq[i], vv[i], kb + t * d, qb + t * d, vb + t * d, row0, col, dh);
-    }
+    FwdStage<DH> stg;
+    fwd_stage_load<DH, EXACT>(stg, 0, q, k, v, ubase, d, T, dh, w, lane);
     float gnext = gsrc[(long)min(gstep, T - 1) * H];
+    fwd_stage_store<DH>(stg, lds, w, lane);
+    __syncthreads();
 
-    for (int t0 = 0; t0 < T; t0 += CK) {
+    for (int ci = 0; ci < nchunk; ++ci) {
+        const int t0 = ci * CK;
+        const float* buf = lds + (ci & 1) * L::BUF_F;
         const float gcur = gnext;
         gnext = gsrc[(long)min(t0 + CK + gstep, T - 1) * H];
+        fwd_stage_load<DH, EXACT>(stg, min(ci + 1, nchunk - 1), q, k, v, ubase, d, T, dh, w, lane);
         {   // checkpoint: S before step t0, as S^T
-            float* dst = ckb + (long)(t0 / CK) * dh2 + (long)col * dh + row0;
+            float* dst = ckb + (long)ci * dh2 + (long)col * dh + row0;
             if constexpr (EXACT) {
 #pragma unroll
                 for (int j = 0; j < R; j += 4)
@@ -168,15 +220,13 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
                 for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr) = s[j];
             }
         }
+        float kk[2][R], qq[2][R], vv[2];
+        fwd_rd<DH>(kk[0], qq[0], vv[0], buf, 0, w, row0, c);
+        float hold_o = 0.0f, hold_s = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < CK; ++jj) {
-            const int t = t0 + jj;
-            {
-                const int ls = (jj + PF - 1) % PF;
-                const long tl = min(t + PF - 1, T - 1);
-                fwd_load<DH, EXACT>(kk[ls], qq[ls], vv[ls], kb + tl * d, qb + tl * d, vb + tl * d, row0, col, dh);
-            }
-            const int cs = jj % PF;
+            if (jj + 1 < CK) fwd_rd<DH>(kk[(jj + 1) & 1], qq[(jj + 1) & 1], vv[(jj + 1) & 1], buf, jj + 1, w, row0, c);
+            const int cs = jj & 1;
             const float a = readlane_f(gcur, jj);
             const float bt = readlane_f(gcur, CK + jj);
             float a0 = 0.0f, a1 = 0.0f;
@@ -196,10 +246,19 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
                 o1 = fmaf(s[j + 1], qq[cs][j + 1], o1);
             }
             const float oo = group_sum<4>(o0 + o1);
-            const bool tv = t < T && col_ok;
-            *((p == 0 && tv) ? ob + (long)t * d + col : tr) = oo;
-            *((p == 1 && tv) ? skb + (long)t * d + col : tr) = sk;
+            // lane p of the column quad keeps the results of step t0 + G*m + p and
+            // writes them once every G steps
+            hold_o = (p == jj % G) ? oo : hold_o;
+            hold_s = (p == jj % G) ? sk : hold_s;
+            if (jj % G == G - 1) {
+                const int ts = t0 + jj - (G - 1) + p;
+                const bool ok = p < G && ts < T && col_ok;
+                *(ok ? ob + (long)ts * d + col : tr) = hold_o;
+                *(ok ? skb + (long)ts * d + col : tr + 64) = hold_s;
+            }
         }
+        fwd_stage_store<DH>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
+        __syncthreads();
     }
 }
 
@@ -230,9 +289,16 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_states_k(
         for (int j = 0; j < R; ++j)
             if (col < dh && row0 + j < dh) st[(long)t * dh2 + (long)(row0 + j) * dh + col] = s[j];
         if (t == T) break;
-        float kk[R], qq[R], vv;
-        fwd_load<DH, false>(kk, qq, vv, k + ubase + (long)t * d, q + ubase + (long)t * d, v + ubase + (long)t * d,
-                            row0, col, dh);
+        float kk[R], qq[R];
+        const float* kt = k + ubase + (long)t * d;
+        const float* qt = q + ubase + (long)t * d;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const bool ok = row0 + j < dh;
+            kk[j] = ok ? kt[row0 + j] : 0.0f;
+            qq[j] = ok ? qt[row0 + j] : 0.0f;
+        }
+        const float vv = col < dh ? v[ubase + (long)t * d + col] : 0.0f;
         const float a = alpha[(long)b * T * H + (long)t * H + h];
         const float bt = beta[(long)b * T * H + (long)t * H + h];
         float a0 = 0.0f, a1 = 0.0f;
@@ -250,24 +316,142 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_states_k(
 
 // ----------------------------------------------------------------- backward
 
-// Per-step operands of the reverse walk, read from LDS: the stash tile of
-// S_{t-1} (rows rowb..rowb+M-1, columns colb..colb+3), q and k rows, the dO, v
-// and sk column quads and the two gates.
+// ----------------------------------------------------------------- backward
+//
+// Shape of the backward: a unit runs on DH/8 waves (two per SIMD at dh = 64),
+// each owning 8 value columns.  Lane (rg = lane & 15, cg = lane >> 4) owns rows
+// rg*M .. rg*M+M-1 (M = DH/16) of columns colb, colb+1 (colb = 8w + 2cg).  A
+// C-step segment is recomputed into registers (the stash), so both phases are
+// unrolled over C steps; a tail segment past T is padded with dO = 0 steps,
+// which leave dS unchanged and whose outputs are dropped.
+
+template <int DH>
+struct BS {
+    static constexpr int W = DH / 8;
+    static constexpr int NT = 64 * W;
+    static constexpr int M = DH / 16;
+    static constexpr int CK = DS<DH>::CK;
+    // one LDS buffer (floats); two are used alternately by consecutive segments
+    static constexpr int RED_F = CK * W * DH;    // dq / dk row sums per wave
+    static constexpr int RAB_F = CK * W * 2;     // dalpha / dbeta per wave
+    static constexpr int STQK_F = CK * DH;       // staged q (and k) rows
+    static constexpr int STW_F = W * CK * 24;    // staged dO, v, sk (8 columns each) per wave
+    static constexpr int STAB_F = 2 * CK;        // staged alpha, beta
+    static constexpr int BUF_F = 2 * RED_F + RAB_F + 2 * STQK_F + STW_F + STAB_F;
+    static constexpr size_t LDS = 2 * (size_t)BUF_F * 4;
+    // staging registers
+    static constexpr int QK4 = CK * DH / 4;             // float4 per staged tensor (q or k)
+    static constexpr int NQ = (2 * QK4 + NT - 1) / NT;  // staged q/k float4 per thread
+    static constexpr int W4 = CK * 6;                   // per-wave float4 of dO, v, sk
+    static constexpr int NW = (W4 + 63) / 64;
+};
+
+template <int DH>
+struct BStage {
+    float4 rq[BS<DH>::NQ], rw[BS<DH>::NW];
+    float rab;
+    float rck[2][BS<DH>::M];  // checkpoint tile: column colb+n, rows rowb..rowb+M-1
+};
+
+template <int DH, bool EXACT>
+ASCA_DEV void bstage_load(BStage<DH>& st, int g, const float* __restrict__ q, const float* __restrict__ k,
+                          const float* __restrict__ v, const float* __restrict__ d_o,
+                          const float* __restrict__ skv, const float* __restrict__ alpha,
+                          const float* __restrict__ beta, const float* __restrict__ ckb, long ubase, long gbase,
+                          long d, long dh2, int T, int H, int dh, int w, int lane, int rowb, int colb) {
+    using S = BS<DH>;
+    constexpr int CK = S::CK, M = S::M;
+    const int t0 = g * CK;
+#pragma unroll
+    for (int i = 0; i < S::NQ; ++i) {
+        const int f0 = (int)threadIdx.x + i * S::NT;
+        const int f = f0 < 2 * S::QK4 ? f0 : 0;
+        const int tsr = f >= S::QK4;
+        const int fl = f - tsr * S::QK4;
+        const int j = fl / (DH / 4), c4 = fl % (DH / 4);
+        const long t = min(t0 + j, T - 1);
+        st.rq[i] = ld4m<EXACT>((tsr ? k : q) + ubase + t * d, 4 * c4, dh);
+    }
+#pragma unroll
+    for (int i = 0; i < S::NW; ++i) {
+        const int f0 = lane + 64 * i;
+        const int f = f0 < S::W4 ? f0 : 0;
+        const int tsr = f / (CK * 2);          // 0: dO, 1: v, 2: sk
+        const int rem = f % (CK * 2);
+        const int j = rem / 2, half = rem % 2;
+        const long t = min(t0 + j, T - 1);
+        const float* src = tsr == 0 ? d_o : (tsr == 1 ? v : skv);
+        float4 x = ld4m<EXACT>(src + ubase + t * d, w * 8 + half * 4, dh);
+        if (tsr == 0 && t0 + j >= T) x = make_float4(0.f, 0.f, 0.f, 0.f);   // padded steps carry dO = 0
+        st.rw[i] = x;
+    }
+    {
+        const int gl = lane & (2 * CK - 1);
+        const long t = min(t0 + gl % CK, T - 1);
+        st.rab = (gl < CK ? alpha : beta)[gbase + t * H];
+    }
+    const float* cks = ckb + (long)g * dh2;
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        const int i = colb + n;
+        if constexpr (EXACT && M % 4 == 0) {
+#pragma unroll
+            for (int m = 0; m < M; m += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(cks + (long)i * dh + rowb + m);
+                st.rck[n][m] = x.x; st.rck[n][m + 1] = x.y; st.rck[n][m + 2] = x.z; st.rck[n][m + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const bool ok = i < dh && rowb + m < dh;
+                const float x = cks[ok ? (long)i * dh + rowb + m : 0];
+                st.rck[n][m] = ok ? x : 0.0f;
+            }
+        }
+    }
+}
+
+template <int DH>
+ASCA_DEV void bstage_store(const BStage<DH>& st, float* __restrict__ st_q, float* __restrict__ st_k,
+                           float* __restrict__ st_w, float* __restrict__ st_ab, int w, int lane) {
+    using S = BS<DH>;
+    constexpr int CK = S::CK;
+#pragma unroll
+    for (int i = 0; i < S::NQ; ++i) {
+        const int f = (int)threadIdx.x + i * S::NT;
+        if (f < 2 * S::QK4) {
+            const int tsr = f >= S::QK4;
+            const int fl = f - tsr * S::QK4;
+            const int j = fl / (DH / 4), c4 = fl % (DH / 4);
+            *reinterpret_cast<float4*>((tsr ? st_k : st_q) + j * DH + 4 * c4) = st.rq[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < S::NW; ++i) {
+        const int f = lane + 64 * i;
+        if (f < S::W4) {
+            const int tsr = f / (CK * 2);
+            const int rem = f % (CK * 2);
+            const int j = rem / 2, half = rem % 2;
+            *reinterpret_cast<float4*>(st_w + (w * CK + j) * 24 + tsr * 8 + half * 4) = st.rw[i];
+        }
+    }
+    if (w == 0 && lane < 2 * CK) st_ab[lane] = st.rab;
+}
+
+// LDS operands of reverse step j: q, k rows and the dO, v, sk column pairs.
 template <int M>
 struct BOps {
-    float4 s[M];
     float q[M], k[M];
-    float4 dO, v, sk;
+    float2 dO, v, sk;
     float a, b;
 };
 
 template <int DH>
-ASCA_DEV void lds_ops(BOps<DH / 16>& o, const float4* __restrict__ stash, const float* __restrict__ st_q,
-                      const float* __restrict__ st_k, const float* __restrict__ st_w,
-                      const float* __restrict__ st_ab, int j, int w, int lane, int rowb, int cg) {
-    constexpr int M = DS<DH>::M, W = DS<DH>::W, CK = DS<DH>::CK;
-#pragma unroll
-    for (int m = 0; m < M; ++m) o.s[m] = stash[((j * W + w) * M + m) * 64 + lane];
+ASCA_DEV void bops_read(BOps<DH / 16>& o, const float* __restrict__ st_q, const float* __restrict__ st_k,
+                        const float* __restrict__ st_w, const float* __restrict__ st_ab, int j, int w, int rowb,
+                        int cg) {
+    constexpr int M = DH / 16, CK = BS<DH>::CK;
     if constexpr (M % 4 == 0) {
 #pragma unroll
         for (int m = 0; m < M; m += 4) {
@@ -283,100 +467,85 @@ ASCA_DEV void lds_ops(BOps<DH / 16>& o, const float4* __restrict__ stash, const 
             o.k[m] = st_k[j * DH + rowb + m];
         }
     }
-    const float* sw = st_w + (w * CK + j) * 48 + cg * 4;
-    o.dO = *reinterpret_cast<const float4*>(sw);
-    o.v = *reinterpret_cast<const float4*>(sw + 16);
-    o.sk = *reinterpret_cast<const float4*>(sw + 32);
+    const float* sw = st_w + (w * CK + j) * 24 + cg * 2;
+    o.dO = *reinterpret_cast<const float2*>(sw);
+    o.v = *reinterpret_cast<const float2*>(sw + 8);
+    o.sk = *reinterpret_cast<const float2*>(sw + 16);
     o.a = st_ab[j];
     o.b = st_ab[CK + j];
 }
 
 // One reverse step of the BPTT for this lane's tile (rust/src/delta.rs:485-572
-// reorganised per value column; see the file header).  Updates ds in place,
-// stores dv, and leaves the dq / dk row sums and the dalpha / dbeta totals of
-// this wave in LDS for the epilogue.
+// reorganised per value column).  sm: S_{t-1} tile from the register stash.
+// Updates ds in place, stores dv, and leaves the dq / dk row sums and the
+// dalpha / dbeta totals of this wave in LDS for the epilogue.
 template <int DH, bool EXACT>
-ASCA_DEV void bwd_step(const BOps<DH / 16>& in, float (&ds)[DH / 16][4], float* __restrict__ red_q,
-                       float* __restrict__ red_k, float* __restrict__ red_ab, float* __restrict__ dv_dst,
-                       float* __restrict__ tr, int jj, int w, int lane, int rg, int cg, int rowb, int colb,
-                       int dh) {
-    constexpr int M = DS<DH>::M, W = DS<DH>::W;
-    float sm[M][4];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        sm[m][0] = in.s[m].x; sm[m][1] = in.s[m].y; sm[m][2] = in.s[m].z; sm[m][3] = in.s[m].w;
-    }
+ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], float (&ds)[DH / 16][2],
+                       float* __restrict__ rq, float* __restrict__ rk, float* __restrict__ rab,
+                       float* __restrict__ dv_dst, float* __restrict__ tr, bool tvalid, int lane, int rg, int cg,
+                       int rowb, int colb, int dh) {
+    constexpr int M = DH / 16;
     const float a = in.a, bb = in.b;
-    const float dO[4] = {in.dO.x, in.dO.y, in.dO.z, in.dO.w};
-    const float vv[4] = {in.v.x, in.v.y, in.v.z, in.v.w};
-    const float sk[4] = {in.sk.x, in.sk.y, in.sk.z, in.sk.w};
+    const float dO[2] = {in.dO.x, in.dO.y};
+    const float vv[2] = {in.v.x, in.v.y};
+    const float sk[2] = {in.sk.x, in.sk.y};
 
     // dS += q dO^T  (delta.rs:508-511)
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ds[m][n] = fmaf(in.q[m], dO[n], ds[m][n]);
+        for (int n = 0; n < 2; ++n) ds[m][n] = fmaf(in.q[m], dO[n], ds[m][n]);
     // du = dS^T k  (delta.rs:536-542): 16-lane butterfly over row groups
-    float du[4];
+    float du[2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < 2; ++n) {
         float acc = 0.0f;
 #pragma unroll
         for (int m = 0; m < M; ++m) acc = fmaf(ds[m][n], in.k[m], acc);
         du[n] = group_sum<16>(acc);
     }
-    float wv[4], u[4], dsk[4];
+    float wv[2], u[2], dsk[2];
     const float c1 = -bb * a;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < 2; ++n) {
         wv[n] = vv[n] - a * sk[n];
         u[n] = bb * wv[n];
         dsk[n] = c1 * du[n];
     }
     // dv = beta du  (delta.rs:550), stored by the lanes of row group 0
     if constexpr (EXACT) {
-        *(rg == 0 ? reinterpret_cast<float4*>(dv_dst) : reinterpret_cast<float4*>(tr)) =
-            make_float4(bb * du[0], bb * du[1], bb * du[2], bb * du[3]);
+        *(rg == 0 && tvalid ? reinterpret_cast<float2*>(dv_dst) : reinterpret_cast<float2*>(tr)) =
+            make_float2(bb * du[0], bb * du[1]);
     } else {
 #pragma unroll
-        for (int n = 0; n < 4; ++n) *((rg == 0 && colb + n < dh) ? dv_dst + n : tr + n) = bb * du[n];
+        for (int n = 0; n < 2; ++n) *((rg == 0 && tvalid && colb + n < dh) ? dv_dst + n : tr + n) = bb * du[n];
     }
 
-    // Off-critical-path partial sums over this lane's 4 columns.
+    // Off-critical-path partial sums over this lane's 2 columns.
     //   dq = S_t dO = alpha S_{t-1} dO + k (u.dO)          (delta.rs:504-507)
     //   dk = dS u + S_{t-1} dsk                           (delta.rs:532-534, 556-558)
     //   dalpha = <dS, S_{t-1}> - beta du.sk               (delta.rs:530, 552)
     //   dbeta = du.(v - alpha sk)                         (delta.rs:549)
-    float y = 0.0f;
-#pragma unroll
-    for (int n = 0; n < 4; ++n) y = fmaf(dO[n], u[n], y);
-    float adO[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) adO[n] = a * dO[n];
+    const float y = fmaf(dO[1], u[1], dO[0] * u[0]);
+    const float adO[2] = {a * dO[0], a * dO[1]};
     float pq[M], pk[M];
     float pa0 = 0.0f, pa1 = 0.0f;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        float xq = in.k[m] * y, xk = 0.0f;
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            xq = fmaf(sm[m][n], adO[n], xq);
-            xk = fmaf(u[n], ds[m][n], xk);
-            xk = fmaf(dsk[n], sm[m][n], xk);
-        }
+        float xq = in.k[m] * y;
+        xq = fmaf(sm[m][0], adO[0], xq);
+        xq = fmaf(sm[m][1], adO[1], xq);
+        float xk = u[0] * ds[m][0];
+        xk = fmaf(u[1], ds[m][1], xk);
+        xk = fmaf(dsk[0], sm[m][0], xk);
+        xk = fmaf(dsk[1], sm[m][1], xk);
         pq[m] = xq;
         pk[m] = xk;
         pa0 = fmaf(ds[m][0], sm[m][0], pa0);
         pa1 = fmaf(ds[m][1], sm[m][1], pa1);
-        pa0 = fmaf(ds[m][2], sm[m][2], pa0);
-        pa1 = fmaf(ds[m][3], sm[m][3], pa1);
     }
-    float ea = 0.0f, eb = 0.0f;
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        ea = fmaf(-bb * du[n], sk[n], ea);
-        eb = fmaf(du[n], wv[n], eb);
-    }
+    const float ea = fmaf(-bb * du[1], sk[1], -bb * du[0] * sk[0]);
+    const float eb = fmaf(du[1], wv[1], du[0] * wv[0]);
     float pa = pa0 + pa1 + (rg == 0 ? ea : 0.0f);
     float pb = rg == 0 ? eb : 0.0f;
 
@@ -384,12 +553,10 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, float (&ds)[DH / 16][4], float* 
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) ds[m][n] = a * ds[m][n] + in.k[m] * dsk[n];
+        for (int n = 0; n < 2; ++n) ds[m][n] = a * ds[m][n] + in.k[m] * dsk[n];
 
     // Column sums of pq, pk over the 4 column groups (lane bits 4,5),
     // transposed so each lane keeps whole-row sums.
-    float* rq = red_q + (jj * W + w) * DH;
-    float* rk = red_k + (jj * W + w) * DH;
     if constexpr (M == 1) {
         const float zq = add_xor16(add_xor32(pq[0]));
         const float zk = add_xor16(add_xor32(pk[0]));
@@ -416,107 +583,7 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, float (&ds)[DH / 16][4], float* 
     }
     pa = wave_sum(pa);
     pb = wave_sum(pb);
-    if (lane == 0) {
-        red_ab[(jj * W + w) * 2 + 0] = pa;
-        red_ab[(jj * W + w) * 2 + 1] = pb;
-    }
-}
-
-// Staged inputs of one segment, loaded one segment ahead into registers.
-template <int DH>
-struct Stage {
-    static constexpr int CK = DS<DH>::CK, NT = DS<DH>::THREADS, M = DS<DH>::M;
-    static constexpr int QK4 = CK * DH / 4;             // float4 per staged tensor (q or k)
-    static constexpr int NQ = (2 * QK4 + NT - 1) / NT;  // staged q/k float4 per thread
-    static constexpr int W4 = CK * 12;                  // per-wave float4 of dO, v, sk
-    static constexpr int NW = (W4 + 63) / 64;
-    float4 rq[NQ], rw[NW];
-    float rab;
-    float rck[4][M];  // checkpoint tile: column colb+n, rows rowb..rowb+M-1
-};
-
-template <int DH, bool EXACT>
-ASCA_DEV void stage_load(Stage<DH>& st, int g, const float* __restrict__ q, const float* __restrict__ k,
-                         const float* __restrict__ v, const float* __restrict__ d_o,
-                         const float* __restrict__ skv, const float* __restrict__ alpha,
-                         const float* __restrict__ beta, const float* __restrict__ ckb, long ubase, long gbase,
-                         long d, long dh2, int T, int H, int dh, int w, int lane, int rowb, int colb) {
-    using SG = Stage<DH>;
-    constexpr int CK = SG::CK, M = SG::M;
-    const int t0 = g * CK;
-#pragma unroll
-    for (int i = 0; i < SG::NQ; ++i) {
-        const int f0 = (int)threadIdx.x + i * SG::NT;
-        const int f = f0 < 2 * SG::QK4 ? f0 : 0;
-        const int tsr = f >= SG::QK4;
-        const int fl = f - tsr * SG::QK4;
-        const int j = fl / (DH / 4), c4 = fl % (DH / 4);
-        const long t = min(t0 + j, T - 1);
-        st.rq[i] = ld4m<EXACT>((tsr ? k : q) + ubase + t * d, 4 * c4, dh);
-    }
-#pragma unroll
-    for (int i = 0; i < SG::NW; ++i) {
-        const int f0 = lane + 64 * i;
-        const int f = f0 < SG::W4 ? f0 : 0;
-        const int tsr = f / (CK * 4);
-        const int rem = f % (CK * 4);
-        const int j = rem / 4, part = rem % 4;
-        const long t = min(t0 + j, T - 1);
-        const float* src = tsr == 0 ? d_o : (tsr == 1 ? v : skv);
-        st.rw[i] = ld4m<EXACT>(src + ubase + t * d, w * 16 + part * 4, dh);
-    }
-    {
-        const int gl = lane & (2 * CK - 1);
-        const long t = min(t0 + gl % CK, T - 1);
-        st.rab = (gl < CK ? alpha : beta)[gbase + t * H];
-    }
-    const float* cks = ckb + (long)g * dh2;
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        const int i = colb + n;
-        if constexpr (EXACT && M % 4 == 0) {
-#pragma unroll
-            for (int m = 0; m < M; m += 4) {
-                const float4 x = *reinterpret_cast<const float4*>(cks + (long)i * dh + rowb + m);
-                st.rck[n][m] = x.x; st.rck[n][m + 1] = x.y; st.rck[n][m + 2] = x.z; st.rck[n][m + 3] = x.w;
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const bool ok = i < dh && rowb + m < dh;
-                const float x = cks[ok ? (long)i * dh + rowb + m : 0];
-                st.rck[n][m] = ok ? x : 0.0f;
-            }
-        }
-    }
-}
-
-template <int DH>
-ASCA_DEV void stage_store(const Stage<DH>& st, float* __restrict__ st_q, float* __restrict__ st_k,
-                          float* __restrict__ st_w, float* __restrict__ st_ab, int w, int lane) {
-    using SG = Stage<DH>;
-    constexpr int CK = SG::CK;
-#pragma unroll
-    for (int i = 0; i < SG::NQ; ++i) {
-        const int f = (int)threadIdx.x + i * SG::NT;
-        if (f < 2 * SG::QK4) {
-            const int tsr = f >= SG::QK4;
-            const int fl = f - tsr * SG::QK4;
-            const int j = fl / (DH / 4), c4 = fl % (DH / 4);
-            *reinterpret_cast<float4*>((tsr ? st_k : st_q) + j * DH + 4 * c4) = st.rq[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < SG::NW; ++i) {
-        const int f = lane + 64 * i;
-        if (f < SG::W4) {
-            const int tsr = f / (CK * 4);
-            const int rem = f % (CK * 4);
-            const int j = rem / 4, part = rem % 4;
-            *reinterpret_cast<float4*>(st_w + ((w * CK + j) * 3 + tsr) * 16 + part * 4) = st.rw[i];
-        }
-    }
-    if (w == 0 && lane < 2 * CK) st_ab[lane] = st.rab;
+    if (lane == 0) *reinterpret_cast<float2*>(rab) = make_float2(pa, pb);
 }
 
 // Backward of one unit per block.  Output pointers are already offset to the
@@ -524,31 +591,23 @@ ASCA_DEV void stage_store(const Stage<DH>& st, float* __restrict__ st_q, float* 
 // and the per-head scalars at ga[r*ldg + h].  FUSED applies the L2-norm backward
 // (rust/src/delta.rs:677-698) and the sigmoid backward (delta.rs:602-611).
 template <int DH, bool EXACT, bool FUSED>
-__global__ __launch_bounds__(DS<DH>::THREADS) void delta_bwd_k(
+__global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ alpha, const float* __restrict__ beta, const float* __restrict__ d_o,
     const float* __restrict__ skv, const float* __restrict__ ckpt, const float* __restrict__ qnorm,
     const float* __restrict__ knorm, float* __restrict__ gq, float* __restrict__ gk,
     float* __restrict__ gv, long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, int B,
     int T, int H, int dh, int nslots) {
-    using S = DS<DH>;
+    using S = BS<DH>;
     constexpr int M = S::M, W = S::W, CK = S::CK;
-
     extern __shared__ float4 lds4[];
-    float4* stash = lds4;                                            // [CK][W][M][64]
-    float* red_q = reinterpret_cast<float*>(lds4 + S::STASH_F4);     // [CK][W][DH]
-    float* red_k = red_q + S::RED_F;                                 // [CK][W][DH]
-    float* red_ab = red_k + S::RED_F;                                // [CK][W][2]
-    float* st_q = red_ab + S::RAB_F;                                 // [CK][DH]
-    float* st_k = st_q + S::STQK_F;                                  // [CK][DH]
-    float* st_w = st_k + S::STQK_F;                                  // [W][CK][3][16]
-    float* st_ab = st_w + S::STW_F;                                  // [2][CK]
+    float* const lds = reinterpret_cast<float*>(lds4);
 
     const int unit = blockIdx.x;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int rg = lane & 15, cg = lane >> 4;
-    const int colb = w * 16 + cg * 4;
+    const int colb = w * 8 + cg * 2;
     const int rowb = rg * M;
     const long d = (long)H * dh;
     const long dh2 = (long)dh * dh;
@@ -557,73 +616,75 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_bwd_k(
     const long hoff = (long)h * dh;
     const float* ckb = ckpt + (long)unit * nslots * dh2;
     const int nseg = (T + CK - 1) / CK;
-    float* const tr = trash_f(threadIdx.x * 4);
+    float* const tr = trash_f(threadIdx.x * 2);
 
-    float ds[M][4];
+    float ds[M][2];
 #pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int n = 0; n < 4; ++n) ds[m][n] = 0.0f;
+    for (int m = 0; m < M; ++m) ds[m][0] = ds[m][1] = 0.0f;
 
-    Stage<DH> stg;
-    stage_load<DH, EXACT>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T, H, dh, w, lane,
-                          rowb, colb);
+    BStage<DH> stg;
+    bstage_load<DH, EXACT>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T, H, dh, w,
+                           lane, rowb, colb);
     for (int g = nseg - 1; g >= 0; --g) {
         const int t0 = g * CK;
-        const int len = min(CK, T - t0);
-        float s[M][4];
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-#pragma unroll
-            for (int n = 0; n < 4; ++n) s[m][n] = stg.rck[n][m];
-        stage_store<DH>(stg, st_q, st_k, st_w, st_ab, w, lane);
-        stage_load<DH, EXACT>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T,
-                              H, dh, w, lane, rowb, colb);
-        __syncthreads();  // staging visible; every wave is past the previous epilogue
+        float* const buf = lds + (g & 1) * S::BUF_F;
+        float* const red_q = buf;                        // [CK][W][DH]
+        float* const red_k = red_q + S::RED_F;           // [CK][W][DH]
+        float* const red_ab = red_k + S::RED_F;          // [CK][W][2]
+        float* const st_q = red_ab + S::RAB_F;           // [CK][DH]
+        float* const st_k = st_q + S::STQK_F;            // [CK][DH]
+        float* const st_w = st_k + S::STQK_F;            // [W][CK][24]
+        float* const st_ab = st_w + S::STW_F;            // [2][CK]
 
-        // ---- phase A: stash S_{t0} .. S_{t0+len-1}
+        // stash[j] = S before step t0 + j (tile of this lane)
+        float stash[CK][M][2];
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-            stash[((0 * W + w) * M + m) * 64 + lane] = make_float4(s[m][0], s[m][1], s[m][2], s[m][3]);
-        for (int j = 1; j < len; ++j) {
+        for (int m = 0; m < M; ++m) {
+            stash[0][m][0] = stg.rck[0][m];
+            stash[0][m][1] = stg.rck[1][m];
+        }
+        bstage_store<DH>(stg, st_q, st_k, st_w, st_ab, w, lane);
+        bstage_load<DH, EXACT>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T,
+                               H, dh, w, lane, rowb, colb);
+        __syncthreads();  // staging of this segment visible to all waves
+
+        // ---- phase A: recompute S_{t0+1} .. S_{t0+CK-1} into the stash
+#pragma unroll
+        for (int j = 1; j < CK; ++j) {
             const int jp = j - 1;
             float km[M];
 #pragma unroll
             for (int m = 0; m < M; ++m) km[m] = st_k[jp * DH + rowb + m];
-            const float* sw = st_w + (w * CK + jp) * 48 + cg * 4;
-            const float4 vv = *reinterpret_cast<const float4*>(sw + 16);
-            const float4 sk = *reinterpret_cast<const float4*>(sw + 32);
+            const float* sw = st_w + (w * CK + jp) * 24 + cg * 2;
+            const float2 vv = *reinterpret_cast<const float2*>(sw + 8);
+            const float2 sk = *reinterpret_cast<const float2*>(sw + 16);
             const float a = st_ab[jp], bt = st_ab[CK + jp];
-            const float u[4] = {bt * (vv.x - a * sk.x), bt * (vv.y - a * sk.y), bt * (vv.z - a * sk.z),
-                                bt * (vv.w - a * sk.w)};
+            const float u0 = bt * (vv.x - a * sk.x), u1 = bt * (vv.y - a * sk.y);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-#pragma unroll
-                for (int n = 0; n < 4; ++n) s[m][n] = a * s[m][n] + km[m] * u[n];
-                stash[((j * W + w) * M + m) * 64 + lane] = make_float4(s[m][0], s[m][1], s[m][2], s[m][3]);
+                stash[j][m][0] = a * stash[jp][m][0] + km[m] * u0;
+                stash[j][m][1] = a * stash[jp][m][1] + km[m] * u1;
             }
         }
 
-        // ---- phase B: steps t0+len-1 .. t0 in reverse, operands prefetched one step ahead
+        // ---- phase B: steps t0+CK-1 .. t0 in reverse, LDS operands one step ahead
         {
-            BOps<M> opA, opB;
-            lds_ops<DH>(opA, stash, st_q, st_k, st_w, st_ab, len - 1, w, lane, rowb, cg);
-            for (int jj = len - 1; jj >= 0; jj -= 2) {
-                lds_ops<DH>(opB, stash, st_q, st_k, st_w, st_ab, jj > 0 ? jj - 1 : 0, w, lane, rowb, cg);
-                bwd_step<DH, EXACT>(opA, ds, red_q, red_k, red_ab, gv + ((long)b * T + t0 + jj) * ldx + hoff + colb,
-                                    tr, jj, w, lane, rg, cg, rowb, colb, dh);
-                if (jj == 0) break;
-                lds_ops<DH>(opA, stash, st_q, st_k, st_w, st_ab, jj > 1 ? jj - 2 : 0, w, lane, rowb, cg);
-                bwd_step<DH, EXACT>(opB, ds, red_q, red_k, red_ab,
-                                    gv + ((long)b * T + t0 + jj - 1) * ldx + hoff + colb, tr, jj - 1, w, lane, rg,
-                                    cg, rowb, colb, dh);
+            BOps<M> op[2];
+            bops_read<DH>(op[(CK - 1) & 1], st_q, st_k, st_w, st_ab, CK - 1, w, rowb, cg);
+#pragma unroll
+            for (int jj = CK - 1; jj >= 0; --jj) {
+                if (jj > 0) bops_read<DH>(op[(jj - 1) & 1], st_q, st_k, st_w, st_ab, jj - 1, w, rowb, cg);
+                const int t = t0 + jj;
+                bwd_step<DH, EXACT>(op[jj & 1], stash[jj], ds, red_q + (jj * W + w) * DH, red_k + (jj * W + w) * DH,
+                                    red_ab + (jj * W + w) * 2, gv + ((long)b * T + t) * ldx + hoff + colb, tr, t < T,
+                                    lane, rg, cg, rowb, colb, dh);
             }
         }
         __syncthreads();  // red_* of this segment complete
 
         // ---- phase C: cross-wave sums, optional norm/sigmoid backward, stores
         constexpr int NA = (DH + 63) / 64;
-        for (int jj = w; jj < len; jj += W) {
+        for (int jj = w; jj < CK && t0 + jj < T; jj += W) {
             const long r = (long)b * T + t0 + jj;
             float dq[NA], dk[NA], qa[NA], ka[NA];
             float dotq = 0.0f, dotk = 0.0f;
@@ -651,8 +712,9 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_bwd_k(
             float dA = 0.0f, dB = 0.0f;
 #pragma unroll
             for (int w2 = 0; w2 < W; ++w2) {
-                dA += red_ab[(jj * W + w2) * 2 + 0];
-                dB += red_ab[(jj * W + w2) * 2 + 1];
+                const float2 x = *reinterpret_cast<const float2*>(red_ab + (jj * W + w2) * 2);
+                dA += x.x;
+                dB += x.y;
             }
             if constexpr (FUSED) {
                 dotq = wave_sum(dotq);
@@ -686,7 +748,6 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_bwd_k(
                 }
             }
         }
-        __syncthreads();  // staging and red_* free for the next segment
     }
 }
 
@@ -784,7 +845,7 @@ static int launch_bwd_t(const float* q, const float* k, const float* v, const fl
                         float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
                         hipStream_t st) {
     static bool attr = false;
-    const size_t lds = DS<DH>::LDS_BWD;
+    const size_t lds = BS<DH>::LDS;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&delta_bwd_k<DH, EXACT, FUSED>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -793,7 +854,7 @@ static int launch_bwd_t(const float* q, const float* k, const float* v, const fl
     }
     int rc = pre_launch("delta_bwd");
     if (rc) return rc;
-    hipLaunchKernelGGL((delta_bwd_k<DH, EXACT, FUSED>), dim3(B * H), dim3(DS<DH>::THREADS), lds, st, q, k, v, alpha,
+    hipLaunchKernelGGL((delta_bwd_k<DH, EXACT, FUSED>), dim3(B * H), dim3(BS<DH>::NT), lds, st, q, k, v, alpha,
                        beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, dh, ws.nslots);
     return post_launch("delta_bwd");
 }
