@@ -7,15 +7,15 @@
 //
 // Design (MI355X-first, not a translation of rust/kernels/asca.cu):
 //  * Column i of S only ever meets k, q, alpha, beta and its own v_i, sk_i, u_i,
-//    so the forward splits each (sequence, head) unit into dh/16 independent
-//    waves of 16 value columns.  Inside a wave, lane = 4*column + part; a lane
-//    keeps dh/4 rows of its column in VGPRs and S^T k, S^T q are 4-lane DPP
-//    butterflies.  The k, q rows and v columns of each C-step chunk are staged
+//    so the forward splits each (sequence, head) unit into dh/8 waves of 8 value
+//    columns that never talk to each other (two waves per SIMD at dh = 64).
+//    Inside a wave, lane = 8*column + part; a lane keeps dh/8 rows of its column
+//    in VGPRs and S^T k, S^T q are 8-lane DPP butterflies.  The k, q rows and v columns of each C-step chunk are staged
 //    once per unit in LDS (double-buffered, loaded one chunk ahead, one barrier
 //    per chunk) because per-lane global loads of the replicated rows saturate
 //    the texture-address path; the step loop is straight-line (unrolled per
 //    chunk), the gates of a chunk arrive as one lane-distributed load and are
-//    broadcast with v_readlane, outputs of 4 steps leave in one store per lane,
+//    broadcast with v_readlane, outputs of 8 steps leave in one store per lane,
 //    and masked lanes store into a trash buffer instead of branching.
 //  * The forward stores S every C steps ("checkpoints", C = 8 at dh = 64, laid
 //    out as S^T so each lane writes 16-byte vectors) and the per-step sk vector,
@@ -41,7 +41,7 @@ struct DS {
     static constexpr int THREADS = 64 * W;
     static constexpr int R = DH / 4;         // forward: rows per lane (4 lanes / column)
     // Checkpoint interval C (forward chunk = backward segment).
-    static constexpr int CK = (DH <= 32) ? 16 : (DH == 64) ? 8 : 2;
+    static constexpr int CK = (DH == 128) ? 2 : 8;
 };
 
 // Sink for the stores of masked-off lanes, so stores never need a branch.
@@ -71,30 +71,39 @@ ASCA_DEV float4 ld4m(const float* __restrict__ p, int col, int dh) {
 }
 
 // ------------------------------------------------------------------ forward
+//
+// Shape of the forward: a unit runs on DH/8 waves (two per SIMD at dh = 64),
+// each owning 8 value columns.  Lane = 8*column + part; a lane keeps rows
+// part*R .. part*R+R-1 (R = DH/8) of its column, so S^T k and S^T q are 8-lane
+// DPP butterflies (quad_perm, row_half_mirror).
 
-// LDS of the forward: two chunk buffers, each holding the k and q rows of CK
-// steps (shared by the unit's waves) and every wave's 16 v columns.
 template <int DH>
-struct FwdL {
-    static constexpr int CK = DS<DH>::CK, W = DS<DH>::W, NT = DS<DH>::THREADS;
-    static constexpr int KQ_F = CK * DH;                      // floats of k (or q) per chunk
-    static constexpr int V_F = W * CK * 16;                   // floats of v per chunk
-    static constexpr int BUF_F = 2 * KQ_F + V_F;              // one chunk buffer
+struct FS {
+    static constexpr int W = DH / 8;
+    static constexpr int NT = 64 * W;
+    static constexpr int R = DH / 8;
+    static constexpr int CK = DS<DH>::CK;
+    static constexpr int G = CK < 8 ? CK : 8;                 // steps per batched output store
+    // LDS: two chunk buffers, each the k and q rows of CK steps (shared by the
+    // unit's waves) and every wave's 8 v columns
+    static constexpr int KQ_F = CK * DH;
+    static constexpr int V_F = W * CK * 8;
+    static constexpr int BUF_F = 2 * KQ_F + V_F;
     static constexpr int NKQ = (2 * KQ_F / 4 + NT - 1) / NT;  // staged k/q float4 per thread
-    static constexpr int NV = (CK * 4 + 63) / 64;             // staged v float4 per lane
+    static constexpr int NV = (CK * 2 + 63) / 64;             // staged v float4 per lane
 };
 
 template <int DH>
 struct FwdStage {
-    float4 kq[FwdL<DH>::NKQ];
-    float4 v[FwdL<DH>::NV];
+    float4 kq[FS<DH>::NKQ];
+    float4 v[FS<DH>::NV];
 };
 
 // Global -> registers for chunk c (steps c*CK .. c*CK+CK-1, clamped to T-1).
 template <int DH, bool EXACT>
 ASCA_DEV void fwd_stage_load(FwdStage<DH>& st, int c, const float* __restrict__ q, const float* __restrict__ k,
                              const float* __restrict__ v, long ubase, long d, int T, int dh, int w, int lane) {
-    using L = FwdL<DH>;
+    using L = FS<DH>;
     constexpr int CK = L::CK;
     const int t0 = c * CK;
 #pragma unroll
@@ -110,16 +119,16 @@ ASCA_DEV void fwd_stage_load(FwdStage<DH>& st, int c, const float* __restrict__ 
 #pragma unroll
     for (int i = 0; i < L::NV; ++i) {
         const int f0 = lane + 64 * i;
-        const int f = f0 < CK * 4 ? f0 : 0;
-        const int j = f / 4, part = f % 4;
+        const int f = f0 < CK * 2 ? f0 : 0;
+        const int j = f / 2, half = f % 2;
         const long t = min(t0 + j, T - 1);
-        st.v[i] = ld4m<EXACT>(v + ubase + t * d, w * 16 + part * 4, dh);
+        st.v[i] = ld4m<EXACT>(v + ubase + t * d, w * 8 + half * 4, dh);
     }
 }
 
 template <int DH>
 ASCA_DEV void fwd_stage_store(const FwdStage<DH>& st, float* __restrict__ buf, int w, int lane) {
-    using L = FwdL<DH>;
+    using L = FS<DH>;
     constexpr int CK = L::CK;
 #pragma unroll
     for (int i = 0; i < L::NKQ; ++i) {
@@ -134,39 +143,47 @@ ASCA_DEV void fwd_stage_store(const FwdStage<DH>& st, float* __restrict__ buf, i
 #pragma unroll
     for (int i = 0; i < L::NV; ++i) {
         const int f = lane + 64 * i;
-        if (f < CK * 4) {
-            const int j = f / 4, part = f % 4;
-            *reinterpret_cast<float4*>(buf + 2 * L::KQ_F + (w * CK + j) * 16 + part * 4) = st.v[i];
+        if (f < CK * 2) {
+            const int j = f / 2, half = f % 2;
+            *reinterpret_cast<float4*>(buf + 2 * L::KQ_F + (w * CK + j) * 8 + half * 4) = st.v[i];
         }
     }
 }
 
 // LDS -> registers: the k, q rows and the v value one lane needs for step jj.
 template <int DH>
-ASCA_DEV void fwd_rd(float (&kk)[DH / 4], float (&qq)[DH / 4], float& vv, const float* __restrict__ buf, int jj,
+ASCA_DEV void fwd_rd(float (&kk)[DH / 8], float (&qq)[DH / 8], float& vv, const float* __restrict__ buf, int jj,
                      int w, int row0, int c) {
-    using L = FwdL<DH>;
+    using L = FS<DH>;
+    constexpr int R = L::R;
+    if constexpr (R % 4 == 0) {
 #pragma unroll
-    for (int j = 0; j < DH / 4; j += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(buf + jj * DH + row0 + j);
-        const float4 e = *reinterpret_cast<const float4*>(buf + L::KQ_F + jj * DH + row0 + j);
-        kk[j] = a.x; kk[j + 1] = a.y; kk[j + 2] = a.z; kk[j + 3] = a.w;
-        qq[j] = e.x; qq[j + 1] = e.y; qq[j + 2] = e.z; qq[j + 3] = e.w;
+        for (int j = 0; j < R; j += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(buf + jj * DH + row0 + j);
+            const float4 e = *reinterpret_cast<const float4*>(buf + L::KQ_F + jj * DH + row0 + j);
+            kk[j] = a.x; kk[j + 1] = a.y; kk[j + 2] = a.z; kk[j + 3] = a.w;
+            qq[j] = e.x; qq[j + 1] = e.y; qq[j + 2] = e.z; qq[j + 3] = e.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            kk[j] = buf[jj * DH + row0 + j];
+            qq[j] = buf[L::KQ_F + jj * DH + row0 + j];
+        }
     }
-    vv = buf[2 * L::KQ_F + (w * L::CK + jj) * 16 + c];
+    vv = buf[2 * L::KQ_F + (w * L::CK + jj) * 8 + c];
 }
 
 // One block per (sequence, head) unit, unit = h*B + b (the reference's s_pre
 // order, rust/src/delta.rs:54-56).  ckpt: nslots = ceil(T/CK) states per unit,
 // slot j = S^T before step j*CK (element (a, i) of S at [i*dh + a]).
 template <int DH, bool EXACT>
-__global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
+__global__ __launch_bounds__(FS<DH>::NT) void delta_fwd_k(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ alpha, const float* __restrict__ beta, float* __restrict__ o,
     float* __restrict__ sk_out, float* __restrict__ ckpt, int B, int T, int H, int dh, int nslots) {
-    using S = DS<DH>;
-    using L = FwdL<DH>;
-    constexpr int R = S::R, CK = S::CK, G = CK < 4 ? CK : 4;
+    using L = FS<DH>;
+    constexpr int R = L::R, CK = L::CK, G = L::G;
     static_assert(2 * CK <= 64 && CK % G == 0, "chunk layout");
     __shared__ float4 lds4[2 * L::BUF_F / 4];
     float* const lds = reinterpret_cast<float*>(lds4);
@@ -174,8 +191,8 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
     const int unit = blockIdx.x;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int p = lane & 3, c = lane >> 2;
-    const int col = w * 16 + c;
+    const int p = lane & 7, c = lane >> 3;
+    const int col = w * 8 + c;
     const int row0 = p * R;
     const long d = (long)H * dh;
     const long dh2 = (long)dh * dh;
@@ -185,7 +202,7 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
     const long gbase = (long)b * T * H + h;
     float* ckb = ckpt + (long)unit * nslots * dh2;
     const bool col_ok = EXACT || col < dh;
-    float* const tr = trash_f(threadIdx.x);
+    float* const tr = trash_f(threadIdx.x * 2);
     const int nchunk = (T + CK - 1) / CK;
 
     // gates of a chunk: lane l < CK holds alpha of step t0+l, CK <= l < 2CK beta of t0+l-CK
@@ -211,13 +228,13 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
         fwd_stage_load<DH, EXACT>(stg, min(ci + 1, nchunk - 1), q, k, v, ubase, d, T, dh, w, lane);
         {   // checkpoint: S before step t0, as S^T
             float* dst = ckb + (long)ci * dh2 + (long)col * dh + row0;
-            if constexpr (EXACT) {
+            if constexpr (EXACT && R % 4 == 0) {
 #pragma unroll
                 for (int j = 0; j < R; j += 4)
                     *reinterpret_cast<float4*>(dst + j) = make_float4(s[j], s[j + 1], s[j + 2], s[j + 3]);
             } else {
 #pragma unroll
-                for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr) = s[j];
+                for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr + j) = s[j];
             }
         }
         float kk[2][R], qq[2][R], vv[2];
@@ -235,7 +252,7 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
                 a0 = fmaf(s[j], kk[cs][j], a0);
                 a1 = fmaf(s[j + 1], kk[cs][j + 1], a1);
             }
-            const float sk = group_sum<4>(a0 + a1);
+            const float sk = group_sum<8>(a0 + a1);
             const float u = bt * (vv[cs] - a * sk);
             float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
@@ -245,8 +262,8 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
                 o0 = fmaf(s[j], qq[cs][j], o0);
                 o1 = fmaf(s[j + 1], qq[cs][j + 1], o1);
             }
-            const float oo = group_sum<4>(o0 + o1);
-            // lane p of the column quad keeps the results of step t0 + G*m + p and
+            const float oo = group_sum<8>(o0 + o1);
+            // lane p of the column group keeps the results of step t0 + G*m + p and
             // writes them once every G steps
             hold_o = (p == jj % G) ? oo : hold_o;
             hold_s = (p == jj % G) ? sk : hold_s;
@@ -254,7 +271,7 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_fwd_k(
                 const int ts = t0 + jj - (G - 1) + p;
                 const bool ok = p < G && ts < T && col_ok;
                 *(ok ? ob + (long)ts * d + col : tr) = hold_o;
-                *(ok ? skb + (long)ts * d + col : tr + 64) = hold_s;
+                *(ok ? skb + (long)ts * d + col : tr + 1) = hold_s;
             }
         }
         fwd_stage_store<DH>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
@@ -481,9 +498,9 @@ ASCA_DEV void bops_read(BOps<DH / 16>& o, const float* __restrict__ st_q, const 
 // dalpha / dbeta totals of this wave in LDS for the epilogue.
 template <int DH, bool EXACT>
 ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], float (&ds)[DH / 16][2],
-                       float* __restrict__ rq, float* __restrict__ rk, float* __restrict__ rab,
-                       float* __restrict__ dv_dst, float* __restrict__ tr, bool tvalid, int lane, int rg, int cg,
-                       int rowb, int colb, int dh) {
+                       float* __restrict__ rq, float* __restrict__ rk, float& pa_out, float& pb_out,
+                       float* __restrict__ dv_dst, float* __restrict__ tr, bool tvalid, int rg, int cg, int rowb,
+                       int colb, int dh) {
     constexpr int M = DH / 16;
     const float a = in.a, bb = in.b;
     const float dO[2] = {in.dO.x, in.dO.y};
@@ -581,9 +598,50 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], f
         rk[rowb + 2 * cg] = tsum16(yk[0], yk[2]);
         rk[rowb + 2 * cg + 1] = tsum16(yk[1], yk[3]);
     }
-    pa = wave_sum(pa);
-    pb = wave_sum(pb);
-    if (lane == 0) *reinterpret_cast<float2*>(rab) = make_float2(pa, pb);
+    pa_out = pa;
+    pb_out = pb;
+}
+
+// Sum of the 2*CK per-lane partials x[j] over all 64 lanes, transposed so that
+// the totals end up spread over lanes (three swap/DPP levels on halving value
+// sets, then a butterfly over the lanes left), and written to red_ab:
+// x[j] (j < CK) is dalpha of step j, x[CK + j] dbeta of step j.
+template <int CK, int W>
+ASCA_DEV void cross_step_sum(float (&x)[2 * CK], float* __restrict__ red_ab, int w, int lane) {
+    constexpr int K = 2 * CK;
+    float y[K / 2];
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) y[i] = tsum32(x[i], x[i + K / 2]);
+    // lane holds y[i] = total over lane bit 5 of x[i + (bit5 ? K/2 : 0)]
+    if constexpr (K / 2 >= 2) {
+        float z[K / 4];
+#pragma unroll
+        for (int i = 0; i < K / 4; ++i) z[i] = tsum16(y[i], y[i + K / 4]);
+        if constexpr (K / 4 >= 2) {
+            const bool b3 = (lane & 8) != 0;
+            float u[K / 8];
+#pragma unroll
+            for (int i = 0; i < K / 8; ++i) {
+                const float keep = b3 ? z[i + K / 8] : z[i];
+                const float send = b3 ? z[i] : z[i + K / 8];
+                u[i] = keep + dpp<DPP_ROW_ROR8>(send);
+            }
+#pragma unroll
+            for (int i = 0; i < K / 8; ++i) {
+                const float tot = group_sum<8>(u[i]);
+                const int idx = i + (b3 ? K / 8 : 0) + ((lane & 16) ? K / 4 : 0) + ((lane & 32) ? K / 2 : 0);
+                if ((lane & 7) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
+            }
+        } else {
+            const float tot = group_sum<16>(z[0]);
+            const int idx = ((lane & 16) ? K / 4 : 0) + ((lane & 32) ? K / 2 : 0);
+            if ((lane & 15) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
+        }
+    } else {
+        const float tot = add_xor16(group_sum<16>(y[0]));
+        const int idx = (lane & 32) ? K / 2 : 0;
+        if ((lane & 31) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
+    }
 }
 
 // Backward of one unit per block.  Output pointers are already offset to the
@@ -670,15 +728,17 @@ __global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
         // ---- phase B: steps t0+CK-1 .. t0 in reverse, LDS operands one step ahead
         {
             BOps<M> op[2];
+            float pab[2 * CK];
             bops_read<DH>(op[(CK - 1) & 1], st_q, st_k, st_w, st_ab, CK - 1, w, rowb, cg);
 #pragma unroll
             for (int jj = CK - 1; jj >= 0; --jj) {
                 if (jj > 0) bops_read<DH>(op[(jj - 1) & 1], st_q, st_k, st_w, st_ab, jj - 1, w, rowb, cg);
                 const int t = t0 + jj;
                 bwd_step<DH, EXACT>(op[jj & 1], stash[jj], ds, red_q + (jj * W + w) * DH, red_k + (jj * W + w) * DH,
-                                    red_ab + (jj * W + w) * 2, gv + ((long)b * T + t) * ldx + hoff + colb, tr, t < T,
-                                    lane, rg, cg, rowb, colb, dh);
+                                    pab[jj], pab[CK + jj], gv + ((long)b * T + t) * ldx + hoff + colb, tr, t < T, rg,
+                                    cg, rowb, colb, dh);
             }
+            cross_step_sum<CK, W>(pab, red_ab, w, lane);
         }
         __syncthreads();  // red_* of this segment complete
 
@@ -808,7 +868,7 @@ static int launch_fwd_t(const float* q, const float* k, const float* v, const fl
                         float* o, const DeltaWs& ws, int B, int T, int H, int dh, hipStream_t st) {
     int rc = pre_launch("delta_fwd");
     if (rc) return rc;
-    hipLaunchKernelGGL((delta_fwd_k<DH, EXACT>), dim3(B * H), dim3(DS<DH>::THREADS), 0, st, q, k, v, alpha, beta, o,
+    hipLaunchKernelGGL((delta_fwd_k<DH, EXACT>), dim3(B * H), dim3(FS<DH>::NT), 0, st, q, k, v, alpha, beta, o,
                        ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
     return post_launch("delta_fwd");
 }

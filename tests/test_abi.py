@@ -36,7 +36,7 @@ def test_workspace_bytes_layout():
     ckpt = 32 * 8 * (512 // 8) * 64 * 64 * 4
     assert out.value == sk + ckpt
     _lib.call("asca_delta_ws_bytes", 4, 128, 4, 32, C.byref(out))
-    assert out.value == 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 16) * 32 * 32 * 4
+    assert out.value == 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 8) * 32 * 32 * 4
     with pytest.raises(_lib.AscaError) as ei:
         _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))
     assert ei.value.code == 3
