@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "asca_delta_bwd_raw": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "asca_delta_bwd_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "asca_delta_states": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "asca_delta_decode_step": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
 }
 
 ERRORS = {

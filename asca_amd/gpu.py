@@ -28,7 +28,7 @@ from . import _lib
 from ._lib import AscaError
 
 ARCH = "gfx950"
-KERNELS = ("delta_fwd", "delta_bwd")
+KERNELS = ("delta_fwd", "delta_bwd", "delta_states", "delta_decode")
 DEFAULT_MIN_FLOPS = 4_000_000
 
 _f32 = np.float32
@@ -223,6 +223,32 @@ class Gpu:
             for b in [ddo, *outs]:
                 b.free()
         return tuple(res)
+
+
+    # -- decode -------------------------------------------------------------
+    def new_decode_states(self, n_seq: int, n_heads: int, dh: int) -> DevBuf:
+        """Zeroed device states (n_seq, H, dh, dh) for delta_decode_step; the
+        device counterpart of Model::new_decode_state (rust/src/model.rs:619)."""
+        buf = DevBuf(n_seq * n_heads * dh * dh * 4)
+        _lib.call("asca_memset32", _vp(buf), 0, C.c_size_t(n_seq * n_heads * dh * dh), None)
+        return buf
+
+    def delta_decode_step(self, states: DevBuf, qkv, gate, n_heads: int, dh: int):
+        """One token of DeltaBlock::step's state math (rust/src/delta.rs:356-407)
+        for every row of qkv (n_seq, 3d) / gate (n_seq, 2H); states stay on the
+        device and are updated in place; returns o (n_seq, d) on the host."""
+        n = qkv.shape[0]
+        d = n_heads * dh
+        if qkv.shape != (n, 3 * d) or gate.shape != (n, 2 * n_heads):
+            raise ValueError(f"delta_decode_step: qkv {qkv.shape}, gate {gate.shape} for H={n_heads} dh={dh}")
+        dq, dg, do = DevBuf.from_host(qkv), DevBuf.from_host(gate), DevBuf(n * d * 4)
+        try:
+            _lib.call("asca_delta_decode_step", _vp(states), _vp(dq), _vp(dg), _vp(do), n, n_heads, dh, None)
+            _lib.call("asca_sync")
+            return do.to_host((n, d))
+        finally:
+            for b in (dq, dg, do):
+                b.free()
 
 
 # --------------------------------------------------------- module functions

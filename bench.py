@@ -118,11 +118,139 @@ def cpu_baseline(x, B, T, H, dh, budget_s=30.0):
     }
 
 
+class Timer:
+    """HIP events on one stream of the library (no torch in this process)."""
+
+    def __init__(self):
+        from asca_amd import _lib
+
+        self._lib = _lib
+        sp = C.c_void_p()
+        _lib.call("asca_stream_create", C.byref(sp))
+        self.stream = sp.value
+
+    def event(self):
+        e = C.c_void_p()
+        self._lib.call("asca_event_create", C.byref(e))
+        return e
+
+    def record(self, e):
+        self._lib.call("asca_event_record", e, C.c_void_p(self.stream))
+
+    def elapsed(self, a, b):
+        ms = C.c_float()
+        self._lib.call("asca_event_elapsed_ms", C.byref(ms), a, b)
+        return ms.value
+
+    def sync(self):
+        self._lib.call("asca_stream_sync", C.c_void_p(self.stream))
+
+    def destroy(self, *evs):
+        for e in evs:
+            self._lib.call("asca_event_destroy", e)
+
+
+def bench_decode(args):
+    """batched single-token decode, 512 sequences, H=16, dh=128,
+    persistent f32 states in HBM; one step reads and writes every state once.
+    Inputs (q, k, v normals, alpha logits 2+N, beta logits N, seed 3) come
+    from the reference Rng stream; a pool of 8 steps' inputs is cycled."""
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf
+
+    g = gpu.gpu()
+    if g is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    n, H, dh, seed, pool = 512, 16, 128, 3, 8
+    d = H * dh
+    lib = _lib.load()
+    st = (C.c_uint64 * 2)()
+    lib.asca_rng_seed(seed, st)
+    qkvs, gates = [], []
+    for _ in range(pool):
+        qkv = np.empty((n, 3 * d), dtype=np.float32)
+        lib.asca_rng_normal(st, qkv.ctypes.data_as(C.c_void_p), qkv.size, 1.0, 0.0)
+        gate = np.empty((n, 2 * H), dtype=np.float32)
+        lib.asca_rng_normal(st, gate.ctypes.data_as(C.c_void_p), gate.size, 1.0, 0.0)
+        gate[:, :H] += 2.0
+        qkvs.append(qkv)
+        gates.append(gate)
+    dq = [DevBuf.from_host(x) for x in qkvs]
+    dg = [DevBuf.from_host(x) for x in gates]
+    states = g.new_decode_states(n, H, dh)
+    o = DevBuf(n * d * 4)
+    tm = Timer()
+
+    def step(i):
+        _lib.call("asca_delta_decode_step", C.c_void_p(states.ptr), C.c_void_p(dq[i % pool].ptr),
+                  C.c_void_p(dg[i % pool].ptr), C.c_void_p(o.ptr), n, H, dh, C.c_void_p(tm.stream))
+
+    K = args.steps or 256
+    W = args.warmup
+    print(f"bench decode: {gpu.describe()}; n{n} H{H} dh{dh}; warmup {W}, steps {K}", flush=True)
+    for i in range(W):
+        step(i)
+    tm.sync()
+    e0, e1 = tm.event(), tm.event()
+    t0 = time.perf_counter()
+    tm.record(e0)
+    for i in range(K):
+        step(i)
+    tm.record(e1)
+    tm.sync()
+    wall = time.perf_counter() - t0
+    dev_ms = tm.elapsed(e0, e1) / K
+    tm.destroy(e0, e1)
+    state_bytes = 2 * n * H * dh * dh * 4
+    io_bytes = n * (3 * d + 2 * H) * 4 + n * d * 4
+    bytes_step = state_bytes + io_bytes
+    achieved = bytes_step / (dev_ms * 1e-3)
+    result = {
+        "metric": "decode tokens/s (512 seq H16 dh128 f32, 256 steps) + HBM GB/s",
+        "value": round(n * K / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (reference Rng stream, configs[4] distributions, seed 3, 8-step input pool)",
+        "config": {"workload": "batched decode step (asca_delta_decode_step)", "n_seq": n, "H": H, "dh": dh},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM, 4), "traffic": None, "kernel": "delta_decode",
+                     "algorithmic_bytes": bytes_step},
+        "kernels_ms": {"delta_decode": round(dev_ms, 4)},
+    }
+    if not args.no_cpu:
+        from oracle import pyoracle as orc
+
+        ns = 64
+        S = np.zeros((ns, H, dh, dh), dtype=np.float32)
+        qkv, gate = np.ascontiguousarray(qkvs[0][:ns]), np.ascontiguousarray(gates[0][:ns])
+        orc.delta_decode_step(S, qkv, gate, H, dh)
+        times = []
+        for _ in range(5):
+            t1 = time.perf_counter()
+            orc.delta_decode_step(S, qkv, gate, H, dh)
+            times.append(time.perf_counter() - t1)
+        med = statistics.median(times)
+        result["cpu_baseline"] = {
+            "value": round(ns / med, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle restatement of DeltaBlock::step state math, {ns} of the 512 sequences, one thread "
+                      f"(the reference's decode is single-threaded per token), median of 5 steps, {med:.4f} s each"}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="delta", choices=["delta", "decode"],
+                    help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib", action="store_true",
                     help="also run the known-size copy kernel (for counter calibration)")
@@ -132,6 +260,11 @@ def main():
         sys.stderr.write("bench.py: this build runs on exactly one GPU (the delta-rule units are independent "
                          "per (sequence, head); see DESIGN.md for how the path shards). Use --gpus 1.\n")
         sys.exit(2)
+    if args.workload == "decode":
+        bench_decode(args)
+        return
+    if args.steps is None:
+        args.steps = 100
 
     from asca_amd import _lib, gpu
     from asca_amd.gpu import DevBuf

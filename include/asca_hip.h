@@ -181,6 +181,18 @@ ASCA_API int asca_delta_states(const float* q, const float* k, const float* v,
                                const float* alpha, const float* beta, float* states,
                                int B, int T, int H, int dh, void* stream);
 
+/* One decode step for n_seq independent sequences: the state math of
+ * DeltaBlock::step (rust/src/delta.rs:356-407) -- per head, q and k of the qkv
+ * row are L2-normalised (x * 1/max(|x|, 1e-8)), alpha = sigmoid(gate[h]),
+ * beta = sigmoid(gate[H+h]), sk = S^T k, u = beta (v - alpha sk),
+ * S = alpha S + k u^T, o = S^T q.  The reference has no GPU decode and caps dh
+ * at 64 (delta.rs:361-362); here 1 <= dh <= 128.
+ *   states : (n_seq, H, dh, dh) row-major S[a][i], updated in place
+ *   qkv    : (n_seq, 3*H*dh) rows of x.w_qkv + b_qkv;  gate : (n_seq, 2*H) logits
+ *   o      : (n_seq, H*dh) output */
+ASCA_API int asca_delta_decode_step(float* states, const float* qkv, const float* gate, float* o,
+                                    int n_seq, int H, int dh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
