@@ -21,6 +21,8 @@ _sz = C.c_size_t
 _p = C.c_void_p
 _fp = C.POINTER(C.c_float)
 _u64p = C.POINTER(C.c_uint64)
+_l = C.c_long
+_f = C.c_float
 
 # name -> (restype, argtypes).  Float tensors travel as void* device pointers.
 SIGNATURES: dict[str, tuple] = {
@@ -57,6 +59,19 @@ SIGNATURES: dict[str, tuple] = {
     "asca_delta_bwd_fused": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "asca_delta_states": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "asca_delta_decode_step": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
+    "asca_rmsnorm": (_i, [_p, _p, _p, _l, _i, _f, _p]),
+    "asca_rmsnorm_bwd": (_i, [_p, _p, _p, _l, _i, _f, _p]),
+    "asca_cross_entropy": (_i, [_p, _p, _l, _i, _p, _p, _p]),
+    "asca_gather_rows": (_i, [_p, _p, _l, _i, _p, _p]),
+    "asca_scatter_rows": (_i, [_p, _p, _l, _i, _p, _p]),
+    "asca_colsum": (_i, [_p, _l, _i, _p, _i, _p]),
+    "asca_adamw_scalars": (_i, [_f, _f, _f, _f, _f, C.c_uint32, _fp]),
+    "asca_adamw": (_i, [_p, _p, _p, _p, _l, _f, _f, _f, _f, _f, _p]),
+    "asca_hash_route_ws_bytes": (_i, [_i, _i, C.POINTER(_sz)]),
+    "asca_hash_route": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
+    "asca_gemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p]),
+    "asca_moe_fwd": (_i, [_p] * 7 + [_i] * 4 + [_p] * 4),
+    "asca_moe_bwd": (_i, [_p] * 8 + [_i] * 4 + [_p] * 6 + [_i, _p]),
 }
 
 ERRORS = {

@@ -11,6 +11,9 @@
 
 namespace asca {
 
+// Accumulator type of the 16x16 MFMA instructions (four f32 per lane).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // DPP control words (GCN3+/CDNA encodings).
 constexpr int DPP_QUAD_XOR1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;   // quad_perm [2,3,0,1]

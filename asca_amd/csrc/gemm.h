@@ -1,0 +1,44 @@
+// Internal interface of the MFMA GEMM (gemm.hip) for the composite operators
+// (moe.hip, model.hip).  Not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace asca {
+
+enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_SILU_BWD = 2 };
+
+// One (possibly grouped, possibly split-K) GEMM:
+//   C = alpha * op(A) op(B) (+ bias per column) (+ beta * C)
+// gmode 0: plain; gmode 1: M varies per group (rows goff[g]..goff[g+1] of the
+// sorted row space); gmode 2: K varies per group.  Row indirections map the
+// operand's storage-row index (sorted space) to the stored row.
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    long lda, ldb, ldc;
+    int M, N, K;  // M (gmode 1) and K (gmode 2) come per group from goff
+    float alpha, beta;
+    const int* a_rows;  // storage-row indirection of A, B and C (or null)
+    const int* b_rows;
+    const int* c_rows;
+    const float* bias;
+    const float* aux;  // EPI_SILU_BWD: pre (rows in group/sorted space)
+    float* aux_out;    // EPI_SILU: hidden
+    long ld_aux;
+    const int* goff;  // group offsets [ngroups + 1]
+    int ngroups, gmode;
+    long a_gs, b_gs, c_gs, bias_gs;  // per-group pointer strides (elements)
+    int tiles_m, tiles_n;
+    long k_per_split;     // split-K: K range of blockIdx.y
+    long c_split_stride;  // split-K: partial buffer stride per split
+};
+
+GemmArgs gemm_args();
+// m_total: for gmode 1, the total rows over all groups (bounds the grid).
+int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t st, const char* name);
+// out[g*N + c] (+)= column sums of X over the rows of group g (or all rows).
+int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, int ngroups, float* out,
+                  int accumulate, hipStream_t st);
+
+}  // namespace asca

@@ -1,0 +1,544 @@
+// f32 GEMM on the CDNA4 matrix cores (v_mfma_f32_16x16x4_f32), with the
+// operand/epilogue variants the model needs:
+//
+//   C = alpha * op(A) op(B) (+ bias per column) (+ beta * C)
+//
+// where op(A) is A (M x K, row-major) or A^T (A stored K x M), op(B) is B
+// (K x N) or B^T (B stored N x K) -- the reference's matmul_f32 / matmul_ta_f32
+// / matmul_ld_f32 family (rust/kernels/asca.cu:14-141) and Mat::matmul /
+// matmul_ta / matmul_t (rust/src/tensor.rs:91-201).  On top of that:
+//   - storage-row indirection per operand (row gather) and on C (row scatter),
+//     replacing gather_rows_f32 / scatter_rows_f32 round trips (asca.cu:576-594);
+//   - grouped launches over expert buckets (CSR offsets on the device): either
+//     M varies per group (expert forward GEMMs, dpre, dxn) or K varies per
+//     group (expert weight gradients), one launch for all experts;
+//   - fused epilogues: bias + SiLU writing both pre and hidden (HashMoe
+//     forward, rust/src/model.rs:236-248), and the SiLU backward
+//     dpre = acc * s (1 + pre (1 - s)) (model.rs:432-440);
+//   - split-K with f32 partials and a deterministic reduction, for the
+//     K = tokens weight-gradient products that have few output tiles.
+//
+// Tiling: 256 threads, a 128 x 128 block tile, k-tiles of 32 double-buffered
+// in LDS, four waves of 64 x 64.  Each operand keeps its global layout in LDS
+// (no transposing stores): a k-contiguous tile is [mn][k] with a 36-float row
+// stride, an mn-contiguous tile is [k][mn].  The MFMA k index is permuted
+// inside every 16-k group (step s, lane l uses k = 4 (l / 16) + s) so every
+// fragment read is one 16-byte ds_read: a [mn][k] read yields four k-steps of
+// one 16-row tile, a [k][mn] read yields one k-step of four tiles whose rows
+// are interleaved by 4.  The epilogue maps rows/columns back accordingly.
+#include <mutex>
+
+#include "common.h"
+#include "gemm.h"
+#include "runtime.h"
+
+namespace asca {
+
+constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_NT = 256;
+constexpr int GM_LDK = GM_BK + 4;  // [mn][k] tile row stride (floats)
+constexpr int GM_LDM = 128;        // [k][mn] tile row stride
+constexpr int GM_KC_F = 128 * GM_LDK;
+constexpr int GM_MC_F = GM_BK * GM_LDM;
+
+ASCA_DEV float silu_ref(float x) { return x / (1.0f + expf(-x)); }
+
+// 4 consecutive floats from p, of which n (<= 0 .. >= 4) are valid; the rest 0.
+template <bool VEC>
+ASCA_DEV float4 ld4(const float* p, int n) {
+    if (VEC && n >= 4) return *reinterpret_cast<const float4*>(p);
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n > 0) r.x = p[0];
+    if (n > 1) r.y = p[1];
+    if (n > 2) r.z = p[2];
+    if (n > 3) r.w = p[3];
+    return r;
+}
+
+ASCA_DEV long srow(const int* rows, long off, long i) { return rows ? (long)rows[off + i] : off + i; }
+
+// Global -> registers for one operand tile (4 float4 per thread).
+//   KC (k-contiguous, stored [mn][k]): 128 mn-rows x 32 k, 8 threads per row.
+//   MC (mn-contiguous, stored [k][mn]): 32 k-rows x 128 mn, 32 threads per row.
+// `lim_mn`, `lim_k`: valid extents relative to the tile origin.
+template <bool KC, bool VEC>
+ASCA_DEV void tile_load(float4 (&r)[4], const float* base, long ld, const int* rows, long row_off, int mn0,
+                        int lim_mn, long k0, long lim_k, int tid) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if constexpr (KC) {
+            const int rr = (tid >> 3) + 32 * j;
+            const int kk = 4 * (tid & 7);
+            const bool ok = rr < lim_mn;
+            const long sr = ok ? srow(rows, row_off, mn0 + rr) : 0;
+            r[j] = ld4<VEC>(base + sr * ld + k0 + kk, ok ? (int)min(lim_k - kk, 4L) : 0);
+        } else {
+            const int kr = (tid >> 5) + 8 * j;
+            const int mm = 4 * (tid & 31);
+            const bool ok = kr < lim_k;
+            const long sr = ok ? srow(rows, row_off, k0 + kr) : 0;
+            r[j] = ld4<VEC>(base + sr * ld + mn0 + mm, ok ? min(lim_mn - mm, 4) : 0);
+        }
+    }
+}
+
+template <bool KC>
+ASCA_DEV void tile_store(const float4 (&r)[4], float* t, int tid) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if constexpr (KC)
+            *reinterpret_cast<float4*>(t + ((tid >> 3) + 32 * j) * GM_LDK + 4 * (tid & 7)) = r[j];
+        else
+            *reinterpret_cast<float4*>(t + ((tid >> 5) + 8 * j) * GM_LDM + 4 * (tid & 31)) = r[j];
+    }
+}
+
+// Fragments of one 16-k group h for the wave's 64 mn-rows starting at w0:
+// f[s][t] = operand value of MFMA k-step s for 16-row tile t.
+template <bool KC>
+ASCA_DEV void frag_read(float (&f)[4][4], const float* t, int w0, int h, int lane) {
+    if constexpr (KC) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const float4 v =
+                *reinterpret_cast<const float4*>(t + (w0 + 16 * x + (lane & 15)) * GM_LDK + 16 * h + 4 * (lane >> 4));
+            f[0][x] = v.x;
+            f[1][x] = v.y;
+            f[2][x] = v.z;
+            f[3][x] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4 v =
+                *reinterpret_cast<const float4*>(t + (16 * h + 4 * (lane >> 4) + s) * GM_LDM + w0 + 4 * (lane & 15));
+            f[s][0] = v.x;
+            f[s][1] = v.y;
+            f[s][2] = v.z;
+            f[s][3] = v.w;
+        }
+    }
+}
+
+template <bool TA, bool TB, int EPI, bool VEC>
+__global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
+    constexpr bool A_KC = !TA, B_KC = TB;
+    constexpr int A_F = A_KC ? GM_KC_F : GM_MC_F;
+    constexpr int B_F = B_KC ? GM_KC_F : GM_MC_F;
+    extern __shared__ float4 lds4[];
+    float* lds = reinterpret_cast<float*>(lds4);
+
+    // block -> tile, XCD-aware: hardware places block i on XCD i % 8, so give
+    // each XCD a contiguous run of logical tiles (neighbours share operand rows)
+    int L = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) L = (L & 7) * (nb >> 3) + (L >> 3);
+    int g = 0, tm, tn = L % p.tiles_n;
+    int Mg = p.M;
+    long K_lo = 0, K_hi = p.K, goff_g = 0;
+    if (p.gmode == 1) {
+        int mt = L / p.tiles_n;
+        for (; g < p.ngroups; ++g) {
+            const int a = p.goff[g], b = p.goff[g + 1];
+            const int nt = (b - a + GM_BM - 1) / GM_BM;
+            if (mt < nt) break;
+            mt -= nt;
+        }
+        if (g >= p.ngroups) return;  // surplus block (grid is an upper bound)
+        tm = mt;
+        goff_g = p.goff[g];
+        Mg = p.goff[g + 1] - p.goff[g];
+    } else if (p.gmode == 2) {
+        const int r = L / p.tiles_n;
+        tm = r % p.tiles_m;
+        g = r / p.tiles_m;
+        goff_g = p.goff[g];
+        K_hi = p.goff[g + 1] - p.goff[g];
+    } else {
+        tm = L / p.tiles_n;
+        K_lo = (long)blockIdx.y * p.k_per_split;
+        K_hi = min((long)p.K, K_lo + p.k_per_split);
+    }
+    const int m0 = tm * GM_BM, n0 = tn * GM_BN;
+    const float* A = p.A + g * p.a_gs;
+    const float* B = p.B + g * p.b_gs;
+    float* C = p.C + g * p.c_gs + (long)blockIdx.y * p.c_split_stride;
+    const float* bias = p.bias ? p.bias + g * p.bias_gs : nullptr;
+    const long a_off = ((p.gmode == 1 && !TA) || (p.gmode == 2 && TA)) ? goff_g : 0;
+    const long b_off = (p.gmode == 2 && !TB) ? goff_g : 0;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    const int lim_m = Mg - m0, lim_n = p.N - n0;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const long nk = (K_hi - K_lo + GM_BK - 1) / GM_BK;
+    float4 ra[4], rb[4];
+    auto load = [&](long k0) {
+        tile_load<A_KC, VEC>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
+        tile_load<B_KC, VEC>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
+    };
+    if (nk > 0) {
+        load(K_lo);
+        tile_store<A_KC>(ra, lds, tid);
+        tile_store<B_KC>(rb, lds + A_F, tid);
+    }
+    __syncthreads();
+    for (long kt = 0; kt < nk; ++kt) {
+        const float* As = lds + (kt & 1) * (A_F + B_F);
+        const float* Bs = As + A_F;
+        const bool more = kt + 1 < nk;
+        if (more) load(K_lo + (kt + 1) * GM_BK);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float fa[4][4], fb[4][4];
+            frag_read<A_KC>(fa, As, wm, h, lane);
+            frag_read<B_KC>(fb, Bs, wn, h, lane);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+#pragma unroll
+                    for (int y = 0; y < 4; ++y)
+                        acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][x], fb[s][y], acc[x][y], 0, 0, 0);
+        }
+        if (more) {
+            float* Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
+            tile_store<A_KC>(ra, Ns, tid);
+            tile_store<B_KC>(rb, Ns + A_F, tid);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: result register r of tile (x, y) sits at tile row 4 (lane / 16) + r,
+    // tile column lane % 16
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tr = 4 * (lane >> 4) + r;
+            const int m = m0 + wm + (A_KC ? 16 * x + tr : 4 * tr + x);
+            if (m >= Mg) continue;
+            const long sorted = (p.gmode == 1 ? goff_g : 0) + m;
+            const long crow = p.c_rows ? (long)p.c_rows[sorted] : sorted;
+            float* Cr = C + crow * p.ldc;
+            float v[4];
+#pragma unroll
+            for (int y = 0; y < 4; ++y) v[y] = acc[x][y][r];
+            if constexpr (!B_KC) {
+                // columns n, n+1, n+2, n+3 of one row
+                const int n = n0 + wn + 4 * (lane & 15);
+                if (n >= p.N) continue;
+                const int cnt = min(p.N - n, 4);
+                float o[4], hb[4];
+#pragma unroll
+                for (int y = 0; y < 4; ++y) {
+                    float a = p.alpha * v[y];
+                    if (y < cnt) {
+                        if (bias) a += bias[n + y];
+                        if constexpr (EPI == EPI_STORE) {
+                            if (p.beta != 0.0f) a += p.beta * Cr[n + y];
+                        } else if constexpr (EPI == EPI_SILU) {
+                            hb[y] = silu_ref(a);
+                        } else {
+                            const float pr = p.aux[sorted * p.ld_aux + n + y];
+                            const float sg = 1.0f / (1.0f + expf(-pr));
+                            a = v[y] * (sg * (1.0f + pr * (1.0f - sg)));
+                        }
+                    }
+                    o[y] = a;
+                }
+                if (VEC && cnt == 4) {
+                    *reinterpret_cast<float4*>(Cr + n) = make_float4(o[0], o[1], o[2], o[3]);
+                    if constexpr (EPI == EPI_SILU)
+                        *reinterpret_cast<float4*>(p.aux_out + sorted * p.ld_aux + n) =
+                            make_float4(hb[0], hb[1], hb[2], hb[3]);
+                } else {
+#pragma unroll
+                    for (int y = 0; y < 4; ++y)
+                        if (y < cnt) {
+                            Cr[n + y] = o[y];
+                            if constexpr (EPI == EPI_SILU) p.aux_out[sorted * p.ld_aux + n + y] = hb[y];
+                        }
+                }
+            } else {
+#pragma unroll
+                for (int y = 0; y < 4; ++y) {
+                    const int n = n0 + wn + 16 * y + (lane & 15);
+                    if (n >= p.N) continue;
+                    float a = p.alpha * v[y];
+                    if (bias) a += bias[n];
+                    if constexpr (EPI == EPI_STORE) {
+                        if (p.beta != 0.0f) a += p.beta * Cr[n];
+                        Cr[n] = a;
+                    } else if constexpr (EPI == EPI_SILU) {
+                        Cr[n] = a;
+                        p.aux_out[sorted * p.ld_aux + n] = silu_ref(a);
+                    } else {
+                        const float pr = p.aux[sorted * p.ld_aux + n];
+                        const float sg = 1.0f / (1.0f + expf(-pr));
+                        Cr[n] = v[y] * (sg * (1.0f + pr * (1.0f - sg)));
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Split-K reduction: C = alpha * sum_s part[s] + bias + beta * C (deterministic order).
+__global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ part, int splits, long MN, int N,
+                                                       float* __restrict__ C, long ldc, float alpha, float beta,
+                                                       const float* __restrict__ bias) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += stride) {
+        float s = 0.0f;
+        for (int k = 0; k < splits; ++k) s += part[(long)k * MN + i];
+        const long r = i / N;
+        const int c = (int)(i - r * N);
+        float a = alpha * s;
+        if (bias) a += bias[c];
+        float* cp = C + r * ldc + c;
+        if (beta != 0.0f) a += beta * *cp;
+        *cp = a;
+    }
+}
+
+// Column sums, optionally per group of rows: out[g*N + c] (+)= sum over the
+// rows of group g of X[r][c] (bias gradients: colsum_raw of
+// rust/src/cuda/mod.rs:642-669 and the per-expert db1 of model.rs:432-440).  One thread per column
+// and row slice, slices summed in a fixed order.
+constexpr int CS_ROWS = 256;
+__global__ __launch_bounds__(256) void colsum_part_k(const float* __restrict__ X, long rows, int N, long ldx,
+                                                     const int* __restrict__ goff, int ngroups,
+                                                     float* __restrict__ part, int nslices) {
+    // grid: (ceil(N / 256), nslices, max(ngroups, 1))
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int g = blockIdx.z;
+    long lo = 0, hi = rows;
+    if (goff) {
+        lo = goff[g];
+        hi = goff[g + 1];
+    }
+    const long span = hi - lo;
+    const long per = (span + nslices - 1) / nslices;
+    const long a = lo + (long)blockIdx.y * per;
+    const long b = min(hi, a + per);
+    if (c >= N) return;
+    float s = 0.0f;
+    for (long r = a; r < b; ++r) s += X[r * ldx + c];
+    part[((long)g * nslices + blockIdx.y) * N + c] = s;
+}
+
+__global__ __launch_bounds__(256) void colsum_fin_k(const float* __restrict__ part, int nslices, int N, int G,
+                                                    float* __restrict__ out, int accumulate) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)G * N) return;
+    const long g = i / N;
+    const int c = (int)(i - g * N);
+    float s = 0.0f;
+    for (int k = 0; k < nslices; ++k) s += part[(g * nslices + k) * N + c];
+    out[i] = accumulate ? out[i] + s : s;
+}
+
+// ---------------------------------------------------------------- host side
+
+// Per-device scratch for split-K partials and column-sum slices; grown on
+// demand (growth waits for the device so in-flight kernels never see a freed
+// buffer).
+struct Scratch {
+    std::mutex mu;
+    void* ptr[16] = {};
+    size_t bytes[16] = {};
+};
+static Scratch g_scratch;
+
+static int scratch_get(size_t bytes, float** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return fail(ASCA_ERR_HIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lk(g_scratch.mu);
+    if (g_scratch.bytes[dev] < bytes) {
+        size_t nb = g_scratch.bytes[dev] ? g_scratch.bytes[dev] : (size_t)1 << 20;
+        while (nb < bytes) nb *= 2;
+        if (g_scratch.ptr[dev]) {
+            hipDeviceSynchronize();
+            hipFree(g_scratch.ptr[dev]);
+            g_scratch.ptr[dev] = nullptr;
+            g_scratch.bytes[dev] = 0;
+        }
+        void* p = nullptr;
+        if (hipMalloc(&p, nb) != hipSuccess) return fail(ASCA_ERR_OOM, "scratch hipMalloc(%zu) failed", nb);
+        g_scratch.ptr[dev] = p;
+        g_scratch.bytes[dev] = nb;
+    }
+    *out = reinterpret_cast<float*>(g_scratch.ptr[dev]);
+    return ASCA_OK;
+}
+
+template <bool TA, bool TB, int EPI, bool VEC>
+static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
+    constexpr int A_F = !TA ? GM_KC_F : GM_MC_F;
+    constexpr int B_F = TB ? GM_KC_F : GM_MC_F;
+    constexpr size_t lds = 2 * (size_t)(A_F + B_F) * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr = true;
+    }
+    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC>), grid, dim3(GM_NT), lds, st, a);
+    return ASCA_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Validates and launches one (possibly grouped) GEMM.  `m_total`: for gmode 1,
+// the total rows over all groups (bounds the grid).
+int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t st, const char* name) {
+    if (a.M < 0 || a.N < 0 || a.K < 0) return fail(ASCA_ERR_INVALID, "%s: negative shape", name);
+    if (a.gmode == 1 && ta) return fail(ASCA_ERR_INVALID, "%s: grouped rows need a non-transposed A", name);
+    if (a.gmode == 2 && (!ta || tb)) return fail(ASCA_ERR_INVALID, "%s: grouped K needs A^T and B", name);
+    if (epi == EPI_SILU && (ta || tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU epilogue is NN only", name);
+    if (epi == EPI_SILU_BWD && (ta || !tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU-bwd epilogue is NT only", name);
+    a.tiles_n = (a.N + GM_BN - 1) / GM_BN;
+    a.tiles_m = (a.M + GM_BM - 1) / GM_BM;
+    long blocks;
+    if (a.gmode == 1)
+        blocks = ((m_total + GM_BM - 1) / GM_BM + a.ngroups) * a.tiles_n;
+    else if (a.gmode == 2)
+        blocks = (long)a.ngroups * a.tiles_m * a.tiles_n;
+    else
+        blocks = (long)a.tiles_m * a.tiles_n;
+    if (blocks == 0 || a.N == 0) return ASCA_OK;
+    if (blocks > 0x7fffffffL) return fail(ASCA_ERR_INVALID, "%s: grid too large", name);
+    const bool vec = (a.lda % 4 == 0) && (a.ldb % 4 == 0) && (a.ldc % 4 == 0) && (a.ld_aux % 4 == 0) &&
+                     aligned16(a.A) && aligned16(a.B) && aligned16(a.C) && (!a.aux || aligned16(a.aux)) &&
+                     (!a.aux_out || aligned16(a.aux_out)) && (a.a_gs % 4 == 0) && (a.b_gs % 4 == 0) &&
+                     (a.c_gs % 4 == 0) && (a.c_split_stride % 4 == 0);
+    int rc = pre_launch(name);
+    if (rc) return rc;
+    const dim3 grid((unsigned)blocks, (unsigned)(a.gmode == 0 && a.k_per_split > 0 ? (a.K + a.k_per_split - 1) / a.k_per_split : 1));
+    if (a.gmode != 0 || a.k_per_split <= 0) a.k_per_split = a.K;
+#define ASCA_GEMM_CASE(TA_, TB_, EPI_)                                                                  \
+    if (ta == TA_ && tb == TB_ && epi == EPI_)                                                          \
+        rc = vec ? launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st) : launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st); \
+    else
+    ASCA_GEMM_CASE(0, 0, EPI_STORE)
+    ASCA_GEMM_CASE(1, 0, EPI_STORE)
+    ASCA_GEMM_CASE(0, 1, EPI_STORE)
+    ASCA_GEMM_CASE(1, 1, EPI_STORE)
+    ASCA_GEMM_CASE(0, 0, EPI_SILU)
+    ASCA_GEMM_CASE(0, 1, EPI_SILU_BWD)
+    rc = fail(ASCA_ERR_UNSUPPORTED, "%s: no kernel for this variant", name);
+#undef ASCA_GEMM_CASE
+    if (rc) return rc;
+    return post_launch(name);
+}
+
+GemmArgs gemm_args() {
+    GemmArgs a{};
+    a.alpha = 1.0f;
+    a.beta = 0.0f;
+    return a;
+}
+
+// Column sums of X (rows x N, ld ldx), per group when goff is given.
+int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, int ngroups, float* out,
+                  int accumulate, hipStream_t st) {
+    if (N == 0) return ASCA_OK;
+    const int G = goff ? ngroups : 1;
+    if (G == 0) return ASCA_OK;
+    const int cb = (N + 255) / 256;
+    // enough slices to fill the chip, each at least CS_ROWS rows on average
+    const long avg = goff ? rows / G + 1 : rows;
+    int ns = (int)min((long)((avg + CS_ROWS - 1) / CS_ROWS), 64L);
+    if (ns < 1) ns = 1;
+    float* part = nullptr;
+    int rc = scratch_get((size_t)G * ns * N * sizeof(float), &part);
+    if (rc) return rc;
+    rc = pre_launch("colsum");
+    if (rc) return rc;
+    hipLaunchKernelGGL(colsum_part_k, dim3(cb, ns, G), dim3(256), 0, st, X, rows, N, ldx, goff, G, part, ns);
+    rc = post_launch("colsum");
+    if (rc) return rc;
+    rc = pre_launch("colsum_fin");
+    if (rc) return rc;
+    const long tot = (long)G * N;
+    hipLaunchKernelGGL(colsum_fin_k, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, part, ns, N, G, out,
+                       accumulate);
+    return post_launch("colsum_fin");
+}
+
+}  // namespace asca
+
+using namespace asca;
+
+extern "C" {
+
+int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
+              long ldb, float beta, float* C, long ldc, const float* bias, void* stream) {
+    if (M < 0 || N < 0 || K < 0) return fail(ASCA_ERR_INVALID, "asca_gemm: negative shape");
+    if (M == 0 || N == 0) return ASCA_OK;
+    if (!C || (K > 0 && (!A || !B))) return fail(ASCA_ERR_INVALID, "asca_gemm: null pointer");
+    const long a_cols = trans_a ? M : K, b_cols = trans_b ? K : N;
+    if (lda < a_cols || ldb < b_cols || ldc < N) return fail(ASCA_ERR_INVALID, "asca_gemm: leading dimension too small");
+    const hipStream_t st = as_stream(stream);
+    GemmArgs a = gemm_args();
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.bias = bias;
+    // split K when the output has too few tiles to fill the chip
+    const long tiles = (long)((M + GM_BM - 1) / GM_BM) * ((N + GM_BN - 1) / GM_BN);
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    int splits = 1;
+    if (tiles < cus && K >= 1024) {
+        splits = (int)min((long)K / 512, (2L * cus + tiles - 1) / tiles);
+        if (splits < 1) splits = 1;
+    }
+    if (splits == 1) return gemm_launch(trans_a, trans_b, EPI_STORE, a, M, st, "gemm");
+    long kps = ((K + splits - 1) / splits + GM_BK - 1) / GM_BK * GM_BK;
+    splits = (int)((K + kps - 1) / kps);
+    const long MN = (long)M * N;
+    float* part = nullptr;
+    int rc = scratch_get((size_t)splits * MN * sizeof(float), &part);
+    if (rc) return rc;
+    GemmArgs s = a;
+    s.C = part;
+    s.ldc = N;
+    s.alpha = 1.0f;
+    s.beta = 0.0f;
+    s.bias = nullptr;
+    s.k_per_split = kps;
+    s.c_split_stride = MN;
+    rc = gemm_launch(trans_a, trans_b, EPI_STORE, s, M, st, "gemm_splitk");
+    if (rc) return rc;
+    rc = pre_launch("splitk_reduce");
+    if (rc) return rc;
+    long blocks = (MN + 255) / 256;
+    if (blocks > 4L * cus * 8) blocks = 4L * cus * 8;
+    hipLaunchKernelGGL(splitk_reduce_k, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, MN, N, C, ldc, alpha,
+                       beta, bias);
+    return post_launch("splitk_reduce");
+}
+
+int asca_colsum(const float* X, long rows, int cols, float* out, int accumulate, void* stream) {
+    if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "asca_colsum: negative shape");
+    if (cols == 0) return ASCA_OK;
+    if (!out || (rows > 0 && !X)) return fail(ASCA_ERR_INVALID, "asca_colsum: null pointer");
+    return colsum_launch(X, rows, cols, cols, nullptr, 0, out, accumulate, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,357 @@
+// Row-wise and element-wise ops around the delta block: RMSNorm fwd/bwd
+// (no gain), AdamW with the CPU path's semantics, hash routing with a stable
+// expert bucketing, row gather/scatter, and softmax cross-entropy.
+//
+// All reductions are wave-level butterflies (no atomics), so results are
+// deterministic; one wave per row.
+#include "common.h"
+#include "runtime.h"
+
+namespace asca {
+
+constexpr int ROW_NT = 256;  // 4 rows per block
+
+// ------------------------------------------------------------------ RMSNorm
+
+// rmsnorm_rows (rust/src/tensor.rs:259-270): y = x / sqrt(mean(x^2) + eps).
+__global__ __launch_bounds__(ROW_NT) void rmsnorm_k(const float* __restrict__ x, float* __restrict__ y,
+                                                   float* __restrict__ inv_out, long rows, int cols, float eps) {
+    const long r = (long)blockIdx.x * (ROW_NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float* xr = x + r * cols;
+    float ss = 0.0f;
+    for (int c = lane; c < cols; c += 64) ss = fmaf(xr[c], xr[c], ss);
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    for (int c = lane; c < cols; c += 64) y[r * cols + c] = xr[c] * inv;
+    if (inv_out && lane == 0) inv_out[r] = inv;
+}
+
+// rmsnorm_rows_backward (rust/src/tensor.rs:282-296):
+// dx = inv * (dy - x * inv * mean(dy * x) * inv), mean over the row.
+__global__ __launch_bounds__(ROW_NT) void rmsnorm_bwd_k(const float* __restrict__ x, const float* __restrict__ dy,
+                                                       float* __restrict__ dx, long rows, int cols, float eps) {
+    const long r = (long)blockIdx.x * (ROW_NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float* xr = x + r * cols;
+    const float* dr = dy + r * cols;
+    float ss = 0.0f, sd = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        ss = fmaf(xr[c], xr[c], ss);
+        sd = fmaf(dr[c], xr[c], sd);
+    }
+    ss = wave_sum(ss);
+    sd = wave_sum(sd);
+    const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    const float mean = sd * inv / (float)cols;
+    for (int c = lane; c < cols; c += 64) dx[r * cols + c] = inv * (dr[c] - xr[c] * inv * mean);
+}
+
+// -------------------------------------------------------------------- AdamW
+
+// The element update of AdamW::update's CPU path (rust/src/tensor.rs:444-453),
+// operation by operation without contraction (Rust never fuses a multiply
+// into an add; HIP's '/' and sqrtf are correctly rounded by default), so the
+// results match the CPU bit for bit:
+//   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g g;  upd = m / (sqrt(v) + eps_t)
+//   p -= wd p;  p -= lr upd
+__global__ __launch_bounds__(256) void adamw_k(float* __restrict__ p, const float* __restrict__ g,
+                                              float* __restrict__ m, float* __restrict__ v, long n, float lr,
+                                              float b1, float b2, float omb1, float omb2, float eps_t, float wd) {
+#pragma clang fp contract(off)
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float gi = g[i];
+        const float mi = b1 * m[i] + omb1 * gi;
+        const float vi = b2 * v[i] + omb2 * gi * gi;
+        m[i] = mi;
+        v[i] = vi;
+        const float upd = mi / (sqrtf(vi) + eps_t);
+        float pi = p[i];
+        pi -= wd * pi;
+        pi -= lr * upd;
+        p[i] = pi;
+    }
+}
+
+// ------------------------------------------------------------ hash routing
+
+// hash_route (rust/src/model.rs:69-77), wrapping u32 arithmetic.
+ASCA_DEV uint32_t hash_expert(uint32_t id, uint32_t n) {
+    uint32_t h = id * 0x9E3779B1u;
+    h ^= h >> 15;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    return h % n;
+}
+
+constexpr int RT_NT = 256;  // tokens per routing block (one per thread)
+
+// Pass 1: expert of every token and the per-block count of every expert.
+__global__ __launch_bounds__(RT_NT) void route_count_k(const uint32_t* __restrict__ ids, int n, int E,
+                                                       int32_t* __restrict__ expert, int32_t* __restrict__ blkcnt) {
+    __shared__ int cnt[64];
+    const int t = blockIdx.x * RT_NT + threadIdx.x;
+    if (threadIdx.x < E) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    if (t < n) {
+        const int e = (int)hash_expert(ids[t], (uint32_t)E);
+        expert[t] = e;
+        atomicAdd(&cnt[e], 1);  // integer counts: order-independent
+    }
+    __syncthreads();
+    if (threadIdx.x < E) blkcnt[blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
+}
+
+// Pass 2 (one block): expert offsets and, per block, where its tokens of each
+// expert start.  blkcnt is rewritten in place as the start positions.
+__global__ __launch_bounds__(64) void route_scan_k(int nblk, int E, int32_t* __restrict__ blkcnt,
+                                                   int32_t* __restrict__ offsets) {
+    const int e = threadIdx.x;
+    int total = 0;
+    if (e < E)
+        for (int b = 0; b < nblk; ++b) total += blkcnt[b * E + e];
+    // exclusive prefix of the totals over experts (E <= 64, one wave)
+    int incl = total;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const int o = __shfl_up(incl, s, 64);
+        if (e >= s) incl += o;
+    }
+    const int base = incl - total;
+    if (e < E) {
+        offsets[e] = base;
+        if (e == E - 1) offsets[E] = incl;
+        int run = base;
+        for (int b = 0; b < nblk; ++b) {
+            const int c = blkcnt[b * E + e];
+            blkcnt[b * E + e] = run;
+            run += c;
+        }
+    }
+}
+
+// Pass 3: stable placement -- a token's rank among the earlier tokens of its
+// block with the same expert comes from wave ballots, so the bucket of each
+// expert lists its tokens in ascending order, as model.rs:190-193 builds them.
+__global__ __launch_bounds__(RT_NT) void route_place_k(int n, int E, const int32_t* __restrict__ expert,
+                                                       const int32_t* __restrict__ blkstart,
+                                                       int32_t* __restrict__ perm) {
+    __shared__ int wcnt[RT_NT / 64][64];
+    const int t = blockIdx.x * RT_NT + threadIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int my = t < n ? expert[t] : -1;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int rank = 0;
+    for (int e = 0; e < E; ++e) {
+        const uint64_t mask = __ballot(my == e);
+        if (my == e) rank = __popcll(mask & below);
+        if (lane == 0) wcnt[w][e] = __popcll(mask);
+    }
+    __syncthreads();
+    if (t < n) {
+        int before = 0;
+        for (int ww = 0; ww < w; ++ww) before += wcnt[ww][my];
+        perm[blkstart[blockIdx.x * E + my] + before + rank] = t;
+    }
+}
+
+// ------------------------------------------------------------ gather/scatter
+
+// dst[r] = src[idx[r]] (gather_rows_f32, rust/kernels/asca.cu:576-584), or with
+// SCATTER dst[idx[r]] = src[r] (asca.cu:586-594; indices unique).
+template <bool SCATTER, bool VEC>
+__global__ __launch_bounds__(ROW_NT) void rows_copy_k(const float* __restrict__ src, const int32_t* __restrict__ idx,
+                                                     long n, int cols, float* __restrict__ dst) {
+    const long r = (long)blockIdx.x * (ROW_NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= n) return;
+    const long sr = SCATTER ? r : (long)idx[r];
+    const long dr = SCATTER ? (long)idx[r] : r;
+    if constexpr (VEC) {
+        const float4* s4 = reinterpret_cast<const float4*>(src + sr * cols);
+        float4* d4 = reinterpret_cast<float4*>(dst + dr * cols);
+        for (int c = lane; c < cols / 4; c += 64) d4[c] = s4[c];
+    } else {
+        for (int c = lane; c < cols; c += 64) dst[dr * cols + c] = src[sr * cols + c];
+    }
+}
+
+// ------------------------------------------------------------ cross-entropy
+
+// Per row t: lse = max + ln(sum exp(x - max)); loss_t = lse - x[target];
+// dlogits = exp(x - lse) / T, minus 1/T at the target (cpu_cross_entropy,
+// rust/src/model.rs:804-844).
+__global__ __launch_bounds__(ROW_NT) void cross_entropy_k(const float* __restrict__ logits,
+                                                         const uint32_t* __restrict__ targets, long T, int V,
+                                                         float inv_t, float* __restrict__ dlogits,
+                                                         float* __restrict__ losses) {
+    const long t = (long)blockIdx.x * (ROW_NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float* row = logits + t * V;
+    float mx = -INFINITY;
+    for (int c = lane; c < V; c += 64) mx = fmaxf(mx, row[c]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+    float sum = 0.0f;
+    for (int c = lane; c < V; c += 64) sum += expf(row[c] - mx);
+    sum = wave_sum(sum);
+    const float lse = mx + logf(sum);
+    const uint32_t tg = targets[t];
+    if (lane == 0) losses[t] = tg < (uint32_t)V ? lse - row[tg] : 0.0f;
+    float* drow = dlogits + t * V;
+    for (int c = lane; c < V; c += 64) {
+        float pr = expf(row[c] - lse) * inv_t;
+        if ((uint32_t)c == tg) pr -= inv_t;
+        drow[c] = pr;
+    }
+}
+
+}  // namespace asca
+
+using namespace asca;
+
+static unsigned row_blocks(long rows) { return (unsigned)((rows + (ROW_NT / 64) - 1) / (ROW_NT / 64)); }
+
+extern "C" {
+
+int asca_rmsnorm(const float* x, float* y, float* inv, long rows, int cols, float eps, void* stream) {
+    if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "negative shape");
+    if (rows == 0 || cols == 0) return ASCA_OK;
+    if (!x || !y) return fail(ASCA_ERR_INVALID, "null pointer in asca_rmsnorm");
+    int rc = pre_launch("rmsnorm");
+    if (rc) return rc;
+    hipLaunchKernelGGL(rmsnorm_k, dim3(row_blocks(rows)), dim3(ROW_NT), 0, as_stream(stream), x, y, inv, rows, cols,
+                       eps);
+    return post_launch("rmsnorm");
+}
+
+int asca_rmsnorm_bwd(const float* x, const float* dy, float* dx, long rows, int cols, float eps, void* stream) {
+    if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "negative shape");
+    if (rows == 0 || cols == 0) return ASCA_OK;
+    if (!x || !dy || !dx) return fail(ASCA_ERR_INVALID, "null pointer in asca_rmsnorm_bwd");
+    int rc = pre_launch("rmsnorm_bwd");
+    if (rc) return rc;
+    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(row_blocks(rows)), dim3(ROW_NT), 0, as_stream(stream), x, dy, dx, rows,
+                       cols, eps);
+    return post_launch("rmsnorm_bwd");
+}
+
+int asca_adamw_scalars(float lr, float beta1, float beta2, float eps, float wd, uint32_t step, float* out) {
+#pragma clang fp contract(off)
+    if (!out) return fail(ASCA_ERR_INVALID, "null output pointer");
+    if (step == 0 || step > 0x7fffffffu) return fail(ASCA_ERR_INVALID, "adamw step %u outside 1..2^31-1", step);
+    // f32::powi with a run-time exponent is binary exponentiation
+    auto powi = [](float a, int b) {
+        float r = 1.0f;
+        for (;;) {
+            if (b & 1) r *= a;
+            b /= 2;
+            if (b == 0) break;
+            a *= a;
+        }
+        return r;
+    };
+    const float bc1 = 1.0f - powi(beta1, (int)step);
+    const float bc2 = 1.0f - powi(beta2, (int)step);
+    out[0] = lr * sqrtf(bc1 / bc2);
+    out[1] = eps * sqrtf(bc2);
+    out[2] = lr * wd;
+    return ASCA_OK;
+}
+
+int asca_adamw(float* p, const float* g, float* m, float* v, long n, float lr, float beta1, float beta2,
+               float eps_t, float wd, void* stream) {
+    if (n < 0) return fail(ASCA_ERR_INVALID, "negative size");
+    if (n == 0) return ASCA_OK;
+    if (!p || !g || !m || !v) return fail(ASCA_ERR_INVALID, "null pointer in asca_adamw");
+    int rc = pre_launch("adamw");
+    if (rc) return rc;
+    long blocks = (n + 255) / 256;
+    const long cap = (long)(cu_count() > 0 ? cu_count() : 256) * 16;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(adamw_k, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), p, g, m, v, n, lr, beta1,
+                       beta2, 1.0f - beta1, 1.0f - beta2, eps_t, wd);
+    return post_launch("adamw");
+}
+
+int asca_hash_route_ws_bytes(int n, int n_experts, size_t* bytes) {
+    if (!bytes) return fail(ASCA_ERR_INVALID, "null output pointer");
+    if (n < 0 || n_experts < 1 || n_experts > 64)
+        return fail(ASCA_ERR_UNSUPPORTED, "hash route: n=%d n_experts=%d (1..64 experts)", n, n_experts);
+    const long nblk = (n + RT_NT - 1) / RT_NT;
+    *bytes = (size_t)(nblk > 0 ? nblk : 1) * n_experts * sizeof(int32_t);
+    return ASCA_OK;
+}
+
+int asca_hash_route(const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm, int32_t* offsets,
+                    void* ws, void* stream) {
+    size_t wsb = 0;
+    int rc = asca_hash_route_ws_bytes(n, n_experts, &wsb);
+    if (rc) return rc;
+    if (!offsets) return fail(ASCA_ERR_INVALID, "null offsets");
+    const int nblk = (n + RT_NT - 1) / RT_NT;
+    if (n > 0 && (!ids || !expert || !perm || !ws)) return fail(ASCA_ERR_INVALID, "null pointer in asca_hash_route");
+    int32_t* blk = reinterpret_cast<int32_t*>(ws);
+    const hipStream_t st = as_stream(stream);
+    if (n > 0) {
+        rc = pre_launch("route_count");
+        if (rc) return rc;
+        hipLaunchKernelGGL(route_count_k, dim3(nblk), dim3(RT_NT), 0, st, ids, n, n_experts, expert, blk);
+        rc = post_launch("route_count");
+        if (rc) return rc;
+    }
+    rc = pre_launch("route_scan");
+    if (rc) return rc;
+    hipLaunchKernelGGL(route_scan_k, dim3(1), dim3(64), 0, st, nblk, n_experts, blk, offsets);
+    rc = post_launch("route_scan");
+    if (rc || n == 0) return rc;
+    rc = pre_launch("route_place");
+    if (rc) return rc;
+    hipLaunchKernelGGL(route_place_k, dim3(nblk), dim3(RT_NT), 0, st, n, n_experts, expert, blk, perm);
+    return post_launch("route_place");
+}
+
+static int rows_copy(bool scatter, const float* src, const int32_t* idx, long n, int cols, float* dst, void* stream) {
+    if (n < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "negative shape");
+    if (n == 0 || cols == 0) return ASCA_OK;
+    if (!src || !idx || !dst) return fail(ASCA_ERR_INVALID, "null pointer in row gather/scatter");
+    const char* name = scatter ? "scatter_rows" : "gather_rows";
+    int rc = pre_launch(name);
+    if (rc) return rc;
+    const bool vec = cols % 4 == 0 && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    const hipStream_t st = as_stream(stream);
+    if (scatter) {
+        if (vec) hipLaunchKernelGGL((rows_copy_k<true, true>), dim3(row_blocks(n)), dim3(ROW_NT), 0, st, src, idx, n, cols, dst);
+        else hipLaunchKernelGGL((rows_copy_k<true, false>), dim3(row_blocks(n)), dim3(ROW_NT), 0, st, src, idx, n, cols, dst);
+    } else {
+        if (vec) hipLaunchKernelGGL((rows_copy_k<false, true>), dim3(row_blocks(n)), dim3(ROW_NT), 0, st, src, idx, n, cols, dst);
+        else hipLaunchKernelGGL((rows_copy_k<false, false>), dim3(row_blocks(n)), dim3(ROW_NT), 0, st, src, idx, n, cols, dst);
+    }
+    return post_launch(name);
+}
+
+int asca_gather_rows(const float* src, const int32_t* idx, long n, int cols, float* dst, void* stream) {
+    return rows_copy(false, src, idx, n, cols, dst, stream);
+}
+
+int asca_scatter_rows(const float* src, const int32_t* idx, long n, int cols, float* dst, void* stream) {
+    return rows_copy(true, src, idx, n, cols, dst, stream);
+}
+
+int asca_cross_entropy(const float* logits, const uint32_t* targets, long T, int V, float* dlogits, float* losses,
+                       void* stream) {
+    if (T < 0 || V <= 0) return fail(ASCA_ERR_INVALID, "bad shape T=%ld V=%d", T, V);
+    if (T == 0) return ASCA_OK;
+    if (!logits || !targets || !dlogits || !losses) return fail(ASCA_ERR_INVALID, "null pointer in asca_cross_entropy");
+    int rc = pre_launch("cross_entropy");
+    if (rc) return rc;
+    hipLaunchKernelGGL(cross_entropy_k, dim3(row_blocks(T)), dim3(ROW_NT), 0, as_stream(stream), logits, targets, T, V,
+                       1.0f / (float)T, dlogits, losses);
+    return post_launch("cross_entropy");
+}
+
+}  // extern "C"

@@ -1,12 +1,14 @@
 // In-bounds check of the wave-level primitives the kernels rely on: DPP
 // quad_perm / row_half_mirror / row_mirror / row_ror:8 and the gfx950
-// permlane16/32 swaps.  One wave, lane-indexed input, results copied back.
+// permlane16/32 swaps, and the operand/result lane layout of
+// v_mfma_f32_16x16x4_f32 that the GEMM kernels assume.  One wave, lane-indexed
+// input, results copied back.
 #include "common.h"
 #include "runtime.h"
 
 namespace asca {
 
-constexpr int SELFTEST_COLS = 10;
+constexpr int SELFTEST_COLS = 14;
 
 __global__ __launch_bounds__(64) void selftest_wave_k(float* __restrict__ out) {
     const int l = threadIdx.x;
@@ -29,6 +31,17 @@ __global__ __launch_bounds__(64) void selftest_wave_k(float* __restrict__ out) {
         r[8] = __uint_as_float(p[1]);
     }
     r[9] = wave_sum(x);
+    {
+        // small integers: the product is exact whatever the summation order
+        const float a = (float)((l * 7) % 13 - 6);
+        const float b = (float)((l * 5) % 11 - 5);
+        f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+        d = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, d, 0, 0, 0);
+        r[10] = d[0];
+        r[11] = d[1];
+        r[12] = d[2];
+        r[13] = d[3];
+    }
 #pragma unroll
     for (int c = 0; c < SELFTEST_COLS; ++c) out[c * 64 + l] = r[c];
 }

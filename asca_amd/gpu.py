@@ -28,7 +28,8 @@ from . import _lib
 from ._lib import AscaError
 
 ARCH = "gfx950"
-KERNELS = ("delta_fwd", "delta_bwd", "delta_states", "delta_decode")
+KERNELS = ("delta_fwd", "delta_bwd", "delta_states", "delta_decode", "rmsnorm", "rmsnorm_bwd", "adamw",
+           "hash_route", "gather_rows", "scatter_rows", "colsum", "cross_entropy", "gemm", "moe_fwd", "moe_bwd")
 DEFAULT_MIN_FLOPS = 4_000_000
 
 _f32 = np.float32
@@ -79,6 +80,14 @@ class DevBuf:
     @classmethod
     def from_host(cls, arr: np.ndarray) -> "DevBuf":
         a = np.ascontiguousarray(arr, dtype=_f32)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "DevBuf":
+        """Upload keeping the array's dtype (index and id buffers)."""
+        a = np.ascontiguousarray(arr)
         b = cls(a.nbytes)
         b.upload(a)
         return b
@@ -148,6 +157,77 @@ class DeltaDev:
         finally:
             buf.free()
         return [flat[i] for i in range(H * B)]
+
+
+class MoeDev:
+    """HashMoE forward state kept on the device for the backward
+    (rust/src/cuda/mod.rs:1416-1431): xn, w1, w2, the expert-sorted pre and
+    hidden activations and the bucketing (perm, offsets)."""
+
+    def __init__(self, xn, w1, w2, pre, hidden, perm, offsets, t_len, d, d_ff, n_experts):
+        self.xn, self.w1, self.w2, self.pre, self.hidden = xn, w1, w2, pre, hidden
+        self.perm, self.offsets = perm, offsets
+        self.t_len, self.d, self.d_ff, self.n_experts = t_len, d, d_ff, n_experts
+
+    def buckets(self) -> tuple[np.ndarray, np.ndarray]:
+        perm = self.perm.to_host((self.t_len,), np.int32)
+        off = self.offsets.to_host((self.n_experts + 1,), np.int32)
+        return perm, off
+
+    def download_pre_hidden(self) -> tuple[list[np.ndarray], list[np.ndarray]]:
+        """Per-expert (n_e x d_ff) pre and hidden (rust/src/cuda/mod.rs:1445-1461)."""
+        _, off = self.buckets()
+        pre = self.pre.to_host((self.t_len, self.d_ff))
+        hid = self.hidden.to_host((self.t_len, self.d_ff))
+        return ([pre[off[e]:off[e + 1]] for e in range(self.n_experts)],
+                [hid[off[e]:off[e + 1]] for e in range(self.n_experts)])
+
+
+class MoeBwd:
+    """Gradients of the MoE backward (rust/src/cuda/mod.rs:1433-1440)."""
+
+    def __init__(self, d_w1, d_b1, d_w2, d_b2, dxn):
+        self.d_w1, self.d_b1, self.d_w2, self.d_b2, self.dxn = d_w1, d_b1, d_w2, d_b2, dxn
+
+
+def _mat(x, name, shape=None) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=_f32)
+    if shape is not None and a.shape != tuple(shape):
+        raise ValueError(f"{name} has shape {a.shape}, expected {tuple(shape)}")
+    return a
+
+
+def _buckets_csr(buckets, t_len: int) -> tuple[np.ndarray, np.ndarray]:
+    perm = np.fromiter((t for rows in buckets for t in rows), dtype=np.int32, count=sum(len(r) for r in buckets))
+    if perm.size != t_len or (t_len and not np.array_equal(np.sort(perm), np.arange(t_len))):
+        raise ValueError("buckets must partition the token rows")
+    off = np.zeros(len(buckets) + 1, dtype=np.int32)
+    off[1:] = np.cumsum([len(r) for r in buckets])
+    return perm, off
+
+
+_param_dev: dict = {}
+
+
+def param_key(m: np.ndarray) -> tuple[int, int]:
+    """Identity of a parameter's moment buffer (rust/src/cuda/mod.rs:57-62)."""
+    return (m.ctypes.data, m.size)
+
+
+def param_moments(key) -> tuple[np.ndarray, np.ndarray] | None:
+    """Device-resident AdamW moments of a parameter, downloaded
+    (rust/src/cuda/mod.rs:64-73)."""
+    ent = _param_dev.get(key)
+    if ent is None:
+        return None
+    dm, dv, n = ent
+    _lib.call("asca_sync")
+    return dm.to_host((n,)), dv.to_host((n,))
+
+
+def reset_param_cache() -> None:
+    """rust/src/cuda/mod.rs:50-55."""
+    _param_dev.clear()
 
 
 # --------------------------------------------------------------------- Gpu
@@ -224,6 +304,235 @@ class Gpu:
                 b.free()
         return tuple(res)
 
+
+    # -- row operations -----------------------------------------------------
+    def rmsnorm(self, x, eps: float):
+        """Gpu::rmsnorm (rust/src/cuda/mod.rs:911-939): (y, inv_rms)."""
+        x = _mat(x, "x")
+        rows, cols = x.shape
+        dx, dy, dinv = DevBuf.from_host(x), DevBuf(x.nbytes), DevBuf(rows * 4)
+        try:
+            _lib.call("asca_rmsnorm", _vp(dx), _vp(dy), _vp(dinv), rows, cols, eps, None)
+            _lib.call("asca_sync")
+            return dy.to_host((rows, cols)), dinv.to_host((rows,))
+        finally:
+            for b in (dx, dy, dinv):
+                b.free()
+
+    def rmsnorm_bwd(self, x, dy, eps: float):
+        """Gpu::rmsnorm_bwd (rust/src/cuda/mod.rs:1122-1153)."""
+        x = _mat(x, "x")
+        dy = _mat(dy, "dy", x.shape)
+        bx, bdy, bdx = DevBuf.from_host(x), DevBuf.from_host(dy), DevBuf(x.nbytes)
+        try:
+            _lib.call("asca_rmsnorm_bwd", _vp(bx), _vp(bdy), _vp(bdx), x.shape[0], x.shape[1], eps, None)
+            _lib.call("asca_sync")
+            return bdx.to_host(x.shape)
+        finally:
+            for b in (bx, bdy, bdx):
+                b.free()
+
+    def cross_entropy_bwd(self, logits, targets):
+        """Gpu::cross_entropy_bwd (rust/src/cuda/mod.rs:945-997): (mean loss,
+        dlogits); the loss is the f32 sum of per-row losses times 1/T."""
+        logits = _mat(logits, "logits")
+        t_len, v = logits.shape
+        tg = np.ascontiguousarray(targets, dtype=np.uint32)
+        if tg.shape != (t_len,):
+            raise ValueError("targets len must equal logits rows")
+        bl, bt, bd, bs = DevBuf.from_host(logits), DevBuf.from_array(tg), DevBuf(logits.nbytes), DevBuf(t_len * 4)
+        try:
+            _lib.call("asca_cross_entropy", _vp(bl), _vp(bt), t_len, v, _vp(bd), _vp(bs), None)
+            _lib.call("asca_sync")
+            losses = bs.to_host((t_len,))
+            inv_t = _f32(1.0) / _f32(t_len)
+            loss = (np.cumsum(losses, dtype=_f32)[-1] if t_len else _f32(0)) * inv_t
+            return float(loss), bd.to_host((t_len, v))
+        finally:
+            for b in (bl, bt, bd, bs):
+                b.free()
+
+    def gather_rows(self, src, idx):
+        """Gpu::gather_rows (rust/src/cuda/mod.rs:1156-1188): src[idx]."""
+        src = _mat(src, "src")
+        ix = np.ascontiguousarray(idx, dtype=np.int32)
+        if ix.size and (ix.min() < 0 or ix.max() >= src.shape[0]):
+            raise ValueError("gather_rows: index out of range")
+        bs, bi, bd = DevBuf.from_host(src), DevBuf.from_array(ix), DevBuf(ix.size * src.shape[1] * 4)
+        try:
+            _lib.call("asca_gather_rows", _vp(bs), _vp(bi), ix.size, src.shape[1], _vp(bd), None)
+            _lib.call("asca_sync")
+            return bd.to_host((ix.size, src.shape[1]))
+        finally:
+            for b in (bs, bi, bd):
+                b.free()
+
+    def scatter_rows(self, src, idx, dst: np.ndarray) -> None:
+        """Gpu::scatter_rows (rust/src/cuda/mod.rs:1190-1222): dst[idx] = src,
+        in place on the host matrix."""
+        src = _mat(src, "src")
+        ix = np.ascontiguousarray(idx, dtype=np.int32)
+        if dst.dtype != _f32 or not dst.flags["C_CONTIGUOUS"] or dst.shape[1] != src.shape[1]:
+            raise ValueError("scatter_rows: dst must be a C-contiguous float32 matrix with src's columns")
+        if ix.size != src.shape[0] or (ix.size and (ix.min() < 0 or ix.max() >= dst.shape[0])):
+            raise ValueError("scatter_rows: bad indices")
+        if np.unique(ix).size != ix.size:
+            raise ValueError("scatter_rows: indices must be distinct")
+        bs, bi, bd = DevBuf.from_host(src), DevBuf.from_array(ix), DevBuf.from_host(dst)
+        try:
+            _lib.call("asca_scatter_rows", _vp(bs), _vp(bi), ix.size, src.shape[1], _vp(bd), None)
+            _lib.call("asca_sync")
+            bd.download(dst)
+        finally:
+            for b in (bs, bi, bd):
+                b.free()
+
+    # -- GEMM ---------------------------------------------------------------
+    def gemm(self, a, b, trans_a: bool = False, trans_b: bool = False, alpha: float = 1.0,
+             beta: float = 0.0, c=None, bias=None):
+        """C = alpha op(A) op(B) + bias + beta C on the matrix cores."""
+        a, b = _mat(a, "a"), _mat(b, "b")
+        m, k = (a.shape[1], a.shape[0]) if trans_a else a.shape
+        k2, n = (b.shape[1], b.shape[0]) if trans_b else b.shape
+        if k != k2:
+            raise ValueError(f"gemm: inner dimensions {k} and {k2} differ")
+        cc = _mat(c, "c", (m, n)) if c is not None else np.zeros((m, n), dtype=_f32)
+        bb = _mat(bias, "bias", (n,)) if bias is not None else None
+        ba, bbuf, bc = DevBuf.from_host(a), DevBuf.from_host(b), DevBuf.from_host(cc)
+        bbias = DevBuf.from_host(bb) if bb is not None else None
+        try:
+            _lib.call("asca_gemm", int(trans_a), int(trans_b), m, n, k, alpha, _vp(ba), a.shape[1], _vp(bbuf),
+                      b.shape[1], beta, _vp(bc), n, _vp(bbias), None)
+            _lib.call("asca_sync")
+            return bc.to_host((m, n))
+        finally:
+            for x in (ba, bbuf, bc, bbias):
+                if x is not None:
+                    x.free()
+
+    def matmul(self, a, b):
+        """Gpu::matmul (rust/src/cuda/mod.rs:286-313): A @ B."""
+        return self.gemm(a, b)
+
+    def matmul_ta(self, a, b):
+        """Gpu::matmul_ta (rust/src/cuda/mod.rs:316-344): A^T @ B."""
+        return self.gemm(a, b, trans_a=True)
+
+    def matmul_t(self, a, b):
+        """A @ B^T (Mat::matmul_t, rust/src/tensor.rs:180-201)."""
+        return self.gemm(a, b, trans_b=True)
+
+    # -- AdamW ----------------------------------------------------------------
+    def adamw_scalars(self, lr, beta1, beta2, eps, wd, step: int):
+        """(lr_bc, eps_t, wd_eff) of AdamW::update (rust/src/tensor.rs:392-402), f32."""
+        out = (C.c_float * 3)()
+        _lib.call("asca_adamw_scalars", lr, beta1, beta2, eps, wd, step, out)
+        return out[0], out[1], out[2]
+
+    def adamw_update(self, val: np.ndarray, grad, m: np.ndarray, v: np.ndarray, lr, beta1, beta2, eps_t, wd):
+        """Gpu::adamw_update (rust/src/cuda/mod.rs:1057-1119): one update of
+        val, m, v in place (host arrays) with the CPU path's element math."""
+        n = val.size
+        for name, x in (("val", val), ("m", m), ("v", v)):
+            if x.dtype != _f32 or not x.flags["C_CONTIGUOUS"] or x.size != n:
+                raise ValueError(f"adamw_update: {name} must be a C-contiguous float32 array of {n}")
+        g = _mat(grad, "grad").reshape(-1)
+        if g.size != n:
+            raise ValueError("adamw_update: grad size differs")
+        bp, bg, bm, bv = DevBuf.from_host(val), DevBuf.from_host(g), DevBuf.from_host(m), DevBuf.from_host(v)
+        try:
+            _lib.call("asca_adamw", _vp(bp), _vp(bg), _vp(bm), _vp(bv), n, lr, beta1, beta2, eps_t, wd, None)
+            _lib.call("asca_sync")
+            bp.download(val)
+            bm.download(m)
+            bv.download(v)
+        finally:
+            for b in (bp, bg, bm, bv):
+                b.free()
+
+    def adamw_resident(self, key, val: np.ndarray, grad, m0, v0, lr, beta1, beta2, eps_t, wd):
+        """Gpu::adamw_resident (rust/src/cuda/mod.rs:1003-1054): moments stay
+        on the device between steps (param_moments downloads them)."""
+        n = val.size
+        ent = _param_dev.get(key)
+        if ent is None:
+            ent = (DevBuf.from_host(np.asarray(m0).reshape(-1)), DevBuf.from_host(np.asarray(v0).reshape(-1)), n)
+            _param_dev[key] = ent
+        dm, dv, _ = ent
+        g = _mat(grad, "grad").reshape(-1)
+        bp, bg = DevBuf.from_host(val), DevBuf.from_host(g)
+        try:
+            _lib.call("asca_adamw", _vp(bp), _vp(bg), _vp(dm), _vp(dv), n, lr, beta1, beta2, eps_t, wd, None)
+            _lib.call("asca_sync")
+            bp.download(val)
+        finally:
+            bp.free()
+            bg.free()
+
+    # -- hash MoE ---------------------------------------------------------------
+    def hash_route(self, ids, n_experts: int):
+        """Expert of every token and the stable buckets as (expert, perm,
+        offsets) (rust/src/model.rs:69-77,190-193), computed on the device."""
+        ix = np.ascontiguousarray(ids, dtype=np.uint32)
+        n = ix.size
+        wsb = C.c_size_t()
+        _lib.call("asca_hash_route_ws_bytes", n, n_experts, C.byref(wsb))
+        bi, be, bp = DevBuf.from_array(ix), DevBuf(n * 4), DevBuf(n * 4)
+        bo, bw = DevBuf((n_experts + 1) * 4), DevBuf(wsb.value)
+        try:
+            _lib.call("asca_hash_route", _vp(bi), n, n_experts, _vp(be), _vp(bp), _vp(bo), _vp(bw), None)
+            _lib.call("asca_sync")
+            return (be.to_host((n,), np.int32), bp.to_host((n,), np.int32),
+                    bo.to_host((n_experts + 1,), np.int32))
+        finally:
+            for b in (bi, be, bp, bo, bw):
+                b.free()
+
+    def moe_forward_dev(self, xn, w1, b1, w2, b2, buckets, d_ff: int):
+        """Gpu::moe_forward_dev (rust/src/cuda/mod.rs:523-607): (out, MoeDev)
+        with every expert product in one grouped launch each."""
+        xn = _mat(xn, "xn")
+        t_len, d = xn.shape
+        n_experts = len(buckets)
+        w1 = _mat(w1, "w1", (d, n_experts * d_ff))
+        w2 = _mat(w2, "w2", (n_experts * d_ff, d))
+        b1 = _mat(b1, "b1").reshape(-1)
+        b2 = _mat(b2, "b2").reshape(-1)
+        if b1.size != n_experts * d_ff or b2.size != d:
+            raise ValueError("moe_forward_dev: bias sizes")
+        perm, off = _buckets_csr(buckets, t_len)
+        bx, bw1, bw2 = DevBuf.from_host(xn), DevBuf.from_host(w1), DevBuf.from_host(w2)
+        bb1, bb2 = DevBuf.from_host(b1), DevBuf.from_host(b2)
+        bperm, boff = DevBuf.from_array(perm), DevBuf.from_array(off)
+        pre, hid, out = DevBuf(t_len * d_ff * 4), DevBuf(t_len * d_ff * 4), DevBuf(t_len * d * 4)
+        try:
+            _lib.call("asca_moe_fwd", _vp(bx), _vp(bw1), _vp(bb1), _vp(bw2), _vp(bb2), _vp(bperm), _vp(boff),
+                      t_len, d, d_ff, n_experts, _vp(out), _vp(pre), _vp(hid), None)
+            _lib.call("asca_sync")
+            o = out.to_host((t_len, d))
+        finally:
+            for b in (bb1, bb2, out):
+                b.free()
+        return o, MoeDev(bx, bw1, bw2, pre, hid, bperm, boff, t_len, d, d_ff, n_experts)
+
+    def moe_bwd_dev(self, dev: MoeDev, dout) -> MoeBwd:
+        """Gpu::moe_bwd_dev (rust/src/cuda/mod.rs:745-824): all expert
+        gradients on the device; the caller applies rmsnorm_bwd to dxn."""
+        t_len, d, d_ff, E = dev.t_len, dev.d, dev.d_ff, dev.n_experts
+        dout = _mat(dout, "dout", (t_len, d))
+        bdo = DevBuf.from_host(dout)
+        bdx, bdw1, bdb1 = DevBuf(t_len * d * 4), DevBuf(d * E * d_ff * 4), DevBuf(E * d_ff * 4)
+        bdw2, bdb2, bws = DevBuf(E * d_ff * d * 4), DevBuf(d * 4), DevBuf(t_len * d_ff * 4)
+        try:
+            _lib.call("asca_moe_bwd", _vp(dev.xn), _vp(dev.w1), _vp(dev.w2), _vp(dev.pre), _vp(dev.hidden),
+                      _vp(dev.perm), _vp(dev.offsets), _vp(bdo), t_len, d, d_ff, E, _vp(bdx), _vp(bdw1),
+                      _vp(bdb1), _vp(bdw2), _vp(bdb2), _vp(bws), 0, None)
+            _lib.call("asca_sync")
+            return MoeBwd(bdw1.to_host((d, E * d_ff)), bdb1.to_host((E * d_ff,)), bdw2.to_host((E * d_ff, d)),
+                          bdb2.to_host((d,)), bdx.to_host((t_len, d)))
+        finally:
+            for b in (bdo, bdx, bdw1, bdb1, bdw2, bdb2, bws):
+                b.free()
 
     # -- decode -------------------------------------------------------------
     def new_decode_states(self, n_seq: int, n_heads: int, dh: int) -> DevBuf:

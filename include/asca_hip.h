@@ -106,8 +106,10 @@ ASCA_API int asca_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Diagnostic: runs one wave through the lane-exchange primitives the kernels
  * use (DPP quad_perm xor1/xor2, row_half_mirror, row_mirror, row_ror:8,
  * permlane32_swap, permlane16_swap, full-wave sum) on x[lane] = lane and
- * y[lane] = 100 + lane, and copies 10 x 64 floats to host_out (row c = result
- * c per lane).  No reference counterpart. */
+ * y[lane] = 100 + lane, then one v_mfma_f32_16x16x4_f32 on small-integer
+ * operands a[lane] = (7 lane) % 13 - 6, b[lane] = (5 lane) % 11 - 5 (rows 10-13:
+ * its four result registers), and copies 14 x 64 floats to host_out (row c =
+ * result c per lane).  No reference counterpart. */
 ASCA_API int asca_selftest_wave(float* host_out);
 
 /* Plain streaming device copy of n floats (n % 4 == 0, 16-byte aligned
@@ -192,6 +194,128 @@ ASCA_API int asca_delta_states(const float* q, const float* k, const float* v,
  *   o      : (n_seq, H*dh) output */
 ASCA_API int asca_delta_decode_step(float* states, const float* qkv, const float* gate, float* o,
                                     int n_seq, int H, int dh, void* stream);
+
+/* ------------------------------------------------------- row operations -- */
+
+/* Row-wise RMSNorm without gain: y = x / sqrt(mean(x^2) + eps) per row of a
+ * (rows, cols) matrix; inv (rows, may be NULL) receives 1/rms.  Replaces
+ * Gpu::rmsnorm (rust/src/cuda/mod.rs:911-939) and kernel rmsnorm_f32
+ * (rust/kernels/asca.cu:198-215); CPU semantics rmsnorm_rows
+ * (rust/src/tensor.rs:251-270).  The model uses eps = 1e-6 (model.rs:14). */
+ASCA_API int asca_rmsnorm(const float* x, float* y, float* inv, long rows, int cols, float eps,
+                          void* stream);
+
+/* RMSNorm backward: dx = inv (dy - x inv mean(dy x inv)) per row.  Replaces
+ * Gpu::rmsnorm_bwd (mod.rs:1122-1153), kernel rmsnorm_bwd_f32 (asca.cu:217-242);
+ * CPU semantics rmsnorm_rows_backward (tensor.rs:272-297). */
+ASCA_API int asca_rmsnorm_bwd(const float* x, const float* dy, float* dx, long rows, int cols, float eps,
+                              void* stream);
+
+/* Softmax cross-entropy with its backward, per row t of (T, V) logits:
+ * losses[t] = lse_t - logits[t][target_t] (0 for a target >= V), dlogits =
+ * softmax / T minus 1/T at the target.  Replaces Gpu::cross_entropy_bwd
+ * (mod.rs:945-997) and kernel cross_entropy_bwd_f32 (asca.cu:490-548); CPU
+ * semantics cpu_cross_entropy (rust/src/model.rs:804-844).  The mean loss is
+ * the sum of losses times 1/T (host side, as the reference does). */
+ASCA_API int asca_cross_entropy(const float* logits, const uint32_t* targets, long T, int V,
+                                float* dlogits, float* losses, void* stream);
+
+/* dst[r] = src[idx[r]] for r < n, rows of `cols` floats.  Replaces
+ * Gpu::gather_rows / gather_raw (mod.rs:401-424,1156-1188) and kernel
+ * gather_rows_f32 (asca.cu:576-584).  idx is a device int32 array. */
+ASCA_API int asca_gather_rows(const float* src, const int32_t* idx, long n, int cols, float* dst,
+                              void* stream);
+
+/* dst[idx[r]] = src[r] for r < n (indices distinct).  Replaces
+ * Gpu::scatter_rows / scatter_raw (mod.rs:426-448,1190-1222) and kernel
+ * scatter_rows_f32 (asca.cu:586-594). */
+ASCA_API int asca_scatter_rows(const float* src, const int32_t* idx, long n, int cols, float* dst,
+                               void* stream);
+
+/* out[c] (+)= sum over rows of X[r][c] (accumulate != 0 adds to out): the bias
+ * gradient, colsum_raw of rust/src/cuda/mod.rs:642-669.  Deterministic. */
+ASCA_API int asca_colsum(const float* X, long rows, int cols, float* out, int accumulate, void* stream);
+
+/* ----------------------------------------------------------------- AdamW -- */
+
+/* The per-step scalars of AdamW::update (rust/src/tensor.rs:392-402), in f32
+ * exactly as the CPU computes them, for step s >= 1 (the counter after its
+ * increment; the reference counts steps per parameter tensor):
+ *   out[0] = lr * sqrt((1 - beta1^s) / (1 - beta2^s))   (bias-corrected lr)
+ *   out[1] = eps * sqrt(1 - beta2^s)                    (eps_t)
+ *   out[2] = lr * wd                                    (decoupled decay) */
+ASCA_API int asca_adamw_scalars(float lr, float beta1, float beta2, float eps, float wd, uint32_t step,
+                                float* out);
+
+/* One AdamW update of n parameters in place, moments m, v resident on the
+ * device; lr, eps_t, wd as produced by asca_adamw_scalars.  Replaces
+ * Gpu::adamw_update / adamw_resident (mod.rs:1003-1119) with the element
+ * update of the CPU path (tensor.rs:444-453), bit-exact to it:
+ *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g g;  p -= wd p;
+ *   p -= lr m / (sqrt(v) + eps_t).
+ * (The reference's adamw_f32 kernel, asca.cu:551-570, scales the decay by lr
+ * a second time; the CPU path is the one followed here.) */
+ASCA_API int asca_adamw(float* p, const float* g, float* m, float* v, long n, float lr, float beta1,
+                        float beta2, float eps_t, float wd, void* stream);
+
+/* ----------------------------------------------------------- hash routing -- */
+
+/* Workspace bytes for asca_hash_route (n tokens, 1..64 experts). */
+ASCA_API int asca_hash_route_ws_bytes(int n, int n_experts, size_t* bytes);
+
+/* Expert of every token, expert = hash_route(id) % n_experts with the
+ * reference's wrapping u32 finaliser (rust/src/model.rs:69-77), and the
+ * buckets of HashMoe::forward (model.rs:190-193) as CSR: perm lists the tokens
+ * of expert 0 in ascending order, then expert 1, ...; offsets[e]..offsets[e+1]
+ * bound expert e (offsets has n_experts + 1 entries).  Bit-exact and
+ * deterministic.  ids: device u32 (n); expert, perm: device int32 (n). */
+ASCA_API int asca_hash_route(const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm,
+                             int32_t* offsets, void* ws, void* stream);
+
+/* ------------------------------------------------------------------ GEMM -- */
+
+/* C = alpha op(A) op(B) + bias (per column, may be NULL) + beta C, f32 on the
+ * matrix cores; op(A) = A (M x K, lda) or A^T (trans_a: A stored K x M),
+ * op(B) = B (K x N, ldb) or B^T (trans_b: B stored N x K).  Column/row offsets
+ * into a wider matrix are expressed by pointer and leading dimension.
+ * Replaces Gpu::matmul / matmul_ta / matmul_raw / matmul_ta_raw /
+ * matmul_ld_raw / matmul_ta_ld_raw / matmul_tb_raw (rust/src/cuda/mod.rs:286-521,
+ * 671-743) with kernels matmul_f32 / matmul_ta_f32 / matmul_ld_f32
+ * (asca.cu:14-141); CPU semantics Mat::matmul / matmul_ta / matmul_t
+ * (rust/src/tensor.rs:91-201).  Deterministic (split-K partials are summed in
+ * a fixed order in a library-owned per-device scratch buffer; calls that
+ * split K on different streams of one device must not overlap). */
+ASCA_API int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda,
+                       const float* B, long ldb, float beta, float* C, long ldc, const float* bias,
+                       void* stream);
+
+/* ------------------------------------------------------------------- MoE -- */
+
+/* HashMoE forward on normalised input xn (T x d), tokens bucketed by
+ * asca_hash_route (perm, offsets): per expert e,
+ *   pre = xn[rows_e] w1[:, e*d_ff:(e+1)*d_ff] + b1[e*d_ff..];  hidden = silu(pre)
+ *   out[rows_e] = hidden w2[e*d_ff:(e+1)*d_ff, :] + b2
+ * as Gpu::moe_forward_dev (rust/src/cuda/mod.rs:523-607) over the CPU
+ * semantics of HashMoe::forward (rust/src/model.rs:187-306).  w1 (d x E*d_ff),
+ * b1 (E*d_ff), w2 (E*d_ff x d), b2 (d).  pre and hidden (T x d_ff) are written
+ * in expert-sorted row order (row i is token perm[i]) and kept for the
+ * backward, like MoeDev (mod.rs:1416-1431). */
+ASCA_API int asca_moe_fwd(const float* xn, const float* w1, const float* b1, const float* w2,
+                          const float* b2, const int32_t* perm, const int32_t* offsets, int T, int d,
+                          int d_ff, int n_experts, float* out, float* pre, float* hidden, void* stream);
+
+/* HashMoE backward from dout (T x d): dW2 = hidden^T dout, db2 = colsum(dout),
+ * dpre = dout w2_e^T * silu'(pre), db1 = colsum(dpre), dW1 = xn^T dpre,
+ * dxn = dpre w1_e^T, per expert (Gpu::moe_bwd_dev, mod.rs:745-824; CPU
+ * semantics HashMoe::backward, model.rs:339-497, before its RMSNorm backward).
+ * With accumulate != 0 the weight and bias gradients are added to dw1, db1,
+ * dw2, db2 (Param::grad accumulation); dxn is overwritten.  dpre_ws: T*d_ff
+ * floats of workspace. */
+ASCA_API int asca_moe_bwd(const float* xn, const float* w1, const float* w2, const float* pre,
+                          const float* hidden, const int32_t* perm, const int32_t* offsets,
+                          const float* dout, int T, int d, int d_ff, int n_experts, float* dxn,
+                          float* dw1, float* db1, float* dw2, float* db2, float* dpre_ws, int accumulate,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -580,3 +580,199 @@ ORC_API void orc_adamw(float* p, const float* g, float* m, float* v, long n,
         p[i] -= lrb * upd;
     }
 }
+
+/* ------------------------------------------------------------------ MoE */
+/* HashMoe::forward CPU path, rust/src/model.rs:187-306: one thread per expert
+ * (model.rs:231-270), tokens of expert e in ascending order (model.rs:190-193),
+ * pre = b1_e + sum_c xn[t][c] w1[c][e*dff..] (axpy per c, zero x skipped),
+ * hidden = silu(pre) = x / (1 + exp(-x)) (model.rs:79-85),
+ * out = b2 + sum_j hidden[t][j] w2[e*dff+j] (axpy per j, zero h skipped).
+ * route[t] is the expert of token t; outputs are in token order. */
+typedef struct {
+    const float *xn, *w1, *b1, *w2, *b2, *pre_in, *hid_in, *dout;
+    const int32_t* route;
+    long T;
+    int d, dff, E, e;
+    float *out, *pre, *hidden;
+    /* backward, per expert */
+    float *dw1, *dw2, *db1, *db2, *dxn;
+    long* rows;
+    long n;
+} moe_job;
+
+static float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+static void moe_rows(moe_job* j) {
+    j->n = 0;
+    for (long t = 0; t < j->T; ++t)
+        if (j->route[t] == j->e) j->rows[j->n++] = t;
+}
+
+static void* moe_fwd_thread(void* p) {
+    moe_job* j = (moe_job*)p;
+    const int d = j->d, dff = j->dff, e = j->e;
+    const long ld1 = (long)j->E * dff;
+    moe_rows(j);
+    for (long i = 0; i < j->n; ++i) memcpy(j->pre + j->rows[i] * dff, j->b1 + (long)e * dff, dff * sizeof(float));
+    for (int c = 0; c < d; ++c) {
+        const float* w1row = j->w1 + c * ld1 + (long)e * dff;
+        for (long i = 0; i < j->n; ++i) {
+            const long t = j->rows[i];
+            const float xc = j->xn[t * d + c];
+            if (xc == 0.0f) continue;
+            saxpy(j->pre + t * dff, xc, w1row, dff);
+        }
+    }
+    for (long i = 0; i < j->n; ++i) {
+        const long t = j->rows[i];
+        for (int q = 0; q < dff; ++q) j->hidden[t * dff + q] = silu_f(j->pre[t * dff + q]);
+        memcpy(j->out + t * d, j->b2, d * sizeof(float));
+    }
+    for (int q = 0; q < dff; ++q) {
+        const float* w2row = j->w2 + ((long)e * dff + q) * d;
+        for (long i = 0; i < j->n; ++i) {
+            const long t = j->rows[i];
+            const float h = j->hidden[t * dff + q];
+            if (h == 0.0f) continue;
+            saxpy(j->out + t * d, h, w2row, d);
+        }
+    }
+    return NULL;
+}
+
+static void moe_run(moe_job* jobs, int E, void* (*fn)(void*)) {
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * E);
+    for (int e = 0; e < E; ++e) pthread_create(&th[e], NULL, fn, &jobs[e]);
+    for (int e = 0; e < E; ++e) pthread_join(th[e], NULL);
+    free(th);
+}
+
+ORC_API void orc_moe_fwd(const float* xn, const float* w1, const float* b1, const float* w2, const float* b2,
+                         const int32_t* route, long T, int d, int dff, int E,
+                         float* out, float* pre, float* hidden) {
+    moe_job* jobs = (moe_job*)calloc(E, sizeof(moe_job));
+    for (int e = 0; e < E; ++e) {
+        moe_job* j = &jobs[e];
+        j->xn = xn; j->w1 = w1; j->b1 = b1; j->w2 = w2; j->b2 = b2; j->route = route;
+        j->T = T; j->d = d; j->dff = dff; j->E = E; j->e = e;
+        j->out = out; j->pre = pre; j->hidden = hidden;
+        j->rows = (long*)malloc(sizeof(long) * (T > 0 ? T : 1));
+    }
+    moe_run(jobs, E, moe_fwd_thread);
+    for (int e = 0; e < E; ++e) free(jobs[e].rows);
+    free(jobs);
+}
+
+/* HashMoe::backward CPU path, rust/src/model.rs:365-497 (before its RMSNorm
+ * backward): per expert, into the expert's own buffers (model.rs:370-397),
+ *   dW2_e[j] += h[t][j] dout[t] (axpy, zero h skipped); db2_e += dout[t];
+ *   dpre = dot(dout[t], w2[e*dff+j]); dh = dpre * s (1 + pre (1 - s)), db1_e += dh;
+ *   dW1_e[c] += xn[t][c] dh (axpy, zero x skipped); dxn_e[i][c] += dot(dh_i, w1[c][e*dff..]);
+ * then merged in expert order (model.rs:466-494).  Gradients are written
+ * (the Param::grad buffers are taken to start at zero). */
+static void* moe_bwd_thread(void* p) {
+    moe_job* j = (moe_job*)p;
+    const int d = j->d, dff = j->dff, e = j->e;
+    const long ld1 = (long)j->E * dff;
+    moe_rows(j);
+    const long n = j->n;
+    if (n == 0) return NULL;
+    float* dpre = (float*)calloc((size_t)n * dff, sizeof(float));
+    for (long i = 0; i < n; ++i) {
+        const long t = j->rows[i];
+        const float* dr = j->dout + t * d;
+        for (int q = 0; q < dff; ++q) {
+            const float h = j->hid_in[t * dff + q];
+            if (h == 0.0f) continue;
+            saxpy(j->dw2 + (long)q * d, h, dr, d);
+        }
+        for (int c = 0; c < d; ++c) j->db2[c] += dr[c];
+    }
+    for (long i = 0; i < n; ++i) {
+        const float* dr = j->dout + j->rows[i] * d;
+        for (int q = 0; q < dff; ++q) dpre[i * dff + q] = sdot(dr, j->w2 + ((long)e * dff + q) * d, d);
+    }
+    for (long i = 0; i < n; ++i) {
+        const long t = j->rows[i];
+        for (int q = 0; q < dff; ++q) {
+            const float pr = j->pre_in[t * dff + q];
+            const float sg = 1.0f / (1.0f + expf(-pr));
+            const float dh = dpre[i * dff + q] * (sg * (1.0f + pr * (1.0f - sg)));
+            j->db1[q] += dh;
+            dpre[i * dff + q] = dh;
+        }
+    }
+    for (int c = 0; c < d; ++c) {
+        const float* w1row = j->w1 + c * ld1 + (long)e * dff;
+        float* gw = j->dw1 + (long)c * dff;
+        for (long i = 0; i < n; ++i) {
+            const float xc = j->xn[j->rows[i] * d + c];
+            if (xc == 0.0f) continue;
+            saxpy(gw, xc, dpre + i * dff, dff);
+        }
+        for (long i = 0; i < n; ++i) j->dxn[i * d + c] += sdot(dpre + i * dff, w1row, dff);
+    }
+    free(dpre);
+    return NULL;
+}
+
+ORC_API void orc_moe_bwd(const float* xn, const float* w1, const float* w2, const float* pre,
+                         const float* hidden, const int32_t* route, const float* dout,
+                         long T, int d, int dff, int E,
+                         float* dxn, float* dw1, float* db1, float* dw2, float* db2) {
+    moe_job* jobs = (moe_job*)calloc(E, sizeof(moe_job));
+    for (int e = 0; e < E; ++e) {
+        moe_job* j = &jobs[e];
+        j->xn = xn; j->w1 = w1; j->w2 = w2; j->pre_in = pre; j->hid_in = hidden; j->dout = dout;
+        j->route = route; j->T = T; j->d = d; j->dff = dff; j->E = E; j->e = e;
+        j->rows = (long*)malloc(sizeof(long) * (T > 0 ? T : 1));
+        j->dw1 = (float*)calloc((size_t)d * dff, sizeof(float));
+        j->dw2 = (float*)calloc((size_t)dff * d, sizeof(float));
+        j->db1 = (float*)calloc(dff, sizeof(float));
+        j->db2 = (float*)calloc(d, sizeof(float));
+        j->dxn = (float*)calloc((size_t)(T > 0 ? T : 1) * d, sizeof(float));
+    }
+    moe_run(jobs, E, moe_bwd_thread);
+    const long ld1 = (long)E * dff;
+    memset(dxn, 0, sizeof(float) * T * d);
+    memset(dw1, 0, sizeof(float) * d * ld1);
+    memset(dw2, 0, sizeof(float) * ld1 * d);
+    memset(db1, 0, sizeof(float) * ld1);
+    memset(db2, 0, sizeof(float) * d);
+    for (int e = 0; e < E; ++e) {
+        moe_job* j = &jobs[e];
+        for (int q = 0; q < dff; ++q)
+            for (int c = 0; c < d; ++c) dw2[((long)e * dff + q) * d + c] += j->dw2[(long)q * d + c];
+        for (int c = 0; c < d; ++c)
+            for (int q = 0; q < dff; ++q) dw1[c * ld1 + (long)e * dff + q] += j->dw1[(long)c * dff + q];
+        for (int q = 0; q < dff; ++q) db1[(long)e * dff + q] += j->db1[q];
+        for (int c = 0; c < d; ++c) db2[c] += j->db2[c];
+        for (long i = 0; i < j->n; ++i)
+            for (int c = 0; c < d; ++c) dxn[j->rows[i] * d + c] += j->dxn[i * d + c];
+        free(j->rows); free(j->dw1); free(j->dw2); free(j->db1); free(j->db2); free(j->dxn);
+    }
+    free(jobs);
+}
+
+/* ------------------------------------------------------- cross-entropy */
+/* cpu_cross_entropy, rust/src/model.rs:804-844, as one chunk (the reference's
+ * per-thread loss partials only regroup the sum): per row lse = max +
+ * ln(sum exp(x - max)); loss += lse - x[target]; dlogits = exp(x - lse) / T,
+ * then minus 1/T at the target.  Returns the mean loss. */
+ORC_API float orc_cross_entropy(const float* logits, const uint32_t* targets, long T, int V, float* dlogits) {
+    const float inv = 1.0f / (float)T;
+    float l = 0.0f;
+    for (long t = 0; t < T; ++t) {
+        const float* row = logits + t * V;
+        float mx = -INFINITY;
+        for (int c = 0; c < V; ++c) mx = fmaxf(mx, row[c]);
+        float sum = 0.0f;
+        for (int c = 0; c < V; ++c) sum += expf(row[c] - mx);
+        const float lse = mx + logf(sum);
+        l += lse - row[targets[t]];
+        float* dr = dlogits + t * V;
+        for (int c = 0; c < V; ++c) dr[c] = expf(row[c] - lse) * inv;
+        dr[targets[t]] -= inv;
+    }
+    return l * inv;
+}

@@ -49,6 +49,9 @@ def lib() -> C.CDLL:
             "orc_rmsnorm_bwd": (None, [vp, vp, vp, l, i, fl]),
             "orc_hash_route": (None, [vp, l, i, vp]),
             "orc_adamw": (None, [vp, vp, vp, vp, l, fl, fl, fl, fl, fl, vp]),
+            "orc_moe_fwd": (None, [vp] * 6 + [l, i, i, i] + [vp] * 3),
+            "orc_moe_bwd": (None, [vp] * 7 + [l, i, i, i] + [vp] * 5),
+            "orc_cross_entropy": (fl, [vp, vp, l, i, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -178,6 +181,50 @@ def adamw(p, g, m, v, lr, step, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01):
     st = np.array([step], dtype=np.uint32)
     lib().orc_adamw(_p(p), _p(g), _p(m), _p(v), p.size, lr, beta1, beta2, eps, wd, _p(st))
     return int(st[0])
+
+
+def buckets(route: np.ndarray, n_experts: int):
+    """perm (tokens sorted by expert, ascending inside an expert) and CSR
+    offsets, the buckets of HashMoe::forward (rust/src/model.rs:190-193)."""
+    route = np.asarray(route, dtype=np.int64)
+    perm = np.concatenate([np.nonzero(route == e)[0] for e in range(n_experts)]).astype(np.int32)
+    counts = np.bincount(route, minlength=n_experts)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return perm, offsets
+
+
+def moe_fwd(xn, w1, b1, w2, b2, route, d_ff):
+    """HashMoe::forward CPU path on normalised input; (out, pre, hidden) in
+    token order."""
+    T, d = xn.shape
+    E = w1.shape[1] // d_ff
+    route = np.ascontiguousarray(route, dtype=np.int32)
+    out, pre, hidden = _z(T, d), _z(T, d_ff), _z(T, d_ff)
+    lib().orc_moe_fwd(_p(xn), _p(w1), _p(b1), _p(w2), _p(b2), _p(route), T, d, d_ff, E,
+                      _p(out), _p(pre), _p(hidden))
+    return out, pre, hidden
+
+
+def moe_bwd(xn, w1, w2, pre, hidden, route, dout, d_ff):
+    """HashMoe::backward CPU path before its RMSNorm backward;
+    (dxn, dw1, db1, dw2, db2) with pre/hidden in token order."""
+    T, d = xn.shape
+    E = w1.shape[1] // d_ff
+    route = np.ascontiguousarray(route, dtype=np.int32)
+    dxn, dw1, db1 = _z(T, d), _z(d, E * d_ff), _z(E * d_ff)
+    dw2, db2 = _z(E * d_ff, d), _z(d)
+    lib().orc_moe_bwd(_p(xn), _p(w1), _p(w2), _p(pre), _p(hidden), _p(route), _p(dout), T, d, d_ff, E,
+                      _p(dxn), _p(dw1), _p(db1), _p(dw2), _p(db2))
+    return dxn, dw1, db1, dw2, db2
+
+
+def cross_entropy(logits, targets):
+    """cpu_cross_entropy: (mean loss, dlogits)."""
+    T, V = logits.shape
+    t = np.ascontiguousarray(targets, dtype=np.uint32)
+    dl = _z(T, V)
+    loss = lib().orc_cross_entropy(_p(logits), _p(t), T, V, _p(dl))
+    return float(loss), dl
 
 
 def rel_err(a: np.ndarray, ref: np.ndarray) -> float:

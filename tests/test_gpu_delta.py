@@ -37,7 +37,7 @@ def test_wave_primitives_lane_semantics(g):
     import ctypes as C
     from asca_amd import _lib
 
-    out = np.zeros((10, 64), dtype=np.float32)
+    out = np.zeros((14, 64), dtype=np.float32)  # rows 10-13: MFMA probe (test_gpu_ops)
     _lib.call("asca_selftest_wave", out.ctypes.data_as(C.c_void_p))
     lane = np.arange(64)
     np.testing.assert_array_equal(out[0], lane ^ 1)
