@@ -69,9 +69,20 @@ SIGNATURES: dict[str, tuple] = {
     "asca_adamw": (_i, [_p, _p, _p, _p, _l, _f, _f, _f, _f, _f, _p]),
     "asca_hash_route_ws_bytes": (_i, [_i, _i, C.POINTER(_sz)]),
     "asca_hash_route": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
+    "asca_bucket_keys": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
     "asca_gemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p]),
     "asca_moe_fwd": (_i, [_p] * 7 + [_i] * 4 + [_p] * 4),
     "asca_moe_bwd": (_i, [_p] * 8 + [_i] * 4 + [_p] * 6 + [_i, _p]),
+    "asca_model_create": (_i, [_i] * 6 + [C.POINTER(_p)]),
+    "asca_model_destroy": (_i, [_p]),
+    "asca_model_num_tensors": (_i, [_p, C.POINTER(_i)]),
+    "asca_model_tensor_info": (_i, [_p, _i, C.c_char_p, _i, C.POINTER(_sz), C.POINTER(_i), C.POINTER(_i)]),
+    "asca_model_buffers": (_i, [_p, C.POINTER(_sz), C.POINTER(_p), C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)]),
+    "asca_model_set_adamw": (_i, [_p, _f, _f, _f, _f, _f, C.c_uint32]),
+    "asca_model_adamw_step_count": (_i, [_p, C.POINTER(C.c_uint32)]),
+    "asca_model_forward_backward": (_i, [_p, _p, _p, _i, _i, _p, _p]),
+    "asca_model_adamw": (_i, [_p, _p]),
+    "asca_model_train_step": (_i, [_p, _p, _p, _i, _i, _p, _p]),
 }
 
 ERRORS = {

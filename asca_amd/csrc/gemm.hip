@@ -364,8 +364,8 @@ static int scratch_get(size_t bytes, float** out) {
         size_t nb = g_scratch.bytes[dev] ? g_scratch.bytes[dev] : (size_t)1 << 20;
         while (nb < bytes) nb *= 2;
         if (g_scratch.ptr[dev]) {
-            hipDeviceSynchronize();
-            hipFree(g_scratch.ptr[dev]);
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g_scratch.ptr[dev]);
             g_scratch.ptr[dev] = nullptr;
             g_scratch.bytes[dev] = 0;
         }

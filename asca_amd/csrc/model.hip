@@ -1,0 +1,582 @@
+// Device-resident training step of the ASCA model: Model::forward,
+// Model::backward and the AdamW step over every parameter
+// (rust/src/model.rs:528-802, rust/src/train.rs:176-186), with DeltaBlock
+// forward/backward (rust/src/delta.rs:121-207,615-674) and HashMoe
+// (model.rs:187-306,339-497) as in the reference, but with weights, gradients,
+// AdamW moments and activations resident in HBM for the whole step and every
+// dense product on the MFMA GEMM.
+//
+// Structure per layer (model.rs:665-678): x_mid = x + Delta(x) (the delta block
+// takes the raw residual stream), x_out = x_mid + MoE(RMSNorm(x_mid)); then
+// h = RMSNorm(x_L), logits = h W_head, softmax cross-entropy against targets.
+// The backward mirrors model.rs:729-794, and AdamW::update runs per parameter
+// tensor with its per-tensor step counter (tensor.rs:392-453), bit-exact.
+//
+// Parameters live in one flat f32 buffer (and gradients, m, v in three more),
+// tensors in the reference's params() order: embed, head, then per layer
+// w_qkv, b_qkv, w_gate, b_gate, w_o, b_o, w1, b1, w2, b2 (model.rs:596-603,
+// delta.rs:96-105, model.rs:103-105).
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gemm.h"
+#include "ops.h"
+#include "runtime.h"
+
+namespace asca {
+
+constexpr float MODEL_EPS = 1e-6f;  // model.rs:14
+
+// q, k, v split out of the projection rows, q and k L2-normalised per head
+// (x / max(|x|, 1e-8)) with the norms kept, and alpha, beta = sigmoid of the
+// gate logits (delta.rs:131-186, tensor.rs:245-248).  One block per row.
+__global__ __launch_bounds__(256) void qkv_prep_k(const float* __restrict__ qkv, const float* __restrict__ gate,
+                                                  int H, int dh, float* __restrict__ q, float* __restrict__ k,
+                                                  float* __restrict__ v, float* __restrict__ qn,
+                                                  float* __restrict__ kn, float* __restrict__ alpha,
+                                                  float* __restrict__ beta) {
+    const long r = blockIdx.x;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int d = H * dh;
+    const float* src = qkv + r * 3 * d;
+    for (int h = w; h < H; h += 4) {
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            const float* s = src + which * d + h * dh;
+            float ss = 0.0f;
+            for (int j = lane; j < dh; j += 64) ss += s[j] * s[j];
+            ss = wave_sum(ss);
+            const float n = fmaxf(sqrtf(ss), 1e-8f);
+            float* dst = (which ? k : q) + r * d + h * dh;
+            for (int j = lane; j < dh; j += 64) dst[j] = s[j] / n;
+            if (lane == 0) (which ? kn : qn)[r * H + h] = n;
+        }
+        const float* s = src + 2 * d + h * dh;
+        for (int j = lane; j < dh; j += 64) v[r * d + h * dh + j] = s[j];
+        if (lane == 0) {
+            alpha[r * H + h] = 1.0f / (1.0f + expf(-gate[r * 2 * H + h]));
+            beta[r * H + h] = 1.0f / (1.0f + expf(-gate[r * 2 * H + H + h]));
+        }
+    }
+}
+
+// x0[t] = embed[id_t] (model.rs:655-661).  Ids >= V wrap (memory safety).
+__global__ __launch_bounds__(256) void embed_k(const float* __restrict__ embed, const uint32_t* __restrict__ ids,
+                                               long T, int d, int V, float* __restrict__ x) {
+    const long t = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float* src = embed + (long)(ids[t] % (uint32_t)V) * d;
+    for (int c = lane; c < d; c += 64) x[t * d + c] = src[c];
+}
+
+// Embedding gradient: row v = sum of dx[t] over the tokens with id v, in
+// ascending t, starting from zero (model.rs:782-789 after zero_grads).
+__global__ __launch_bounds__(256) void embed_grad_k(const float* __restrict__ dx, const int32_t* __restrict__ perm,
+                                                    const int32_t* __restrict__ off, int d,
+                                                    float* __restrict__ g) {
+    const int vrow = blockIdx.x;
+    const int lo = off[vrow], hi = off[vrow + 1];
+    for (int c = threadIdx.x; c < d; c += 256) {
+        float acc = 0.0f;
+        for (int i = lo; i < hi; ++i) acc += dx[(long)perm[i] * d + c];
+        g[(long)vrow * d + c] = acc;
+    }
+}
+
+// Mean loss = (sum of per-row losses) / T, one block, fixed order.
+__global__ __launch_bounds__(256) void loss_mean_k(const float* __restrict__ losses, long T, float inv_t,
+                                                   float* __restrict__ out) {
+    __shared__ float part[4];
+    float s = 0.0f;
+    for (long i = threadIdx.x; i < T; i += 256) s += losses[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = (part[0] + part[1] + part[2] + part[3]) * inv_t;
+}
+
+// AdamW over all tensors in one launch: block b updates chunk b of tensor j
+// with the scalars of step base + j + 1 (the reference increments its step
+// counter once per parameter tensor, tensor.rs:393).  Scalars are computed
+// per block with the host's f32 operation sequence (binary-exponentiation
+// powi, correctly rounded sqrt and division, no contraction), so every
+// element update is bit-identical to AdamW::update's CPU body.
+struct AdamChunk {
+    int tensor;
+    int pad;
+    long start;
+    long len;
+};
+
+ASCA_DEV float powi_dev(float a, int b) {
+#pragma clang fp contract(off)
+    float r = 1.0f;
+    for (;;) {
+        if (b & 1) r *= a;
+        b /= 2;
+        if (b == 0) break;
+        a *= a;
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void adamw_multi_k(float* __restrict__ p, const float* __restrict__ g,
+                                                     float* __restrict__ m, float* __restrict__ v,
+                                                     const AdamChunk* __restrict__ chunks, uint32_t base, float lr0,
+                                                     float b1, float b2, float eps, float wd0) {
+#pragma clang fp contract(off)
+    const AdamChunk c = chunks[blockIdx.x];
+    const int step = (int)(base + (uint32_t)c.tensor + 1u);
+    const float bc1 = 1.0f - powi_dev(b1, step);
+    const float bc2 = 1.0f - powi_dev(b2, step);
+    const float lr = lr0 * sqrtf(bc1 / bc2);
+    const float eps_t = eps * sqrtf(bc2);
+    const float wd = lr0 * wd0;
+    const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+    for (long i = c.start + threadIdx.x; i < c.start + c.len; i += 256) {
+        const float gi = g[i];
+        const float mi = b1 * m[i] + omb1 * gi;
+        const float vi = b2 * v[i] + omb2 * gi * gi;
+        m[i] = mi;
+        v[i] = vi;
+        const float upd = mi / (sqrtf(vi) + eps_t);
+        float pi = p[i];
+        pi -= wd * pi;
+        pi -= lr * upd;
+        p[i] = pi;
+    }
+}
+
+struct MTensor {
+    std::string name;
+    size_t off, n;
+    int rows, cols;
+};
+
+struct MLayer {
+    size_t w_qkv, b_qkv, w_gate, b_gate, w_o, b_o, w1, b1, w2, b2;
+};
+
+struct MActs {  // per-layer activations kept for the backward
+    float *x_out, *q, *k, *v, *qn, *kn, *al, *be, *o, *x_mid, *xn, *pre, *hid;
+    void* dws;
+};
+
+}  // namespace asca
+
+using namespace asca;
+
+struct asca_model {
+    int V = 0, d = 0, H = 0, dh = 0, L = 0, E = 0, dff = 0;
+    size_t n_params = 0;
+    float *p = nullptr, *g = nullptr, *m = nullptr, *v = nullptr;
+    std::vector<MTensor> t;
+    std::vector<MLayer> lay;
+    AdamChunk* chunks = nullptr;
+    int n_chunks = 0;
+    float lr = 3e-4f, b1 = 0.9f, b2 = 0.95f, eps = 1e-8f, wd = 0.01f;
+    uint32_t adam_step = 0;
+    // activation workspace, sized for one (batch, seq)
+    int batch = 0, seq = 0;
+    std::vector<void*> allocs;
+    std::vector<MActs> acts;
+    float *x0 = nullptr, *qkv_t = nullptr, *gate_t = nullptr, *h_final = nullptr, *logits = nullptr;
+    float *dlogits = nullptr, *losses = nullptr, *loss = nullptr, *dx = nullptr, *dmid = nullptr;
+    float *dxn = nullptr, *dtmp = nullptr, *dqkv = nullptr, *dgate = nullptr, *dpre = nullptr;
+    int32_t *route_e = nullptr, *perm = nullptr, *off = nullptr, *emb_b = nullptr, *emb_perm = nullptr,
+            *emb_off = nullptr;
+    void *route_ws = nullptr, *emb_ws = nullptr;
+    bool fwd_done = false;
+};
+
+static void free_acts(asca_model* M) {
+    if (!M->allocs.empty()) (void)hipDeviceSynchronize();
+    for (void* a : M->allocs) (void)hipFree(a);
+    M->allocs.clear();
+    M->acts.clear();
+    M->batch = M->seq = 0;
+    M->fwd_done = false;
+}
+
+template <typename T>
+static int dalloc(asca_model* M, T** out, size_t count) {
+    void* p = nullptr;
+    const size_t bytes = (count ? count : 1) * sizeof(T);
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(ASCA_ERR_OOM, "model: hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    M->allocs.push_back(p);
+    *out = reinterpret_cast<T*>(p);
+    return ASCA_OK;
+}
+
+static int ensure_acts(asca_model* M, int batch, int seq) {
+    if (M->batch == batch && M->seq == seq) return ASCA_OK;
+    free_acts(M);
+    const size_t T = (size_t)batch * seq, d = M->d, H = M->H, dff = M->dff, V = M->V;
+    size_t dws = 0;
+    int rc = asca_delta_ws_bytes(batch, seq, M->H, M->dh, &dws);
+    if (rc) return rc;
+    size_t rws = 0, ews = 0;
+    if ((rc = asca_hash_route_ws_bytes((int)T, M->E, &rws)) || (rc = asca_hash_route_ws_bytes((int)T, M->V, &ews)))
+        return rc;
+    M->acts.resize(M->L);
+    for (int l = 0; l < M->L; ++l) {
+        MActs& a = M->acts[l];
+        char* dw = nullptr;
+        if ((rc = dalloc(M, &a.x_out, T * d)) || (rc = dalloc(M, &a.q, T * d)) || (rc = dalloc(M, &a.k, T * d)) ||
+            (rc = dalloc(M, &a.v, T * d)) || (rc = dalloc(M, &a.qn, T * H)) || (rc = dalloc(M, &a.kn, T * H)) ||
+            (rc = dalloc(M, &a.al, T * H)) || (rc = dalloc(M, &a.be, T * H)) || (rc = dalloc(M, &a.o, T * d)) ||
+            (rc = dalloc(M, &a.x_mid, T * d)) || (rc = dalloc(M, &a.xn, T * d)) ||
+            (rc = dalloc(M, &a.pre, T * dff)) || (rc = dalloc(M, &a.hid, T * dff)) || (rc = dalloc(M, &dw, dws)))
+            goto oom;
+        a.dws = dw;
+    }
+    {
+        char *rw = nullptr, *ew = nullptr;
+        if ((rc = dalloc(M, &M->x0, T * d)) || (rc = dalloc(M, &M->qkv_t, T * 3 * d)) ||
+            (rc = dalloc(M, &M->gate_t, T * 2 * H)) || (rc = dalloc(M, &M->h_final, T * d)) ||
+            (rc = dalloc(M, &M->logits, T * V)) || (rc = dalloc(M, &M->dlogits, T * V)) ||
+            (rc = dalloc(M, &M->losses, T)) || (rc = dalloc(M, &M->loss, 1)) || (rc = dalloc(M, &M->dx, T * d)) ||
+            (rc = dalloc(M, &M->dmid, T * d)) || (rc = dalloc(M, &M->dxn, T * d)) ||
+            (rc = dalloc(M, &M->dtmp, T * d)) || (rc = dalloc(M, &M->dqkv, T * 3 * d)) ||
+            (rc = dalloc(M, &M->dgate, T * 2 * H)) || (rc = dalloc(M, &M->dpre, T * dff)) ||
+            (rc = dalloc(M, &M->route_e, T)) || (rc = dalloc(M, &M->perm, T)) ||
+            (rc = dalloc(M, &M->off, (size_t)M->E + 1)) || (rc = dalloc(M, &M->emb_b, T)) ||
+            (rc = dalloc(M, &M->emb_perm, T)) || (rc = dalloc(M, &M->emb_off, V + 1)) ||
+            (rc = dalloc(M, &rw, rws)) || (rc = dalloc(M, &ew, ews)))
+            goto oom;
+        M->route_ws = rw;
+        M->emb_ws = ew;
+    }
+    M->batch = batch;
+    M->seq = seq;
+    return ASCA_OK;
+oom:
+    free_acts(M);
+    return rc;
+}
+
+static GemmArgs gemm_plain(const float* A, long lda, const float* B, long ldb, float* C, long ldc, int M, int N, int K) {
+    GemmArgs a = gemm_args();
+    a.A = A;
+    a.lda = lda;
+    a.B = B;
+    a.ldb = ldb;
+    a.C = C;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    return a;
+}
+
+static int d2d(void* dst, const void* src, size_t bytes, hipStream_t st) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st);
+    return e == hipSuccess ? ASCA_OK : fail(ASCA_ERR_HIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+}
+
+// Forward of the whole model, keeping what the backward needs.
+static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* targets, hipStream_t st) {
+    const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V;
+    int rc;
+    // routing of this batch (the same ids for every layer) and the id buckets
+    if ((rc = bucket_launch(true, ids, T, E, M->route_e, M->perm, M->off, M->route_ws, st))) return rc;
+    if ((rc = bucket_launch(false, ids, T, V, M->emb_b, M->emb_perm, M->emb_off, M->emb_ws, st))) return rc;
+    if ((rc = pre_launch("embed"))) return rc;
+    hipLaunchKernelGGL(embed_k, dim3((T + 3) / 4), dim3(256), 0, st, M->p + M->t[0].off, ids, (long)T, d, V, M->x0);
+    if ((rc = post_launch("embed"))) return rc;
+    const float* x = M->x0;
+    for (int l = 0; l < M->L; ++l) {
+        const MLayer& P = M->lay[l];
+        MActs& a = M->acts[l];
+        // qkv = x W_qkv + b_qkv ; gate = x W_gate + b_gate
+        GemmArgs q = gemm_plain(x, d, M->p + P.w_qkv, 3 * d, M->qkv_t, 3 * d, T, 3 * d, d);
+        q.bias = M->p + P.b_qkv;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, q, T, st, "qkv_proj"))) return rc;
+        GemmArgs gg = gemm_plain(x, d, M->p + P.w_gate, 2 * H, M->gate_t, 2 * H, T, 2 * H, d);
+        gg.bias = M->p + P.b_gate;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, gg, T, st, "gate_proj"))) return rc;
+        if ((rc = pre_launch("qkv_prep"))) return rc;
+        hipLaunchKernelGGL(qkv_prep_k, dim3(T), dim3(256), 0, st, M->qkv_t, M->gate_t, H, dh, a.q, a.k, a.v, a.qn,
+                           a.kn, a.al, a.be);
+        if ((rc = post_launch("qkv_prep"))) return rc;
+        if ((rc = asca_delta_fwd(a.q, a.k, a.v, a.al, a.be, a.o, a.dws, M->batch, M->seq, H, dh, st))) return rc;
+        // x_mid = x + (o W_o + b_o)
+        if ((rc = d2d(a.x_mid, x, (size_t)T * d * 4, st))) return rc;
+        GemmArgs yo = gemm_plain(a.o, d, M->p + P.w_o, d, a.x_mid, d, T, d, d);
+        yo.bias = M->p + P.b_o;
+        yo.beta = 1.0f;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, yo, T, st, "out_proj"))) return rc;
+        // MoE on RMSNorm(x_mid); x_out = x_mid + moe
+        if ((rc = asca_rmsnorm(a.x_mid, a.xn, nullptr, T, d, MODEL_EPS, st))) return rc;
+        GemmArgs w1 = gemm_args();
+        w1.A = a.xn;
+        w1.lda = d;
+        w1.a_rows = M->perm;
+        w1.B = M->p + P.w1;
+        w1.ldb = (long)E * dff;
+        w1.b_gs = dff;
+        w1.C = a.pre;
+        w1.ldc = dff;
+        w1.bias = M->p + P.b1;
+        w1.bias_gs = dff;
+        w1.aux_out = a.hid;
+        w1.ld_aux = dff;
+        w1.M = T;
+        w1.N = dff;
+        w1.K = d;
+        w1.goff = M->off;
+        w1.ngroups = E;
+        w1.gmode = 1;
+        if ((rc = gemm_launch(0, 0, EPI_SILU, w1, T, st, "moe_fwd_w1"))) return rc;
+        if ((rc = d2d(a.x_out, a.x_mid, (size_t)T * d * 4, st))) return rc;
+        GemmArgs w2 = gemm_args();
+        w2.A = a.hid;
+        w2.lda = dff;
+        w2.B = M->p + P.w2;
+        w2.ldb = d;
+        w2.b_gs = (long)dff * d;
+        w2.C = a.x_out;
+        w2.ldc = d;
+        w2.c_rows = M->perm;
+        w2.bias = M->p + P.b2;
+        w2.beta = 1.0f;
+        w2.M = T;
+        w2.N = d;
+        w2.K = dff;
+        w2.goff = M->off;
+        w2.ngroups = E;
+        w2.gmode = 1;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, w2, T, st, "moe_fwd_w2"))) return rc;
+        x = a.x_out;
+    }
+    // head and loss
+    if ((rc = asca_rmsnorm(x, M->h_final, nullptr, T, d, MODEL_EPS, st))) return rc;
+    GemmArgs hd = gemm_plain(M->h_final, d, M->p + M->t[1].off, V, M->logits, V, T, V, d);
+    if ((rc = gemm_launch(0, 0, EPI_STORE, hd, T, st, "head"))) return rc;
+    if ((rc = asca_cross_entropy(M->logits, targets, T, V, M->dlogits, M->losses, st))) return rc;
+    if ((rc = pre_launch("loss_mean"))) return rc;
+    hipLaunchKernelGGL(loss_mean_k, dim3(1), dim3(256), 0, st, M->losses, (long)T, 1.0f / (float)T, M->loss);
+    if ((rc = post_launch("loss_mean"))) return rc;
+    M->fwd_done = true;
+    return ASCA_OK;
+}
+
+static int gemm_wgrad(const float* X, int ldx, const float* D, int ldd, float* G, int M_, int N_, int T,
+                      hipStream_t st) {
+    // G (M_ x N_) = X^T D over T rows; split K when the output is small
+    return asca_gemm(1, 0, M_, N_, T, 1.0f, X, ldx, D, ldd, 0.0f, G, N_, nullptr, st);
+}
+
+// Backward of the whole model into the gradient buffer (overwritten).
+static int model_backward(asca_model* M, hipStream_t st) {
+    const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V;
+    int rc;
+    float* G = M->g;
+    const float* x_last = M->acts[M->L - 1].x_out;
+    // head: d_head = h^T dlogits ; dh = dlogits W_head^T ; dx = rmsnorm_bwd(x_L, dh)
+    if ((rc = gemm_wgrad(M->h_final, d, M->dlogits, V, G + M->t[1].off, d, V, T, st))) return rc;
+    GemmArgs dhh = gemm_plain(M->dlogits, V, M->p + M->t[1].off, V, M->dtmp, d, T, d, V);
+    if ((rc = gemm_launch(0, 1, EPI_STORE, dhh, T, st, "head_dx"))) return rc;
+    if ((rc = rmsnorm_bwd_launch(x_last, M->dtmp, nullptr, M->dx, T, d, MODEL_EPS, st))) return rc;
+    for (int l = M->L - 1; l >= 0; --l) {
+        const MLayer& P = M->lay[l];
+        MActs& a = M->acts[l];
+        const float* x_in = l ? M->acts[l - 1].x_out : M->x0;
+        // MoE backward from dout = dx; d_mid = dx + rmsnorm_bwd(x_mid, dxn)
+        if ((rc = asca_moe_bwd(a.xn, M->p + P.w1, M->p + P.w2, a.pre, a.hid, M->perm, M->off, M->dx, T, d, dff, E,
+                               M->dxn, G + P.w1, G + P.b1, G + P.w2, G + P.b2, M->dpre, 0, st)))
+            return rc;
+        if ((rc = rmsnorm_bwd_launch(a.x_mid, M->dxn, M->dx, M->dmid, T, d, MODEL_EPS, st))) return rc;
+        // delta block backward (delta.rs:615-674) from dy = d_mid
+        GemmArgs dov = gemm_plain(M->dmid, d, M->p + P.w_o, d, M->dtmp, d, T, d, d);
+        if ((rc = gemm_launch(0, 1, EPI_STORE, dov, T, st, "out_proj_dx"))) return rc;
+        if ((rc = gemm_wgrad(a.o, d, M->dmid, d, G + P.w_o, d, d, T, st))) return rc;
+        if ((rc = asca_colsum(M->dmid, T, d, G + P.b_o, 0, st))) return rc;
+        if ((rc = asca_delta_bwd_fused(a.q, a.k, a.v, a.al, a.be, a.qn, a.kn, M->dtmp, a.dws, M->dqkv, M->dgate,
+                                       M->batch, M->seq, H, dh, st)))
+            return rc;
+        if ((rc = gemm_wgrad(x_in, d, M->dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, st))) return rc;
+        if ((rc = asca_colsum(M->dqkv, T, 3 * d, G + P.b_qkv, 0, st))) return rc;
+        if ((rc = gemm_wgrad(x_in, d, M->dgate, 2 * H, G + P.w_gate, d, 2 * H, T, st))) return rc;
+        if ((rc = asca_colsum(M->dgate, T, 2 * H, G + P.b_gate, 0, st))) return rc;
+        // dx = d_mid + d_qkv W_qkv^T + d_gate W_gate^T
+        if ((rc = d2d(M->dx, M->dmid, (size_t)T * d * 4, st))) return rc;
+        GemmArgs dq = gemm_plain(M->dqkv, 3 * d, M->p + P.w_qkv, 3 * d, M->dx, d, T, d, 3 * d);
+        dq.beta = 1.0f;
+        if ((rc = gemm_launch(0, 1, EPI_STORE, dq, T, st, "qkv_proj_dx"))) return rc;
+        GemmArgs dg = gemm_plain(M->dgate, 2 * H, M->p + P.w_gate, 2 * H, M->dx, d, T, d, 2 * H);
+        dg.beta = 1.0f;
+        if ((rc = gemm_launch(0, 1, EPI_STORE, dg, T, st, "gate_proj_dx"))) return rc;
+    }
+    // embedding gradient
+    if ((rc = pre_launch("embed_grad"))) return rc;
+    hipLaunchKernelGGL(embed_grad_k, dim3(V), dim3(256), 0, st, M->dx, M->emb_perm, M->emb_off, d, G + M->t[0].off);
+    return post_launch("embed_grad");
+}
+
+static int model_adamw(asca_model* M, hipStream_t st) {
+    int rc = pre_launch("adamw_multi");
+    if (rc) return rc;
+    hipLaunchKernelGGL(adamw_multi_k, dim3(M->n_chunks), dim3(256), 0, st, M->p, M->g, M->m, M->v, M->chunks,
+                       M->adam_step, M->lr, M->b1, M->b2, M->eps, M->wd);
+    rc = post_launch("adamw_multi");
+    if (rc) return rc;
+    M->adam_step += (uint32_t)M->t.size();
+    return ASCA_OK;
+}
+
+static void destroy_model(asca_model* M) {
+    free_acts(M);
+    (void)hipDeviceSynchronize();
+    for (void* q : {(void*)M->p, (void*)M->g, (void*)M->m, (void*)M->v, (void*)M->chunks})
+        if (q) (void)hipFree(q);
+    delete M;
+}
+
+extern "C" {
+
+int asca_model_create(int vocab, int d_model, int n_heads, int n_layers, int n_experts, int d_ff, asca_model** out) {
+    if (!out) return fail(ASCA_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    if (vocab < 1 || vocab > 256 || d_model < 1 || n_heads < 1 || d_model % n_heads || n_layers < 1 ||
+        n_experts < 1 || n_experts > 256 || d_ff < 1)
+        return fail(ASCA_ERR_INVALID, "model: bad config V=%d d=%d H=%d L=%d E=%d d_ff=%d", vocab, d_model, n_heads,
+                    n_layers, n_experts, d_ff);
+    if (d_model / n_heads > 128) return fail(ASCA_ERR_UNSUPPORTED, "model: head dim %d > 128", d_model / n_heads);
+    int rc = ensure_device();
+    if (rc) return rc;
+    asca_model* M = new asca_model();
+    M->V = vocab;
+    M->d = d_model;
+    M->H = n_heads;
+    M->dh = d_model / n_heads;
+    M->L = n_layers;
+    M->E = n_experts;
+    M->dff = d_ff;
+    auto add = [&](const char* name, int rows, int cols) {
+        const size_t n = (size_t)rows * cols;
+        M->t.push_back({name, M->n_params, n, rows, cols});
+        M->n_params += (n + 3) / 4 * 4;  // 16-byte aligned tensor starts
+        return M->t.back().off;
+    };
+    const int d = d_model, H = n_heads;
+    add("embed", vocab, d);
+    add("head", d, vocab);
+    for (int l = 0; l < n_layers; ++l) {
+        MLayer P;
+        P.w_qkv = add("delta.w_qkv", d, 3 * d);
+        P.b_qkv = add("delta.b_qkv", 1, 3 * d);
+        P.w_gate = add("delta.w_gate", d, 2 * H);
+        P.b_gate = add("delta.b_gate", 1, 2 * H);
+        P.w_o = add("delta.w_o", d, d);
+        P.b_o = add("delta.b_o", 1, d);
+        P.w1 = add("moe.w1", d, n_experts * d_ff);
+        P.b1 = add("moe.b1", 1, n_experts * d_ff);
+        P.w2 = add("moe.w2", n_experts * d_ff, d);
+        P.b2 = add("moe.b2", 1, d);
+        M->lay.push_back(P);
+    }
+    // AdamW chunk table
+    std::vector<AdamChunk> ch;
+    const long CH = 16384;
+    for (size_t j = 0; j < M->t.size(); ++j)
+        for (long s = 0; s < (long)M->t[j].n; s += CH)
+            ch.push_back({(int)j, 0, (long)M->t[j].off + s, std::min(CH, (long)M->t[j].n - s)});
+    M->n_chunks = (int)ch.size();
+    const size_t bytes = M->n_params * sizeof(float);
+    hipError_t e = hipSuccess;
+    for (float** q : {&M->p, &M->g, &M->m, &M->v}) {
+        if ((e = hipMalloc(q, bytes)) != hipSuccess) break;
+        if ((e = hipMemset(*q, 0, bytes)) != hipSuccess) break;
+    }
+    if (e == hipSuccess) e = hipMalloc(&M->chunks, ch.size() * sizeof(AdamChunk));
+    if (e == hipSuccess) e = hipMemcpy(M->chunks, ch.data(), ch.size() * sizeof(AdamChunk), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        destroy_model(M);
+        return fail(ASCA_ERR_OOM, "model: allocation of %zu parameters failed: %s", M->n_params, hipGetErrorString(e));
+    }
+    *out = M;
+    return ASCA_OK;
+}
+
+int asca_model_destroy(asca_model* M) {
+    if (M) destroy_model(M);
+    return ASCA_OK;
+}
+
+int asca_model_num_tensors(const asca_model* M, int* n) {
+    if (!M || !n) return fail(ASCA_ERR_INVALID, "null pointer");
+    *n = (int)M->t.size();
+    return ASCA_OK;
+}
+
+int asca_model_tensor_info(const asca_model* M, int i, char* name, int name_len, size_t* offset, int* rows,
+                           int* cols) {
+    if (!M || i < 0 || i >= (int)M->t.size()) return fail(ASCA_ERR_INVALID, "tensor index %d out of range", i);
+    const MTensor& t = M->t[i];
+    if (name && name_len > 0) {
+        snprintf(name, name_len, "%s", t.name.c_str());
+    }
+    if (offset) *offset = t.off;
+    if (rows) *rows = t.rows;
+    if (cols) *cols = t.cols;
+    return ASCA_OK;
+}
+
+int asca_model_buffers(asca_model* M, size_t* n_floats, float** params, float** grads, float** m, float** v) {
+    if (!M) return fail(ASCA_ERR_INVALID, "null model");
+    if (n_floats) *n_floats = M->n_params;
+    if (params) *params = M->p;
+    if (grads) *grads = M->g;
+    if (m) *m = M->m;
+    if (v) *v = M->v;
+    return ASCA_OK;
+}
+
+int asca_model_set_adamw(asca_model* M, float lr, float beta1, float beta2, float eps, float wd, uint32_t step) {
+    if (!M) return fail(ASCA_ERR_INVALID, "null model");
+    M->lr = lr;
+    M->b1 = beta1;
+    M->b2 = beta2;
+    M->eps = eps;
+    M->wd = wd;
+    M->adam_step = step;
+    return ASCA_OK;
+}
+
+int asca_model_adamw_step_count(const asca_model* M, uint32_t* step) {
+    if (!M || !step) return fail(ASCA_ERR_INVALID, "null pointer");
+    *step = M->adam_step;
+    return ASCA_OK;
+}
+
+int asca_model_forward_backward(asca_model* M, const uint32_t* ids, const uint32_t* targets, int batch, int seq,
+                                float* loss, void* stream) {
+    if (!M || !ids || !targets) return fail(ASCA_ERR_INVALID, "null pointer");
+    if (batch < 1 || seq < 1 || (long)batch * seq > 0x7fffffffL) return fail(ASCA_ERR_INVALID, "bad batch/seq");
+    int rc = ensure_acts(M, batch, seq);
+    if (rc) return rc;
+    const hipStream_t st = as_stream(stream);
+    if ((rc = model_forward(M, ids, targets, st))) return rc;
+    if ((rc = model_backward(M, st))) return rc;
+    if (loss) return d2d(loss, M->loss, sizeof(float), st);
+    return ASCA_OK;
+}
+
+int asca_model_adamw(asca_model* M, void* stream) {
+    if (!M) return fail(ASCA_ERR_INVALID, "null model");
+    return model_adamw(M, as_stream(stream));
+}
+
+int asca_model_train_step(asca_model* M, const uint32_t* ids, const uint32_t* targets, int batch, int seq,
+                          float* loss, void* stream) {
+    int rc = asca_model_forward_backward(M, ids, targets, batch, seq, loss, stream);
+    if (rc) return rc;
+    return model_adamw(M, as_stream(stream));
+}
+
+}  // extern "C"

@@ -5,6 +5,7 @@
 // All reductions are wave-level butterflies (no atomics), so results are
 // deterministic; one wave per row.
 #include "common.h"
+#include "ops.h"
 #include "runtime.h"
 
 namespace asca {
@@ -29,9 +30,11 @@ __global__ __launch_bounds__(ROW_NT) void rmsnorm_k(const float* __restrict__ x,
 }
 
 // rmsnorm_rows_backward (rust/src/tensor.rs:282-296):
-// dx = inv * (dy - x * inv * mean(dy * x) * inv), mean over the row.
+// dx = inv * (dy - x * inv * mean(dy * x) * inv), mean over the row; with
+// `res`, the residual gradient it joins is added (model.rs:769-777).
 __global__ __launch_bounds__(ROW_NT) void rmsnorm_bwd_k(const float* __restrict__ x, const float* __restrict__ dy,
-                                                       float* __restrict__ dx, long rows, int cols, float eps) {
+                                                       const float* __restrict__ res, float* __restrict__ dx,
+                                                       long rows, int cols, float eps) {
     const long r = (long)blockIdx.x * (ROW_NT / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;
@@ -46,7 +49,12 @@ __global__ __launch_bounds__(ROW_NT) void rmsnorm_bwd_k(const float* __restrict_
     sd = wave_sum(sd);
     const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
     const float mean = sd * inv / (float)cols;
-    for (int c = lane; c < cols; c += 64) dx[r * cols + c] = inv * (dr[c] - xr[c] * inv * mean);
+    if (res) {
+        const float* rr = res + r * cols;
+        for (int c = lane; c < cols; c += 64) dx[r * cols + c] = rr[c] + inv * (dr[c] - xr[c] * inv * mean);
+    } else {
+        for (int c = lane; c < cols; c += 64) dx[r * cols + c] = inv * (dr[c] - xr[c] * inv * mean);
+    }
 }
 
 // -------------------------------------------------------------------- AdamW
@@ -87,39 +95,46 @@ ASCA_DEV uint32_t hash_expert(uint32_t id, uint32_t n) {
     return h % n;
 }
 
-constexpr int RT_NT = 256;  // tokens per routing block (one per thread)
+constexpr int RT_NT = 256;     // tokens per routing block (one per thread)
+constexpr int RT_MAXB = 256;   // buckets (experts, or vocabulary ids)
 
-// Pass 1: expert of every token and the per-block count of every expert.
+// Pass 1: bucket of every token and the per-block count of every bucket.
+// HASH: bucket = hash_route(id) % E; otherwise the key itself (key < E).
+template <bool HASH>
 __global__ __launch_bounds__(RT_NT) void route_count_k(const uint32_t* __restrict__ ids, int n, int E,
                                                        int32_t* __restrict__ expert, int32_t* __restrict__ blkcnt) {
-    __shared__ int cnt[64];
+    __shared__ int cnt[RT_MAXB];
     const int t = blockIdx.x * RT_NT + threadIdx.x;
-    if (threadIdx.x < E) cnt[threadIdx.x] = 0;
+    for (int e = threadIdx.x; e < E; e += RT_NT) cnt[e] = 0;
     __syncthreads();
     if (t < n) {
-        const int e = (int)hash_expert(ids[t], (uint32_t)E);
+        // keys >= E wrap (memory safety); callers pass keys < E
+        const int e = (int)(HASH ? hash_expert(ids[t], (uint32_t)E) : ids[t] % (uint32_t)E);
         expert[t] = e;
         atomicAdd(&cnt[e], 1);  // integer counts: order-independent
     }
     __syncthreads();
-    if (threadIdx.x < E) blkcnt[blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
+    for (int e = threadIdx.x; e < E; e += RT_NT) blkcnt[blockIdx.x * E + e] = cnt[e];
 }
 
-// Pass 2 (one block): expert offsets and, per block, where its tokens of each
-// expert start.  blkcnt is rewritten in place as the start positions.
-__global__ __launch_bounds__(64) void route_scan_k(int nblk, int E, int32_t* __restrict__ blkcnt,
-                                                   int32_t* __restrict__ offsets) {
-    const int e = threadIdx.x;
+// Pass 2 (one block, thread e = bucket): bucket offsets and, per block, where
+// its tokens of each bucket start; blkcnt is rewritten in place as the starts.
+__global__ __launch_bounds__(RT_MAXB) void route_scan_k(int nblk, int E, int32_t* __restrict__ blkcnt,
+                                                        int32_t* __restrict__ offsets) {
+    __shared__ int wtot[RT_MAXB / 64];
+    const int e = threadIdx.x, lane = e & 63, w = e >> 6;
     int total = 0;
     if (e < E)
         for (int b = 0; b < nblk; ++b) total += blkcnt[b * E + e];
-    // exclusive prefix of the totals over experts (E <= 64, one wave)
-    int incl = total;
+    int incl = total;  // inclusive scan inside the wave
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) {
         const int o = __shfl_up(incl, s, 64);
-        if (e >= s) incl += o;
+        if (lane >= s) incl += o;
     }
+    if (lane == 63) wtot[w] = incl;
+    __syncthreads();
+    for (int ww = 0; ww < w; ++ww) incl += wtot[ww];
     const int base = incl - total;
     if (e < E) {
         offsets[e] = base;
@@ -134,12 +149,12 @@ __global__ __launch_bounds__(64) void route_scan_k(int nblk, int E, int32_t* __r
 }
 
 // Pass 3: stable placement -- a token's rank among the earlier tokens of its
-// block with the same expert comes from wave ballots, so the bucket of each
-// expert lists its tokens in ascending order, as model.rs:190-193 builds them.
+// block in the same bucket comes from wave ballots, so every bucket lists its
+// tokens in ascending order, as model.rs:190-193 builds them.
 __global__ __launch_bounds__(RT_NT) void route_place_k(int n, int E, const int32_t* __restrict__ expert,
                                                        const int32_t* __restrict__ blkstart,
                                                        int32_t* __restrict__ perm) {
-    __shared__ int wcnt[RT_NT / 64][64];
+    __shared__ unsigned char wcnt[RT_NT / 64][RT_MAXB];  // tokens per (wave, bucket), <= 64
     const int t = blockIdx.x * RT_NT + threadIdx.x;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int my = t < n ? expert[t] : -1;
@@ -148,7 +163,7 @@ __global__ __launch_bounds__(RT_NT) void route_place_k(int n, int E, const int32
     for (int e = 0; e < E; ++e) {
         const uint64_t mask = __ballot(my == e);
         if (my == e) rank = __popcll(mask & below);
-        if (lane == 0) wcnt[w][e] = __popcll(mask);
+        if (lane == 0) wcnt[w][e] = (unsigned char)__popcll(mask);
     }
     __syncthreads();
     if (t < n) {
@@ -156,6 +171,33 @@ __global__ __launch_bounds__(RT_NT) void route_place_k(int n, int E, const int32
         for (int ww = 0; ww < w; ++ww) before += wcnt[ww][my];
         perm[blkstart[blockIdx.x * E + my] + before + rank] = t;
     }
+}
+
+// Counting sort of n tokens into E <= 256 buckets (stable).  ws: nblk * E ints.
+int bucket_launch(bool hash, const uint32_t* ids, int n, int E, int32_t* expert, int32_t* perm, int32_t* offsets,
+                  void* ws, hipStream_t st) {
+    const int nblk = (n + RT_NT - 1) / RT_NT;
+    int32_t* blk = reinterpret_cast<int32_t*>(ws);
+    int rc;
+    if (n > 0) {
+        rc = pre_launch("route_count");
+        if (rc) return rc;
+        if (hash)
+            hipLaunchKernelGGL(route_count_k<true>, dim3(nblk), dim3(RT_NT), 0, st, ids, n, E, expert, blk);
+        else
+            hipLaunchKernelGGL(route_count_k<false>, dim3(nblk), dim3(RT_NT), 0, st, ids, n, E, expert, blk);
+        rc = post_launch("route_count");
+        if (rc) return rc;
+    }
+    rc = pre_launch("route_scan");
+    if (rc) return rc;
+    hipLaunchKernelGGL(route_scan_k, dim3(1), dim3(RT_MAXB), 0, st, nblk, E, blk, offsets);
+    rc = post_launch("route_scan");
+    if (rc || n == 0) return rc;
+    rc = pre_launch("route_place");
+    if (rc) return rc;
+    hipLaunchKernelGGL(route_place_k, dim3(nblk), dim3(RT_NT), 0, st, n, E, expert, blk, perm);
+    return post_launch("route_place");
 }
 
 // ------------------------------------------------------------ gather/scatter
@@ -216,6 +258,15 @@ using namespace asca;
 
 static unsigned row_blocks(long rows) { return (unsigned)((rows + (ROW_NT / 64) - 1) / (ROW_NT / 64)); }
 
+int asca::rmsnorm_bwd_launch(const float* x, const float* dy, const float* res, float* dx, long rows, int cols,
+                             float eps, hipStream_t st) {
+    if (rows == 0 || cols == 0) return ASCA_OK;
+    int rc = pre_launch("rmsnorm_bwd");
+    if (rc) return rc;
+    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(row_blocks(rows)), dim3(ROW_NT), 0, st, x, dy, res, dx, rows, cols, eps);
+    return post_launch("rmsnorm_bwd");
+}
+
 extern "C" {
 
 int asca_rmsnorm(const float* x, float* y, float* inv, long rows, int cols, float eps, void* stream) {
@@ -233,11 +284,7 @@ int asca_rmsnorm_bwd(const float* x, const float* dy, float* dx, long rows, int 
     if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "negative shape");
     if (rows == 0 || cols == 0) return ASCA_OK;
     if (!x || !dy || !dx) return fail(ASCA_ERR_INVALID, "null pointer in asca_rmsnorm_bwd");
-    int rc = pre_launch("rmsnorm_bwd");
-    if (rc) return rc;
-    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(row_blocks(rows)), dim3(ROW_NT), 0, as_stream(stream), x, dy, dx, rows,
-                       cols, eps);
-    return post_launch("rmsnorm_bwd");
+    return rmsnorm_bwd_launch(x, dy, nullptr, dx, rows, cols, eps, as_stream(stream));
 }
 
 int asca_adamw_scalars(float lr, float beta1, float beta2, float eps, float wd, uint32_t step, float* out) {
@@ -280,39 +327,31 @@ int asca_adamw(float* p, const float* g, float* m, float* v, long n, float lr, f
 
 int asca_hash_route_ws_bytes(int n, int n_experts, size_t* bytes) {
     if (!bytes) return fail(ASCA_ERR_INVALID, "null output pointer");
-    if (n < 0 || n_experts < 1 || n_experts > 64)
-        return fail(ASCA_ERR_UNSUPPORTED, "hash route: n=%d n_experts=%d (1..64 experts)", n, n_experts);
+    if (n < 0 || n_experts < 1 || n_experts > RT_MAXB)
+        return fail(ASCA_ERR_UNSUPPORTED, "bucketing: n=%d buckets=%d (1..%d buckets)", n, n_experts, RT_MAXB);
     const long nblk = (n + RT_NT - 1) / RT_NT;
     *bytes = (size_t)(nblk > 0 ? nblk : 1) * n_experts * sizeof(int32_t);
     return ASCA_OK;
 }
 
-int asca_hash_route(const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm, int32_t* offsets,
-                    void* ws, void* stream) {
+static int bucket_entry(bool hash, const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm,
+                        int32_t* offsets, void* ws, void* stream) {
     size_t wsb = 0;
     int rc = asca_hash_route_ws_bytes(n, n_experts, &wsb);
     if (rc) return rc;
     if (!offsets) return fail(ASCA_ERR_INVALID, "null offsets");
-    const int nblk = (n + RT_NT - 1) / RT_NT;
-    if (n > 0 && (!ids || !expert || !perm || !ws)) return fail(ASCA_ERR_INVALID, "null pointer in asca_hash_route");
-    int32_t* blk = reinterpret_cast<int32_t*>(ws);
-    const hipStream_t st = as_stream(stream);
-    if (n > 0) {
-        rc = pre_launch("route_count");
-        if (rc) return rc;
-        hipLaunchKernelGGL(route_count_k, dim3(nblk), dim3(RT_NT), 0, st, ids, n, n_experts, expert, blk);
-        rc = post_launch("route_count");
-        if (rc) return rc;
-    }
-    rc = pre_launch("route_scan");
-    if (rc) return rc;
-    hipLaunchKernelGGL(route_scan_k, dim3(1), dim3(64), 0, st, nblk, n_experts, blk, offsets);
-    rc = post_launch("route_scan");
-    if (rc || n == 0) return rc;
-    rc = pre_launch("route_place");
-    if (rc) return rc;
-    hipLaunchKernelGGL(route_place_k, dim3(nblk), dim3(RT_NT), 0, st, n, n_experts, expert, blk, perm);
-    return post_launch("route_place");
+    if (n > 0 && (!ids || !expert || !perm || !ws)) return fail(ASCA_ERR_INVALID, "null pointer in bucketing");
+    return bucket_launch(hash, ids, n, n_experts, expert, perm, offsets, ws, as_stream(stream));
+}
+
+int asca_hash_route(const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm, int32_t* offsets,
+                    void* ws, void* stream) {
+    return bucket_entry(true, ids, n, n_experts, expert, perm, offsets, ws, stream);
+}
+
+int asca_bucket_keys(const uint32_t* keys, int n, int n_buckets, int32_t* bucket, int32_t* perm, int32_t* offsets,
+                     void* ws, void* stream) {
+    return bucket_entry(false, keys, n, n_buckets, bucket, perm, offsets, ws, stream);
 }
 
 static int rows_copy(bool scatter, const float* src, const int32_t* idx, long n, int cols, float* dst, void* stream) {

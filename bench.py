@@ -244,13 +244,112 @@ def bench_decode(args):
     print(json.dumps(result), flush=True)
 
 
+TRAIN_CFG = dict(V=256, d=512, H=8, L=8, E=16, dff=1024, B=16, T=1024, seed=2)
+
+
+def train_flops_per_token(V, d, H, L, E, dff):
+    """Algorithmic flops of one training step per token: every dense product
+    once forward and twice backward, the recurrence's 24 dh^2 per head
+    (7 forward + 17 backward, delta.rs:289-314,504-564), the output head."""
+    dh = d // H
+    gemm_fwd = 2 * d * 3 * d + 2 * d * 2 * H + 2 * d * d + 2 * 2 * d * dff
+    return L * (3 * gemm_fwd + 24 * dh * dh * H) + 3 * 2 * d * V
+
+
+def bench_train(args):
+    """one full training step (forward, BPTT backward, AdamW over
+    all 143.1M parameters) of the 8-layer model, B=16 x T=1024 byte tokens,
+    weights N(0, 0.02) from the reference Rng (seed 2), targets = ids shifted
+    by one (Data::batch, rust/src/train.rs:145-155)."""
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf
+    from asca_amd.model import DeviceModel
+
+    c = TRAIN_CFG
+    V, d, H, L, E, dff, B, T = c["V"], c["d"], c["H"], c["L"], c["E"], c["dff"], c["B"], c["T"]
+    if gpu.gpu() is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    lib = _lib.load()
+    st = (C.c_uint64 * 2)()
+    lib.asca_rng_seed(c["seed"], st)
+    dm = DeviceModel(V, d, H, L, E, dff)
+    params = []
+    for _, _, r, cc in dm.tensors:
+        a = np.empty(r * cc, dtype=np.float32)
+        lib.asca_rng_normal(st, a.ctypes.data_as(C.c_void_p), a.size, 0.02, 0.0)
+        params.append(a)
+    dm.set_params(params)
+    dm.set_adamw(3e-4)
+    raw = np.empty(B * (T + 1), dtype=np.uint64)
+    lib.asca_rng_u64(st, raw.ctypes.data_as(C.POINTER(C.c_uint64)), raw.size)
+    toks = (raw % 256).astype(np.uint32).reshape(B, T + 1)
+    ids, tgts = toks[:, :T].reshape(-1), toks[:, 1:].reshape(-1)
+    di, dt = DevBuf.from_array(ids), DevBuf.from_array(tgts)
+    tm = Timer()
+    K = args.steps or 10
+    W = args.warmup
+    print(f"bench train: {gpu.describe()}; V{V} d{d} L{L} H{H} E{E} dff{dff} B{B} T{T}; "
+          f"{dm.num_params()} params; warmup {W}, steps {K}", flush=True)
+    for _ in range(W):
+        dm.train_step_dev(di, dt, B, T, sync=False, stream=C.c_void_p(tm.stream))
+    tm.sync()
+    loss0 = dm._read_loss()
+    e0, e1 = tm.event(), tm.event()
+    t0 = time.perf_counter()
+    tm.record(e0)
+    for _ in range(K):
+        dm.train_step_dev(di, dt, B, T, sync=False, stream=C.c_void_p(tm.stream))
+    tm.record(e1)
+    tm.sync()
+    wall = time.perf_counter() - t0
+    dev_ms = tm.elapsed(e0, e1) / K
+    tm.destroy(e0, e1)
+    loss = dm._read_loss()
+    fpt = train_flops_per_token(V, d, H, L, E, dff)
+    achieved = fpt * B * T / (dev_ms * 1e-3)
+    result = {
+        "metric": "training tokens/s (configs[3]: V256 d512 L8 H8 E16 dff1024, B16 T1024, f32, fwd+BPTT+AdamW)",
+        "value": round(B * T * K / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic bytes from the reference Rng (seed {c['seed']}), N(0,0.02) weights; "
+                f"loss {loss0:.4f} -> {loss:.4f} over the timed steps",
+        "config": {"workload": "full training step (asca_model_train_step)", "global_batch": B, "seq_len": T,
+                   "d_model": d, "layers": L, "heads": H, "experts": E, "d_ff": dff, "vocab": V},
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_F32 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32, 4), "traffic": None, "kernel": "step",
+                     "algorithmic_flops_per_token": fpt},
+    }
+    if not args.no_cpu:
+        from oracle import model_oracle as mo
+
+        om = mo.OracleModel(V, d, H, L, E, dff, [p.reshape(r, cc) for p, (_, _, r, cc) in zip(params, dm.tensors)])
+        t1 = time.perf_counter()
+        om.forward_backward(ids[:T], tgts[:T], 1)
+        el = time.perf_counter() - t1
+        result["cpu_baseline"] = {
+            "value": round(T / el, 1), "unit": "tokens/s", "cores": min(os.cpu_count() or 1, 16), "kind": "port",
+            "sample": f"oracle restatement of Model::forward+backward (C oracle: delta scan/BPTT threaded per head / "
+                      f"(head, seq), MoE threaded per expert; numpy f32 GEMMs), 1 of the {B} sequences "
+                      f"({T} tokens), no optimiser step, {el:.1f} s"}
+    dm.close()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="delta", choices=["delta", "decode"],
-                    help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]")
+    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train"],
+                    help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]; train: configs[3]")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib", action="store_true",
                     help="also run the known-size copy kernel (for counter calibration)")
@@ -262,6 +361,9 @@ def main():
         sys.exit(2)
     if args.workload == "decode":
         bench_decode(args)
+        return
+    if args.workload == "train":
+        bench_train(args)
         return
     if args.steps is None:
         args.steps = 100

@@ -260,7 +260,7 @@ ASCA_API int asca_adamw(float* p, const float* g, float* m, float* v, long n, fl
 
 /* ----------------------------------------------------------- hash routing -- */
 
-/* Workspace bytes for asca_hash_route (n tokens, 1..64 experts). */
+/* Workspace bytes for asca_hash_route / asca_bucket_keys (n tokens, 1..256 buckets). */
 ASCA_API int asca_hash_route_ws_bytes(int n, int n_experts, size_t* bytes);
 
 /* Expert of every token, expert = hash_route(id) % n_experts with the
@@ -271,6 +271,13 @@ ASCA_API int asca_hash_route_ws_bytes(int n, int n_experts, size_t* bytes);
  * deterministic.  ids: device u32 (n); expert, perm: device int32 (n). */
 ASCA_API int asca_hash_route(const uint32_t* ids, int n, int n_experts, int32_t* expert, int32_t* perm,
                              int32_t* offsets, void* ws, void* stream);
+
+/* The same stable bucketing keyed by the value itself (bucket = key, keys <
+ * n_buckets <= 256; larger keys wrap modulo n_buckets): tokens grouped by id,
+ * the order in which Model::backward accumulates the embedding gradient
+ * (rust/src/model.rs:782-789).  Workspace as asca_hash_route_ws_bytes. */
+ASCA_API int asca_bucket_keys(const uint32_t* keys, int n, int n_buckets, int32_t* bucket, int32_t* perm,
+                              int32_t* offsets, void* ws, void* stream);
 
 /* ------------------------------------------------------------------ GEMM -- */
 
@@ -316,6 +323,47 @@ ASCA_API int asca_moe_bwd(const float* xn, const float* w1, const float* w2, con
                           const float* dout, int T, int d, int d_ff, int n_experts, float* dxn,
                           float* dw1, float* db1, float* dw2, float* db2, float* dpre_ws, int accumulate,
                           void* stream);
+
+/* ----------------------------------------------------- training step -- */
+
+/* A device-resident ASCA model (rust/src/model.rs:528-802): parameters,
+ * gradients and AdamW moments in four flat f32 device buffers, tensors in the
+ * reference's params() order -- embed (V x d), head (d x V), then per layer
+ * delta.w_qkv (d x 3d), delta.b_qkv, delta.w_gate (d x 2H), delta.b_gate,
+ * delta.w_o (d x d), delta.b_o, moe.w1 (d x E*d_ff), moe.b1, moe.w2
+ * (E*d_ff x d), moe.b2 -- each starting at a 16-byte aligned offset
+ * (asca_model_tensor_info).  It replaces the Rust host's Model + Param
+ * residency of the reference's GPU backend (Param values/grads shuttled per
+ * op, rust/src/cuda/mod.rs) by whole-step residency.  Parameters start at zero;
+ * the caller uploads its initialisation into the params buffer. */
+typedef struct asca_model asca_model;
+
+ASCA_API int asca_model_create(int vocab, int d_model, int n_heads, int n_layers, int n_experts, int d_ff,
+                               asca_model** out);
+ASCA_API int asca_model_destroy(asca_model* model);
+ASCA_API int asca_model_num_tensors(const asca_model* model, int* n);
+ASCA_API int asca_model_tensor_info(const asca_model* model, int i, char* name, int name_len, size_t* offset,
+                                   int* rows, int* cols);
+/* Device pointers of the flat buffers (n_floats entries each). */
+ASCA_API int asca_model_buffers(asca_model* model, size_t* n_floats, float** params, float** grads, float** m,
+                                float** v);
+/* AdamW hyper-parameters and step counter (AdamW::new / ::update,
+ * rust/src/tensor.rs:381-402); the counter advances once per tensor per step. */
+ASCA_API int asca_model_set_adamw(asca_model* model, float lr, float beta1, float beta2, float eps, float wd,
+                                  uint32_t step);
+ASCA_API int asca_model_adamw_step_count(const asca_model* model, uint32_t* step);
+
+/* Model::forward + Model::backward after zero_grads (rust/src/train.rs:176-186):
+ * ids, targets are device u32 arrays of batch*seq tokens (sequence b is rows
+ * b*seq..); gradients are written into the grads buffer; *loss (device, may
+ * be NULL) receives the mean cross-entropy. */
+ASCA_API int asca_model_forward_backward(asca_model* model, const uint32_t* ids, const uint32_t* targets,
+                                         int batch, int seq, float* loss, void* stream);
+/* The optimiser step over every tensor (model.rs:797-802 / AdamW::update). */
+ASCA_API int asca_model_adamw(asca_model* model, void* stream);
+/* forward_backward followed by asca_model_adamw: one training step. */
+ASCA_API int asca_model_train_step(asca_model* model, const uint32_t* ids, const uint32_t* targets, int batch,
+                                   int seq, float* loss, void* stream);
 
 #ifdef __cplusplus
 }
