@@ -242,6 +242,7 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
                         if (bias) a += bias[n + y];
                         if constexpr (EPI == EPI_STORE) {
                             if (p.beta != 0.0f) a += p.beta * Cr[n + y];
+                            if (p.resid) a += p.resid[crow * p.ld_resid + n + y];
                         } else if constexpr (EPI == EPI_SILU) {
                             hb[y] = silu_ref(a);
                         } else {
@@ -274,6 +275,7 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
                     if (bias) a += bias[n];
                     if constexpr (EPI == EPI_STORE) {
                         if (p.beta != 0.0f) a += p.beta * Cr[n];
+                        if (p.resid) a += p.resid[crow * p.ld_resid + n];
                         Cr[n] = a;
                     } else if constexpr (EPI == EPI_SILU) {
                         Cr[n] = a;
@@ -309,39 +311,61 @@ __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__
 
 // Column sums, optionally per group of rows: out[g*N + c] (+)= sum over the
 // rows of group g of X[r][c] (bias gradients: colsum_raw of
-// rust/src/cuda/mod.rs:642-669 and the per-expert db1 of model.rs:432-440).  One thread per column
-// and row slice, slices summed in a fixed order.
-constexpr int CS_ROWS = 256;
+// rust/src/cuda/mod.rs:642-669 and the per-expert db1 of model.rs:432-440).
+// Pass 1: a block sums 64 columns over one row slice, its four waves taking
+// every fourth row with four independent accumulators; pass 2 sums the slices.
+// Every sum has a fixed order, so results are deterministic.
+constexpr int CS_SLICE = 128;  // target rows per slice
 __global__ __launch_bounds__(256) void colsum_part_k(const float* __restrict__ X, long rows, int N, long ldx,
-                                                     const int* __restrict__ goff, int ngroups,
-                                                     float* __restrict__ part, int nslices) {
-    // grid: (ceil(N / 256), nslices, max(ngroups, 1))
-    const int c = blockIdx.x * 256 + threadIdx.x;
+                                                     const int* __restrict__ goff, float* __restrict__ part,
+                                                     int nslices) {
+    // grid: (ceil(N / 64), nslices, groups)
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
     const int g = blockIdx.z;
     long lo = 0, hi = rows;
     if (goff) {
         lo = goff[g];
         hi = goff[g + 1];
     }
-    const long span = hi - lo;
-    const long per = (span + nslices - 1) / nslices;
+    const long per = (hi - lo + nslices - 1) / nslices;
     const long a = lo + (long)blockIdx.y * per;
     const long b = min(hi, a + per);
-    if (c >= N) return;
-    float s = 0.0f;
-    for (long r = a; r < b; ++r) s += X[r * ldx + c];
-    part[((long)g * nslices + blockIdx.y) * N + c] = s;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    if (c < N) {
+        long r = a + w;
+        for (; r + 12 < b; r += 16) {
+            s0 += X[r * ldx + c];
+            s1 += X[(r + 4) * ldx + c];
+            s2 += X[(r + 8) * ldx + c];
+            s3 += X[(r + 12) * ldx + c];
+        }
+        for (; r < b; r += 4) s0 += X[r * ldx + c];
+    }
+    red[w][lane] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (w == 0 && c < N)
+        part[((long)g * nslices + blockIdx.y) * N + c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
-__global__ __launch_bounds__(256) void colsum_fin_k(const float* __restrict__ part, int nslices, int N, int G,
+__global__ __launch_bounds__(256) void colsum_fin_k(const float* __restrict__ part, int nslices, int N,
                                                     float* __restrict__ out, int accumulate) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (long)G * N) return;
-    const long g = i / N;
-    const int c = (int)(i - g * N);
+    // grid: (ceil(N / 64), groups)
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    const long g = blockIdx.y;
     float s = 0.0f;
-    for (int k = 0; k < nslices; ++k) s += part[(g * nslices + k) * N + c];
-    out[i] = accumulate ? out[i] + s : s;
+    if (c < N)
+        for (int k = w; k < nslices; k += 4) s += part[(g * nslices + k) * N + c];
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && c < N) {
+        const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+        const long o = g * N + c;
+        out[o] = accumulate ? out[o] + t : t;
+    }
 }
 
 // ---------------------------------------------------------------- host side
@@ -401,6 +425,8 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t st, const char* name) {
     if (a.M < 0 || a.N < 0 || a.K < 0) return fail(ASCA_ERR_INVALID, "%s: negative shape", name);
     if (a.gmode == 1 && ta) return fail(ASCA_ERR_INVALID, "%s: grouped rows need a non-transposed A", name);
+    if (a.resid && (epi != EPI_STORE || a.k_per_split > 0))
+        return fail(ASCA_ERR_UNSUPPORTED, "%s: residual input needs the plain epilogue without split-K", name);
     if (a.gmode == 2 && (!ta || tb)) return fail(ASCA_ERR_INVALID, "%s: grouped K needs A^T and B", name);
     if (epi == EPI_SILU && (ta || tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU epilogue is NN only", name);
     if (epi == EPI_SILU_BWD && (ta || !tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU-bwd epilogue is NT only", name);
@@ -452,24 +478,22 @@ int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, i
     if (N == 0) return ASCA_OK;
     const int G = goff ? ngroups : 1;
     if (G == 0) return ASCA_OK;
-    const int cb = (N + 255) / 256;
-    // enough slices to fill the chip, each at least CS_ROWS rows on average
-    const long avg = goff ? rows / G + 1 : rows;
-    int ns = (int)min((long)((avg + CS_ROWS - 1) / CS_ROWS), 64L);
+    const int cb = (N + 63) / 64;
+    // slices of about CS_SLICE rows (twice as many per group: group sizes vary)
+    const long avg = goff ? (2 * rows) / G + 1 : rows;
+    int ns = (int)min((avg + CS_SLICE - 1) / CS_SLICE, 1024L);
     if (ns < 1) ns = 1;
     float* part = nullptr;
     int rc = scratch_get((size_t)G * ns * N * sizeof(float), &part);
     if (rc) return rc;
     rc = pre_launch("colsum");
     if (rc) return rc;
-    hipLaunchKernelGGL(colsum_part_k, dim3(cb, ns, G), dim3(256), 0, st, X, rows, N, ldx, goff, G, part, ns);
+    hipLaunchKernelGGL(colsum_part_k, dim3(cb, ns, G), dim3(256), 0, st, X, rows, N, ldx, goff, part, ns);
     rc = post_launch("colsum");
     if (rc) return rc;
     rc = pre_launch("colsum_fin");
     if (rc) return rc;
-    const long tot = (long)G * N;
-    hipLaunchKernelGGL(colsum_fin_k, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, part, ns, N, G, out,
-                       accumulate);
+    hipLaunchKernelGGL(colsum_fin_k, dim3(cb, G), dim3(256), 0, st, part, ns, N, out, accumulate);
     return post_launch("colsum_fin");
 }
 

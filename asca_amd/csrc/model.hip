@@ -305,10 +305,10 @@ static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* tar
         if ((rc = post_launch("qkv_prep"))) return rc;
         if ((rc = asca_delta_fwd(a.q, a.k, a.v, a.al, a.be, a.o, a.dws, M->batch, M->seq, H, dh, st))) return rc;
         // x_mid = x + (o W_o + b_o)
-        if ((rc = d2d(a.x_mid, x, (size_t)T * d * 4, st))) return rc;
         GemmArgs yo = gemm_plain(a.o, d, M->p + P.w_o, d, a.x_mid, d, T, d, d);
         yo.bias = M->p + P.b_o;
-        yo.beta = 1.0f;
+        yo.resid = x;
+        yo.ld_resid = d;
         if ((rc = gemm_launch(0, 0, EPI_STORE, yo, T, st, "out_proj"))) return rc;
         // MoE on RMSNorm(x_mid); x_out = x_mid + moe
         if ((rc = asca_rmsnorm(a.x_mid, a.xn, nullptr, T, d, MODEL_EPS, st))) return rc;
@@ -332,7 +332,6 @@ static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* tar
         w1.ngroups = E;
         w1.gmode = 1;
         if ((rc = gemm_launch(0, 0, EPI_SILU, w1, T, st, "moe_fwd_w1"))) return rc;
-        if ((rc = d2d(a.x_out, a.x_mid, (size_t)T * d * 4, st))) return rc;
         GemmArgs w2 = gemm_args();
         w2.A = a.hid;
         w2.lda = dff;
@@ -343,7 +342,8 @@ static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* tar
         w2.ldc = d;
         w2.c_rows = M->perm;
         w2.bias = M->p + P.b2;
-        w2.beta = 1.0f;
+        w2.resid = a.x_mid;
+        w2.ld_resid = d;
         w2.M = T;
         w2.N = d;
         w2.K = dff;
@@ -404,9 +404,9 @@ static int model_backward(asca_model* M, hipStream_t st) {
         if ((rc = gemm_wgrad(x_in, d, M->dgate, 2 * H, G + P.w_gate, d, 2 * H, T, st))) return rc;
         if ((rc = asca_colsum(M->dgate, T, 2 * H, G + P.b_gate, 0, st))) return rc;
         // dx = d_mid + d_qkv W_qkv^T + d_gate W_gate^T
-        if ((rc = d2d(M->dx, M->dmid, (size_t)T * d * 4, st))) return rc;
         GemmArgs dq = gemm_plain(M->dqkv, 3 * d, M->p + P.w_qkv, 3 * d, M->dx, d, T, d, 3 * d);
-        dq.beta = 1.0f;
+        dq.resid = M->dmid;
+        dq.ld_resid = d;
         if ((rc = gemm_launch(0, 1, EPI_STORE, dq, T, st, "qkv_proj_dx"))) return rc;
         GemmArgs dg = gemm_plain(M->dgate, 2 * H, M->p + P.w_gate, 2 * H, M->dx, d, T, d, 2 * H);
         dg.beta = 1.0f;
