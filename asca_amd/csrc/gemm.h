@@ -10,7 +10,8 @@ enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_SILU_BWD = 2 };
 // One (possibly grouped, possibly split-K) GEMM:
 //   C = alpha * op(A) op(B) (+ bias per column) (+ beta * C) (+ R)
 // gmode 0: plain; gmode 1: M varies per group (rows goff[g]..goff[g+1] of the
-// sorted row space); gmode 2: K varies per group.  Row indirections map the
+// sorted row space); gmode 2: K varies per group; gmode 3: ngroups independent
+// products of one shape, operand g at A + g*a_gs, B + g*b_gs, C + g*c_gs.  Row indirections map the
 // operand's storage-row index (sorted space) to the stored row.
 struct GemmArgs {
     const float* A;
@@ -25,6 +26,7 @@ struct GemmArgs {
     const float* bias;
     const float* resid;  // EPI_STORE: residual added per element (rows as C's, stride ld_resid), or null
     long ld_resid;
+    long r_gs;           // per-group stride of resid
     const float* aux;  // EPI_SILU_BWD: pre (rows in group/sorted space)
     float* aux_out;    // EPI_SILU: hidden
     long ld_aux;

@@ -34,11 +34,15 @@
 
 namespace asca {
 
-constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_NT = 256;
+// Block tiles are (64 WM) x (64 WN) with one 64 x 64 wave tile per wave:
+// 128 x 128 on 4 waves for the large products, 64 x 128 on 2 waves for the
+// 64-row batched per-chunk products of the chunked delta rule.
+constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32;
 constexpr int GM_LDK = GM_BK + 4;  // [mn][k] tile row stride (floats)
-constexpr int GM_LDM = 128;        // [k][mn] tile row stride
-constexpr int GM_KC_F = 128 * GM_LDK;
-constexpr int GM_MC_F = GM_BK * GM_LDM;
+
+// floats of one LDS operand tile with R mn-rows
+template <bool KC, int R>
+constexpr int tile_floats() { return KC ? R * GM_LDK : GM_BK * R; }
 
 ASCA_DEV float silu_ref(float x) { return x / (1.0f + expf(-x)); }
 
@@ -56,24 +60,25 @@ ASCA_DEV float4 ld4(const float* p, int n) {
 
 ASCA_DEV long srow(const int* rows, long off, long i) { return rows ? (long)rows[off + i] : off + i; }
 
-// Global -> registers for one operand tile (4 float4 per thread).
-//   KC (k-contiguous, stored [mn][k]): 128 mn-rows x 32 k, 8 threads per row.
-//   MC (mn-contiguous, stored [k][mn]): 32 k-rows x 128 mn, 32 threads per row.
+// Global -> registers for one operand tile (8 R / NT float4 per thread).
+//   KC (k-contiguous, stored [mn][k]): R mn-rows x 32 k, 8 threads per row.
+//   MC (mn-contiguous, stored [k][mn]): 32 k-rows x R mn, R/4 threads per row.
 // `lim_mn`, `lim_k`: valid extents relative to the tile origin.
-template <bool KC, bool VEC>
-ASCA_DEV void tile_load(float4 (&r)[4], const float* base, long ld, const int* rows, long row_off, int mn0,
-                        int lim_mn, long k0, long lim_k, int tid) {
+template <bool KC, bool VEC, int R, int NT>
+ASCA_DEV void tile_load(float4 (&r)[8 * R / NT], const float* base, long ld, const int* rows, long row_off,
+                        int mn0, int lim_mn, long k0, long lim_k, int tid) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8 * R / NT; ++j) {
+        const int sl = tid + NT * j;
         if constexpr (KC) {
-            const int rr = (tid >> 3) + 32 * j;
-            const int kk = 4 * (tid & 7);
+            const int rr = sl >> 3;
+            const int kk = 4 * (sl & 7);
             const bool ok = rr < lim_mn;
             const long sr = ok ? srow(rows, row_off, mn0 + rr) : 0;
             r[j] = ld4<VEC>(base + sr * ld + k0 + kk, ok ? (int)min(lim_k - kk, 4L) : 0);
         } else {
-            const int kr = (tid >> 5) + 8 * j;
-            const int mm = 4 * (tid & 31);
+            const int kr = sl / (R / 4);
+            const int mm = 4 * (sl % (R / 4));
             const bool ok = kr < lim_k;
             const long sr = ok ? srow(rows, row_off, k0 + kr) : 0;
             r[j] = ld4<VEC>(base + sr * ld + mn0 + mm, ok ? min(lim_mn - mm, 4) : 0);
@@ -81,20 +86,21 @@ ASCA_DEV void tile_load(float4 (&r)[4], const float* base, long ld, const int* r
     }
 }
 
-template <bool KC>
-ASCA_DEV void tile_store(const float4 (&r)[4], float* t, int tid) {
+template <bool KC, int R, int NT>
+ASCA_DEV void tile_store(const float4 (&r)[8 * R / NT], float* t, int tid) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8 * R / NT; ++j) {
+        const int sl = tid + NT * j;
         if constexpr (KC)
-            *reinterpret_cast<float4*>(t + ((tid >> 3) + 32 * j) * GM_LDK + 4 * (tid & 7)) = r[j];
+            *reinterpret_cast<float4*>(t + (sl >> 3) * GM_LDK + 4 * (sl & 7)) = r[j];
         else
-            *reinterpret_cast<float4*>(t + ((tid >> 5) + 8 * j) * GM_LDM + 4 * (tid & 31)) = r[j];
+            *reinterpret_cast<float4*>(t + (sl / (R / 4)) * R + 4 * (sl % (R / 4))) = r[j];
     }
 }
 
 // Fragments of one 16-k group h for the wave's 64 mn-rows starting at w0:
 // f[s][t] = operand value of MFMA k-step s for 16-row tile t.
-template <bool KC>
+template <bool KC, int R>
 ASCA_DEV void frag_read(float (&f)[4][4], const float* t, int w0, int h, int lane) {
     if constexpr (KC) {
 #pragma unroll
@@ -110,7 +116,7 @@ ASCA_DEV void frag_read(float (&f)[4][4], const float* t, int w0, int h, int lan
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const float4 v =
-                *reinterpret_cast<const float4*>(t + (16 * h + 4 * (lane >> 4) + s) * GM_LDM + w0 + 4 * (lane & 15));
+                *reinterpret_cast<const float4*>(t + (16 * h + 4 * (lane >> 4) + s) * R + w0 + 4 * (lane & 15));
             f[s][0] = v.x;
             f[s][1] = v.y;
             f[s][2] = v.z;
@@ -119,11 +125,12 @@ ASCA_DEV void frag_read(float (&f)[4][4], const float* t, int w0, int h, int lan
     }
 }
 
-template <bool TA, bool TB, int EPI, bool VEC>
-__global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
+template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
+    constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 64 * WN;
     constexpr bool A_KC = !TA, B_KC = TB;
-    constexpr int A_F = A_KC ? GM_KC_F : GM_MC_F;
-    constexpr int B_F = B_KC ? GM_KC_F : GM_MC_F;
+    constexpr int A_F = tile_floats<A_KC, BM>();
+    constexpr int B_F = tile_floats<B_KC, BN>();
     extern __shared__ float4 lds4[];
     float* lds = reinterpret_cast<float*>(lds4);
 
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
         int mt = L / p.tiles_n;
         for (; g < p.ngroups; ++g) {
             const int a = p.goff[g], b = p.goff[g + 1];
-            const int nt = (b - a + GM_BM - 1) / GM_BM;
+            const int nt = (b - a + BM - 1) / BM;
             if (mt < nt) break;
             mt -= nt;
         }
@@ -153,21 +160,26 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
         g = r / p.tiles_m;
         goff_g = p.goff[g];
         K_hi = p.goff[g + 1] - p.goff[g];
+    } else if (p.gmode == 3) {
+        const int r = L / p.tiles_n;
+        tm = r % p.tiles_m;
+        g = r / p.tiles_m;
     } else {
         tm = L / p.tiles_n;
         K_lo = (long)blockIdx.y * p.k_per_split;
         K_hi = min((long)p.K, K_lo + p.k_per_split);
     }
-    const int m0 = tm * GM_BM, n0 = tn * GM_BN;
+    const int m0 = tm * BM, n0 = tn * BN;
     const float* A = p.A + g * p.a_gs;
     const float* B = p.B + g * p.b_gs;
     float* C = p.C + g * p.c_gs + (long)blockIdx.y * p.c_split_stride;
     const float* bias = p.bias ? p.bias + g * p.bias_gs : nullptr;
+    const float* resid = p.resid ? p.resid + g * p.r_gs : nullptr;
     const long a_off = ((p.gmode == 1 && !TA) || (p.gmode == 2 && TA)) ? goff_g : 0;
     const long b_off = (p.gmode == 2 && !TB) ? goff_g : 0;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    const int wm = (w / WN) * 64, wn = (w % WN) * 64;
     const int lim_m = Mg - m0, lim_n = p.N - n0;
 
     f32x4 acc[4][4];
@@ -177,15 +189,15 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
         for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const long nk = (K_hi - K_lo + GM_BK - 1) / GM_BK;
-    float4 ra[4], rb[4];
+    float4 ra[8 * BM / NT], rb[8 * BN / NT];
     auto load = [&](long k0) {
-        tile_load<A_KC, VEC>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
-        tile_load<B_KC, VEC>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
+        tile_load<A_KC, VEC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
+        tile_load<B_KC, VEC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
     };
     if (nk > 0) {
         load(K_lo);
-        tile_store<A_KC>(ra, lds, tid);
-        tile_store<B_KC>(rb, lds + A_F, tid);
+        tile_store<A_KC, BM, NT>(ra, lds, tid);
+        tile_store<B_KC, BN, NT>(rb, lds + A_F, tid);
     }
     __syncthreads();
     for (long kt = 0; kt < nk; ++kt) {
@@ -196,8 +208,8 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             float fa[4][4], fb[4][4];
-            frag_read<A_KC>(fa, As, wm, h, lane);
-            frag_read<B_KC>(fb, Bs, wn, h, lane);
+            frag_read<A_KC, BM>(fa, As, wm, h, lane);
+            frag_read<B_KC, BN>(fb, Bs, wn, h, lane);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -208,8 +220,8 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
         }
         if (more) {
             float* Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
-            tile_store<A_KC>(ra, Ns, tid);
-            tile_store<B_KC>(rb, Ns + A_F, tid);
+            tile_store<A_KC, BM, NT>(ra, Ns, tid);
+            tile_store<B_KC, BN, NT>(rb, Ns + A_F, tid);
         }
         __syncthreads();
     }
@@ -242,7 +254,7 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
                         if (bias) a += bias[n + y];
                         if constexpr (EPI == EPI_STORE) {
                             if (p.beta != 0.0f) a += p.beta * Cr[n + y];
-                            if (p.resid) a += p.resid[crow * p.ld_resid + n + y];
+                            if (resid) a += resid[crow * p.ld_resid + n + y];
                         } else if constexpr (EPI == EPI_SILU) {
                             hb[y] = silu_ref(a);
                         } else {
@@ -275,7 +287,7 @@ __global__ __launch_bounds__(GM_NT, 2) void gemm_k(GemmArgs p) {
                     if (bias) a += bias[n];
                     if constexpr (EPI == EPI_STORE) {
                         if (p.beta != 0.0f) a += p.beta * Cr[n];
-                        if (p.resid) a += p.resid[crow * p.ld_resid + n];
+                        if (resid) a += resid[crow * p.ld_resid + n];
                         Cr[n] = a;
                     } else if constexpr (EPI == EPI_SILU) {
                         Cr[n] = a;
@@ -402,19 +414,18 @@ static int scratch_get(size_t bytes, float** out) {
     return ASCA_OK;
 }
 
-template <bool TA, bool TB, int EPI, bool VEC>
+template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2>
 static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
-    constexpr int A_F = !TA ? GM_KC_F : GM_MC_F;
-    constexpr int B_F = TB ? GM_KC_F : GM_MC_F;
-    constexpr size_t lds = 2 * (size_t)(A_F + B_F) * sizeof(float);
+    constexpr size_t lds =
+        2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 64 * WN>()) * sizeof(float);
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
         attr = true;
     }
-    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC>), grid, dim3(GM_NT), lds, st, a);
+    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN>), grid, dim3(64 * WM * WN), lds, st, a);
     return ASCA_OK;
 }
 
@@ -430,21 +441,26 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     if (a.gmode == 2 && (!ta || tb)) return fail(ASCA_ERR_INVALID, "%s: grouped K needs A^T and B", name);
     if (epi == EPI_SILU && (ta || tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU epilogue is NN only", name);
     if (epi == EPI_SILU_BWD && (ta || !tb)) return fail(ASCA_ERR_UNSUPPORTED, "%s: SiLU-bwd epilogue is NT only", name);
-    a.tiles_n = (a.N + GM_BN - 1) / GM_BN;
-    a.tiles_m = (a.M + GM_BM - 1) / GM_BM;
+    if (a.gmode == 3 && (a.a_rows || a.b_rows || a.c_rows || epi != EPI_STORE))
+        return fail(ASCA_ERR_UNSUPPORTED, "%s: batched products take no row indirection or fused epilogue", name);
+    const bool vec = (a.lda % 4 == 0) && (a.ldb % 4 == 0) && (a.ldc % 4 == 0) && (a.ld_aux % 4 == 0) &&
+                     aligned16(a.A) && aligned16(a.B) && aligned16(a.C) && (!a.aux || aligned16(a.aux)) &&
+                     (!a.aux_out || aligned16(a.aux_out)) && (a.a_gs % 4 == 0) && (a.b_gs % 4 == 0) &&
+                     (a.c_gs % 4 == 0) && (a.c_split_stride % 4 == 0);
+    // batched per-chunk products with at most 64 rows use 64 x 128 tiles
+    const int wm = (a.gmode == 3 && vec && a.M <= 64) ? 1 : 2;
+    const int wn = 2;  // a 64 x 64 tile needs 8 staged float4 per operand per lane and spills
+    a.tiles_n = (a.N + 64 * wn - 1) / (64 * wn);
+    a.tiles_m = (a.M + 64 * wm - 1) / (64 * wm);
     long blocks;
     if (a.gmode == 1)
         blocks = ((m_total + GM_BM - 1) / GM_BM + a.ngroups) * a.tiles_n;
-    else if (a.gmode == 2)
+    else if (a.gmode == 2 || a.gmode == 3)
         blocks = (long)a.ngroups * a.tiles_m * a.tiles_n;
     else
         blocks = (long)a.tiles_m * a.tiles_n;
     if (blocks == 0 || a.N == 0) return ASCA_OK;
     if (blocks > 0x7fffffffL) return fail(ASCA_ERR_INVALID, "%s: grid too large", name);
-    const bool vec = (a.lda % 4 == 0) && (a.ldb % 4 == 0) && (a.ldc % 4 == 0) && (a.ld_aux % 4 == 0) &&
-                     aligned16(a.A) && aligned16(a.B) && aligned16(a.C) && (!a.aux || aligned16(a.aux)) &&
-                     (!a.aux_out || aligned16(a.aux_out)) && (a.a_gs % 4 == 0) && (a.b_gs % 4 == 0) &&
-                     (a.c_gs % 4 == 0) && (a.c_split_stride % 4 == 0);
     int rc = pre_launch(name);
     if (rc) return rc;
     const dim3 grid((unsigned)blocks, (unsigned)(a.gmode == 0 && a.k_per_split > 0 ? (a.K + a.k_per_split - 1) / a.k_per_split : 1));
@@ -453,6 +469,20 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     if (ta == TA_ && tb == TB_ && epi == EPI_)                                                          \
         rc = vec ? launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st) : launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st); \
     else
+#define ASCA_GEMM_SMALL(TA_, TB_)                                                                       \
+    if (ta == TA_ && tb == TB_)                                                                         \
+        rc = launch_gemm_t<TA_, TB_, EPI_STORE, true, 1, 2>(a, grid, st);                               \
+    else
+    if (wm == 1) {
+        ASCA_GEMM_SMALL(0, 0)
+        ASCA_GEMM_SMALL(1, 0)
+        ASCA_GEMM_SMALL(0, 1)
+        ASCA_GEMM_SMALL(1, 1)
+        rc = fail(ASCA_ERR_UNSUPPORTED, "%s: no kernel for this variant", name);
+        if (rc) return rc;
+        return post_launch(name);
+    }
+#undef ASCA_GEMM_SMALL
     ASCA_GEMM_CASE(0, 0, EPI_STORE)
     ASCA_GEMM_CASE(1, 0, EPI_STORE)
     ASCA_GEMM_CASE(0, 1, EPI_STORE)

@@ -29,7 +29,8 @@ from ._lib import AscaError
 
 ARCH = "gfx950"
 KERNELS = ("delta_fwd", "delta_bwd", "delta_states", "delta_decode", "rmsnorm", "rmsnorm_bwd", "adamw",
-           "hash_route", "gather_rows", "scatter_rows", "colsum", "cross_entropy", "gemm", "moe_fwd", "moe_bwd")
+           "hash_route", "gather_rows", "scatter_rows", "colsum", "cross_entropy", "gemm", "moe_fwd", "moe_bwd",
+           "chunk_fwd", "chunk_bwd", "model_train_step")
 DEFAULT_MIN_FLOPS = 4_000_000
 
 _f32 = np.float32
@@ -228,6 +229,26 @@ def param_moments(key) -> tuple[np.ndarray, np.ndarray] | None:
 def reset_param_cache() -> None:
     """rust/src/cuda/mod.rs:50-55."""
     _param_dev.clear()
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even."""
+    b = np.ascontiguousarray(x, dtype=_f32).view(np.uint32)
+    return ((b + (0x7FFF + ((b >> 16) & 1))) >> 16).astype(np.uint16)
+
+
+def from_bf16(x: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 (exact)."""
+    return (np.ascontiguousarray(x, dtype=np.uint16).astype(np.uint32) << 16).view(_f32)
+
+
+class ChunkDev:
+    """Chunked-form forward state on the device: the workspace holding the
+    unit-major inputs and every per-chunk intermediate the backward reads."""
+
+    def __init__(self, ws, batch, seq, n_heads, dh, chunk):
+        self.ws = ws
+        self.batch, self.seq, self.n_heads, self.dh, self.chunk = batch, seq, n_heads, dh, chunk
 
 
 # --------------------------------------------------------------------- Gpu
@@ -532,6 +553,47 @@ class Gpu:
                           bdb2.to_host((d,)), bdx.to_host((t_len, d)))
         finally:
             for b in (bdo, bdx, bdw1, bdb1, bdw2, bdb2, bws):
+                b.free()
+
+    # -- chunked form ---------------------------------------------------------
+    def delta_chunked(self, q, k, v, alpha, beta, batch: int, seq: int, n_heads: int, dh: int, chunk: int = 64):
+        """Forward of the chunked (WY/UT) form (docs/SPEC_V2.md:50-69) on bf16
+        q, k, v (uint16 bit patterns, or float32 rounded to bf16 here) and f32
+        gates; returns (o f32, ChunkDev)."""
+        d, t_len = n_heads * dh, batch * seq
+        bf = [x if x.dtype == np.uint16 else to_bf16(x) for x in (q, k, v)]
+        for name, m in zip("qkv", bf):
+            if m.shape != (t_len, d):
+                raise ValueError(f"delta_chunked: {name} has shape {m.shape}, expected {(t_len, d)}")
+        wsb = C.c_size_t()
+        _lib.call("asca_chunk_ws_bytes", batch, seq, n_heads, dh, chunk, C.byref(wsb))
+        ins = [DevBuf.from_array(x) for x in bf]
+        ga, gb = DevBuf.from_host(alpha), DevBuf.from_host(beta)
+        ws, out = DevBuf(wsb.value), DevBuf(t_len * d * 4)
+        try:
+            _lib.call("asca_chunk_fwd", *[_vp(x) for x in ins], _vp(ga), _vp(gb), _vp(out), _vp(ws), batch, seq,
+                      n_heads, dh, chunk, None)
+            _lib.call("asca_sync")
+            o = out.to_host((t_len, d))
+        finally:
+            for x in (*ins, ga, gb, out):
+                x.free()
+        return o, ChunkDev(ws, batch, seq, n_heads, dh, chunk)
+
+    def delta_chunked_bwd(self, dev: ChunkDev, d_o):
+        """Raw gradients (dq, dk, dv, dalpha, dbeta) of the chunked form given
+        dO (bf16 bit patterns or float32 rounded to bf16)."""
+        B, T, H, dh, Cc = dev.batch, dev.seq, dev.n_heads, dev.dh, dev.chunk
+        t_len, d = B * T, H * dh
+        x = d_o if d_o.dtype == np.uint16 else to_bf16(d_o)
+        bdo = DevBuf.from_array(x)
+        outs = [DevBuf(t_len * d * 4) for _ in range(3)] + [DevBuf(t_len * H * 4) for _ in range(2)]
+        try:
+            _lib.call("asca_chunk_bwd", _vp(bdo), _vp(dev.ws), *[_vp(o) for o in outs], B, T, H, dh, Cc, None)
+            _lib.call("asca_sync")
+            return tuple([o.to_host((t_len, d)) for o in outs[:3]] + [o.to_host((t_len, H)) for o in outs[3:]])
+        finally:
+            for b in (bdo, *outs):
                 b.free()
 
     # -- decode -------------------------------------------------------------

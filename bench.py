@@ -244,6 +244,105 @@ def bench_decode(args):
     print(json.dumps(result), flush=True)
 
 
+def bench_chunk(args):
+    """chunked (WY/UT) delta-rule fwd+BPTT, chunk 64, B=8, T=4096,
+    H=16, dh=128; q, k, v, dO in bf16 (q, k L2-normalised first), gates f32;
+    inputs from the reference Rng in the order of configs[0] (seed 0, the
+    config states none)."""
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf, to_bf16
+
+    B, T, H, dh, Cc, seed = 8, 4096, 16, 128, 64, 0
+    g = gpu.gpu()
+    if g is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    x = synth_inputs(B, T, H, dh, seed)
+    bf = {n: to_bf16(x[n]) for n in ("q", "k", "v", "d_o")}
+    dev = {n: DevBuf.from_array(a) for n, a in bf.items()}
+    da, db = DevBuf.from_host(x["alpha"]), DevBuf.from_host(x["beta"])
+    wsb = C.c_size_t()
+    _lib.call("asca_chunk_ws_bytes", B, T, H, dh, Cc, C.byref(wsb))
+    ws = DevBuf(wsb.value)
+    o = DevBuf(B * T * H * dh * 4)
+    grads = [DevBuf(B * T * H * dh * 4) for _ in range(3)] + [DevBuf(B * T * H * 4) for _ in range(2)]
+    tm = Timer()
+    sp = C.c_void_p(tm.stream)
+
+    def fwd():
+        _lib.call("asca_chunk_fwd", C.c_void_p(dev["q"].ptr), C.c_void_p(dev["k"].ptr), C.c_void_p(dev["v"].ptr),
+                  C.c_void_p(da.ptr), C.c_void_p(db.ptr), C.c_void_p(o.ptr), C.c_void_p(ws.ptr), B, T, H, dh, Cc, sp)
+
+    def bwd():
+        _lib.call("asca_chunk_bwd", C.c_void_p(dev["d_o"].ptr), C.c_void_p(ws.ptr),
+                  *[C.c_void_p(b.ptr) for b in grads], B, T, H, dh, Cc, sp)
+
+    K = args.steps or 10
+    W = min(args.warmup, 3)
+    print(f"bench chunk: {gpu.describe()}; B{B} T{T} H{H} dh{dh} C{Cc}; ws {wsb.value / 2**30:.2f} GiB; "
+          f"warmup {W}, steps {K}", flush=True)
+    for _ in range(W):
+        fwd()
+        bwd()
+    tm.sync()
+    ev = [tm.event() for _ in range(3)]
+    f_ms = b_ms = 0.0
+    t0 = time.perf_counter()
+    for _ in range(K):
+        tm.record(ev[0])
+        fwd()
+        tm.record(ev[1])
+        bwd()
+        tm.record(ev[2])
+        tm.sync()
+        f_ms += tm.elapsed(ev[0], ev[1])
+        b_ms += tm.elapsed(ev[1], ev[2])
+    wall = time.perf_counter() - t0
+    tm.destroy(*ev)
+    f_ms /= K
+    b_ms /= K
+    tokens = B * T
+    flops = 24 * dh * dh * B * T * H  # 18 C d^2 + 12 C^2 d per chunk = 24 d^2 per token-head at C = d/2
+    step_ms = f_ms + b_ms
+    achieved = flops / (step_ms * 1e-3)
+    result = {
+        "metric": "chunked delta fwd+BPTT tokens/s (configs[2]: B8 T4096 H16 dh128, chunk 64, bf16 in, f32 acc)",
+        "value": round(tokens * K / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 in / f32 MFMA",
+        "data": f"synthetic (reference Rng stream, configs[0] distributions, seed {seed}), bf16-rounded",
+        "config": {"workload": "chunked delta-rule fwd+BPTT (asca_chunk_fwd + asca_chunk_bwd)", "B": B, "T": T,
+                   "H": H, "dh": dh, "chunk": Cc},
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_F32 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32, 4), "traffic": None, "kernel": "step",
+                     "algorithmic_flops": flops},
+        "kernels_ms": {"chunk_fwd": round(f_ms, 3), "chunk_bwd": round(b_ms, 3)},
+    }
+    if not args.no_cpu:
+        from oracle import pyoracle as orc
+        from asca_amd.gpu import from_bf16
+
+        # the recurrent CPU path on one sequence x 4 heads of the same bf16-rounded inputs
+        Hs = 4
+        cols = slice(0, Hs * dh)
+        sub = {n: np.ascontiguousarray(from_bf16(bf[n][:T, cols])) for n in ("q", "k", "v", "d_o")}
+        a, bt = (np.ascontiguousarray(x[n][:T, :Hs]) for n in ("alpha", "beta"))
+        t1 = time.perf_counter()
+        orc.delta_fwd_bwd(sub["q"], sub["k"], sub["v"], a, bt, sub["d_o"], 1, T, Hs, dh, nthreads=Hs)
+        el = time.perf_counter() - t1
+        result["cpu_baseline"] = {
+            "value": round(T * Hs / H / el, 1), "unit": "tokens/s", "cores": Hs, "kind": "port",
+            "sample": f"oracle recurrent fwd+BPTT (scan_cpu + bptt_cpu restatement) on 1 sequence x {Hs} of "
+                      f"the {H} heads (one thread per head), {el:.1f} s; tokens/s scaled to all {H} heads"}
+    print(json.dumps(result), flush=True)
+
+
 TRAIN_CFG = dict(V=256, d=512, H=8, L=8, E=16, dff=1024, B=16, T=1024, seed=2)
 
 
@@ -348,8 +447,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train"],
-                    help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]; train: configs[3]")
+    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train", "chunk"],
+                    help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]; train: configs[3]; "
+                         "chunk: configs[2]")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib", action="store_true",
                     help="also run the known-size copy kernel (for counter calibration)")
@@ -364,6 +464,9 @@ def main():
         return
     if args.workload == "train":
         bench_train(args)
+        return
+    if args.workload == "chunk":
+        bench_chunk(args)
         return
     if args.steps is None:
         args.steps = 100

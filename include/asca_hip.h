@@ -324,6 +324,29 @@ ASCA_API int asca_moe_bwd(const float* xn, const float* w1, const float* w2, con
                           float* dw1, float* db1, float* dw2, float* db2, float* dpre_ws, int accumulate,
                           void* stream);
 
+/* ------------------------------------------- delta rule (chunked form) -- */
+
+/* The chunked (WY/UT-transform) form of the same recurrence, specified but not
+ * implemented by the reference (docs/SPEC_V2.md:50-69): chunks of C steps,
+ * per chunk T = (I + strict_tril(diag(beta)(Gamma o K K^T)))^-1,
+ * U = T diag(beta)(V - diag(gamma) K S), O = diag(gamma) Q S + tril(Gamma o Q K^T) U,
+ * S' = gamma_C S + (diag(Gamma[C-1,:]) K)^T U, with every product on the
+ * matrix cores (f32 MFMA) batched over chunks, and the state carried across
+ * chunks by one d x d product per chunk.  Same results as asca_delta_fwd /
+ * asca_delta_bwd_raw (DeltaBlock::scan_cpu / bptt_cpu, rust/src/delta.rs:244-334,
+ * 475-587) up to f32 rounding.
+ *   q, k, v, d_o : (B*T, H*dh) bf16 (raw 16-bit patterns); alpha, beta : (B*T, H) f32
+ *   o, dq, dk, dv : (B*T, H*dh) f32; dalpha, dbeta : (B*T, H) f32 (raw, not logits)
+ *   1 <= C <= 64; dh a multiple of 4, at most 256.
+ *   ws : asca_chunk_ws_bytes bytes; the forward leaves in it what the backward
+ *   needs (call asca_chunk_bwd with the forward's ws). */
+ASCA_API int asca_chunk_ws_bytes(int B, int T, int H, int dh, int C, size_t* bytes);
+ASCA_API int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* alpha,
+                            const float* beta, float* o, void* ws, int B, int T, int H, int dh, int C,
+                            void* stream);
+ASCA_API int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha,
+                            float* dbeta, int B, int T, int H, int dh, int C, void* stream);
+
 /* ----------------------------------------------------- training step -- */
 
 /* A device-resident ASCA model (rust/src/model.rs:528-802): parameters,

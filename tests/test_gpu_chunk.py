@@ -1,0 +1,50 @@
+"""GPU parity of the chunked (WY/UT) form (asca_chunk_fwd / asca_chunk_bwd)
+against the recurrent CPU oracle (the reference's scan_cpu / bptt_cpu
+restatement) on the same bf16-rounded inputs, as configs[2] prescribes.
+
+Bars: forward <= 2e-5 and every raw gradient <= 1e-4 as max|gpu-cpu|/max|cpu|
+(rust/src/main.rs:1021-1029).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 2e-5
+GRAD_TOL = 1e-4
+
+
+def _check(orc, g, seed, B, T, H, dh, C, tag):
+    from asca_amd.gpu import from_bf16, to_bf16
+
+    print(f"[chunk] {tag} B={B} T={T} H={H} dh={dh} C={C}", flush=True)
+    x = orc.DeltaInputs(seed, B, T, H, dh)
+    qb, kb, vb, db_ = (to_bf16(a) for a in (x.q, x.k, x.v, x.d_o))
+    q, k, v, d_o = (np.ascontiguousarray(from_bf16(a)) for a in (qb, kb, vb, db_))
+    o_ref, dq, dk, dv, da, dbt = orc.delta_fwd_bwd(q, k, v, x.alpha, x.beta, d_o, B, T, H, dh)
+    o, dev = g.delta_chunked(qb, kb, vb, x.alpha, x.beta, B, T, H, dh, C)
+    errs = {"o": orc.rel_err(o, o_ref)}
+    got = g.delta_chunked_bwd(dev, db_)
+    for name, a, ref in zip(("dq", "dk", "dv", "dalpha", "dbeta"), got, (dq, dk, dv, da, dbt)):
+        errs[name] = orc.rel_err(a, ref)
+    print(f"[chunk] {tag} rel errors " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    assert errs["o"] <= FWD_TOL, errs
+    for kk in errs:
+        assert errs[kk] <= GRAD_TOL, (kk, errs)
+
+
+@pytest.mark.parametrize("B,T,H,dh,C", [
+    (4, 128, 4, 32, 64),    # configs[0] shape
+    (2, 100, 2, 64, 64),    # ragged last chunk
+    (2, 70, 3, 16, 16),     # small chunks
+    (1, 256, 2, 128, 64),   # configs[2] head size
+    (1, 5, 1, 8, 64),       # one short chunk
+    (2, 96, 2, 128, 32),
+])
+def test_chunked_matches_recurrent(orc, g, B, T, H, dh, C):
+    _check(orc, g, 40 + T, B, T, H, dh, C, "shape")
+
+
+def test_chunked_config2_full_size(orc, g):
+    # B=8, T=4096, H=16, dh=128, chunk 64, bf16 inputs, seed 0
+    _check(orc, g, 0, 8, 4096, 16, 128, 64, "configs[2]")
