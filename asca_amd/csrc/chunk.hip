@@ -123,17 +123,24 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
 
 ASCA_DEV float bf16_to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
-// token-major bf16 (B*T, H*dh) -> unit-major f32 [u][Tp][dh], zero padding
+// token-major bf16 (B*T, H*dh) -> unit-major f32 [u][Tp][dh], zero padding;
+// four elements per thread (dh % 4 == 0), 32-bit indices (sizes checked)
 __global__ __launch_bounds__(256) void ck_in_k(const uint16_t* __restrict__ src, float* __restrict__ dst, int T,
-                                               int H, int dh, int Tp, long total) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    const int j = (int)(i % dh);
-    const long r = i / dh;
-    const int t = (int)(r % Tp);
-    const long u = r / Tp;
-    const long b = u / H, h = u % H;
-    dst[i] = t < T ? bf16_to_f32(src[(b * T + t) * (long)H * dh + h * dh + j]) : 0.0f;
+                                               int H, int dh, int Tp, int total4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= total4) return;
+    const int q4 = dh >> 2;
+    const int j = 4 * (i % q4);
+    const int r = i / q4;
+    const int t = r % Tp, u = r / Tp;
+    const int b = u / H, h = u - b * H;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < T) {
+        const uint2 x = *reinterpret_cast<const uint2*>(src + ((size_t)(b * T + t) * H + h) * dh + j);
+        v = make_float4(__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
+                        __uint_as_float(x.y & 0xffff0000u));
+    }
+    reinterpret_cast<float4*>(dst)[i] = v;
 }
 
 // gates (B*T, H) -> unit-major [u][Tp]; padding steps are identities (alpha 1, beta 0)
@@ -201,27 +208,27 @@ __global__ __launch_bounds__(256) void ck_gamma_k(const float* __restrict__ al, 
     }
 }
 
-// Per chunk (one wave, thread = column): L from A, Gamma, beta; T = (I + L)^-1
-// by forward substitution down each column; M = tril(Gamma o B).
-__global__ __launch_bounds__(64) void ck_tri_k(const float* __restrict__ Am, const float* __restrict__ Bm,
-                                               const float* __restrict__ Gam, const float* __restrict__ be, int C,
-                                               float* __restrict__ Tm, float* __restrict__ Mm) {
+// Per chunk: L from A, Gamma, beta (all 256 threads, four rows at a time);
+// T = (I + L)^-1 by forward substitution down each column (thread = column);
+// M = tril(Gamma o B).
+__global__ __launch_bounds__(256) void ck_tri_k(const float* __restrict__ Am, const float* __restrict__ Bm,
+                                                const float* __restrict__ Gam, const float* __restrict__ be, int C,
+                                                float* __restrict__ Tm, float* __restrict__ Mm) {
     __shared__ float L[64][65];
     __shared__ float Tc[64][65];
     const long n = blockIdx.x;
-    const int m = threadIdx.x;
-    const float* A = Am + n * C * C;
-    const float* Bq = Bm + n * C * C;
-    const float* G = Gam + n * C * C;
+    const int tid = threadIdx.x, m = tid & 63, r4 = tid >> 6;
+    const long cc = n * C * C;
     if (m < C) {
-        for (int j = 0; j < C; ++j) {
-            const float g = G[j * C + m];
-            L[j][m] = m < j ? be[n * C + j] * (g * A[j * C + m]) : 0.0f;
-            Mm[n * C * C + j * C + m] = m <= j ? g * Bq[j * C + m] : 0.0f;
+        for (int j = r4; j < C; j += 4) {
+            const long o = cc + (long)j * C + m;
+            const float g = Gam[o];
+            L[j][m] = m < j ? be[n * C + j] * (g * Am[o]) : 0.0f;
+            Mm[o] = m <= j ? g * Bm[o] : 0.0f;
         }
     }
     __syncthreads();
-    if (m < C) {
+    if (tid < C) {
         for (int j = 0; j < C; ++j) {
             float t;
             if (j < m) {
@@ -229,14 +236,21 @@ __global__ __launch_bounds__(64) void ck_tri_k(const float* __restrict__ Am, con
             } else if (j == m) {
                 t = 1.0f;
             } else {
-                float s = 0.0f;
-                for (int i = m; i < j; ++i) s += L[j][i] * Tc[i][m];
-                t = -s;
+                float s0 = 0.0f, s1 = 0.0f;
+                int i = m;
+                for (; i + 1 < j; i += 2) {
+                    s0 += L[j][i] * Tc[i][m];
+                    s1 += L[j][i + 1] * Tc[i + 1][m];
+                }
+                if (i < j) s0 += L[j][i] * Tc[i][m];
+                t = -(s0 + s1);
             }
             Tc[j][m] = t;
-            Tm[n * C * C + j * C + m] = t;
         }
     }
+    __syncthreads();
+    if (m < C)
+        for (int j = r4; j < C; j += 4) Tm[cc + (long)j * C + m] = Tc[j][m];
 }
 
 // G'[n] += gamma_C[n] I  (the GEMM wrote -Kt^T W)
@@ -249,25 +263,32 @@ __global__ __launch_bounds__(256) void ck_diag_k(float* __restrict__ Gp, const f
     Gp[n * (long)dh * dh + (long)j * dh + j] += gC[n];
 }
 
-// unit-major [u][Tp][w] -> token-major (B*T, H*w), dropping the padding
+// unit-major [u][Tp][w] -> token-major (B*T, H*w), dropping the padding (w % 4 == 0)
 __global__ __launch_bounds__(256) void ck_out_k(const float* __restrict__ src, float* __restrict__ dst, int T, int H,
-                                                int w, int Tp, long total) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;  // over token-major elements
-    if (i >= total) return;
-    const int col = (int)(i % ((long)H * w));
-    const long row = i / ((long)H * w);
-    const long b = row / T;
-    const int t = (int)(row % T);
-    const int h = col / w, j = col % w;
-    dst[i] = src[((b * H + h) * Tp + t) * (long)w + j];
+                                                int w, int Tp, int total4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;  // float4 index over token-major elements
+    if (i >= total4) return;
+    const int hw4 = (H * w) >> 2;
+    const int col = 4 * (i % hw4);
+    const int row = i / hw4;
+    const int b = row / T, t = row - b * T;
+    const int h = col / w, j = col - h * w;
+    reinterpret_cast<float4*>(dst)[i] =
+        *reinterpret_cast<const float4*>(src + ((size_t)(b * H + h) * Tp + t) * w + j);
 }
 
-// rows scaled: out[n][t][:] = s[n*C + t] * in[n][t][:]
+// rows scaled: out[n][t][:] = s[n*C + t] * in[n][t][:]  (dh % 4 == 0)
 __global__ __launch_bounds__(256) void ck_rowscale_k(const float* __restrict__ in, const float* __restrict__ s,
-                                                     float* __restrict__ out, int dh, long total) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    out[i] = s[i / dh] * in[i];
+                                                     float* __restrict__ out, int dh, int total4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= total4) return;
+    const float f = s[i / (dh >> 2)];
+    float4 v = reinterpret_cast<const float4*>(in)[i];
+    v.x *= f;
+    v.y *= f;
+    v.z *= f;
+    v.w *= f;
+    reinterpret_cast<float4*>(out)[i] = v;
 }
 
 // Per chunk: the C x C gradient terms and the scalar gradients.
@@ -287,6 +308,7 @@ __global__ __launch_bounds__(256) void ck_bwd_scalars_k(
     __shared__ float yv[64], zk[64], op[64], kk[64], dg[64], red[4];
     __shared__ float R[64][65];
     __shared__ float dAl[64][65];
+    __shared__ float Pb[64][65];
     const long n = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const long cd = n * C * dh, cc = n * C * C;
@@ -319,43 +341,52 @@ __global__ __launch_bounds__(256) void ck_bwd_scalars_k(
     if (lane == 0) red[w] = f;
     __syncthreads();
     const float fro = (red[0] + red[1]) + (red[2] + red[3]);
-    // C x C terms: thread = column i (first C threads), rows j
-    if (tid < C) {
-        const int i = tid;
-        for (int j = 0; j < C; ++j) {
-            const long o = cc + (long)j * C + i;
-            const float g = Gam[o], dm = i <= j ? dMr[o] : 0.0f;
-            const float dl = i < j ? -dLs[o] : 0.0f;
-            const float bj = be[n * C + j];
-            GdM[o] = g * dm;
-            dAl[j][i] = dl * bj * g;
-            float dG = dm * Bm[o] + dl * bj * Am[o];
-            if (j == C - 1) dG += kk[i];
-            R[j][i] = i < j ? dG * g : 0.0f;
+    // C x C terms, four rows at a time: thread (i = tid & 63, rows j = tid >> 6 + 4k)
+    {
+        const int i = tid & 63;
+        if (i < C) {
+            for (int j = tid >> 6; j < C; j += 4) {
+                const long o = cc + (long)j * C + i;
+                const float g = Gam[o], dm = i <= j ? dMr[o] : 0.0f;
+                const float dl = i < j ? -dLs[o] : 0.0f;
+                const float bj = be[n * C + j], a = Am[o];
+                GdM[o] = g * dm;
+                dAl[j][i] = dl * bj * g;
+                float dG = dm * Bm[o] + dl * bj * a;
+                if (j == C - 1) dG += kk[i];
+                R[j][i] = i < j ? dG * g : 0.0f;
+                Pb[j][i] = dl * g * a;  // dbeta row terms
+            }
         }
     }
     __syncthreads();
+    {
+        const int i = tid & 63;
+        if (i < C)
+            for (int j = tid >> 6; j < C; j += 4) dAs[cc + (long)j * C + i] = dAl[j][i] + dAl[i][j];
+    }
     if (tid < C) {
         const int j = tid;
-        // dA + dA^T, row j
-        for (int i = 0; i < C; ++i) dAs[cc + (long)j * C + i] = dAl[j][i] + dAl[i][j];
-        // dbeta_j
         float s = 0.0f;
-        for (int i = 0; i < j; ++i) s += (-dLs[cc + (long)j * C + i]) * Gam[cc + (long)j * C + i] * Am[cc + (long)j * C + i];
+        for (int i = 0; i < j; ++i) s += Pb[j][i];
         const float gj = gam[n * C + j];
         dbe[n * C + j] = yv[j] + gj * zk[j] + s;
         float dgam = be[n * C + j] * zk[j] + op[j];
         if (j == C - 1) dgam += fro;
         dg[j] = dgam * gj;
+        // row j of R becomes its exclusive prefix along i: R[j][m] = sum_{i<m} R[j][i]
+        float run = 0.0f;
+        for (int i2 = 0; i2 < C; ++i2) {
+            const float x = R[j][i2];
+            R[j][i2] = run;
+            run += x;
+        }
     }
     __syncthreads();
     if (tid < C) {
         const int m = tid;
         float s = 0.0f;
-        for (int t = m; t < C; ++t) {
-            s += dg[t];
-            for (int i = 0; i < m; ++i) s += R[t][i];
-        }
+        for (int t = m; t < C; ++t) s += dg[t] + R[t][m];
         dal[n * C + m] = s / al[n * C + m];
     }
 }
@@ -366,19 +397,26 @@ __global__ __launch_bounds__(256) void ck_bwd_out_k(const float* __restrict__ dq
                                                     const float* __restrict__ Y, const float* __restrict__ be,
                                                     const float* __restrict__ gam, const float* __restrict__ gt,
                                                     int T, int H, int dh, int Tp, float* __restrict__ dq,
-                                                    float* __restrict__ dk, float* __restrict__ dv, long total) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    const int col = (int)(i % ((long)H * dh));
-    const long row = i / ((long)H * dh);
-    const long b = row / T;
-    const int t = (int)(row % T);
-    const int h = col / dh, j = col % dh;
-    const long r = (b * H + h) * Tp + t;  // unit-major row
-    const long o = r * dh + j;
-    dq[i] = dqu[o];
-    dk[i] = dku[o] + (be[r] * gam[r]) * Z[o] + gt[r] * dKt[o];
-    dv[i] = be[r] * Y[o];
+                                                    float* __restrict__ dk, float* __restrict__ dv, int total4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= total4) return;
+    const int hw4 = (H * dh) >> 2;
+    const int col = 4 * (i % hw4);
+    const int row = i / hw4;
+    const int b = row / T, t = row - b * T;
+    const int h = col / dh, j = col - h * dh;
+    const int r = (b * H + h) * Tp + t;  // unit-major row
+    const size_t o = (size_t)r * dh + j;
+    const float bg = be[r] * gam[r], g = gt[r], bb = be[r];
+    const float4 zq = *reinterpret_cast<const float4*>(dqu + o);
+    const float4 zk = *reinterpret_cast<const float4*>(dku + o);
+    const float4 zz = *reinterpret_cast<const float4*>(Z + o);
+    const float4 zt = *reinterpret_cast<const float4*>(dKt + o);
+    const float4 zy = *reinterpret_cast<const float4*>(Y + o);
+    reinterpret_cast<float4*>(dq)[i] = zq;
+    reinterpret_cast<float4*>(dk)[i] = make_float4(zk.x + bg * zz.x + g * zt.x, zk.y + bg * zz.y + g * zt.y,
+                                                   zk.z + bg * zz.z + g * zt.z, zk.w + bg * zz.w + g * zt.w);
+    reinterpret_cast<float4*>(dv)[i] = make_float4(bb * zy.x, bb * zy.y, bb * zy.z, bb * zy.w);
 }
 
 __global__ __launch_bounds__(256) void ck_gates_out_k(const float* __restrict__ dal, const float* __restrict__ dbe,
@@ -393,6 +431,143 @@ __global__ __launch_bounds__(256) void ck_gates_out_k(const float* __restrict__ 
     const long r = (b * H + h) * Tp + t;
     da[i] = dal[r];
     db[i] = dbe[r];
+}
+
+// Persistent state scan for dh = 128, one block per (unit, 64-column half):
+//   forward  (TR = false): X_0 = 0,       X_{c+1} = G'_c   X_c + R_c, c = 0 .. NC-2
+//   backward (TR = true):  X_{NC-1} = 0,  X_{c-1} = G'_c^T X_c + R_c, c = NC-1 .. 1
+// X, G', R are [unit][chunk][128][128] row-major.  The block's columns are
+// independent of the other half.  X^T of the block lives in LDS ([col][row],
+// k-contiguous B fragments); G'_c is staged in LDS row-major, read as
+// k-contiguous A fragments (forward) or as mn-contiguous A fragments
+// (backward: the transpose for free), and the next chunk's G' is prefetched
+// into registers during the MFMAs.  Wave w: columns 16 (w & 3) .. +15, rows
+// 64 (w >> 2) .. +63 as four 16 x 16 tiles.
+constexpr int SC_D = 128, SC_LD = SC_D + 4, SC_NT = 512;
+
+template <bool TR>
+__global__ __launch_bounds__(SC_NT) void ck_scan_k(const float* __restrict__ Gp, const float* __restrict__ R,
+                                                   float* __restrict__ X, int NC) {
+    extern __shared__ float4 sc_lds4[];
+    float* As = reinterpret_cast<float*>(sc_lds4);  // [128][132]
+    float* Xt = As + SC_D * SC_LD;                  // [64][132]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const long u = blockIdx.x >> 1;
+    const int col0 = (blockIdx.x & 1) * 64;
+    const long DD = (long)SC_D * SC_D;
+    const float* Gu = Gp + u * NC * DD;
+    const float* Ru = R + u * NC * DD;
+    float* Xu = X + u * NC * DD;
+    const int ny = w & 3, mb = (w >> 2) * 64;
+    const int g4 = lane >> 4, l16 = lane & 15;
+    const int ncol = 16 * ny + l16;  // column within the block's 64
+
+    // the starting slot is zero
+    const int c_first = TR ? NC - 1 : 0;
+    for (int e = tid; e < 64 * SC_D; e += SC_NT) {
+        const int n = e & 63, m = e >> 6;
+        Xt[n * SC_LD + m] = 0.0f;
+        Xu[(long)c_first * DD + (long)m * SC_D + col0 + n] = 0.0f;
+    }
+    if (NC < 2) return;
+    // element (m, n) of this lane in tile x, register r
+    auto row_of = [=](int x, int r) { return TR ? mb + 4 * (4 * g4 + r) + x : mb + 16 * x + 4 * g4 + r; };
+
+    // G' of the next step (128 x 128 / 512 threads = 8 float4 per thread) in
+    // named registers, R of the next step at this lane's 16 output elements
+    float4 p0, p1, p2, p3, p4, p5, p6, p7;
+    float rv[4][4];
+#define SC_LOAD_G(cc)                                                                       \
+    do {                                                                                    \
+        const float4* src_ = reinterpret_cast<const float4*>(Gu + (long)(cc) * DD) + tid;   \
+        p0 = src_[0];                                                                       \
+        p1 = src_[SC_NT];                                                                   \
+        p2 = src_[2 * SC_NT];                                                               \
+        p3 = src_[3 * SC_NT];                                                               \
+        p4 = src_[4 * SC_NT];                                                               \
+        p5 = src_[5 * SC_NT];                                                               \
+        p6 = src_[6 * SC_NT];                                                               \
+        p7 = src_[7 * SC_NT];                                                               \
+    } while (0)
+#define SC_STORE_G(j, pj) \
+    *reinterpret_cast<float4*>(As + ((tid + SC_NT * (j)) >> 5) * SC_LD + 4 * ((tid + SC_NT * (j)) & 31)) = (pj)
+    int c = TR ? NC - 1 : 0;
+    SC_LOAD_G(c);
+    {
+        const float* Rc = Ru + (long)c * DD;
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rv[x][r] = Rc[(long)row_of(x, r) * SC_D + col0 + ncol];
+    }
+    for (int s = 0; s < NC - 1; ++s) {
+        const int cn = TR ? c - 1 : c + 1;  // output slot
+        __syncthreads();                     // previous step's readers of As are done
+        SC_STORE_G(0, p0);
+        SC_STORE_G(1, p1);
+        SC_STORE_G(2, p2);
+        SC_STORE_G(3, p3);
+        SC_STORE_G(4, p4);
+        SC_STORE_G(5, p5);
+        SC_STORE_G(6, p6);
+        SC_STORE_G(7, p7);
+        __syncthreads();  // As and Xt ready
+        f32x4 acc[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) acc[x] = f32x4{rv[x][0], rv[x][1], rv[x][2], rv[x][3]};
+        {
+            // prefetch the next step (the last step re-reads its own chunk, unused)
+            const int cl = s + 1 < NC - 1 ? cn : c;
+            SC_LOAD_G(cl);
+            const float* Rc = Ru + (long)cl * DD;
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rv[x][r] = Rc[(long)row_of(x, r) * SC_D + col0 + ncol];
+        }
+#pragma unroll
+        for (int h = 0; h < SC_D / 16; ++h) {
+            float fa[4][4];
+            if constexpr (!TR) {
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    const float4 v = *reinterpret_cast<const float4*>(As + (mb + 16 * x + l16) * SC_LD + 16 * h + 4 * g4);
+                    fa[0][x] = v.x;
+                    fa[1][x] = v.y;
+                    fa[2][x] = v.z;
+                    fa[3][x] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v = *reinterpret_cast<const float4*>(As + (16 * h + 4 * g4 + q) * SC_LD + mb + 4 * l16);
+                    fa[q][0] = v.x;
+                    fa[q][1] = v.y;
+                    fa[q][2] = v.z;
+                    fa[q][3] = v.w;
+                }
+            }
+            const float4 b = *reinterpret_cast<const float4*>(Xt + ncol * SC_LD + 16 * h + 4 * g4);
+            const float fb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int x = 0; x < 4; ++x) acc[x] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[q][x], fb[q], acc[x], 0, 0, 0);
+        }
+        __syncthreads();  // every wave has read Xt
+        float* Xn = Xu + (long)cn * DD;
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = row_of(x, r);
+                Xt[ncol * SC_LD + m] = acc[x][r];
+                Xn[(long)m * SC_D + col0 + ncol] = acc[x][r];
+            }
+        c = cn;
+    }
+#undef SC_LOAD_G
+#undef SC_STORE_G
 }
 
 // zero one d x d slot per unit: base[u * us + off + e], e < dd
@@ -436,6 +611,9 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
     if (B < 0 || T < 0 || H < 0) return fail(ASCA_ERR_INVALID, "chunked: negative shape");
     if (C < 1 || C > 64) return fail(ASCA_ERR_UNSUPPORTED, "chunked: chunk %d outside 1..64", C);
     if (dh < 4 || dh > 256 || dh % 4) return fail(ASCA_ERR_UNSUPPORTED, "chunked: dh=%d (multiple of 4, 4..256)", dh);
+    const ChunkDims d = chunk_dims(B, T, H, dh, C);
+    if (d.U * d.Tp * dh >= (1L << 31) || d.N * d.DD >= (1L << 31) || (long)B * T * H * dh >= (1L << 31))
+        return fail(ASCA_ERR_UNSUPPORTED, "chunked: tensors beyond 2^31 elements");
     return ASCA_OK;
 }
 
@@ -447,6 +625,42 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
         rc_ = post_launch(name);                                  \
         if (rc_) return rc_;                                      \
     } while (0)
+
+// The state scan over chunks: the persistent kernel for dh = 128, else one
+// batched GEMM launch per chunk.
+static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, float* X, hipStream_t st) {
+    const long us = (long)d.NC * d.DD;
+    if (d.dh == SC_D) {
+        constexpr size_t lds = (size_t)(SC_D + 64) * SC_LD * sizeof(float);
+        static bool attr[2] = {false, false};
+        const void* fn = tr ? reinterpret_cast<const void*>(&ck_scan_k<true>)
+                            : reinterpret_cast<const void*>(&ck_scan_k<false>);
+        if (!attr[tr]) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+            attr[tr] = true;
+        }
+        int rc = pre_launch("chunk_scan");
+        if (rc) return rc;
+        if (tr)
+            hipLaunchKernelGGL(ck_scan_k<true>, dim3((unsigned)(2 * d.U)), dim3(SC_NT), lds, st, Gp, R, X, d.NC);
+        else
+            hipLaunchKernelGGL(ck_scan_k<false>, dim3((unsigned)(2 * d.U)), dim3(SC_NT), lds, st, Gp, R, X, d.NC);
+        return post_launch("chunk_scan");
+    }
+    const int first = tr ? d.NC - 1 : 0;
+    CK_LAUNCH("chunk_zero", ck_zero_slot_k, dim3(nblk(d.U * d.DD)), dim3(256), X, us, (long)first * d.DD, d.DD,
+              d.U * d.DD);
+    for (int s = 0; s + 1 < d.NC; ++s) {
+        const int c = tr ? d.NC - 1 - s : s;
+        const long oc = (long)c * d.DD;
+        float* out = X + (tr ? oc - d.DD : oc + d.DD);
+        int rc = bgemm(tr ? 1 : 0, 0, d.dh, d.dh, d.dh, 1.f, Gp + oc, d.dh, us, X + oc, d.dh, us, 0.f, out, d.dh, us,
+                       R + oc, us, d.U, st, "chunk_scan");
+        if (rc) return rc;
+    }
+    return ASCA_OK;
+}
 
 }  // namespace asca
 
@@ -471,10 +685,10 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     const ChunkDims d = chunk_dims(B, T, H, dh, C);
     const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws));
     const hipStream_t st = as_stream(stream);
-    const long tot_in = d.U * d.Tp * dh;
-    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in)), dim3(256), q, w.Qu, T, H, dh, d.Tp, tot_in);
-    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in)), dim3(256), k, w.Ku, T, H, dh, d.Tp, tot_in);
-    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in)), dim3(256), v, w.Vu, T, H, dh, d.Tp, tot_in);
+    const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
+    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), q, w.Qu, T, H, dh, d.Tp, tot_in4);
+    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), k, w.Ku, T, H, dh, d.Tp, tot_in4);
+    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), v, w.Vu, T, H, dh, d.Tp, tot_in4);
     CK_LAUNCH("chunk_gates_in", ck_gates_in_k, dim3(nblk(d.U * d.Tp)), dim3(256), alpha, beta, w.al, w.be, T, H, d.Tp,
               d.U * d.Tp);
     // per-chunk state-independent parts
@@ -486,7 +700,7 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
         return rc;
     CK_LAUNCH("chunk_gamma", ck_gamma_k, dim3((unsigned)d.N), dim3(256), w.al, w.be, w.Qu, w.Ku, w.Vu, C, dh, w.gam,
               w.gt, w.gC, w.Gam, w.Vb, w.Kbg, w.Kt, w.Qg);
-    CK_LAUNCH("chunk_tri", ck_tri_k, dim3((unsigned)d.N), dim3(64), w.Am, w.Bm, w.Gam, w.be, C, w.Tm, w.Mm);
+    CK_LAUNCH("chunk_tri", ck_tri_k, dim3((unsigned)d.N), dim3(256), w.Am, w.Bm, w.Gam, w.be, C, w.Tm, w.Mm);
     if ((rc = bgemm(0, 0, C, dh, C, 1.f, w.Tm, C, d.CC, w.Vb, dh, d.CD, 0.f, w.Uv, dh, d.CD, nullptr, 0, d.N, st,
                     "chunk_Uv")) ||
         (rc = bgemm(0, 0, C, dh, C, 1.f, w.Tm, C, d.CC, w.Kbg, dh, d.CD, 0.f, w.W, dh, d.CD, nullptr, 0, d.N, st,
@@ -500,22 +714,15 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
         return rc;
     CK_LAUNCH("chunk_diag", ck_diag_k, dim3(nblk(d.N * dh)), dim3(256), w.Gp, w.gC, dh, d.N * dh);
     // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
-    const long us = (long)d.NC * d.DD;  // per-unit stride of per-chunk d x d blocks
-    CK_LAUNCH("chunk_zero", ck_zero_slot_k, dim3(nblk(d.U * d.DD)), dim3(256), w.S, us, 0L, d.DD, d.U * d.DD);
-    for (int c = 0; c + 1 < d.NC; ++c) {
-        const long oc = (long)c * d.DD;
-        if ((rc = bgemm(0, 0, dh, dh, dh, 1.f, w.Gp + oc, dh, us, w.S + oc, dh, us, 0.f, w.S + oc + d.DD, dh, us,
-                        w.H + oc, us, d.U, st, "chunk_scan")))
-            return rc;
-    }
+    if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
     // outputs: O = Qp S + M Uv
     if ((rc = bgemm(0, 0, C, dh, dh, 1.f, w.Qp, dh, d.CD, w.S, dh, d.DD, 0.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
                     "chunk_O1")) ||
         (rc = bgemm(0, 0, C, dh, C, 1.f, w.Mm, C, d.CC, w.Uv, dh, d.CD, 1.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
                     "chunk_O2")))
         return rc;
-    const long tot_out = (long)B * T * H * dh;
-    CK_LAUNCH("chunk_out", ck_out_k, dim3(nblk(tot_out)), dim3(256), w.Ou, o, T, H, dh, d.Tp, tot_out);
+    const int tot_out4 = (int)((long)B * T * H * dh / 4);
+    CK_LAUNCH("chunk_out", ck_out_k, dim3(nblk(tot_out4)), dim3(256), w.Ou, o, T, H, dh, d.Tp, tot_out4);
     return ASCA_OK;
 }
 
@@ -529,22 +736,14 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
     const ChunkDims d = chunk_dims(B, T, H, dh, C);
     const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws));
     const hipStream_t st = as_stream(stream);
-    const long tot_in = d.U * d.Tp * dh;
-    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in);
-    CK_LAUNCH("chunk_rowscale", ck_rowscale_k, dim3(nblk(tot_in)), dim3(256), w.dOu, w.gam, w.dOg, dh, tot_in);
+    const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
+    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in4);
+    CK_LAUNCH("chunk_rowscale", ck_rowscale_k, dim3(nblk(tot_in4)), dim3(256), w.dOu, w.gam, w.dOg, dh, tot_in4);
     // E_c = Qp^T dO_c; reverse scan dS'_{c-1} = G'_c^T dS'_c + E_c, dS'_{NC-1} = 0
     if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N, st,
                     "chunk_E")))
         return rc;
-    const long us = (long)d.NC * d.DD;
-    CK_LAUNCH("chunk_zero", ck_zero_slot_k, dim3(nblk(d.U * d.DD)), dim3(256), w.dSp, us, (long)(d.NC - 1) * d.DD,
-              d.DD, d.U * d.DD);
-    for (int c = d.NC - 1; c >= 1; --c) {
-        const long oc = (long)c * d.DD;
-        if ((rc = bgemm(1, 0, dh, dh, dh, 1.f, w.Gp + oc, dh, us, w.dSp + oc, dh, us, 0.f, w.dSp + oc - d.DD, dh, us,
-                        w.E + oc, us, d.U, st, "chunk_scan_bwd")))
-            return rc;
-    }
+    if ((rc = scan(true, d, w.Gp, w.E, w.dSp, st))) return rc;
     // per-chunk gradients
     const long N = d.N, CD = d.CD, CC = d.CC, DD = d.DD;
     if ((rc = bgemm(0, 0, C, dh, dh, -1.f, w.W, dh, CD, w.S, dh, DD, 0.f, w.Uu, dh, CD, w.Uv, CD, N, st, "chunk_U")) ||
@@ -581,9 +780,9 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
         (rc = bgemm(0, 0, C, dh, C, 1.f, w.dAs, C, CC, w.Ku, dh, CD, 1.f, w.dku, dh, CD, nullptr, 0, N, st,
                     "chunk_dk2")))
         return rc;
-    const long tot_out = (long)B * T * H * dh;
-    CK_LAUNCH("chunk_bwd_out", ck_bwd_out_k, dim3(nblk(tot_out)), dim3(256), w.dqu, w.dku, w.Z, w.dKt, w.Y, w.be,
-              w.gam, w.gt, T, H, dh, d.Tp, dq, dk, dv, tot_out);
+    const int tot_out4 = (int)((long)B * T * H * dh / 4);
+    CK_LAUNCH("chunk_bwd_out", ck_bwd_out_k, dim3(nblk(tot_out4)), dim3(256), w.dqu, w.dku, w.Z, w.dKt, w.Y, w.be,
+              w.gam, w.gt, T, H, dh, d.Tp, dq, dk, dv, tot_out4);
     const long tot_g = (long)B * T * H;
     CK_LAUNCH("chunk_gates_out", ck_gates_out_k, dim3(nblk(tot_g)), dim3(256), w.dal, w.dbe, T, H, d.Tp, dalpha, dbeta,
               tot_g);
