@@ -626,6 +626,334 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
         if (rc_) return rc_;                                      \
     } while (0)
 
+// ---------------------------------------------------------------- fused prep
+// One block per chunk for C = 64, dh = 128: everything of a chunk that does
+// not depend on the state, with the chunk's operands in LDS and every product
+// on the matrix cores through wave_mm.  It writes the same workspace arrays as
+// the separate kernels above (the backward reads them), so both paths are
+// interchangeable.
+constexpr int FP_C = 64, FP_D = 128, FP_LK = FP_D + 4, FP_LC = FP_C + 4, FP_NT = 512;
+constexpr int FP_LDS_F = 3 * FP_C * FP_LK + 2 * FP_C * FP_LC + 5 * FP_C;
+
+// acc[TM][TN] (16 x 16 tiles at rows m0 + 16x, columns n0 + 16y) += op(A) op(B)
+// over k in [k_lo, k_hi) (a multiple of 16), operands in LDS.  A element
+// (m, k) is A[m*lda + k] if AK (contiguous in k, read four k at once) else
+// A[k*lda + m]; B element (k, n) is B[n*ldb + k] if BK else B[k*ldb + n];
+// optional per-k scales sa[k], sb[k].  Within each 16-k block lane l feeds k =
+// 4(l/16) + s at step s of v_mfma_f32_16x16x4_f32 (any order of k gives the
+// same sum), so both operands' four k come from one 16-byte read when
+// contiguous.
+template <int TM, int TN, bool AK, bool BK, bool SA, bool SB>
+ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const float* A, int lda, const float* sa,
+                      const float* B, int ldb, const float* sb, int m0, int n0, int lane) {
+    const int li = lane & 15, kq = lane >> 4;
+    for (int kb = k_lo; kb < k_hi; kb += 16) {
+        const int k = kb + 4 * kq;
+        f32x4 a[TM], b[TN];
+#pragma unroll
+        for (int x = 0; x < TM; ++x) {
+            const int m = m0 + 16 * x + li;
+            if (AK) {
+                a[x] = *reinterpret_cast<const f32x4*>(A + m * lda + k);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) a[x][s] = A[(k + s) * lda + m];
+            }
+            if (SA) a[x] *= *reinterpret_cast<const f32x4*>(sa + k);
+        }
+#pragma unroll
+        for (int y = 0; y < TN; ++y) {
+            const int nn = n0 + 16 * y + li;
+            if (BK) {
+                b[y] = *reinterpret_cast<const f32x4*>(B + nn * ldb + k);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) b[y][s] = B[(k + s) * ldb + nn];
+            }
+            if (SB) b[y] *= *reinterpret_cast<const f32x4*>(sb + k);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int x = 0; x < TM; ++x)
+#pragma unroll
+                for (int y = 0; y < TN; ++y)
+                    acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[x][s], b[y][s], acc[x][y], 0, 0, 0);
+    }
+}
+
+template <int TM, int TN>
+ASCA_DEV void acc_zero(f32x4 (&acc)[TM][TN]) {
+#pragma unroll
+    for (int x = 0; x < TM; ++x)
+#pragma unroll
+        for (int y = 0; y < TN; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// 64 x 128 bf16 rows of one chunk -> LDS f32 [t][f] (stride FP_LK) and, if
+// gdst is set, the unit-major f32 copy; rows past T are zero.  tid counts from
+// 0 over the nthr threads taking part.
+ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, float* __restrict__ gdst, long rowbase,
+                           long rowstride, int valid_rows, int tid, int nthr) {
+    for (int e = tid; e < FP_C * FP_D / 4; e += nthr) {
+        const int t = e >> 5, f = 4 * (e & 31);
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < valid_rows) {
+            const uint2 r = *reinterpret_cast<const uint2*>(src + rowbase + (long)t * rowstride + f);
+            x = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                            __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+        }
+        *reinterpret_cast<float4*>(lds + t * FP_LK + f) = x;
+        if (gdst) *reinterpret_cast<float4*>(gdst + t * FP_D + f) = x;
+    }
+}
+
+// Off-diagonal 16 x 16 block (i, j), i > j, of T = (I + L)^-1 from the blocks
+// already known: T_ij = -T_ii (L[i, j..i) T[j..i, j]), one wave.  Ls holds L,
+// Ts holds T (both stride FP_LC).  The product's accumulator feeds the second
+// product directly as its B operand (lane l, register s = row 4(l/16) + s).
+ASCA_DEV void fp_tri_block(const float* Ls, float* Ts, int i, int j, int lane) {
+    const int li = lane & 15, kq = lane >> 4;
+    f32x4 x[1][1];
+    acc_zero(x);
+    wave_mm<1, 1, true, false, false, false>(x, 16 * j, 16 * i, Ls, FP_LC, nullptr, Ts, FP_LC, nullptr, 16 * i, 16 * j,
+                                             lane);
+    const f32x4 d = *reinterpret_cast<const f32x4*>(Ts + (16 * i + li) * FP_LC + 16 * i + 4 * kq);
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) y = __builtin_amdgcn_mfma_f32_16x16x4f32(d[s], x[0][0][s], y, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Ts[(16 * i + 4 * kq + r) * FP_LC + 16 * j + li] = -y[r];
+}
+
+__global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                       const uint16_t* __restrict__ v, const float* __restrict__ alpha,
+                                                       const float* __restrict__ beta, int T, int H, int NC, ChunkWs w) {
+    extern __shared__ float4 fp_lds4[];
+    float* const Ks = reinterpret_cast<float*>(fp_lds4);  // K           [64][132]
+    float* const X = Ks + FP_C * FP_LK;                    // Q, then V, then Q
+    float* const Y = X + FP_C * FP_LK;                     // Gamma, then T [64][68]; Uv, then W [64][132]
+    float* const Ls = Y + FP_C * FP_LK;                    // L, then T  [64][68]
+    float* const Ms = Ls + FP_C * FP_LC;                   // M          [64][68]
+    float* const a_s = Ms + FP_C * FP_LC;
+    float* const b_s = a_s + FP_C;
+    float* const g_s = b_s + FP_C;
+    float* const gt_s = g_s + FP_C;
+    float* const bg_s = gt_s + FP_C;
+    float* const Gs = Y;
+    float* const Ts = Y;
+
+    const long n = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = n / NC;
+    const int c = (int)(n - u * NC);
+    const int b = (int)(u / H), h = (int)(u - (long)b * H);
+    const int t0 = c * FP_C;
+    const int valid = min(FP_C, T - t0);
+    const long rowbase = ((long)b * T + t0) * H * FP_D + (long)h * FP_D;
+    const long rowstride = (long)H * FP_D;
+    const long cd = n * FP_C * FP_D, cc = n * FP_C * FP_C, dd = n * FP_D * FP_D;
+
+    // gates (padding steps are identities), K and Q
+    if (tid < FP_C) {
+        const bool in = tid < valid;
+        const long gi = ((long)b * T + t0 + tid) * H + h;
+        a_s[tid] = in ? alpha[gi] : 1.0f;
+        b_s[tid] = in ? beta[gi] : 0.0f;
+        w.al[n * FP_C + tid] = a_s[tid];
+        w.be[n * FP_C + tid] = b_s[tid];
+    }
+    fp_load_rows(k, Ks, w.Ku + cd, rowbase, rowstride, valid, tid, FP_NT);
+    fp_load_rows(q, X, w.Qu + cd, rowbase, rowstride, valid, tid, FP_NT);
+    __syncthreads();
+    // gamma (one thread), Gamma by columns (first wave)
+    if (tid == 0) {
+        float g = 1.0f;
+        for (int t = 0; t < FP_C; ++t) {
+            g *= a_s[t];
+            g_s[t] = g;
+        }
+    }
+    if (tid < FP_C) {
+        const int i = tid;
+        float x = 1.0f;
+        for (int t = 0; t < FP_C; ++t) {
+            if (t > i) x *= a_s[t];
+            const float val = t >= i ? x : 0.0f;
+            Gs[t * FP_LC + i] = val;
+            w.Gam[cc + t * FP_C + i] = val;
+        }
+        gt_s[i] = x;
+    }
+    __syncthreads();
+    if (tid < FP_C) {
+        w.gam[n * FP_C + tid] = g_s[tid];
+        w.gt[n * FP_C + tid] = gt_s[tid];
+        bg_s[tid] = b_s[tid] * g_s[tid];
+    }
+    if (tid == 0) w.gC[n] = g_s[FP_C - 1];
+    // A = K K^T -> L = strict_tril(beta_j Gamma A);  B = Q K^T -> M = tril(Gamma B)
+    {
+        const int m0 = 16 * (wv >> 1), n0 = 32 * (wv & 1);
+        f32x4 aa[1][2], ab[1][2];
+        acc_zero(aa);
+        acc_zero(ab);
+        wave_mm<1, 2, true, true, false, false>(aa, 0, FP_D, Ks, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<1, 2, true, true, false, false>(ab, 0, FP_D, X, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = m0 + 4 * l4 + r, i = n0 + 16 * y + li;
+                const float g = Gs[j * FP_LC + i];
+                const float va = aa[0][y][r], vb = ab[0][y][r];
+                w.Am[cc + j * FP_C + i] = va;
+                w.Bm[cc + j * FP_C + i] = vb;
+                Ls[j * FP_LC + i] = i < j ? b_s[j] * (g * va) : 0.0f;
+                const float mv = i <= j ? g * vb : 0.0f;
+                Ms[j * FP_LC + i] = mv;
+                w.Mm[cc + j * FP_C + i] = mv;
+            }
+    }
+    __syncthreads();
+    // T = (I + L)^-1 into Ts.  First wave: the four 16 x 16 diagonal blocks,
+    // lane = (block, column), the column in registers, right-looking forward
+    // substitution.  The other waves zero the blocks above the diagonal, bring
+    // V in where Q was and write Kt = Gamma[C-1, :] K.
+    if (wv == 0) {
+        const int o = 16 * l4, m = li;
+        float d[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[r] = r == m ? 1.0f : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 15; ++jj)
+#pragma unroll
+            for (int r = jj + 1; r < 16; ++r) d[r] -= Ls[(o + r) * FP_LC + o + jj] * d[jj];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Ts[(o + r) * FP_LC + o + m] = d[r];
+    } else {
+        const int t2 = tid - 64;
+        for (int e = t2; e < 6 * 256; e += FP_NT - 64) {  // blocks (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+            const int blk = e >> 8, bi = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
+            const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
+            Ts[(16 * bi + ((e >> 4) & 15)) * FP_LC + 16 * bj + (e & 15)] = 0.0f;
+        }
+        fp_load_rows(v, X, w.Vu + cd, rowbase, rowstride, valid, t2, FP_NT - 64);
+        for (int e = t2; e < FP_C * FP_D / 4; e += FP_NT - 64) {
+            const int t = e >> 5, f = 4 * (e & 31);
+            float4 x = *reinterpret_cast<const float4*>(Ks + t * FP_LK + f);
+            const float gg = gt_s[t];
+            x.x *= gg;
+            x.y *= gg;
+            x.z *= gg;
+            x.w *= gg;
+            *reinterpret_cast<float4*>(w.Kt + cd + t * FP_D + f) = x;
+        }
+    }
+    __syncthreads();
+    // the blocks below the diagonal, one block diagonal at a time
+    if (wv < 3) fp_tri_block(Ls, Ts, wv + 1, wv, lane);
+    __syncthreads();
+    if (wv < 2) fp_tri_block(Ls, Ts, wv + 2, wv, lane);
+    __syncthreads();
+    if (wv == 0) fp_tri_block(Ls, Ts, 3, 0, lane);
+    __syncthreads();
+    for (int e = tid; e < FP_C * FP_C; e += FP_NT) {
+        const float t = Ts[(e >> 6) * FP_LC + (e & 63)];
+        Ls[(e >> 6) * FP_LC + (e & 63)] = t;
+        w.Tm[cc + e] = t;
+    }
+    __syncthreads();
+    // Uv = T diag(beta) V  -> Y and the workspace
+    {
+        const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
+        f32x4 acc[2][2];
+        acc_zero(acc);
+        wave_mm<2, 2, true, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, X, FP_LK, b_s, m0, n0, lane);
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                    Y[t * FP_LK + f] = acc[x][y][r];
+                    w.Uv[cd + t * FP_D + f] = acc[x][y][r];
+                }
+    }
+    __syncthreads();
+    // H = Kt^T Uv
+    {
+        const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
+        f32x4 acc[2][4];
+        acc_zero(acc);
+        wave_mm<2, 4, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 4; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                    w.H[dd + a * FP_D + f] = acc[x][y][r];
+                }
+    }
+    __syncthreads();
+    // W = T diag(beta gamma) K -> Y; Q back into X
+    {
+        const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
+        f32x4 acc[2][2];
+        acc_zero(acc);
+        wave_mm<2, 2, true, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, Ks, FP_LK, bg_s, m0, n0, lane);
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                    Y[t * FP_LK + f] = acc[x][y][r];
+                    w.W[cd + t * FP_D + f] = acc[x][y][r];
+                }
+        fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
+    }
+    __syncthreads();
+    // G' = gamma_C I - Kt^T W
+    {
+        const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
+        f32x4 acc[2][4];
+        acc_zero(acc);
+        wave_mm<2, 4, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
+        const float gC = g_s[FP_C - 1];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 4; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                    w.Gp[dd + a * FP_D + f] = (a == f ? gC : 0.0f) - acc[x][y][r];
+                }
+    }
+    // Qp = diag(gamma) Q - M W
+    {
+        const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
+        f32x4 acc[2][2];
+        acc_zero(acc);
+        wave_mm<2, 2, true, false, false, false>(acc, 0, FP_C, Ms, FP_LC, nullptr, Y, FP_LK, nullptr, m0, n0, lane);
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                    w.Qp[cd + t * FP_D + f] = g_s[t] * X[t * FP_LK + f] - acc[x][y][r];
+                }
+    }
+}
+
 // The state scan over chunks: the persistent kernel for dh = 128, else one
 // batched GEMM launch per chunk.
 static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, float* X, hipStream_t st) {
@@ -662,6 +990,22 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
     return ASCA_OK;
 }
 
+// The state scan and the outputs O = Qp S + M Uv.
+static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, float* o, hipStream_t st) {
+    const int C = d.C, dh = d.dh;
+    int rc;
+    // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
+    if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
+    if ((rc = bgemm(0, 0, C, dh, dh, 1.f, w.Qp, dh, d.CD, w.S, dh, d.DD, 0.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
+                    "chunk_O1")) ||
+        (rc = bgemm(0, 0, C, dh, C, 1.f, w.Mm, C, d.CC, w.Uv, dh, d.CD, 1.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
+                    "chunk_O2")))
+        return rc;
+    const int tot_out4 = (int)((long)d.B * d.T * d.H * dh / 4);
+    CK_LAUNCH("chunk_out", ck_out_k, dim3(nblk(tot_out4)), dim3(256), w.Ou, o, d.T, d.H, dh, d.Tp, tot_out4);
+    return ASCA_OK;
+}
+
 }  // namespace asca
 
 using namespace asca;
@@ -685,6 +1029,23 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     const ChunkDims d = chunk_dims(B, T, H, dh, C);
     const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws));
     const hipStream_t st = as_stream(stream);
+    if (C == FP_C && dh == FP_D) {
+        // one fused kernel for every state-independent part of every chunk
+        constexpr size_t lds = (size_t)FP_LDS_F * sizeof(float);
+        static bool attr = false;
+        if (!attr) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_fwd_prep_k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+            attr = true;
+        }
+        rc = pre_launch("chunk_fwd_prep");
+        if (rc) return rc;
+        hipLaunchKernelGGL(ck_fwd_prep_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, alpha, beta, T, H,
+                           d.NC, w);
+        if ((rc = post_launch("chunk_fwd_prep"))) return rc;
+        return chunk_fwd_tail(d, w, o, st);
+    }
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), q, w.Qu, T, H, dh, d.Tp, tot_in4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), k, w.Ku, T, H, dh, d.Tp, tot_in4);
@@ -713,17 +1074,7 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
                     "chunk_H")))
         return rc;
     CK_LAUNCH("chunk_diag", ck_diag_k, dim3(nblk(d.N * dh)), dim3(256), w.Gp, w.gC, dh, d.N * dh);
-    // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
-    if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
-    // outputs: O = Qp S + M Uv
-    if ((rc = bgemm(0, 0, C, dh, dh, 1.f, w.Qp, dh, d.CD, w.S, dh, d.DD, 0.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
-                    "chunk_O1")) ||
-        (rc = bgemm(0, 0, C, dh, C, 1.f, w.Mm, C, d.CC, w.Uv, dh, d.CD, 1.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
-                    "chunk_O2")))
-        return rc;
-    const int tot_out4 = (int)((long)B * T * H * dh / 4);
-    CK_LAUNCH("chunk_out", ck_out_k, dim3(nblk(tot_out4)), dim3(256), w.Ou, o, T, H, dh, d.Tp, tot_out4);
-    return ASCA_OK;
+    return chunk_fwd_tail(d, w, o, st);
 }
 
 int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha, float* dbeta, int B,

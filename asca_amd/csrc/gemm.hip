@@ -303,6 +303,143 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
     }
 }
 
+// Persistent batched products (gmode 3, plain epilogue): a block walks work
+// items (batch g, tile tm, tn) with a stride of gridDim.x and the k-tile
+// pipeline runs across item boundaries, so the first k-tile of the next item
+// loads while the last one of the current item is multiplied.  The per-chunk
+// products of the chunked delta rule are small (K = 64 or 128), and as one
+// block per product each paid its whole load latency up front.
+template <bool TA, bool TB, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_batched_k(
+    GemmArgs p) {
+    constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 64 * WN;
+    constexpr bool A_KC = !TA, B_KC = TB;
+    constexpr int A_F = tile_floats<A_KC, BM>();
+    constexpr int B_F = tile_floats<B_KC, BN>();
+    extern __shared__ float4 lds4[];
+    float* lds = reinterpret_cast<float*>(lds4);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = (w / WN) * 64, wn = (w % WN) * 64;
+    const int per = p.tiles_m * p.tiles_n;
+    const long items = (long)p.ngroups * per;
+    const int nk = (p.K + GM_BK - 1) / GM_BK;  // the host guarantees K > 0
+    long item = blockIdx.x;
+    if (item >= items) return;
+
+    long g = item / per;
+    int m0 = (int)(item % per) / p.tiles_n * BM, n0 = (int)(item % per) % p.tiles_n * BN;
+    const float* A = p.A + g * p.a_gs;
+    const float* B = p.B + g * p.b_gs;
+    float4 ra[8 * BM / NT], rb[8 * BN / NT];
+    tile_load<A_KC, true, BM, NT>(ra, A, p.lda, nullptr, 0, m0, p.M - m0, 0, p.K, tid);
+    tile_load<B_KC, true, BN, NT>(rb, B, p.ldb, nullptr, 0, n0, p.N - n0, 0, p.K, tid);
+    tile_store<A_KC, BM, NT>(ra, lds, tid);
+    tile_store<B_KC, BN, NT>(rb, lds + A_F, tid);
+    __syncthreads();
+    int it = 0;  // k-iterations so far (LDS buffer parity)
+    for (;;) {
+        const long next = item + gridDim.x;
+        const bool has_next = next < items;
+        const long gn = has_next ? next / per : g;
+        const int rn = has_next ? (int)(next % per) : 0;
+        const int m0n = rn / p.tiles_n * BM, n0n = rn % p.tiles_n * BN;
+        const float* An = p.A + gn * p.a_gs;
+        const float* Bn = p.B + gn * p.b_gs;
+        f32x4 acc[4][4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < nk; ++kt, ++it) {
+            const float* As = lds + (it & 1) * (A_F + B_F);
+            const float* Bs = As + A_F;
+            const bool more = kt + 1 < nk || has_next;
+            if (kt + 1 < nk) {
+                const long k0 = (long)(kt + 1) * GM_BK;
+                tile_load<A_KC, true, BM, NT>(ra, A, p.lda, nullptr, 0, m0, p.M - m0, k0, p.K - k0, tid);
+                tile_load<B_KC, true, BN, NT>(rb, B, p.ldb, nullptr, 0, n0, p.N - n0, k0, p.K - k0, tid);
+            } else if (has_next) {
+                tile_load<A_KC, true, BM, NT>(ra, An, p.lda, nullptr, 0, m0n, p.M - m0n, 0, p.K, tid);
+                tile_load<B_KC, true, BN, NT>(rb, Bn, p.ldb, nullptr, 0, n0n, p.N - n0n, 0, p.K, tid);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float fa[4][4], fb[4][4];
+                frag_read<A_KC, BM>(fa, As, wm, h, lane);
+                frag_read<B_KC, BN>(fb, Bs, wn, h, lane);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+#pragma unroll
+                        for (int y = 0; y < 4; ++y)
+                            acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][x], fb[s][y], acc[x][y], 0, 0, 0);
+            }
+            if (more) {
+                float* Ns = lds + ((it + 1) & 1) * (A_F + B_F);
+                tile_store<A_KC, BM, NT>(ra, Ns, tid);
+                tile_store<B_KC, BN, NT>(rb, Ns + A_F, tid);
+            }
+            __syncthreads();
+        }
+        // epilogue of this item: C = alpha acc + bias + beta C + resid
+        float* C = p.C + g * p.c_gs;
+        const float* bias = p.bias ? p.bias + g * p.bias_gs : nullptr;
+        const float* resid = p.resid ? p.resid + g * p.r_gs : nullptr;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 4 * (lane >> 4) + r;
+                const int m = m0 + wm + (A_KC ? 16 * x + tr : 4 * tr + x);
+                if (m >= p.M) continue;
+                float* Cr = C + (long)m * p.ldc;
+                const float* Rr = resid ? resid + (long)m * p.ld_resid : nullptr;
+                if constexpr (!B_KC) {
+                    const int n = n0 + wn + 4 * (lane & 15);
+                    if (n >= p.N) continue;
+                    float o[4];
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) {
+                        float a = p.alpha * acc[x][y][r];
+                        if (n + y < p.N) {
+                            if (bias) a += bias[n + y];
+                            if (p.beta != 0.0f) a += p.beta * Cr[n + y];
+                            if (Rr) a += Rr[n + y];
+                        }
+                        o[y] = a;
+                    }
+                    if (n + 3 < p.N) {
+                        *reinterpret_cast<float4*>(Cr + n) = make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+#pragma unroll
+                        for (int y = 0; y < 4; ++y)
+                            if (n + y < p.N) Cr[n + y] = o[y];
+                    }
+                } else {
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) {
+                        const int n = n0 + wn + 16 * y + (lane & 15);
+                        if (n >= p.N) continue;
+                        float a = p.alpha * acc[x][y][r];
+                        if (bias) a += bias[n];
+                        if (p.beta != 0.0f) a += p.beta * Cr[n];
+                        if (Rr) a += Rr[n];
+                        Cr[n] = a;
+                    }
+                }
+            }
+        }
+        if (!has_next) break;
+        item = next;
+        g = gn;
+        m0 = m0n;
+        n0 = n0n;
+        A = An;
+        B = Bn;
+    }
+}
+
 // Split-K reduction: C = alpha * sum_s part[s] + bias + beta * C (deterministic order).
 __global__ __launch_bounds__(256) void splitk_reduce_k(const float* __restrict__ part, int splits, long MN, int N,
                                                        float* __restrict__ C, long ldc, float alpha, float beta,
@@ -431,6 +568,24 @@ static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+template <bool TA, bool TB, int WM, int WN>
+static int launch_batched_t(const GemmArgs& a, long items, hipStream_t st) {
+    constexpr size_t lds =
+        2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 64 * WN>()) * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_batched_k<TA, TB, WM, WN>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr = true;
+    }
+    // two resident blocks per CU, each walking items with a grid stride
+    const long cap = 2L * (cu_count() > 0 ? cu_count() : 256);
+    const unsigned grid = (unsigned)(items < cap ? items : cap);
+    hipLaunchKernelGGL((gemm_batched_k<TA, TB, WM, WN>), dim3(grid), dim3(64 * WM * WN), lds, st, a);
+    return ASCA_OK;
+}
+
 // Validates and launches one (possibly grouped) GEMM.  `m_total`: for gmode 1,
 // the total rows over all groups (bounds the grid).
 int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t st, const char* name) {
@@ -473,6 +628,21 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     if (ta == TA_ && tb == TB_)                                                                         \
         rc = launch_gemm_t<TA_, TB_, EPI_STORE, true, 1, 2>(a, grid, st);                               \
     else
+#define ASCA_GEMM_BATCHED(TA_, TB_)                                                                     \
+    if (ta == TA_ && tb == TB_)                                                                         \
+        rc = wm == 1 ? launch_batched_t<TA_, TB_, 1, 2>(a, blocks, st)                                  \
+                     : launch_batched_t<TA_, TB_, 2, 2>(a, blocks, st);                                 \
+    else
+    if (a.gmode == 3 && vec && a.K > 0) {
+        ASCA_GEMM_BATCHED(0, 0)
+        ASCA_GEMM_BATCHED(1, 0)
+        ASCA_GEMM_BATCHED(0, 1)
+        ASCA_GEMM_BATCHED(1, 1)
+        rc = fail(ASCA_ERR_UNSUPPORTED, "%s: no kernel for this variant", name);
+        if (rc) return rc;
+        return post_launch(name);
+    }
+#undef ASCA_GEMM_BATCHED
     if (wm == 1) {
         ASCA_GEMM_SMALL(0, 0)
         ASCA_GEMM_SMALL(1, 0)
