@@ -635,41 +635,57 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
 constexpr int FP_C = 64, FP_D = 128, FP_LK = FP_D + 4, FP_LC = FP_C + 4, FP_NT = 512;
 constexpr int FP_LDS_F = 3 * FP_C * FP_LK + 2 * FP_C * FP_LC + 5 * FP_C;
 
+// Four k-consecutive elements of an LDS operand at (mn, k .. k+3): element
+// (mn, k) at P[mn*ld + k] if KC (one 8- or 16-byte read) else P[k*ld + mn];
+// BF: the operand is stored as bf16 (exact for bf16 inputs), else f32.
+template <bool KC, bool BF>
+ASCA_DEV f32x4 lds_frag(const void* P, int ld, int mn, int k) {
+    f32x4 r;
+    if constexpr (BF) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(P);
+        if constexpr (KC) {
+            const uint2 x = *reinterpret_cast<const uint2*>(p + mn * ld + k);
+            r = f32x4{__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
+                      __uint_as_float(x.y & 0xffff0000u)};
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) r[s] = __uint_as_float((uint32_t)p[(k + s) * ld + mn] << 16);
+        }
+    } else {
+        const float* p = reinterpret_cast<const float*>(P);
+        if constexpr (KC) {
+            r = *reinterpret_cast<const f32x4*>(p + mn * ld + k);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) r[s] = p[(k + s) * ld + mn];
+        }
+    }
+    return r;
+}
+
 // acc[TM][TN] (16 x 16 tiles at rows m0 + 16x, columns n0 + 16y) += op(A) op(B)
 // over k in [k_lo, k_hi) (a multiple of 16), operands in LDS.  A element
-// (m, k) is A[m*lda + k] if AK (contiguous in k, read four k at once) else
-// A[k*lda + m]; B element (k, n) is B[n*ldb + k] if BK else B[k*ldb + n];
+// (m, k) is A[m*lda + k] if AK (contiguous in k) else A[k*lda + m]; B element
+// (k, n) is B[n*ldb + k] if BK else B[k*ldb + n]; AB / BB: bf16 storage;
 // optional per-k scales sa[k], sb[k].  Within each 16-k block lane l feeds k =
 // 4(l/16) + s at step s of v_mfma_f32_16x16x4_f32 (any order of k gives the
-// same sum), so both operands' four k come from one 16-byte read when
-// contiguous.
-template <int TM, int TN, bool AK, bool BK, bool SA, bool SB>
-ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const float* A, int lda, const float* sa,
-                      const float* B, int ldb, const float* sb, int m0, int n0, int lane) {
+// same sum), so an operand contiguous in k is one 8- or 16-byte read.
+template <int TM, int TN, bool AK, bool AB, bool BK, bool BB, bool SA = false, bool SB = false>
+ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const void* A, int lda, const float* sa,
+                      const void* B, int ldb, const float* sb, int m0, int n0, int lane) {
     const int li = lane & 15, kq = lane >> 4;
+#pragma unroll 2
     for (int kb = k_lo; kb < k_hi; kb += 16) {
         const int k = kb + 4 * kq;
         f32x4 a[TM], b[TN];
 #pragma unroll
         for (int x = 0; x < TM; ++x) {
-            const int m = m0 + 16 * x + li;
-            if (AK) {
-                a[x] = *reinterpret_cast<const f32x4*>(A + m * lda + k);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) a[x][s] = A[(k + s) * lda + m];
-            }
+            a[x] = lds_frag<AK, AB>(A, lda, m0 + 16 * x + li, k);
             if (SA) a[x] *= *reinterpret_cast<const f32x4*>(sa + k);
         }
 #pragma unroll
         for (int y = 0; y < TN; ++y) {
-            const int nn = n0 + 16 * y + li;
-            if (BK) {
-                b[y] = *reinterpret_cast<const f32x4*>(B + nn * ldb + k);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) b[y][s] = B[(k + s) * ldb + nn];
-            }
+            b[y] = lds_frag<BK, BB>(B, ldb, n0 + 16 * y + li, k);
             if (SB) b[y] *= *reinterpret_cast<const f32x4*>(sb + k);
         }
 #pragma unroll
@@ -716,7 +732,7 @@ ASCA_DEV void fp_tri_block(const float* Ls, float* Ts, int i, int j, int lane) {
     const int li = lane & 15, kq = lane >> 4;
     f32x4 x[1][1];
     acc_zero(x);
-    wave_mm<1, 1, true, false, false, false>(x, 16 * j, 16 * i, Ls, FP_LC, nullptr, Ts, FP_LC, nullptr, 16 * i, 16 * j,
+    wave_mm<1, 1, true, false, false, false, false, false>(x, 16 * j, 16 * i, Ls, FP_LC, nullptr, Ts, FP_LC, nullptr, 16 * i, 16 * j,
                                              lane);
     const f32x4 d = *reinterpret_cast<const f32x4*>(Ts + (16 * i + li) * FP_LC + 16 * i + 4 * kq);
     f32x4 y = {0.f, 0.f, 0.f, 0.f};
@@ -799,8 +815,8 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         f32x4 aa[1][2], ab[1][2];
         acc_zero(aa);
         acc_zero(ab);
-        wave_mm<1, 2, true, true, false, false>(aa, 0, FP_D, Ks, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
-        wave_mm<1, 2, true, true, false, false>(ab, 0, FP_D, X, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<1, 2, true, false, true, false, false, false>(aa, 0, FP_D, Ks, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<1, 2, true, false, true, false, false, false>(ab, 0, FP_D, X, FP_LK, nullptr, Ks, FP_LK, nullptr, m0, n0, lane);
 #pragma unroll
         for (int y = 0; y < 2; ++y)
 #pragma unroll
@@ -870,7 +886,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
         f32x4 acc[2][2];
         acc_zero(acc);
-        wave_mm<2, 2, true, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, X, FP_LK, b_s, m0, n0, lane);
+        wave_mm<2, 2, true, false, false, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, X, FP_LK, b_s, m0, n0, lane);
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -888,7 +904,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
         f32x4 acc[2][4];
         acc_zero(acc);
-        wave_mm<2, 4, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<2, 4, false, false, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -905,7 +921,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
         f32x4 acc[2][2];
         acc_zero(acc);
-        wave_mm<2, 2, true, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, Ks, FP_LK, bg_s, m0, n0, lane);
+        wave_mm<2, 2, true, false, false, false, false, true>(acc, 0, FP_C, Ls, FP_LC, nullptr, Ks, FP_LK, bg_s, m0, n0, lane);
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -924,7 +940,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
         f32x4 acc[2][4];
         acc_zero(acc);
-        wave_mm<2, 4, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<2, 4, false, false, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
         const float gC = g_s[FP_C - 1];
 #pragma unroll
         for (int x = 0; x < 2; ++x)
@@ -941,7 +957,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
         f32x4 acc[2][2];
         acc_zero(acc);
-        wave_mm<2, 2, true, false, false, false>(acc, 0, FP_C, Ms, FP_LC, nullptr, Y, FP_LK, nullptr, m0, n0, lane);
+        wave_mm<2, 2, true, false, false, false, false, false>(acc, 0, FP_C, Ms, FP_LC, nullptr, Y, FP_LK, nullptr, m0, n0, lane);
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -951,6 +967,387 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
                     const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
                     w.Qp[cd + t * FP_D + f] = g_s[t] * X[t * FP_LK + f] - acc[x][y][r];
                 }
+    }
+}
+
+// ---------------------------------------------------------------- fused backward
+// One block per chunk for C = 64, dh = 128, after the reverse state scan: all
+// per-chunk gradients of q, k, v, alpha, beta, written token-major.  It uses
+//   Z = T^T dW = -Y S^T          (dW = -dU S^T, Y = T^T dU)
+//   dL = -strict_tril(Y Uv^T + Z W^T) = -strict_tril(Y U^T)   (U = Uv - W S)
+//   dO_t . (Q S)_t = Q_t . (dO S^T)_t
+// so neither dW nor Q S is formed.  The 128 x 128 states S and dS' pass through
+// LDS in 64-row halves; K, Q, dO sit in LDS as bf16 (exact: they are bf16
+// inputs).  Wave w owns rows 16 (w >> 1) .. +15 of every C x dh result and the
+// columns 32 (w & 1) + {0, 16} of each 64-column half, so the halves of the
+// state products never leave a wave idle.
+constexpr int FB_LB = FP_D + 8;              // bf16 row stride of the [64][128] bf16 operands
+constexpr int FB_BIG = FP_C * FP_LK;         // f32 [64][132]
+constexpr int FB_SMALL = FP_C * FP_LC;       // f32 [64][68], or bf16 [64][136]
+constexpr int FB_LDS_F = 3 * FB_BIG + 3 * FB_SMALL + 1536;
+
+ASCA_DEV float bf_at(const uint16_t* p, int i) { return __uint_as_float((uint32_t)p[i] << 16); }
+
+ASCA_DEV float sum16(float x) {
+    x += __shfl_xor(x, 1);
+    x += __shfl_xor(x, 2);
+    x += __shfl_xor(x, 4);
+    x += __shfl_xor(x, 8);
+    return x;
+}
+
+// Row partials p[r] of a wave's 16-row strip (row m0 + 4 (lane / 16) + r)
+// summed over the 16 lanes of a row -> dst[row].
+ASCA_DEV void rows_out(const float (&p)[4], float* dst, int m0, int lane) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float x = sum16(p[r]);
+        if ((lane & 15) == 0) dst[m0 + 4 * (lane >> 4) + r] = x;
+    }
+}
+
+// 64 rows x 128 f32 from global (row stride 128) into LDS (row stride FP_LK).
+ASCA_DEV void fb_rows_f32(const float* __restrict__ src, float* dst, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+        *reinterpret_cast<float4*>(dst + r * FP_LK + f) = *reinterpret_cast<const float4*>(src + r * FP_D + f);
+    }
+}
+
+// 64 x 64 f32 (row stride ld_src) into LDS (row stride FP_LC).
+ASCA_DEV void fb_sq_f32(const float* __restrict__ src, int ld_src, float* dst, int tid) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int e = tid + i * FP_NT, r = e >> 4, f = 4 * (e & 15);
+        *reinterpret_cast<float4*>(dst + r * FP_LC + f) = *reinterpret_cast<const float4*>(src + r * ld_src + f);
+    }
+}
+
+// 64 x 128 f32 holding bf16 values -> bf16 LDS (row stride FB_LB).
+ASCA_DEV void fb_rows_bf16(const float* __restrict__ src, uint16_t* dst, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+        const float4 x = *reinterpret_cast<const float4*>(src + r * FP_D + f);
+        *reinterpret_cast<uint2*>(dst + r * FB_LB + f) =
+            make_uint2((__float_as_uint(x.x) >> 16) | (__float_as_uint(x.y) & 0xffff0000u),
+                       (__float_as_uint(x.z) >> 16) | (__float_as_uint(x.w) & 0xffff0000u));
+    }
+}
+
+__global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restrict__ d_o, int T, int H, int NC,
+                                                        ChunkWs w, float* __restrict__ dq, float* __restrict__ dk,
+                                                        float* __restrict__ dv, float* __restrict__ dalpha,
+                                                        float* __restrict__ dbeta) {
+    extern __shared__ float4 fb_lds4[];
+    float* const RA = reinterpret_cast<float*>(fb_lds4);  // S / dS' halves; T; GdM | dA
+    float* const RB = RA + FB_BIG;                         // dS' half; U
+    float* const RC = RB + FB_BIG;                         // dU, then Y
+    float* const RE = RC + FB_BIG;                         // W half; M; R; Q (bf16)
+    uint16_t* const Kb = reinterpret_cast<uint16_t*>(RE + FB_SMALL);
+    uint16_t* const Ob = reinterpret_cast<uint16_t*>(RE + 2 * FB_SMALL);
+    uint16_t* const Qb = reinterpret_cast<uint16_t*>(RE);
+    float* const a_s = RE + 3 * FB_SMALL;
+    float* const b_s = a_s + 64;
+    float* const g_s = b_s + 64;
+    float* const gt_s = g_s + 64;
+    float* const pz = gt_s + 64;  // [2][64] row partials: Z.K
+    float* const pk = pz + 128;   // K.dKt
+    float* const pq = pk + 128;   // Q.(dO S^T)
+    float* const pyv = pq + 128;  // Y.V
+    float* const ppb = pyv + 128; // sum_i dL Gamma A
+    float* const pr = ppb + 128;  // [8][64] partials of the R term of d log alpha
+    float* const dlr = pr + 512;
+    float* const fr = dlr + 64;   // [8]
+
+    const long n = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = n / NC;
+    const int c = (int)(n - u * NC);
+    const int b = (int)(u / H), h = (int)(u - (long)b * H);
+    const int t0 = c * FP_C;
+    const int valid = min(FP_C, T - t0);
+    const long rowbase = ((long)b * T + t0) * H * FP_D + (long)h * FP_D;
+    const long rowstride = (long)H * FP_D;
+    const long cd = n * FP_C * FP_D, cc = n * FP_C * FP_C, dd = n * FP_D * FP_D;
+    const int rm0 = 16 * (wv >> 1), cn0 = 32 * (wv & 1);
+
+    if (tid < FP_C) {
+        a_s[tid] = w.al[n * FP_C + tid];
+        b_s[tid] = w.be[n * FP_C + tid];
+        g_s[tid] = w.gam[n * FP_C + tid];
+        gt_s[tid] = w.gt[n * FP_C + tid];
+    }
+    fb_rows_bf16(w.Ku + cd, Kb, tid);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
+        uint2 x = make_uint2(0u, 0u);
+        if (t < valid) x = *reinterpret_cast<const uint2*>(d_o + rowbase + (long)t * rowstride + f);
+        *reinterpret_cast<uint2*>(Ob + t * FB_LB + f) = x;
+    }
+
+    // ---- U = Uv - W S and dU = diag(gt) K dS' + M^T dO, over the two row halves of S, dS'
+    f32x4 U0[1][2], U1[1][2], D0[1][2], D1[1][2];
+    acc_zero(U0);
+    acc_zero(U1);
+    acc_zero(D0);
+    acc_zero(D1);
+    float fro = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+            const long o = dd + (long)(64 * hh + r) * FP_D + f;
+            const float4 sv = *reinterpret_cast<const float4*>(w.S + o);
+            const float4 gv = *reinterpret_cast<const float4*>(w.dSp + o);
+            *reinterpret_cast<float4*>(RA + r * FP_LK + f) = sv;
+            *reinterpret_cast<float4*>(RB + r * FP_LK + f) = gv;
+            fro += (sv.x * gv.x + sv.y * gv.y) + (sv.z * gv.z + sv.w * gv.w);
+        }
+        fb_sq_f32(w.W + cd + 64 * hh, FP_D, RE, tid);
+        __syncthreads();
+        wave_mm<1, 2, true, false, false, false>(U0, 0, 64, RE, FP_LC, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
+        wave_mm<1, 2, true, false, false, false>(U1, 0, 64, RE, FP_LC, nullptr, RA, FP_LK, nullptr, rm0, 64 + cn0,
+                                                 lane);
+        wave_mm<1, 2, true, true, false, false>(D0, 0, 64, Kb + 64 * hh, FB_LB, nullptr, RB, FP_LK, nullptr, rm0, cn0,
+                                                lane);
+        wave_mm<1, 2, true, true, false, false>(D1, 0, 64, Kb + 64 * hh, FB_LB, nullptr, RB, FP_LK, nullptr, rm0,
+                                                64 + cn0, lane);
+        __syncthreads();
+    }
+    fb_sq_f32(w.Mm + cc, FP_C, RE, tid);
+    fb_sq_f32(w.Tm + cc, FP_C, RA, tid);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float g = gt_s[rm0 + 4 * l4 + r];
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+            D0[0][y][r] *= g;
+            D1[0][y][r] *= g;
+        }
+    }
+    wave_mm<1, 2, false, false, false, true>(D0, 0, 64, RE, FP_LC, nullptr, Ob, FB_LB, nullptr, rm0, cn0, lane);
+    wave_mm<1, 2, false, false, false, true>(D1, 0, 64, RE, FP_LC, nullptr, Ob, FB_LB, nullptr, rm0, 64 + cn0, lane);
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = rm0 + 4 * l4 + r, f = 64 * g2 + cn0 + 16 * y + li;
+                const float pu = g2 ? U1[0][y][r] : U0[0][y][r];
+                RB[t * FP_LK + f] = w.Uv[cd + t * FP_D + f] - pu;
+                RC[t * FP_LK + f] = g2 ? D1[0][y][r] : D0[0][y][r];
+            }
+    __syncthreads();
+
+    // ---- Y = T^T dU; dv = beta Y
+    {
+        f32x4 Y0[1][2], Y1[1][2];
+        acc_zero(Y0);
+        acc_zero(Y1);
+        wave_mm<1, 2, false, false, false, false>(Y0, 0, 64, RA, FP_LC, nullptr, RC, FP_LK, nullptr, rm0, cn0, lane);
+        wave_mm<1, 2, false, false, false, false>(Y1, 0, 64, RA, FP_LC, nullptr, RC, FP_LK, nullptr, rm0, 64 + cn0,
+                                                  lane);
+        float yv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = rm0 + 4 * l4 + r, f = 64 * g2 + cn0 + 16 * y + li;
+                    const float yy = g2 ? Y1[0][y][r] : Y0[0][y][r];
+                    if (t < valid) dv[rowbase + (long)t * rowstride + f] = b_s[t] * yy;
+                    yv[r] += yy * w.Vu[cd + t * FP_D + f];
+                }
+        rows_out(yv, pyv + 64 * (wv & 1), rm0, lane);
+        __syncthreads();  // every read of dU and T is done
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = rm0 + 4 * l4 + r, f = 64 * g2 + cn0 + 16 * y + li;
+                    RC[t * FP_LK + f] = g2 ? Y1[0][y][r] : Y0[0][y][r];
+                }
+    }
+    __syncthreads();
+
+    // ---- dM = tril(dO U^T), dL = -strict_tril(Y U^T) -> GdM, dA (RA), R (RE), row sums of dL Gamma A
+    {
+        f32x4 Mx[1][2], Lx[1][2];
+        acc_zero(Mx);
+        acc_zero(Lx);
+        wave_mm<1, 2, true, true, true, false>(Mx, 0, FP_D, Ob, FB_LB, nullptr, RB, FP_LK, nullptr, rm0, cn0, lane);
+        wave_mm<1, 2, true, false, true, false>(Lx, 0, FP_D, RC, FP_LK, nullptr, RB, FP_LK, nullptr, rm0, cn0, lane);
+        float pb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = rm0 + 4 * l4 + r, i = cn0 + 16 * y + li;
+                const long o = cc + j * FP_C + i;
+                const float g = w.Gam[o], am = w.Am[o], bj = b_s[j];
+                const float dm = i <= j ? Mx[0][y][r] : 0.0f;
+                const float dl = i < j ? -Lx[0][y][r] : 0.0f;
+                RA[j * FP_LK + i] = g * dm;
+                RA[j * FP_LK + 64 + i] = dl * bj * g;
+                const float dG = dm * w.Bm[o] + dl * bj * am;
+                RE[j * FP_LC + i] = i < j ? dG * g : 0.0f;
+                pb[r] += dl * g * am;
+            }
+        rows_out(pb, ppb + 64 * (wv & 1), rm0, lane);
+    }
+    // Q (exact in bf16) staged in registers while R is reduced
+    uint2 qst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+        const float4 x = *reinterpret_cast<const float4*>(w.Qu + cd + r * FP_D + f);
+        qst[i] = make_uint2((__float_as_uint(x.x) >> 16) | (__float_as_uint(x.y) & 0xffff0000u),
+                            (__float_as_uint(x.z) >> 16) | (__float_as_uint(x.w) & 0xffff0000u));
+    }
+    __syncthreads();
+    // R term of d log alpha_m: sum_{t >= m} sum_{i < m} R[t][i]; wave w takes rows 8w .. 8w+7
+    {
+        float acc = 0.0f;
+        for (int t = 8 * wv; t < 8 * wv + 8; ++t) {
+            float sc = RE[t * FP_LC + lane];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(sc, o);
+                if (lane >= o) sc += y;
+            }
+            float ex = __shfl_up(sc, 1);
+            if (lane == 0) ex = 0.0f;
+            if (t >= lane) acc += ex;
+        }
+        pr[wv * 64 + lane] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+        *reinterpret_cast<uint2*>(Qb + r * FB_LB + f) = qst[i];
+    }
+    if (tid < 64) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < 8; ++k2) sacc += pr[k2 * 64 + tid];
+        dlr[tid] = sacc;
+    }
+    __syncthreads();
+
+    // ---- dq = GdM K (+ gamma dO S^T below); dk = GdM^T Q + (dA + dA^T) K (+ beta gamma Z + gt dKt below)
+    f32x4 Q0[1][2], Q1[1][2], K0[1][2], K1[1][2];
+    acc_zero(Q0);
+    acc_zero(Q1);
+    acc_zero(K0);
+    acc_zero(K1);
+    wave_mm<1, 2, true, false, false, true>(Q0, 0, 64, RA, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, cn0, lane);
+    wave_mm<1, 2, true, false, false, true>(Q1, 0, 64, RA, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, 64 + cn0, lane);
+    wave_mm<1, 2, false, false, false, true>(K0, 0, 64, RA, FP_LK, nullptr, Qb, FB_LB, nullptr, rm0, cn0, lane);
+    wave_mm<1, 2, false, false, false, true>(K1, 0, 64, RA, FP_LK, nullptr, Qb, FB_LB, nullptr, rm0, 64 + cn0, lane);
+    wave_mm<1, 2, true, false, false, true>(K0, 0, 64, RA + 64, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, cn0, lane);
+    wave_mm<1, 2, true, false, false, true>(K1, 0, 64, RA + 64, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, 64 + cn0,
+                                            lane);
+    wave_mm<1, 2, false, false, false, true>(K0, 0, 64, RA + 64, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, cn0, lane);
+    wave_mm<1, 2, false, false, false, true>(K1, 0, 64, RA + 64, FP_LK, nullptr, Kb, FB_LB, nullptr, rm0, 64 + cn0,
+                                             lane);
+    __syncthreads();
+
+    // ---- per row half of S and dS': Z = -Y S^T, P = dO S^T, dKt = U dS'^T (columns of that half)
+    float zk[4] = {0.f, 0.f, 0.f, 0.f}, kk[4] = {0.f, 0.f, 0.f, 0.f}, qd[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        fb_rows_f32(w.S + dd + 64 * hh * FP_D, RA, tid);
+        __syncthreads();
+        f32x4 Zx[1][2], Px[1][2], Tx[1][2];
+        acc_zero(Zx);
+        acc_zero(Px);
+        acc_zero(Tx);
+        wave_mm<1, 2, true, false, true, false>(Zx, 0, FP_D, RC, FP_LK, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
+        wave_mm<1, 2, true, true, true, false>(Px, 0, FP_D, Ob, FB_LB, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
+        __syncthreads();
+        fb_rows_f32(w.dSp + dd + 64 * hh * FP_D, RA, tid);
+        __syncthreads();
+        wave_mm<1, 2, true, false, true, false>(Tx, 0, FP_D, RB, FP_LK, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = rm0 + 4 * l4 + r, a = 64 * hh + cn0 + 16 * y + li;
+                const float z = -Zx[0][y][r], pp = Px[0][y][r], dkt = Tx[0][y][r];
+                const float kv = bf_at(Kb, t * FB_LB + a), qv = bf_at(Qb, t * FB_LB + a);
+                zk[r] += z * kv;
+                kk[r] += kv * dkt;
+                qd[r] += qv * pp;
+                const float dqv = g_s[t] * pp, dkv = (b_s[t] * g_s[t]) * z + gt_s[t] * dkt;
+                if (hh) {
+                    Q1[0][y][r] += dqv;
+                    K1[0][y][r] += dkv;
+                } else {
+                    Q0[0][y][r] += dqv;
+                    K0[0][y][r] += dkv;
+                }
+            }
+        __syncthreads();
+    }
+
+    // ---- outputs
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = rm0 + 4 * l4 + r, a = 64 * g2 + cn0 + 16 * y + li;
+                if (t < valid) {
+                    const long o = rowbase + (long)t * rowstride + a;
+                    dq[o] = g2 ? Q1[0][y][r] : Q0[0][y][r];
+                    dk[o] = g2 ? K1[0][y][r] : K0[0][y][r];
+                }
+            }
+    rows_out(zk, pz + 64 * (wv & 1), rm0, lane);
+    rows_out(kk, pk + 64 * (wv & 1), rm0, lane);
+    rows_out(qd, pq + 64 * (wv & 1), rm0, lane);
+    fro = wave_sum(fro);
+    if (lane == 0) fr[wv] = fro;
+    __syncthreads();
+    if (wv == 0) {
+        const int t = lane;
+        const float zkt = pz[t] + pz[64 + t], kkt = pk[t] + pk[64 + t], qdt = pq[t] + pq[64 + t];
+        const float gm = g_s[t];
+        const float dbt = (pyv[t] + pyv[64 + t]) + gm * zkt + (ppb[t] + ppb[64 + t]);
+        float dgam = b_s[t] * zkt + qdt;
+        if (t == FP_C - 1) dgam += ((fr[0] + fr[1]) + (fr[2] + fr[3])) + ((fr[4] + fr[5]) + (fr[6] + fr[7]));
+        // suffix sum over t >= m of dgamma_t gamma_t; exclusive prefix over i < m of gt_i (K.dKt)_i
+        float suf = dgam * gm;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_down(suf, o);
+            if (lane + o < 64) suf += y;
+        }
+        float pre = gt_s[t] * kkt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_up(pre, o);
+            if (lane >= o) pre += y;
+        }
+        float ex = __shfl_up(pre, 1);
+        if (lane == 0) ex = 0.0f;
+        if (t < valid) {
+            const long gi = ((long)b * T + t0 + t) * H + h;
+            dalpha[gi] = (suf + dlr[t] + ex) / a_s[t];
+            dbeta[gi] = dbt;
+        }
     }
 }
 
@@ -1089,6 +1486,25 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
     const hipStream_t st = as_stream(stream);
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in4);
+    if (C == FP_C && dh == FP_D) {
+        // E, the reverse scan, then one fused kernel for all per-chunk gradients
+        if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N,
+                        st, "chunk_E")))
+            return rc;
+        if ((rc = scan(true, d, w.Gp, w.E, w.dSp, st))) return rc;
+        constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
+        static bool attr = false;
+        if (!attr) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_bwd_fused_k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+            attr = true;
+        }
+        if ((rc = pre_launch("chunk_bwd_fused"))) return rc;
+        hipLaunchKernelGGL(ck_bwd_fused_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, d_o, T, H, d.NC, w, dq, dk, dv,
+                           dalpha, dbeta);
+        return post_launch("chunk_bwd_fused");
+    }
     CK_LAUNCH("chunk_rowscale", ck_rowscale_k, dim3(nblk(tot_in4)), dim3(256), w.dOu, w.gam, w.dOg, dh, tot_in4);
     // E_c = Qp^T dO_c; reverse scan dS'_{c-1} = G'_c^T dS'_c + E_c, dS'_{NC-1} = 0
     if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N, st,
