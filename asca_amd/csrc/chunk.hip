@@ -626,6 +626,16 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
         if (rc_) return rc_;                                      \
     } while (0)
 
+// As CK_LAUNCH with dynamic LDS (at most 64 KB: no attribute needed).
+#define CK_LAUNCH_LDS(name, kern, grid, block, lds, ...)             \
+    do {                                                             \
+        int rc_ = pre_launch(name);                                  \
+        if (rc_) return rc_;                                         \
+        hipLaunchKernelGGL(kern, grid, block, lds, st, __VA_ARGS__); \
+        rc_ = post_launch(name);                                     \
+        if (rc_) return rc_;                                         \
+    } while (0)
+
 // ---------------------------------------------------------------- fused prep
 // One block per chunk for C = 64, dh = 128: everything of a chunk that does
 // not depend on the state, with the chunk's operands in LDS and every product
@@ -835,8 +845,9 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     __syncthreads();
     // T = (I + L)^-1 into Ts.  First wave: the four 16 x 16 diagonal blocks,
     // lane = (block, column), the column in registers, right-looking forward
-    // substitution.  The other waves zero the blocks above the diagonal, bring
-    // V in where Q was and write Kt = Gamma[C-1, :] K.
+    // substitution.  The other waves zero the blocks above the diagonal and
+    // bring V in where Q was.  (Kt = Gamma[C-1, :] K is not stored: the fused
+    // backward forms it from K and Gamma[C-1, :].)
     if (wv == 0) {
         const int o = 16 * l4, m = li;
         float d[16];
@@ -856,16 +867,6 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
             Ts[(16 * bi + ((e >> 4) & 15)) * FP_LC + 16 * bj + (e & 15)] = 0.0f;
         }
         fp_load_rows(v, X, w.Vu + cd, rowbase, rowstride, valid, t2, FP_NT - 64);
-        for (int e = t2; e < FP_C * FP_D / 4; e += FP_NT - 64) {
-            const int t = e >> 5, f = 4 * (e & 31);
-            float4 x = *reinterpret_cast<const float4*>(Ks + t * FP_LK + f);
-            const float gg = gt_s[t];
-            x.x *= gg;
-            x.y *= gg;
-            x.z *= gg;
-            x.w *= gg;
-            *reinterpret_cast<float4*>(w.Kt + cd + t * FP_D + f) = x;
-        }
     }
     __syncthreads();
     // the blocks below the diagonal, one block diagonal at a time
@@ -1351,6 +1352,99 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
     }
 }
 
+// ---------------------------------------------------------------- outputs and E
+// O = Qp S + M Uv for one chunk (C = 64, dh = 128), written token-major; and
+// E = Qp^T dO for the reverse scan, reading the bf16 dO directly.  256 threads,
+// 51 KB of LDS (three blocks per CU).
+constexpr int FO_NT = 256;
+constexpr int FO_LDS_F = FP_C * FP_LC + FP_C * FP_LK;
+static_assert(FO_LDS_F * 4 <= 65536 && FP_C * FP_LK + FP_C * FB_LB / 2 <= FO_LDS_F, "LDS of the out / E kernels");
+
+__global__ __launch_bounds__(FO_NT) void ck_out_fused_k(int T, int H, int NC, ChunkWs w, float* __restrict__ o) {
+    extern __shared__ float4 fo_lds4[];
+    float* const QM = reinterpret_cast<float*>(fo_lds4);  // Qp k-half, then M   [64][68]
+    float* const SU = QM + FP_C * FP_LC;                   // S k-half, then Uv   [64][132]
+    const long n = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = n / NC;
+    const int c = (int)(n - u * NC);
+    const int b = (int)(u / H), h = (int)(u - (long)b * H);
+    const int t0 = c * FP_C;
+    const int valid = min(FP_C, T - t0);
+    const long cd = n * FP_C * FP_D, cc = n * FP_C * FP_C, dd = n * FP_D * FP_D;
+    const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
+    f32x4 acc[2][4];
+    acc_zero(acc);
+#pragma unroll
+    for (int ph = 0; ph < 3; ++ph) {
+        const float* a_src = ph < 2 ? w.Qp + cd + 64 * ph : w.Mm + cc;
+        const int a_ld = ph < 2 ? FP_D : FP_C;
+        const float* b_src = ph < 2 ? w.S + dd + 64 * ph * FP_D : w.Uv + cd;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * FO_NT, r = e >> 4, f = 4 * (e & 15);
+            *reinterpret_cast<float4*>(QM + r * FP_LC + f) = *reinterpret_cast<const float4*>(a_src + r * a_ld + f);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + i * FO_NT, r = e >> 5, f = 4 * (e & 31);
+            *reinterpret_cast<float4*>(SU + r * FP_LK + f) = *reinterpret_cast<const float4*>(b_src + r * FP_D + f);
+        }
+        __syncthreads();
+        wave_mm<2, 4, true, false, false, false>(acc, 0, 64, QM, FP_LC, nullptr, SU, FP_LK, nullptr, m0, n0, lane);
+        __syncthreads();
+    }
+    const long rowbase = ((long)b * T + t0) * H * FP_D + (long)h * FP_D;
+    const long rowstride = (long)H * FP_D;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
+                if (t < valid) o[rowbase + (long)t * rowstride + f] = acc[x][y][r];
+            }
+}
+
+__global__ __launch_bounds__(FO_NT) void ck_E_k(const uint16_t* __restrict__ d_o, int T, int H, int NC, ChunkWs w) {
+    extern __shared__ float4 fo_lds4[];
+    float* const Qs = reinterpret_cast<float*>(fo_lds4);                 // Qp [t][a] (stride FP_LK)
+    uint16_t* const Ob = reinterpret_cast<uint16_t*>(Qs + FP_C * FP_LK);  // dO bf16 [t][f] (stride FB_LB)
+    const long n = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = n / NC;
+    const int c = (int)(n - u * NC);
+    const int b = (int)(u / H), h = (int)(u - (long)b * H);
+    const int t0 = c * FP_C;
+    const int valid = min(FP_C, T - t0);
+    const long rowbase = ((long)b * T + t0) * H * FP_D + (long)h * FP_D;
+    const long rowstride = (long)H * FP_D;
+    const long cd = n * FP_C * FP_D, dd = n * FP_D * FP_D;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int e = tid + i * FO_NT, r = e >> 5, f = 4 * (e & 31);
+        *reinterpret_cast<float4*>(Qs + r * FP_LK + f) = *reinterpret_cast<const float4*>(w.Qp + cd + r * FP_D + f);
+        uint2 x = make_uint2(0u, 0u);
+        if (r < valid) x = *reinterpret_cast<const uint2*>(d_o + rowbase + (long)r * rowstride + f);
+        *reinterpret_cast<uint2*>(Ob + r * FB_LB + f) = x;
+    }
+    __syncthreads();
+    const int m0 = 64 * (wv >> 1), n0 = 64 * (wv & 1);
+    f32x4 acc[4][4];
+    acc_zero(acc);
+    wave_mm<4, 4, false, false, false, true>(acc, 0, FP_C, Qs, FP_LK, nullptr, Ob, FB_LB, nullptr, m0, n0, lane);
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                w.E[dd + (m0 + 16 * x + 4 * l4 + r) * FP_D + n0 + 16 * y + li] = acc[x][y][r];
+}
+
 // The state scan over chunks: the persistent kernel for dh = 128, else one
 // batched GEMM launch per chunk.
 static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, float* X, hipStream_t st) {
@@ -1393,6 +1487,11 @@ static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, float* o, hipStr
     int rc;
     // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
     if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
+    if (C == FP_C && dh == FP_D) {
+        CK_LAUNCH_LDS("chunk_out_fused", ck_out_fused_k, dim3((unsigned)d.N), dim3(FO_NT),
+                  (size_t)FO_LDS_F * sizeof(float), d.T, d.H, d.NC, w, o);
+        return ASCA_OK;
+    }
     if ((rc = bgemm(0, 0, C, dh, dh, 1.f, w.Qp, dh, d.CD, w.S, dh, d.DD, 0.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
                     "chunk_O1")) ||
         (rc = bgemm(0, 0, C, dh, C, 1.f, w.Mm, C, d.CC, w.Uv, dh, d.CD, 1.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
@@ -1484,13 +1583,10 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
     const ChunkDims d = chunk_dims(B, T, H, dh, C);
     const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws));
     const hipStream_t st = as_stream(stream);
-    const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
-    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in4);
     if (C == FP_C && dh == FP_D) {
         // E, the reverse scan, then one fused kernel for all per-chunk gradients
-        if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N,
-                        st, "chunk_E")))
-            return rc;
+        CK_LAUNCH_LDS("chunk_E", ck_E_k, dim3((unsigned)d.N), dim3(FO_NT), (size_t)FO_LDS_F * sizeof(float), d_o, T, H,
+                  d.NC, w);
         if ((rc = scan(true, d, w.Gp, w.E, w.dSp, st))) return rc;
         constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
         static bool attr = false;
@@ -1505,6 +1601,8 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
                            dalpha, dbeta);
         return post_launch("chunk_bwd_fused");
     }
+    const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
+    CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in4);
     CK_LAUNCH("chunk_rowscale", ck_rowscale_k, dim3(nblk(tot_in4)), dim3(256), w.dOu, w.gam, w.dOg, dh, tot_in4);
     // E_c = Qp^T dO_c; reverse scan dS'_{c-1} = G'_c^T dS'_c + E_c, dS'_{NC-1} = 0
     if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N, st,
