@@ -331,8 +331,10 @@ ASCA_API int asca_moe_bwd(const float* xn, const float* w1, const float* w2, con
  * per chunk T = (I + strict_tril(diag(beta)(Gamma o K K^T)))^-1,
  * U = T diag(beta)(V - diag(gamma) K S), O = diag(gamma) Q S + tril(Gamma o Q K^T) U,
  * S' = gamma_C S + (diag(Gamma[C-1,:]) K)^T U, with every product on the
- * matrix cores (f32 MFMA) batched over chunks, and the state carried across
- * chunks by one d x d product per chunk.  Same results as asca_delta_fwd /
+ * matrix cores (f32 MFMA) and the state carried across chunks by one d x d
+ * product per chunk.  At C = 64, dh = 128 each direction is one fused
+ * per-chunk kernel around a persistent state scan; other shapes run batched
+ * GEMMs over chunks.  Same results as asca_delta_fwd /
  * asca_delta_bwd_raw (DeltaBlock::scan_cpu / bptt_cpu, rust/src/delta.rs:244-334,
  * 475-587) up to f32 rounding.
  *   q, k, v, d_o : (B*T, H*dh) bf16 (raw 16-bit patterns); alpha, beta : (B*T, H) f32

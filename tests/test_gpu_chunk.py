@@ -40,6 +40,8 @@ def _check(orc, g, seed, B, T, H, dh, C, tag):
     (1, 256, 2, 128, 64),   # configs[2] head size
     (1, 5, 1, 8, 64),       # one short chunk
     (2, 96, 2, 128, 32),
+    (2, 200, 2, 128, 64),   # fused C=64 dh=128 path, ragged last chunk (8 steps)
+    (1, 37, 3, 128, 64),    # fused path, a single partial chunk
 ])
 def test_chunked_matches_recurrent(orc, g, B, T, H, dh, C):
     _check(orc, g, 40 + T, B, T, H, dh, C, "shape")
