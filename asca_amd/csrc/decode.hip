@@ -9,29 +9,39 @@
 // S = alpha S + k u^T (row-wise scale_axpy); o = S^T q.
 //
 // HBM-bound: S (dh^2 floats) is read and written once per step, the I/O is
-// 3dh + 2 floats in and dh out.  One 256-thread block per (sequence, head):
-// thread = (row group rg = tid / 32 of 16 rows, column quad cq = tid % 32), so
-// each row of S is read and written by 32 consecutive threads with 16-byte
-// accesses.  S^T k and S^T q are reduced over the two row groups of a wave
-// with one permlane32 swap, then over the four waves through LDS.
+// 3dh + 2 floats in and dh out.  One block per (sequence, head), thread = (row
+// group rg = tid / 32 of RPT rows, column quad cq = tid % 32), so each row of S
+// is read and written by 32 consecutive threads with 16-byte accesses.  The
+// aligned path uses RPT = 8 (512 threads, ~80 VGPRs, six waves per SIMD) and
+// non-temporal loads and stores for S, which is touched once per step and is
+// far larger than the caches (measured: 73.8% of HBM peak against 62.9% with
+// 16 rows per thread and ordinary accesses).  S^T k and S^T q are reduced over
+// the two row groups of a wave with one permlane32 swap, then over the waves
+// through LDS.
 #include "common.h"
 #include "runtime.h"
 
 namespace asca {
 
-constexpr int DEC_NT = 256;
+template <int RPT>
+struct Dec {
+    static constexpr int NT = 32 * (128 / RPT);  // threads: 32 column quads x row groups
+    static constexpr int W = NT / 64;
+};
 
-template <bool VEC>
-__global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ states, const float* __restrict__ qkv,
-                                                         const float* __restrict__ gate, float* __restrict__ o,
-                                                         int H, int dh) {
-    __shared__ float4 red[4][32];
+template <bool VEC, int RPT, bool NTMP>
+__global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict__ states,
+                                                               const float* __restrict__ qkv,
+                                                               const float* __restrict__ gate, float* __restrict__ o,
+                                                               int H, int dh) {
+    constexpr int W = Dec<RPT>::W;
+    __shared__ float4 red[W][32];
     __shared__ float4 sk_s[32];
     const int unit = blockIdx.x;               // n * H + h
     const int n = unit / H, h = unit - n * H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int cq = tid & 31, rg = tid >> 5;    // column quad, row group (0..7)
-    const int c0 = cq * 4, r0 = rg * 16;
+    const int cq = tid & 31, rg = tid >> 5;    // column quad, row group
+    const int c0 = cq * 4, r0 = rg * RPT;
     const long d = (long)H * dh;
     const float* row = qkv + (long)n * 3 * d;
     const float* qh = row + (long)h * dh;
@@ -39,14 +49,19 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
     const float* vh = row + 2 * d + (long)h * dh;
     float* S = states + (long)unit * dh * dh;
 
-    // state tile: rows r0..r0+15, columns c0..c0+3 (loads issued first)
-    float4 s[16];
+    // state tile: rows r0..r0+RPT-1, columns c0..c0+3 (loads issued first)
+    float4 s[RPT];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
         if constexpr (VEC) {
-            s[j] = (a < dh && c0 < dh) ? *reinterpret_cast<const float4*>(S + (long)a * dh + c0)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a < dh && c0 < dh) {
+                const f32x4* src = reinterpret_cast<const f32x4*>(S + (long)a * dh + c0);
+                const f32x4 x = NTMP ? __builtin_nontemporal_load(src) : *src;
+                s[j] = make_float4(x[0], x[1], x[2], x[3]);
+            } else {
+                s[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         } else {
             float* e = reinterpret_cast<float*>(&s[j]);
 #pragma unroll
@@ -69,9 +84,9 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
     const float ki = 1.0f / fmaxf(sqrtf(kk), 1e-8f);
     const float al = sigmoid_f(gate[(long)n * 2 * H + h]);
     const float be = sigmoid_f(gate[(long)n * 2 * H + H + h]);
-    float kr[16], qr[16];
+    float kr[RPT], qr[RPT];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
         kr[j] = a < dh ? kh[a] * ki : 0.0f;
         qr[j] = a < dh ? qh[a] * qi : 0.0f;
@@ -80,10 +95,10 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
 #pragma unroll
     for (int x = 0; x < 4; ++x) vv[x] = c0 + x < dh ? vh[c0 + x] : 0.0f;
 
-    // sk = S^T k over this thread's 16 rows, then the 8 row groups
+    // sk = S^T k over this thread's rows, then the row groups
     float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         p.x = fmaf(kr[j], s[j].x, p.x);
         p.y = fmaf(kr[j], s[j].y, p.y);
         p.z = fmaf(kr[j], s[j].z, p.z);
@@ -98,7 +113,7 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
     if (tid < 32) {
         float4 t = red[0][tid];
 #pragma unroll
-        for (int ww = 1; ww < 4; ++ww) {
+        for (int ww = 1; ww < W; ++ww) {
             const float4 x = red[ww][tid];
             t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
         }
@@ -112,7 +127,7 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
     // S = alpha S + k u^T (fma(k_a, u_i, alpha S), the order of simd::scale_axpy), o = S^T q
     float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         s[j].x = fmaf(kr[j], u[0], al * s[j].x);
         s[j].y = fmaf(kr[j], u[1], al * s[j].y);
         s[j].z = fmaf(kr[j], u[2], al * s[j].z);
@@ -123,10 +138,17 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
         po.w = fmaf(qr[j], s[j].w, po.w);
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
         if constexpr (VEC) {
-            if (a < dh && c0 < dh) *reinterpret_cast<float4*>(S + (long)a * dh + c0) = s[j];
+            if (a < dh && c0 < dh) {
+                f32x4* dst = reinterpret_cast<f32x4*>(S + (long)a * dh + c0);
+                const f32x4 x = {s[j].x, s[j].y, s[j].z, s[j].w};
+                if (NTMP)
+                    __builtin_nontemporal_store(x, dst);
+                else
+                    *dst = x;
+            }
         } else {
             const float* e = reinterpret_cast<const float*>(&s[j]);
 #pragma unroll
@@ -144,7 +166,7 @@ __global__ __launch_bounds__(DEC_NT) void delta_decode_k(float* __restrict__ sta
     if (tid < 32) {
         float4 t = red[0][tid];
 #pragma unroll
-        for (int ww = 1; ww < 4; ++ww) {
+        for (int ww = 1; ww < W; ++ww) {
             const float4 x = red[ww][tid];
             t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
         }
@@ -171,11 +193,12 @@ extern "C" int asca_delta_decode_step(float* states, const float* qkv, const flo
     int rc = pre_launch("delta_decode");
     if (rc) return rc;
     const bool vec = dh % 4 == 0 && (reinterpret_cast<uintptr_t>(states) & 15) == 0;
+    const hipStream_t st = as_stream(stream);
     if (vec)
-        hipLaunchKernelGGL(delta_decode_k<true>, dim3(n_seq * H), dim3(DEC_NT), 0, as_stream(stream), states, qkv,
+        hipLaunchKernelGGL((delta_decode_k<true, 8, true>), dim3(n_seq * H), dim3(Dec<8>::NT), 0, st, states, qkv,
                            gate, o, H, dh);
     else
-        hipLaunchKernelGGL(delta_decode_k<false>, dim3(n_seq * H), dim3(DEC_NT), 0, as_stream(stream), states, qkv,
-                           gate, o, H, dh);
+        hipLaunchKernelGGL((delta_decode_k<false, 16, false>), dim3(n_seq * H), dim3(Dec<16>::NT), 0, st, states,
+                           qkv, gate, o, H, dh);
     return post_launch("delta_decode");
 }
