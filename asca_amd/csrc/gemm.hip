@@ -86,6 +86,24 @@ ASCA_DEV void tile_load(float4 (&r)[8 * R / NT], const float* base, long ld, con
     }
 }
 
+// As tile_load for a tile that lies wholly inside the operand (aligned, no
+// edge): unconditional 16-byte loads.
+template <bool KC, int R, int NT>
+ASCA_DEV void tile_load_full(float4 (&r)[8 * R / NT], const float* base, long ld, const int* rows, long row_off,
+                             int mn0, long k0, int tid) {
+#pragma unroll
+    for (int j = 0; j < 8 * R / NT; ++j) {
+        const int sl = tid + NT * j;
+        if constexpr (KC) {
+            const int rr = sl >> 3, kk = 4 * (sl & 7);
+            r[j] = *reinterpret_cast<const float4*>(base + srow(rows, row_off, mn0 + rr) * ld + k0 + kk);
+        } else {
+            const int kr = sl / (R / 4), mm = 4 * (sl % (R / 4));
+            r[j] = *reinterpret_cast<const float4*>(base + srow(rows, row_off, k0 + kr) * ld + mn0 + mm);
+        }
+    }
+}
+
 template <bool KC, int R, int NT>
 ASCA_DEV void tile_store(const float4 (&r)[8 * R / NT], float* t, int tid) {
 #pragma unroll
@@ -125,9 +143,53 @@ ASCA_DEV void frag_read(float (&f)[4][4], const float* t, int w0, int h, int lan
     }
 }
 
-template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN>
-__global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
-    constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 64 * WN;
+// As frag_read for NTL 16-row tiles (NTL = 2 or 4): the wave's 16 NTL
+// mn-rows starting at w0.  In the mn-contiguous layout tile x holds the rows
+// w0 + NTL i + x (i = lane % 16), one 8- or 16-byte read per k-step.
+template <bool KC, int R, int NTL>
+ASCA_DEV void frag_read_n(float (&f)[4][NTL], const float* t, int w0, int h, int lane) {
+    if constexpr (NTL == 4) {
+        frag_read<KC, R>(f, t, w0, h, lane);
+    } else if constexpr (KC) {
+#pragma unroll
+        for (int x = 0; x < NTL; ++x) {
+            const float4 v =
+                *reinterpret_cast<const float4*>(t + (w0 + 16 * x + (lane & 15)) * GM_LDK + 16 * h + 4 * (lane >> 4));
+            f[0][x] = v.x;
+            f[1][x] = v.y;
+            f[2][x] = v.z;
+            f[3][x] = v.w;
+        }
+    } else {
+        static_assert(NTL == 2, "tile count");
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float2 v =
+                *reinterpret_cast<const float2*>(t + (16 * h + 4 * (lane >> 4) + s) * R + w0 + 2 * (lane & 15));
+            f[s][0] = v.x;
+            f[s][1] = v.y;
+        }
+    }
+}
+
+// acc (4 x TN tiles of 16 x 16) += the 16-k group whose fragments are fa, fb.
+template <int TN>
+ASCA_DEV void mfma_4xn(f32x4 (&acc)[4][TN], const float (&fa)[4][4], const float (&fb)[4][TN]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int y = 0; y < TN; ++y)
+                acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][x], fb[s][y], acc[x][y], 0, 0, 0);
+}
+
+// Block tile (64 WM) x (16 TNW WN) on WM x WN waves; a wave owns 64 rows x
+// 16 TNW columns (TNW = 4, or 2 for the narrower tile that lets three blocks
+// share a CU).
+template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN, int TNW = 4>
+__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_k(GemmArgs p) {
+    constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 16 * TNW * WN;
     constexpr bool A_KC = !TA, B_KC = TB;
     constexpr int A_F = tile_floats<A_KC, BM>();
     constexpr int B_F = tile_floats<B_KC, BN>();
@@ -179,51 +241,66 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
     const long b_off = (p.gmode == 2 && !TB) ? goff_g : 0;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int wm = (w / WN) * 64, wn = (w % WN) * 64;
+    const int wm = (w / WN) * 64, wn = (w % WN) * 16 * TNW;
     const int lim_m = Mg - m0, lim_n = p.N - n0;
 
-    f32x4 acc[4][4];
+    f32x4 acc[4][TNW];
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int y = 0; y < TNW; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const long nk = (K_hi - K_lo + GM_BK - 1) / GM_BK;
     float4 ra[8 * BM / NT], rb[8 * BN / NT];
+    // interior blocks (whole tiles in M and N) load without edge checks,
+    // except in a partial last k-tile
+    const bool interior = VEC && lim_m >= BM && lim_n >= BN;
     auto load = [&](long k0) {
-        tile_load<A_KC, VEC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
-        tile_load<B_KC, VEC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
+        if (interior && K_hi - k0 >= GM_BK) {
+            tile_load_full<A_KC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, k0, tid);
+            tile_load_full<B_KC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, k0, tid);
+        } else {
+            tile_load<A_KC, VEC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
+            tile_load<B_KC, VEC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
+        }
     };
+    // Pipeline per k-tile kt (fragments of both 16-k halves of kt already in
+    // registers): issue the global loads of kt+1; MFMAs of half 0; store kt+1
+    // to the other LDS buffer; barrier; read half 0 of kt+1 while the MFMAs of
+    // half 1 run, then half 1 of kt+1.  A buffer is rewritten only after the
+    // barrier that follows the last read of its previous tile.
+    float fa0[4][4], fb0[4][TNW], fa1[4][4], fb1[4][TNW];
     if (nk > 0) {
         load(K_lo);
         tile_store<A_KC, BM, NT>(ra, lds, tid);
         tile_store<B_KC, BN, NT>(rb, lds + A_F, tid);
     }
     __syncthreads();
+    if (nk > 0) {
+        frag_read<A_KC, BM>(fa0, lds, wm, 0, lane);
+        frag_read_n<B_KC, BN, TNW>(fb0, lds + A_F, wn, 0, lane);
+        frag_read<A_KC, BM>(fa1, lds, wm, 1, lane);
+        frag_read_n<B_KC, BN, TNW>(fb1, lds + A_F, wn, 1, lane);
+    }
     for (long kt = 0; kt < nk; ++kt) {
-        const float* As = lds + (kt & 1) * (A_F + B_F);
-        const float* Bs = As + A_F;
         const bool more = kt + 1 < nk;
+        float* const Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
         if (more) load(K_lo + (kt + 1) * GM_BK);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float fa[4][4], fb[4][4];
-            frag_read<A_KC, BM>(fa, As, wm, h, lane);
-            frag_read<B_KC, BN>(fb, Bs, wn, h, lane);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int x = 0; x < 4; ++x)
-#pragma unroll
-                    for (int y = 0; y < 4; ++y)
-                        acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][x], fb[s][y], acc[x][y], 0, 0, 0);
-        }
+        mfma_4xn<TNW>(acc, fa0, fb0);
         if (more) {
-            float* Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
             tile_store<A_KC, BM, NT>(ra, Ns, tid);
             tile_store<B_KC, BN, NT>(rb, Ns + A_F, tid);
         }
         __syncthreads();
+        if (more) {
+            frag_read<A_KC, BM>(fa0, Ns, wm, 0, lane);
+            frag_read_n<B_KC, BN, TNW>(fb0, Ns + A_F, wn, 0, lane);
+        }
+        mfma_4xn<TNW>(acc, fa1, fb1);
+        if (more) {
+            frag_read<A_KC, BM>(fa1, Ns, wm, 1, lane);
+            frag_read_n<B_KC, BN, TNW>(fb1, Ns + A_F, wn, 1, lane);
+        }
     }
 
     // epilogue: result register r of tile (x, y) sits at tile row 4 (lane / 16) + r,
@@ -238,17 +315,17 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
             const long sorted = (p.gmode == 1 ? goff_g : 0) + m;
             const long crow = p.c_rows ? (long)p.c_rows[sorted] : sorted;
             float* Cr = C + crow * p.ldc;
-            float v[4];
+            float v[TNW];
 #pragma unroll
-            for (int y = 0; y < 4; ++y) v[y] = acc[x][y][r];
+            for (int y = 0; y < TNW; ++y) v[y] = acc[x][y][r];
             if constexpr (!B_KC) {
-                // columns n, n+1, n+2, n+3 of one row
-                const int n = n0 + wn + 4 * (lane & 15);
+                // columns n .. n + TNW - 1 of one row
+                const int n = n0 + wn + TNW * (lane & 15);
                 if (n >= p.N) continue;
-                const int cnt = min(p.N - n, 4);
-                float o[4], hb[4];
+                const int cnt = min(p.N - n, TNW);
+                float o[TNW], hb[TNW];
 #pragma unroll
-                for (int y = 0; y < 4; ++y) {
+                for (int y = 0; y < TNW; ++y) {
                     float a = p.alpha * v[y];
                     if (y < cnt) {
                         if (bias) a += bias[n + y];
@@ -265,14 +342,18 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
                     }
                     o[y] = a;
                 }
-                if (VEC && cnt == 4) {
-                    *reinterpret_cast<float4*>(Cr + n) = make_float4(o[0], o[1], o[2], o[3]);
+                if (VEC && cnt == TNW && TNW == 4) {
+                    *reinterpret_cast<float4*>(Cr + n) = make_float4(o[0], o[1], o[TNW - 2], o[TNW - 1]);
                     if constexpr (EPI == EPI_SILU)
                         *reinterpret_cast<float4*>(p.aux_out + sorted * p.ld_aux + n) =
-                            make_float4(hb[0], hb[1], hb[2], hb[3]);
+                            make_float4(hb[0], hb[1], hb[TNW - 2], hb[TNW - 1]);
+                } else if (VEC && cnt == TNW && TNW == 2) {
+                    *reinterpret_cast<float2*>(Cr + n) = make_float2(o[0], o[TNW - 1]);
+                    if constexpr (EPI == EPI_SILU)
+                        *reinterpret_cast<float2*>(p.aux_out + sorted * p.ld_aux + n) = make_float2(hb[0], hb[TNW - 1]);
                 } else {
 #pragma unroll
-                    for (int y = 0; y < 4; ++y)
+                    for (int y = 0; y < TNW; ++y)
                         if (y < cnt) {
                             Cr[n + y] = o[y];
                             if constexpr (EPI == EPI_SILU) p.aux_out[sorted * p.ld_aux + n + y] = hb[y];
@@ -280,7 +361,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_k(GemmArgs p) {
                 }
             } else {
 #pragma unroll
-                for (int y = 0; y < 4; ++y) {
+                for (int y = 0; y < TNW; ++y) {
                     const int n = n0 + wn + 16 * y + (lane & 15);
                     if (n >= p.N) continue;
                     float a = p.alpha * v[y];
@@ -551,19 +632,27 @@ static int scratch_get(size_t bytes, float** out) {
     return ASCA_OK;
 }
 
-template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2>
+template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2, int TNW = 4>
 static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds =
-        2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 64 * WN>()) * sizeof(float);
+        2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 16 * TNW * WN>()) * sizeof(float);
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN, TNW>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
         attr = true;
     }
-    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN>), grid, dim3(64 * WM * WN), lds, st, a);
+    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN, TNW>), grid, dim3(64 * WM * WN), lds, st, a);
     return ASCA_OK;
+}
+
+// Fraction of the block slots used over the rounds a launch of `tiles` blocks
+// takes, `per_cu` blocks resident per CU.
+static double round_fill(long tiles, int per_cu) {
+    const long slots = (long)per_cu * (cu_count() > 0 ? cu_count() : 256);
+    const long rounds = (tiles + slots - 1) / slots;
+    return rounds ? (double)tiles / (double)(rounds * slots) : 1.0;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -605,7 +694,27 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     // batched per-chunk products with at most 64 rows use 64 x 128 tiles
     const int wm = (a.gmode == 3 && vec && a.M <= 64) ? 1 : 2;
     const int wn = 2;  // a 64 x 64 tile needs 8 staged float4 per operand per lane and spills
-    a.tiles_n = (a.N + 64 * wn - 1) / (64 * wn);
+    // block count for a block-tile width bn
+    auto count = [&](int bn) -> long {
+        const long tn = (a.N + bn - 1) / bn, tm = (a.M + 64 * wm - 1) / (64 * wm);
+        const long splits = a.gmode == 0 && a.k_per_split > 0 ? (a.K + a.k_per_split - 1) / a.k_per_split : 1;
+        if (a.gmode == 1) return ((m_total + GM_BM - 1) / GM_BM + a.ngroups) * tn;
+        if (a.gmode == 2 || a.gmode == 3) return (long)a.ngroups * tm * tn;
+        return tm * tn * splits;
+    };
+    // 128 x 64 tiles when the 128 x 128 grid would leave a mostly idle last
+    // round.  Measured per-flop efficiency of the narrow tile against the wide
+    // one: ~0.8 with two blocks per CU (NN, NT), ~0.95 with three (A^T)
+    const size_t lds64 = 2 * (size_t)(ta ? GM_BK * 128 : 128 * GM_LDK) * sizeof(float) +
+                         2 * (size_t)(tb ? 64 * GM_LDK : GM_BK * 64) * sizeof(float);
+    // resident narrow blocks per CU: LDS, and registers (the A^T variants fit
+    // three waves per SIMD, the others two)
+    const int per_cu64 = (int)min((size_t)(ta ? 3 : 2), (size_t)(160 * 1024) / lds64);
+    const bool narrow =
+        vec && wm == 2 && a.gmode != 3 &&
+        round_fill(count(64), per_cu64) * (per_cu64 >= 3 ? 0.95 : 0.8) > round_fill(count(128), 2);
+    const int bn = narrow ? 64 : 128;
+    a.tiles_n = (a.N + bn - 1) / bn;
     a.tiles_m = (a.M + 64 * wm - 1) / (64 * wm);
     long blocks;
     if (a.gmode == 1)
@@ -622,7 +731,9 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     if (a.gmode != 0 || a.k_per_split <= 0) a.k_per_split = a.K;
 #define ASCA_GEMM_CASE(TA_, TB_, EPI_)                                                                  \
     if (ta == TA_ && tb == TB_ && epi == EPI_)                                                          \
-        rc = vec ? launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st) : launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st); \
+        rc = !vec ? launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st)                                   \
+             : narrow ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 2, 2>(a, grid, st)                       \
+                      : launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st);                                \
     else
 #define ASCA_GEMM_SMALL(TA_, TB_)                                                                       \
     if (ta == TA_ && tb == TB_)                                                                         \
