@@ -77,9 +77,11 @@ ASCA_DEV float4 ld4m(const float* __restrict__ p, int col, int dh) {
 // part*R .. part*R+R-1 (R = DH/8) of its column, so S^T k and S^T q are 8-lane
 // DPP butterflies (quad_perm, row_half_mirror).
 
-template <int DH>
+// CS: the unit's value columns are split over CS blocks (1 or 2); each block
+// runs W waves of 8 columns.
+template <int DH, int CS = 1>
 struct FS {
-    static constexpr int W = DH / 8;
+    static constexpr int W = DH / 8 / CS;
     static constexpr int NT = 64 * W;
     static constexpr int R = DH / 8;
     static constexpr int CK = DS<DH>::CK;
@@ -93,17 +95,18 @@ struct FS {
     static constexpr int NV = (CK * 2 + 63) / 64;             // staged v float4 per lane
 };
 
-template <int DH>
+template <int DH, int CS>
 struct FwdStage {
-    float4 kq[FS<DH>::NKQ];
-    float4 v[FS<DH>::NV];
+    float4 kq[FS<DH, CS>::NKQ];
+    float4 v[FS<DH, CS>::NV];
 };
 
-// Global -> registers for chunk c (steps c*CK .. c*CK+CK-1, clamped to T-1).
-template <int DH, bool EXACT>
-ASCA_DEV void fwd_stage_load(FwdStage<DH>& st, int c, const float* __restrict__ q, const float* __restrict__ k,
-                             const float* __restrict__ v, long ubase, long d, int T, int dh, int w, int lane) {
-    using L = FS<DH>;
+// Global -> registers for chunk c (steps c*CK .. c*CK+CK-1, clamped to T-1);
+// wg: the wave's index among all waves of the unit (its value columns).
+template <int DH, int CS, bool EXACT>
+ASCA_DEV void fwd_stage_load(FwdStage<DH, CS>& st, int c, const float* __restrict__ q, const float* __restrict__ k,
+                             const float* __restrict__ v, long ubase, long d, int T, int dh, int wg, int lane) {
+    using L = FS<DH, CS>;
     constexpr int CK = L::CK;
     const int t0 = c * CK;
 #pragma unroll
@@ -122,13 +125,13 @@ ASCA_DEV void fwd_stage_load(FwdStage<DH>& st, int c, const float* __restrict__ 
         const int f = f0 < CK * 2 ? f0 : 0;
         const int j = f / 2, half = f % 2;
         const long t = min(t0 + j, T - 1);
-        st.v[i] = ld4m<EXACT>(v + ubase + t * d, w * 8 + half * 4, dh);
+        st.v[i] = ld4m<EXACT>(v + ubase + t * d, wg * 8 + half * 4, dh);
     }
 }
 
-template <int DH>
-ASCA_DEV void fwd_stage_store(const FwdStage<DH>& st, float* __restrict__ buf, int w, int lane) {
-    using L = FS<DH>;
+template <int DH, int CS>
+ASCA_DEV void fwd_stage_store(const FwdStage<DH, CS>& st, float* __restrict__ buf, int w, int lane) {
+    using L = FS<DH, CS>;
     constexpr int CK = L::CK;
 #pragma unroll
     for (int i = 0; i < L::NKQ; ++i) {
@@ -177,22 +180,23 @@ ASCA_DEV void fwd_rd(float (&kk)[DH / 8], float (&qq)[DH / 8], float& vv, const 
 // One block per (sequence, head) unit, unit = h*B + b (the reference's s_pre
 // order, rust/src/delta.rs:54-56).  ckpt: nslots = ceil(T/CK) states per unit,
 // slot j = S^T before step j*CK (element (a, i) of S at [i*dh + a]).
-template <int DH, bool EXACT>
-__global__ __launch_bounds__(FS<DH>::NT) void delta_fwd_k(
+template <int DH, int CS, bool EXACT>
+__global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ alpha, const float* __restrict__ beta, float* __restrict__ o,
     float* __restrict__ sk_out, float* __restrict__ ckpt, int B, int T, int H, int dh, int nslots) {
-    using L = FS<DH>;
+    using L = FS<DH, CS>;
     constexpr int R = L::R, CK = L::CK, G = L::G;
     static_assert(2 * CK <= 64 && CK % G == 0, "chunk layout");
     __shared__ float4 lds4[2 * L::BUF_F / 4];
     float* const lds = reinterpret_cast<float*>(lds4);
 
-    const int unit = blockIdx.x;
+    const int unit = blockIdx.x / CS, part = blockIdx.x - unit * CS;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wg = part * L::W + w;
     const int p = lane & 7, c = lane >> 3;
-    const int col = w * 8 + c;
+    const int col = wg * 8 + c;
     const int row0 = p * R;
     const long d = (long)H * dh;
     const long dh2 = (long)dh * dh;
@@ -214,10 +218,10 @@ __global__ __launch_bounds__(FS<DH>::NT) void delta_fwd_k(
 #pragma unroll
     for (int j = 0; j < R; ++j) s[j] = 0.0f;
 
-    FwdStage<DH> stg;
-    fwd_stage_load<DH, EXACT>(stg, 0, q, k, v, ubase, d, T, dh, w, lane);
+    FwdStage<DH, CS> stg;
+    fwd_stage_load<DH, CS, EXACT>(stg, 0, q, k, v, ubase, d, T, dh, wg, lane);
     float gnext = gsrc[(long)min(gstep, T - 1) * H];
-    fwd_stage_store<DH>(stg, lds, w, lane);
+    fwd_stage_store<DH, CS>(stg, lds, w, lane);
     __syncthreads();
 
     for (int ci = 0; ci < nchunk; ++ci) {
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(FS<DH>::NT) void delta_fwd_k(
         const float* buf = lds + (ci & 1) * L::BUF_F;
         const float gcur = gnext;
         gnext = gsrc[(long)min(t0 + CK + gstep, T - 1) * H];
-        fwd_stage_load<DH, EXACT>(stg, min(ci + 1, nchunk - 1), q, k, v, ubase, d, T, dh, w, lane);
+        fwd_stage_load<DH, CS, EXACT>(stg, min(ci + 1, nchunk - 1), q, k, v, ubase, d, T, dh, wg, lane);
         {   // checkpoint: S before step t0, as S^T
             float* dst = ckb + (long)ci * dh2 + (long)col * dh + row0;
             if constexpr (EXACT && R % 4 == 0) {
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(FS<DH>::NT) void delta_fwd_k(
                 *(ok ? skb + (long)ts * d + col : tr + 1) = hold_s;
             }
         }
-        fwd_stage_store<DH>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
+        fwd_stage_store<DH, CS>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
         __syncthreads();
     }
 }
@@ -342,9 +346,9 @@ __global__ __launch_bounds__(DS<DH>::THREADS) void delta_states_k(
 // unrolled over C steps; a tail segment past T is padded with dO = 0 steps,
 // which leave dS unchanged and whose outputs are dropped.
 
-template <int DH>
+template <int DH, int CS = 1>
 struct BS {
-    static constexpr int W = DH / 8;
+    static constexpr int W = DH / 8 / CS;
     static constexpr int NT = 64 * W;
     static constexpr int M = DH / 16;
     static constexpr int CK = DS<DH>::CK;
@@ -363,20 +367,21 @@ struct BS {
     static constexpr int NW = (W4 + 63) / 64;
 };
 
-template <int DH>
+template <int DH, int CS>
 struct BStage {
-    float4 rq[BS<DH>::NQ], rw[BS<DH>::NW];
+    float4 rq[BS<DH, CS>::NQ], rw[BS<DH, CS>::NW];
     float rab;
-    float rck[2][BS<DH>::M];  // checkpoint tile: column colb+n, rows rowb..rowb+M-1
+    float rck[2][BS<DH, CS>::M];  // checkpoint tile: column colb+n, rows rowb..rowb+M-1
 };
 
-template <int DH, bool EXACT>
-ASCA_DEV void bstage_load(BStage<DH>& st, int g, const float* __restrict__ q, const float* __restrict__ k,
+// wg: the wave's index among all waves of the unit (its value columns)
+template <int DH, int CS, bool EXACT>
+ASCA_DEV void bstage_load(BStage<DH, CS>& st, int g, const float* __restrict__ q, const float* __restrict__ k,
                           const float* __restrict__ v, const float* __restrict__ d_o,
                           const float* __restrict__ skv, const float* __restrict__ alpha,
                           const float* __restrict__ beta, const float* __restrict__ ckb, long ubase, long gbase,
-                          long d, long dh2, int T, int H, int dh, int w, int lane, int rowb, int colb) {
-    using S = BS<DH>;
+                          long d, long dh2, int T, int H, int dh, int wg, int lane, int rowb, int colb) {
+    using S = BS<DH, CS>;
     constexpr int CK = S::CK, M = S::M;
     const int t0 = g * CK;
 #pragma unroll
@@ -398,7 +403,7 @@ ASCA_DEV void bstage_load(BStage<DH>& st, int g, const float* __restrict__ q, co
         const int j = rem / 2, half = rem % 2;
         const long t = min(t0 + j, T - 1);
         const float* src = tsr == 0 ? d_o : (tsr == 1 ? v : skv);
-        float4 x = ld4m<EXACT>(src + ubase + t * d, w * 8 + half * 4, dh);
+        float4 x = ld4m<EXACT>(src + ubase + t * d, wg * 8 + half * 4, dh);
         if (tsr == 0 && t0 + j >= T) x = make_float4(0.f, 0.f, 0.f, 0.f);   // padded steps carry dO = 0
         st.rw[i] = x;
     }
@@ -428,10 +433,10 @@ ASCA_DEV void bstage_load(BStage<DH>& st, int g, const float* __restrict__ q, co
     }
 }
 
-template <int DH>
-ASCA_DEV void bstage_store(const BStage<DH>& st, float* __restrict__ st_q, float* __restrict__ st_k,
+template <int DH, int CS>
+ASCA_DEV void bstage_store(const BStage<DH, CS>& st, float* __restrict__ st_q, float* __restrict__ st_k,
                            float* __restrict__ st_w, float* __restrict__ st_ab, int w, int lane) {
-    using S = BS<DH>;
+    using S = BS<DH, CS>;
     constexpr int CK = S::CK;
 #pragma unroll
     for (int i = 0; i < S::NQ; ++i) {
@@ -644,28 +649,33 @@ ASCA_DEV void cross_step_sum(float (&x)[2 * CK], float* __restrict__ red_ab, int
     }
 }
 
-// Backward of one unit per block.  Output pointers are already offset to the
-// head-0 column of their quantity; element (r, h*dh + i) is at ptr[r*ldx + h*dh + i]
-// and the per-head scalars at ga[r*ldg + h].  FUSED applies the L2-norm backward
+// Backward of one unit per block (CS = 1), or of half of its value columns
+// per block (CS = 2).  Output pointers are already offset to the head-0 column
+// of their quantity; element (r, h*dh + i) is at ptr[r*ldx + h*dh + i] and the
+// per-head scalars at ga[r*ldg + h].  FUSED applies the L2-norm backward
 // (rust/src/delta.rs:677-698) and the sigmoid backward (delta.rs:602-611).
-template <int DH, bool EXACT, bool FUSED>
-__global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
+// With CS = 2 the row sums dq, dk and dalpha, dbeta cover only the block's
+// columns: they go to the partial buffers (part_x [CS][B*T][H*dh], part_g
+// [CS][B*T][2H]) and delta_combine_k finishes them; dv is complete per column.
+template <int DH, int CS, bool EXACT, bool FUSED>
+__global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ alpha, const float* __restrict__ beta, const float* __restrict__ d_o,
     const float* __restrict__ skv, const float* __restrict__ ckpt, const float* __restrict__ qnorm,
     const float* __restrict__ knorm, float* __restrict__ gq, float* __restrict__ gk,
-    float* __restrict__ gv, long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, int B,
-    int T, int H, int dh, int nslots) {
-    using S = BS<DH>;
+    float* __restrict__ gv, long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg,
+    float* __restrict__ part_x, float* __restrict__ part_g, int B, int T, int H, int dh, int nslots) {
+    using S = BS<DH, CS>;
     constexpr int M = S::M, W = S::W, CK = S::CK;
     extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
 
-    const int unit = blockIdx.x;
+    const int unit = blockIdx.x / CS, part = blockIdx.x - unit * CS;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wg = part * W + w;
     const int rg = lane & 15, cg = lane >> 4;
-    const int colb = w * 8 + cg * 2;
+    const int colb = wg * 8 + cg * 2;
     const int rowb = rg * M;
     const long d = (long)H * dh;
     const long dh2 = (long)dh * dh;
@@ -680,9 +690,9 @@ __global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
 #pragma unroll
     for (int m = 0; m < M; ++m) ds[m][0] = ds[m][1] = 0.0f;
 
-    BStage<DH> stg;
-    bstage_load<DH, EXACT>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T, H, dh, w,
-                           lane, rowb, colb);
+    BStage<DH, CS> stg;
+    bstage_load<DH, CS, EXACT>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T, H, dh,
+                               wg, lane, rowb, colb);
     for (int g = nseg - 1; g >= 0; --g) {
         const int t0 = g * CK;
         float* const buf = lds + (g & 1) * S::BUF_F;
@@ -701,9 +711,9 @@ __global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
             stash[0][m][0] = stg.rck[0][m];
             stash[0][m][1] = stg.rck[1][m];
         }
-        bstage_store<DH>(stg, st_q, st_k, st_w, st_ab, w, lane);
-        bstage_load<DH, EXACT>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T,
-                               H, dh, w, lane, rowb, colb);
+        bstage_store<DH, CS>(stg, st_q, st_k, st_w, st_ab, w, lane);
+        bstage_load<DH, CS, EXACT>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2,
+                                   T, H, dh, wg, lane, rowb, colb);
         __syncthreads();  // staging of this segment visible to all waves
 
         // ---- phase A: recompute S_{t0+1} .. S_{t0+CK-1} into the stash
@@ -776,7 +786,22 @@ __global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
                 dA += x.x;
                 dB += x.y;
             }
-            if constexpr (FUSED) {
+            if constexpr (CS > 1) {
+                float* const px = part_x + ((long)part * B * T + r) * d + hoff;
+#pragma unroll
+                for (int ia = 0; ia < NA; ++ia) {
+                    const int a = lane + 64 * ia;
+                    if (a < dh) {
+                        px[a] = dq[ia];
+                        px[(long)B * T * d * CS + a] = dk[ia];
+                    }
+                }
+                if (lane == 0) {
+                    float* const pg = part_g + ((long)part * B * T + r) * 2 * H;
+                    pg[h] = dA;
+                    pg[H + h] = dB;
+                }
+            } else if constexpr (FUSED) {
                 dotq = wave_sum(dotq);
                 dotk = wave_sum(dotk);
                 const float qn = qnorm[r * H + h], kn = knorm[r * H + h];
@@ -811,6 +836,76 @@ __global__ __launch_bounds__(BS<DH>::NT) void delta_bwd_k(
     }
 }
 
+// Finish a column-split backward: sum the CS = 2 partial row sums of dq, dk
+// and dalpha, dbeta and apply the fused norm / sigmoid backward as
+// delta_bwd_k does for CS = 1.  One wave per (row, head).
+template <bool FUSED>
+__global__ __launch_bounds__(256) void delta_combine_k(
+    const float* __restrict__ part_x, const float* __restrict__ part_g, const float* __restrict__ q,
+    const float* __restrict__ k, const float* __restrict__ alpha, const float* __restrict__ beta,
+    const float* __restrict__ qnorm, const float* __restrict__ knorm, float* __restrict__ gq,
+    float* __restrict__ gk, long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, long rows, int H,
+    int dh) {
+    const long id = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // r * H + h
+    if (id >= rows * H) return;
+    const int lane = threadIdx.x & 63;
+    const long r = id / H;
+    const int h = (int)(id - r * H);
+    const long d = (long)H * dh, n = rows * d;
+    const long o = r * d + (long)h * dh;
+    float dq[2], dk[2], qa[2], ka[2];
+    float dotq = 0.0f, dotk = 0.0f;
+#pragma unroll
+    for (int ia = 0; ia < 2; ++ia) {
+        const int a = lane + 64 * ia;
+        dq[ia] = dk[ia] = qa[ia] = ka[ia] = 0.0f;
+        if (a < dh) {
+            dq[ia] = part_x[o + a] + part_x[n + o + a];
+            dk[ia] = part_x[2 * n + o + a] + part_x[3 * n + o + a];
+            if (FUSED) {
+                qa[ia] = q[o + a];
+                ka[ia] = k[o + a];
+            }
+        }
+        dotq = fmaf(qa[ia], dq[ia], dotq);
+        dotk = fmaf(ka[ia], dk[ia], dotk);
+    }
+    const long og = r * 2 * H + h, ng = rows * 2 * H;
+    const float dA = part_g[og] + part_g[ng + og];
+    const float dB = part_g[og + H] + part_g[ng + og + H];
+    if constexpr (FUSED) {
+        dotq = wave_sum(dotq);
+        dotk = wave_sum(dotk);
+        const float qn = qnorm[r * H + h], kn = knorm[r * H + h];
+#pragma unroll
+        for (int ia = 0; ia < 2; ++ia) {
+            const int a = lane + 64 * ia;
+            if (a < dh) {
+                gq[r * ldx + (long)h * dh + a] = (dq[ia] - qa[ia] * dotq) / qn;
+                gk[r * ldx + (long)h * dh + a] = (dk[ia] - ka[ia] * dotk) / kn;
+            }
+        }
+        if (lane == 0) {
+            const float al = alpha[r * H + h], be = beta[r * H + h];
+            ga[r * ldg + h] = dA * al * (1.0f - al);
+            gb[r * ldg + h] = dB * be * (1.0f - be);
+        }
+    } else {
+#pragma unroll
+        for (int ia = 0; ia < 2; ++ia) {
+            const int a = lane + 64 * ia;
+            if (a < dh) {
+                gq[r * ldx + (long)h * dh + a] = dq[ia];
+                gk[r * ldx + (long)h * dh + a] = dk[ia];
+            }
+        }
+        if (lane == 0) {
+            ga[r * ldg + h] = dA;
+            gb[r * ldg + h] = dB;
+        }
+    }
+}
+
 // ------------------------------------------------------------------- host
 
 static int dh_class(int dh) {
@@ -834,10 +929,20 @@ static int ck_for(int dhc) {
 struct DeltaWs {
     float* sk;
     float* ckpt;
+    float* part_x;  // column split: partial dq, dk  [2][CS][B*T][H*dh]
+    float* part_g;  // column split: partial dalpha, dbeta  [CS][B*T][2H]
     int ck;
     int nslots;
+    int cs;
     size_t bytes;
 };
+
+// Units (sequence, head) at or below which each unit's value columns run on two
+// blocks: half of MI355X's 256 CUs, so that a small batch still fills the chip.
+// A function of the shape only, so the workspace size never depends on the
+// device state.
+constexpr long SPLIT_UNITS = 128;
+static int col_split(int B, int H) { return (long)B * H <= SPLIT_UNITS ? 2 : 1; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -848,9 +953,15 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     w.nslots = (T + w.ck - 1) / w.ck;
     const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
+    w.cs = col_split(B, H);
+    const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
+    const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
+    char* c = reinterpret_cast<char*>(base);
     w.sk = reinterpret_cast<float*>(base);
-    w.ckpt = base ? reinterpret_cast<float*>(reinterpret_cast<char*>(base) + sk_bytes) : nullptr;
-    w.bytes = sk_bytes + ck_bytes;
+    w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
+    w.part_x = base && px_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
+    w.part_g = base && pg_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes) : nullptr;
+    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes;
     return w;
 }
 
@@ -868,8 +979,12 @@ static int launch_fwd_t(const float* q, const float* k, const float* v, const fl
                         float* o, const DeltaWs& ws, int B, int T, int H, int dh, hipStream_t st) {
     int rc = pre_launch("delta_fwd");
     if (rc) return rc;
-    hipLaunchKernelGGL((delta_fwd_k<DH, EXACT>), dim3(B * H), dim3(FS<DH>::NT), 0, st, q, k, v, alpha, beta, o,
-                       ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
+    if (ws.cs > 1)
+        hipLaunchKernelGGL((delta_fwd_k<DH, 2, EXACT>), dim3(B * H * 2), dim3(FS<DH, 2>::NT), 0, st, q, k, v, alpha,
+                           beta, o, ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
+    else
+        hipLaunchKernelGGL((delta_fwd_k<DH, 1, EXACT>), dim3(B * H), dim3(FS<DH, 1>::NT), 0, st, q, k, v, alpha,
+                           beta, o, ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
     return post_launch("delta_fwd");
 }
 
@@ -899,24 +1014,43 @@ static int launch_states_t(const float* q, const float* k, const float* v, const
     return post_launch("delta_states");
 }
 
-template <int DH, bool EXACT, bool FUSED>
-static int launch_bwd_t(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
-                        const float* d_o, const DeltaWs& ws, const float* qn, const float* kn, float* gq, float* gk,
-                        float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
-                        hipStream_t st) {
+template <int DH, int CS, bool EXACT, bool FUSED>
+static int launch_bwd_cs(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                         const float* d_o, const DeltaWs& ws, const float* qn, const float* kn, float* gq, float* gk,
+                         float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
+                         hipStream_t st) {
     static bool attr = false;
-    const size_t lds = BS<DH>::LDS;
+    const size_t lds = BS<DH, CS>::LDS;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&delta_bwd_k<DH, EXACT, FUSED>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&delta_bwd_k<DH, CS, EXACT, FUSED>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu): %s", lds, hipGetErrorString(e));
         attr = true;
     }
     int rc = pre_launch("delta_bwd");
     if (rc) return rc;
-    hipLaunchKernelGGL((delta_bwd_k<DH, EXACT, FUSED>), dim3(B * H), dim3(BS<DH>::NT), lds, st, q, k, v, alpha,
-                       beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, dh, ws.nslots);
-    return post_launch("delta_bwd");
+    hipLaunchKernelGGL((delta_bwd_k<DH, CS, EXACT, FUSED>), dim3(B * H * CS), dim3(BS<DH, CS>::NT), lds, st, q, k,
+                       v, alpha, beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, ws.part_x,
+                       ws.part_g, B, T, H, dh, ws.nslots);
+    if ((rc = post_launch("delta_bwd"))) return rc;
+    if (CS == 1) return ASCA_OK;
+    if ((rc = pre_launch("delta_combine"))) return rc;
+    const long rows = (long)B * T;
+    hipLaunchKernelGGL((delta_combine_k<FUSED>), dim3((unsigned)((rows * H + 3) / 4)), dim3(256), 0, st, ws.part_x,
+                       ws.part_g, q, k, alpha, beta, qn, kn, gq, gk, ldx, ga, gb, ldg, rows, H, dh);
+    return post_launch("delta_combine");
+}
+
+template <int DH, bool EXACT, bool FUSED>
+static int launch_bwd_t(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                        const float* d_o, const DeltaWs& ws, const float* qn, const float* kn, float* gq, float* gk,
+                        float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
+                        hipStream_t st) {
+    if (ws.cs > 1)
+        return launch_bwd_cs<DH, 2, EXACT, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg,
+                                                  B, T, H, dh, st);
+    return launch_bwd_cs<DH, 1, EXACT, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B,
+                                              T, H, dh, st);
 }
 
 template <bool FUSED>
