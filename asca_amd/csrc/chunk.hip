@@ -643,7 +643,7 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
 // the separate kernels above (the backward reads them), so both paths are
 // interchangeable.
 constexpr int FP_C = 64, FP_D = 128, FP_LK = FP_D + 4, FP_LC = FP_C + 4, FP_NT = 512;
-constexpr int FP_LDS_F = 3 * FP_C * FP_LK + 2 * FP_C * FP_LC + 5 * FP_C;
+constexpr int FP_LDS_F = 3 * FP_C * FP_LK + 2 * FP_C * FP_LC + 5 * FP_C + 8 * FP_C;
 
 // Four k-consecutive elements of an LDS operand at (mn, k .. k+3): element
 // (mn, k) at P[mn*ld + k] if KC (one 8- or 16-byte read) else P[k*ld + mn];
@@ -716,6 +716,12 @@ ASCA_DEV void acc_zero(f32x4 (&acc)[TM][TN]) {
         for (int y = 0; y < TN; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
+// Streaming stores for workspace arrays read back only by later kernels.
+ASCA_DEV void st_nt(float* p, float v) { __builtin_nontemporal_store(v, p); }
+ASCA_DEV void st_nt4(float* p, float4 v) {
+    __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(p));
+}
+
 // 64 x 128 bf16 rows of one chunk -> LDS f32 [t][f] (stride FP_LK) and, if
 // gdst is set, the unit-major f32 copy; rows past T are zero.  tid counts from
 // 0 over the nthr threads taking part.
@@ -730,7 +736,7 @@ ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, float* 
                             __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
         }
         *reinterpret_cast<float4*>(lds + t * FP_LK + f) = x;
-        if (gdst) *reinterpret_cast<float4*>(gdst + t * FP_D + f) = x;
+        if (gdst) st_nt4(gdst + t * FP_D + f, x);
     }
 }
 
@@ -766,6 +772,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     float* const g_s = b_s + FP_C;
     float* const gt_s = g_s + FP_C;
     float* const bg_s = gt_s + FP_C;
+    float* const seg_s = bg_s + FP_C;  // [8][64] per-segment products of Gamma's columns
     float* const Gs = Y;
     float* const Ts = Y;
 
@@ -793,24 +800,44 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     fp_load_rows(k, Ks, w.Ku + cd, rowbase, rowstride, valid, tid, FP_NT);
     fp_load_rows(q, X, w.Qu + cd, rowbase, rowstride, valid, tid, FP_NT);
     __syncthreads();
-    // gamma (one thread), Gamma by columns (first wave)
-    if (tid == 0) {
-        float g = 1.0f;
-        for (int t = 0; t < FP_C; ++t) {
-            g *= a_s[t];
-            g_s[t] = g;
-        }
-    }
+    // gamma: inclusive product scan over the first wave.  Gamma[t][i] =
+    // prod_{i < s <= t} alpha_s (t >= i), never by division (gamma can
+    // underflow): thread (column i, segment sg) forms the running products of
+    // rows 8 sg .. 8 sg + 7, then scales them by the product of the column's
+    // earlier segments.
     if (tid < FP_C) {
-        const int i = tid;
+        float g = a_s[tid];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_up(g, o);
+            if (tid >= o) g *= y;
+        }
+        g_s[tid] = g;
+    }
+    {
+        const int i = tid & 63, sg = tid >> 6;
         float x = 1.0f;
-        for (int t = 0; t < FP_C; ++t) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int t = 8 * sg + r;
             if (t > i) x *= a_s[t];
-            const float val = t >= i ? x : 0.0f;
+            Gs[t * FP_LC + i] = t >= i ? x : 0.0f;
+        }
+        seg_s[sg * 64 + i] = x;
+    }
+    __syncthreads();
+    {
+        const int i = tid & 63, sg = tid >> 6;
+        float pre = 1.0f;
+        for (int s2 = 0; s2 < sg; ++s2) pre *= seg_s[s2 * 64 + i];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int t = 8 * sg + r;
+            const float val = Gs[t * FP_LC + i] * pre;
             Gs[t * FP_LC + i] = val;
             w.Gam[cc + t * FP_C + i] = val;
         }
-        gt_s[i] = x;
+        if (sg == 7) gt_s[i] = pre * seg_s[7 * 64 + i];
     }
     __syncthreads();
     if (tid < FP_C) {
@@ -896,7 +923,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
                 for (int r = 0; r < 4; ++r) {
                     const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
                     Y[t * FP_LK + f] = acc[x][y][r];
-                    w.Uv[cd + t * FP_D + f] = acc[x][y][r];
+                    st_nt(w.Uv + cd + t * FP_D + f, acc[x][y][r]);
                 }
     }
     __syncthreads();
@@ -913,7 +940,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    w.H[dd + a * FP_D + f] = acc[x][y][r];
+                    st_nt(w.H + dd + a * FP_D + f, acc[x][y][r]);
                 }
     }
     __syncthreads();
@@ -931,7 +958,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
                 for (int r = 0; r < 4; ++r) {
                     const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
                     Y[t * FP_LK + f] = acc[x][y][r];
-                    w.W[cd + t * FP_D + f] = acc[x][y][r];
+                    st_nt(w.W + cd + t * FP_D + f, acc[x][y][r]);
                 }
         fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
     }
@@ -950,7 +977,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    w.Gp[dd + a * FP_D + f] = (a == f ? gC : 0.0f) - acc[x][y][r];
+                    st_nt(w.Gp + dd + a * FP_D + f, (a == f ? gC : 0.0f) - acc[x][y][r]);
                 }
     }
     // Qp = diag(gamma) Q - M W
@@ -966,7 +993,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    w.Qp[cd + t * FP_D + f] = g_s[t] * X[t * FP_LK + f] - acc[x][y][r];
+                    st_nt(w.Qp + cd + t * FP_D + f, g_s[t] * X[t * FP_LK + f] - acc[x][y][r]);
                 }
     }
 }
