@@ -1176,6 +1176,14 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 
     // ---- Y = T^T dU; dv = beta Y
     {
+        float pV[2][2][4];
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pV[g2][y][r] = w.Vu[cd + (rm0 + 4 * l4 + r) * FP_D + 64 * g2 + cn0 + 16 * y + li];
         f32x4 Y0[1][2], Y1[1][2];
         acc_zero(Y0);
         acc_zero(Y1);
@@ -1192,7 +1200,7 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
                     const int t = rm0 + 4 * l4 + r, f = 64 * g2 + cn0 + 16 * y + li;
                     const float yy = g2 ? Y1[0][y][r] : Y0[0][y][r];
                     if (t < valid) dv[rowbase + (long)t * rowstride + f] = b_s[t] * yy;
-                    yv[r] += yy * w.Vu[cd + t * FP_D + f];
+                    yv[r] += yy * pV[g2][y][r];
                 }
         rows_out(yv, pyv + 64 * (wv & 1), rm0, lane);
         __syncthreads();  // every read of dU and T is done
@@ -1210,6 +1218,16 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 
     // ---- dM = tril(dO U^T), dL = -strict_tril(Y U^T) -> GdM, dA (RA), R (RE), row sums of dL Gamma A
     {
+        float pGa[2][4], pAm[2][4], pBm[2][4];
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const long o = cc + (rm0 + 4 * l4 + r) * FP_C + cn0 + 16 * y + li;
+                pGa[y][r] = w.Gam[o];
+                pAm[y][r] = w.Am[o];
+                pBm[y][r] = w.Bm[o];
+            }
         f32x4 Mx[1][2], Lx[1][2];
         acc_zero(Mx);
         acc_zero(Lx);
@@ -1221,13 +1239,12 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int j = rm0 + 4 * l4 + r, i = cn0 + 16 * y + li;
-                const long o = cc + j * FP_C + i;
-                const float g = w.Gam[o], am = w.Am[o], bj = b_s[j];
+                const float g = pGa[y][r], am = pAm[y][r], bj = b_s[j];
                 const float dm = i <= j ? Mx[0][y][r] : 0.0f;
                 const float dl = i < j ? -Lx[0][y][r] : 0.0f;
                 RA[j * FP_LK + i] = g * dm;
                 RA[j * FP_LK + 64 + i] = dl * bj * g;
-                const float dG = dm * w.Bm[o] + dl * bj * am;
+                const float dG = dm * pBm[y][r] + dl * bj * am;
                 RE[j * FP_LC + i] = i < j ? dG * g : 0.0f;
                 pb[r] += dl * g * am;
             }
