@@ -86,17 +86,30 @@ ASCA_DEV void tile_load(float4 (&r)[8 * R / NT], const float* base, long ld, con
     }
 }
 
+// Row offsets (source row * ld) of this thread's mn-rows of a k-contiguous
+// tile; they do not change along K, so they are read once per block.
+template <int R, int NT>
+ASCA_DEV void tile_rows(long (&ro)[8 * R / NT], long ld, const int* rows, long row_off, int mn0, int lim_mn,
+                        int tid) {
+#pragma unroll
+    for (int j = 0; j < 8 * R / NT; ++j) {
+        const int rr = (tid + NT * j) >> 3;
+        ro[j] = rr < lim_mn ? srow(rows, row_off, mn0 + rr) * ld : 0;
+    }
+}
+
 // As tile_load for a tile that lies wholly inside the operand (aligned, no
-// edge): unconditional 16-byte loads.
+// edge): unconditional 16-byte loads; a k-contiguous tile takes its row
+// offsets from tile_rows.
 template <bool KC, int R, int NT>
 ASCA_DEV void tile_load_full(float4 (&r)[8 * R / NT], const float* base, long ld, const int* rows, long row_off,
-                             int mn0, long k0, int tid) {
+                             const long (&ro)[8 * R / NT], int mn0, long k0, int tid) {
 #pragma unroll
     for (int j = 0; j < 8 * R / NT; ++j) {
         const int sl = tid + NT * j;
         if constexpr (KC) {
-            const int rr = sl >> 3, kk = 4 * (sl & 7);
-            r[j] = *reinterpret_cast<const float4*>(base + srow(rows, row_off, mn0 + rr) * ld + k0 + kk);
+            const int kk = 4 * (sl & 7);
+            r[j] = *reinterpret_cast<const float4*>(base + ro[j] + k0 + kk);
         } else {
             const int kr = sl / (R / 4), mm = 4 * (sl % (R / 4));
             r[j] = *reinterpret_cast<const float4*>(base + srow(rows, row_off, k0 + kr) * ld + mn0 + mm);
@@ -255,10 +268,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_k(GemmArgs p) {
     // interior blocks (whole tiles in M and N) load without edge checks,
     // except in a partial last k-tile
     const bool interior = VEC && lim_m >= BM && lim_n >= BN;
+    long roa[8 * BM / NT], rob[8 * BN / NT];
+    if (A_KC) tile_rows<BM, NT>(roa, p.lda, p.a_rows, a_off, m0, lim_m, tid);
+    if (B_KC) tile_rows<BN, NT>(rob, p.ldb, p.b_rows, b_off, n0, lim_n, tid);
     auto load = [&](long k0) {
         if (interior && K_hi - k0 >= GM_BK) {
-            tile_load_full<A_KC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, k0, tid);
-            tile_load_full<B_KC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, k0, tid);
+            tile_load_full<A_KC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, roa, m0, k0, tid);
+            tile_load_full<B_KC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, rob, n0, k0, tid);
         } else {
             tile_load<A_KC, VEC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, m0, lim_m, k0, K_hi - k0, tid);
             tile_load<B_KC, VEC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
