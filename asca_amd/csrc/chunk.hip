@@ -639,9 +639,10 @@ static int chunk_check(int B, int T, int H, int dh, int C) {
 // ---------------------------------------------------------------- fused prep
 // One block per chunk for C = 64, dh = 128: everything of a chunk that does
 // not depend on the state, with the chunk's operands in LDS and every product
-// on the matrix cores through wave_mm.  It writes the same workspace arrays as
-// the separate kernels above (the backward reads them), so both paths are
-// interchangeable.
+// on the matrix cores through wave_mm.  It writes the workspace arrays that
+// the factorised scan (ck_scan2_k), the output kernel and the fused backward
+// read; G' and H of the decomposed path are not formed (the scan works from W
+// and Kt directly).
 constexpr int FP_C = 64, FP_D = 128, FP_LK = FP_D + 4, FP_LC = FP_C + 4, FP_NT = 512;
 constexpr int FP_LDS_F = 3 * FP_C * FP_LK + 2 * FP_C * FP_LC + 5 * FP_C + 8 * FP_C;
 
@@ -764,7 +765,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     extern __shared__ float4 fp_lds4[];
     float* const Ks = reinterpret_cast<float*>(fp_lds4);  // K           [64][132]
     float* const X = Ks + FP_C * FP_LK;                    // Q, then V, then Q
-    float* const Y = X + FP_C * FP_LK;                     // Gamma, then T [64][68]; Uv, then W [64][132]
+    float* const Y = X + FP_C * FP_LK;                     // Gamma, then T [64][68]; then W [64][132]
     float* const Ls = Y + FP_C * FP_LK;                    // L, then T  [64][68]
     float* const Ms = Ls + FP_C * FP_LC;                   // M          [64][68]
     float* const a_s = Ms + FP_C * FP_LC;
@@ -909,7 +910,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         w.Tm[cc + e] = t;
     }
     __syncthreads();
-    // Uv = T diag(beta) V  -> Y and the workspace
+    // Uv = T diag(beta) V -> the workspace
     {
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
         f32x4 acc[2][2];
@@ -922,28 +923,10 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    Y[t * FP_LK + f] = acc[x][y][r];
                     st_nt(w.Uv + cd + t * FP_D + f, acc[x][y][r]);
                 }
     }
-    __syncthreads();
-    // H = Kt^T Uv
-    {
-        const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
-        f32x4 acc[2][4];
-        acc_zero(acc);
-        wave_mm<2, 4, false, false, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-            for (int y = 0; y < 4; ++y)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    st_nt(w.H + dd + a * FP_D + f, acc[x][y][r]);
-                }
-    }
-    __syncthreads();
+    __syncthreads();  // every read of V is done before Q comes back into X
     // W = T diag(beta gamma) K -> Y; Q back into X
     {
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
@@ -963,23 +946,6 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
     }
     __syncthreads();
-    // G' = gamma_C I - Kt^T W
-    {
-        const int m0 = 32 * (wv >> 1), n0 = 64 * (wv & 1);
-        f32x4 acc[2][4];
-        acc_zero(acc);
-        wave_mm<2, 4, false, false, false, false, true, false>(acc, 0, FP_C, Ks, FP_LK, gt_s, Y, FP_LK, nullptr, m0, n0, lane);
-        const float gC = g_s[FP_C - 1];
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-            for (int y = 0; y < 4; ++y)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int a = m0 + 16 * x + 4 * l4 + r, f = n0 + 16 * y + li;
-                    st_nt(w.Gp + dd + a * FP_D + f, (a == f ? gC : 0.0f) - acc[x][y][r]);
-                }
-    }
     // Qp = diag(gamma) Q - M W
     {
         const int m0 = 32 * (wv >> 2), n0 = 32 * (wv & 3);
@@ -1489,6 +1455,157 @@ __global__ __launch_bounds__(FO_NT) void ck_E_k(const uint16_t* __restrict__ d_o
                 w.E[dd + (m0 + 16 * x + 4 * l4 + r) * FP_D + n0 + 16 * y + li] = acc[x][y][r];
 }
 
+// State scan of the fused C = 64, dh = 128 path, from the per-chunk factors
+// instead of G' = gamma_C I - Kt^T W and H = Kt^T Uv (Kt = diag(Gamma[C-1,:]) K):
+//   forward  (TR = false): X_0 = 0,       X_{c+1} = gamma_C X_c + Kt^T (Uv - W X_c)
+//   backward (TR = true):  X_{NC-1} = 0,  X_{c-1} = gamma_C X_c + E_c - W^T (Kt X_c)
+// One block per (unit, 64-column half), 8 waves; per chunk two dependent
+// products, 64 x 64 x 128 (Z) and 128 x 64 x 64 (the update).  W and Kt of the
+// next chunk (and Uv or E at this lane's outputs) are prefetched into
+// registers during the products.  LDS: W, Kt [64][132], X^T [64][132], Z [64][68].
+constexpr int S2_LDS_F = 3 * FP_C * FP_LK + FP_C * FP_LC;
+
+template <bool TR>
+__global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict__ X, int NC) {
+    extern __shared__ float4 s2_lds4[];
+    float* const Ws = reinterpret_cast<float*>(s2_lds4);  // W_c   [t][a]
+    float* const Ks = Ws + FP_C * FP_LK;                  // Kt_c  [t][a]
+    float* const Xt = Ks + FP_C * FP_LK;                  // X^T   [n][a], this block's 64 columns
+    float* const Zs = Xt + FP_C * FP_LK;                  // Z     [t][n]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = blockIdx.x >> 1;
+    const int col0 = (blockIdx.x & 1) * 64;
+    const long DD = (long)FP_D * FP_D, CD = (long)FP_C * FP_D;
+    float* const Xu = X + u * NC * DD;
+    const int m1 = 16 * (wv >> 1), n1 = 32 * (wv & 1);  // step 1 tile: t x n
+    const int m2 = 32 * (wv >> 1), n2 = 32 * (wv & 1);  // step 2 tile: a x n
+    const float* const A1s = TR ? Ks : Ws;
+    const float* const A2s = TR ? Ws : Ks;
+
+    // the starting slot is zero
+    const int c_first = TR ? NC - 1 : 0;
+    for (int e = tid; e < 64 * FP_D; e += FP_NT) {
+        const int nn = e & 63, a = e >> 6;
+        Xt[nn * FP_LK + a] = 0.0f;
+        Xu[(long)c_first * DD + (long)a * FP_D + col0 + nn] = 0.0f;
+    }
+    if (NC < 2) return;
+
+    // chunk n's W, K rows and Gamma[C-1, :] of this thread, gamma_C, and the
+    // additive term at this lane's outputs (Uv forward, E backward), held in
+    // named registers (arrays carried across the chunk loop go to scratch)
+    float4 w0, w1, w2, w3, k0, k1, k2, k3;
+    float g0, g1, g2, g3, gC = 0.0f;
+    float r1[2][4], r2[2][2][4];
+#define S2_ROW(i) ((tid + (i) * FP_NT) >> 5)
+#define S2_COL(i) (4 * ((tid + (i) * FP_NT) & 31))
+#define S2_STAGE(nn)                                                                                   \
+    do {                                                                                               \
+        const long n_ = (nn);                                                                          \
+        const float* W_ = w.W + n_ * CD;                                                               \
+        const float* K_ = w.Ku + n_ * CD;                                                              \
+        w0 = *reinterpret_cast<const float4*>(W_ + S2_ROW(0) * FP_D + S2_COL(0));                      \
+        w1 = *reinterpret_cast<const float4*>(W_ + S2_ROW(1) * FP_D + S2_COL(1));                      \
+        w2 = *reinterpret_cast<const float4*>(W_ + S2_ROW(2) * FP_D + S2_COL(2));                      \
+        w3 = *reinterpret_cast<const float4*>(W_ + S2_ROW(3) * FP_D + S2_COL(3));                      \
+        k0 = *reinterpret_cast<const float4*>(K_ + S2_ROW(0) * FP_D + S2_COL(0));                      \
+        k1 = *reinterpret_cast<const float4*>(K_ + S2_ROW(1) * FP_D + S2_COL(1));                      \
+        k2 = *reinterpret_cast<const float4*>(K_ + S2_ROW(2) * FP_D + S2_COL(2));                      \
+        k3 = *reinterpret_cast<const float4*>(K_ + S2_ROW(3) * FP_D + S2_COL(3));                      \
+        g0 = w.gt[n_ * FP_C + S2_ROW(0)];                                                              \
+        g1 = w.gt[n_ * FP_C + S2_ROW(1)];                                                              \
+        g2 = w.gt[n_ * FP_C + S2_ROW(2)];                                                              \
+        g3 = w.gt[n_ * FP_C + S2_ROW(3)];                                                              \
+        gC = w.gC[n_];                                                                                 \
+        if (!TR) {                                                                                     \
+            _Pragma("unroll") for (int y = 0; y < 2; ++y) _Pragma("unroll") for (int r = 0; r < 4; ++r) \
+                r1[y][r] = w.Uv[n_ * CD + (m1 + 4 * l4 + r) * FP_D + col0 + n1 + 16 * y + li];         \
+        } else {                                                                                       \
+            _Pragma("unroll") for (int x = 0; x < 2; ++x) _Pragma("unroll") for (int y = 0; y < 2; ++y) \
+                _Pragma("unroll") for (int r = 0; r < 4; ++r) r2[x][y][r] =                            \
+                    w.E[n_ * DD + (m2 + 16 * x + 4 * l4 + r) * FP_D + col0 + n2 + 16 * y + li];        \
+        }                                                                                              \
+    } while (0)
+#define S2_PUT(i, wi, ki, gi)                                                                          \
+    do {                                                                                               \
+        *reinterpret_cast<float4*>(Ws + S2_ROW(i) * FP_LK + S2_COL(i)) = (wi);                         \
+        *reinterpret_cast<float4*>(Ks + S2_ROW(i) * FP_LK + S2_COL(i)) =                               \
+            make_float4((gi) * (ki).x, (gi) * (ki).y, (gi) * (ki).z, (gi) * (ki).w);                   \
+    } while (0)
+    int c = c_first;
+    S2_STAGE(u * NC + c);
+    for (int s = 0; s < NC - 1; ++s) {
+        const int cn = TR ? c - 1 : c + 1;  // output slot
+        __syncthreads();                     // the previous chunk's readers of Ws, Ks, Zs are done
+        S2_PUT(0, w0, k0, g0);
+        S2_PUT(1, w1, k1, g1);
+        S2_PUT(2, w2, k2, g2);
+        S2_PUT(3, w3, k3, g3);
+        const float gCc = gC;
+        float z1[2][4], z2[2][2][4];
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) z1[y][r] = TR ? 0.0f : r1[y][r];
+        if constexpr (TR) {
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) z2[x][y][r] = r2[x][y][r];
+        }
+        __syncthreads();  // Ws, Ks and X^T ready
+        if (s + 1 < NC - 1) S2_STAGE(u * NC + cn);
+        // step 1: Z = R1 - A1 X  (forward: Uv - W X; backward: -Kt X)
+        {
+            f32x4 acc[1][2];
+            acc_zero(acc);
+            wave_mm<1, 2, true, false, true, false>(acc, 0, FP_D, A1s, FP_LK, nullptr, Xt, FP_LK, nullptr, m1, n1,
+                                                    lane);
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    Zs[(m1 + 4 * l4 + r) * FP_LC + n1 + 16 * y + li] = z1[y][r] - acc[0][y][r];
+        }
+        __syncthreads();  // Z ready
+        // step 2: X' = gamma_C X + R2 + A2^T Z  (R2 = E in the backward); each
+        // wave reads and then overwrites only its own elements of X^T
+        {
+            f32x4 acc[2][2];
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float xv = Xt[(n2 + 16 * y + li) * FP_LK + m2 + 16 * x + 4 * l4 + r];
+                        acc[x][y][r] = TR ? gCc * xv + z2[x][y][r] : gCc * xv;
+                    }
+            wave_mm<2, 2, false, false, false, false>(acc, 0, FP_C, A2s, FP_LK, nullptr, Zs, FP_LC, nullptr, m2, n2,
+                                                      lane);
+            float* const Xn = Xu + (long)cn * DD;
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int a = m2 + 16 * x + 4 * l4 + r, nn = n2 + 16 * y + li;
+                        Xt[nn * FP_LK + a] = acc[x][y][r];
+                        Xn[(long)a * FP_D + col0 + nn] = acc[x][y][r];
+                    }
+        }
+        c = cn;
+    }
+#undef S2_ROW
+#undef S2_COL
+#undef S2_STAGE
+#undef S2_PUT
+}
+
 // The state scan over chunks: the persistent kernel for dh = 128, else one
 // batched GEMM launch per chunk.
 static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, float* X, hipStream_t st) {
@@ -1525,17 +1642,38 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
     return ASCA_OK;
 }
 
+// The factorised state scan of the fused C = 64, dh = 128 path.
+static int scan2(bool tr, const ChunkDims& d, const ChunkWs& w, float* X, hipStream_t st) {
+    constexpr size_t lds = (size_t)S2_LDS_F * sizeof(float);
+    static bool attr[2] = {false, false};
+    const void* fn = tr ? reinterpret_cast<const void*>(&ck_scan2_k<true>)
+                        : reinterpret_cast<const void*>(&ck_scan2_k<false>);
+    if (!attr[tr]) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr[tr] = true;
+    }
+    int rc = pre_launch("chunk_scan2");
+    if (rc) return rc;
+    if (tr)
+        hipLaunchKernelGGL(ck_scan2_k<true>, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, X, d.NC);
+    else
+        hipLaunchKernelGGL(ck_scan2_k<false>, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, X, d.NC);
+    return post_launch("chunk_scan2");
+}
+
 // The state scan and the outputs O = Qp S + M Uv.
 static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, float* o, hipStream_t st) {
     const int C = d.C, dh = d.dh;
     int rc;
-    // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
-    if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
     if (C == FP_C && dh == FP_D) {
+        if ((rc = scan2(false, d, w, w.S, st))) return rc;
         CK_LAUNCH_LDS("chunk_out_fused", ck_out_fused_k, dim3((unsigned)d.N), dim3(FO_NT),
                   (size_t)FO_LDS_F * sizeof(float), d.T, d.H, d.NC, w, o);
         return ASCA_OK;
     }
+    // state scan over chunks: S_0 = 0, S_{c+1} = G'_c S_c + H_c
+    if ((rc = scan(false, d, w.Gp, w.H, w.S, st))) return rc;
     if ((rc = bgemm(0, 0, C, dh, dh, 1.f, w.Qp, dh, d.CD, w.S, dh, d.DD, 0.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
                     "chunk_O1")) ||
         (rc = bgemm(0, 0, C, dh, C, 1.f, w.Mm, C, d.CC, w.Uv, dh, d.CD, 1.f, w.Ou, dh, d.CD, nullptr, 0, d.N, st,
@@ -1631,7 +1769,7 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
         // E, the reverse scan, then one fused kernel for all per-chunk gradients
         CK_LAUNCH_LDS("chunk_E", ck_E_k, dim3((unsigned)d.N), dim3(FO_NT), (size_t)FO_LDS_F * sizeof(float), d_o, T, H,
                   d.NC, w);
-        if ((rc = scan(true, d, w.Gp, w.E, w.dSp, st))) return rc;
+        if ((rc = scan2(true, d, w, w.dSp, st))) return rc;
         constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
         static bool attr = false;
         if (!attr) {
