@@ -74,6 +74,10 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
         return p;
     };
     const size_t N = d.N, CD = d.CD, CC = d.CC, DD = d.DD, C = d.C;
+    // the fused C = 64, dh = 128 kernels need only the forward factors, the
+    // states and E; the decomposed path's other regions are left out
+    const bool fused = d.C == 64 && d.dh == 128;
+    auto opt = [&](size_t n) -> float* { return fused ? nullptr : take(n); };
     w.Qu = take(N * CD);
     w.Ku = take(N * CD);
     w.Vu = take(N * CD);
@@ -90,33 +94,33 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     w.Uv = take(N * CD);
     w.W = take(N * CD);
     w.Qp = take(N * CD);
-    w.Kt = take(N * CD);
-    w.Gp = take(N * DD);
+    w.Kt = opt(N * CD);
+    w.Gp = opt(N * DD);
     w.S = take(N * DD);
-    w.Vb = take(N * CD);
-    w.Kbg = take(N * CD);
-    w.Qg = take(N * CD);
-    w.H = take(N * DD);
-    w.Ou = take(N * CD);
-    w.dOu = take(N * CD);
-    w.dOg = take(N * CD);
+    w.Vb = opt(N * CD);
+    w.Kbg = opt(N * CD);
+    w.Qg = opt(N * CD);
+    w.H = opt(N * DD);
+    w.Ou = opt(N * CD);
+    w.dOu = opt(N * CD);
+    w.dOg = opt(N * CD);
     w.E = take(N * DD);
     w.dSp = take(N * DD);
-    w.Uu = take(N * CD);
-    w.dU = take(N * CD);
-    w.dMr = take(N * CC);
-    w.dW = take(N * CD);
-    w.Y = take(N * CD);
-    w.Z = take(N * CD);
-    w.dKt = take(N * CD);
-    w.Pqs = take(N * CD);
-    w.dLs = take(N * CC);
-    w.GdM = take(N * CC);
-    w.dAs = take(N * CC);
-    w.dqu = take(N * CD);
-    w.dku = take(N * CD);
-    w.dal = take(N * C);
-    w.dbe = take(N * C);
+    w.Uu = opt(N * CD);
+    w.dU = opt(N * CD);
+    w.dMr = opt(N * CC);
+    w.dW = opt(N * CD);
+    w.Y = opt(N * CD);
+    w.Z = opt(N * CD);
+    w.dKt = opt(N * CD);
+    w.Pqs = opt(N * CD);
+    w.dLs = opt(N * CC);
+    w.GdM = opt(N * CC);
+    w.dAs = opt(N * CC);
+    w.dqu = opt(N * CD);
+    w.dku = opt(N * CD);
+    w.dal = opt(N * C);
+    w.dbe = opt(N * C);
     w.total = off;
     return w;
 }
