@@ -75,7 +75,7 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     };
     const size_t N = d.N, CD = d.CD, CC = d.CC, DD = d.DD, C = d.C;
     // the fused C = 64, dh = 128 kernels need only the forward factors, the
-    // states and E; the decomposed path's other regions are left out
+    // states, U and E; the decomposed path's other regions are left out
     const bool fused = d.C == 64 && d.dh == 128;
     auto opt = [&](size_t n) -> float* { return fused ? nullptr : take(n); };
     w.Qu = take(N * CD);
@@ -106,7 +106,7 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     w.dOg = opt(N * CD);
     w.E = take(N * DD);
     w.dSp = take(N * DD);
-    w.Uu = opt(N * CD);
+    w.Uu = take(N * CD);
     w.dU = opt(N * CD);
     w.dMr = opt(N * CC);
     w.dW = opt(N * CD);
@@ -1087,39 +1087,25 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         *reinterpret_cast<uint2*>(Ob + t * FB_LB + f) = x;
     }
 
-    // ---- U = Uv - W S and dU = diag(gt) K dS' + M^T dO, over the two row halves of S, dS'
-    f32x4 U0[1][2], U1[1][2], D0[1][2], D1[1][2];
-    acc_zero(U0);
-    acc_zero(U1);
+    // ---- dU = diag(gt) K dS' + M^T dO over the two row halves of dS'; U = Uv - W S
+    // was stored by the forward scan
+    f32x4 D0[1][2], D1[1][2];
     acc_zero(D0);
     acc_zero(D1);
     float fro = 0.0f;
+    fb_sq_f32(w.Mm + cc, FP_C, RE, tid);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
-            const long o = dd + (long)(64 * hh + r) * FP_D + f;
-            const float4 sv = *reinterpret_cast<const float4*>(w.S + o);
-            const float4 gv = *reinterpret_cast<const float4*>(w.dSp + o);
-            *reinterpret_cast<float4*>(RA + r * FP_LK + f) = sv;
-            *reinterpret_cast<float4*>(RB + r * FP_LK + f) = gv;
-            fro += (sv.x * gv.x + sv.y * gv.y) + (sv.z * gv.z + sv.w * gv.w);
-        }
-        fb_sq_f32(w.W + cd + 64 * hh, FP_D, RE, tid);
+        fb_rows_f32(w.dSp + dd + 64 * hh * FP_D, RB, tid);
         __syncthreads();
-        wave_mm<1, 2, true, false, false, false>(U0, 0, 64, RE, FP_LC, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
-        wave_mm<1, 2, true, false, false, false>(U1, 0, 64, RE, FP_LC, nullptr, RA, FP_LK, nullptr, rm0, 64 + cn0,
-                                                 lane);
         wave_mm<1, 2, true, true, false, false>(D0, 0, 64, Kb + 64 * hh, FB_LB, nullptr, RB, FP_LK, nullptr, rm0, cn0,
                                                 lane);
         wave_mm<1, 2, true, true, false, false>(D1, 0, 64, Kb + 64 * hh, FB_LB, nullptr, RB, FP_LK, nullptr, rm0,
                                                 64 + cn0, lane);
         __syncthreads();
     }
-    fb_sq_f32(w.Mm + cc, FP_C, RE, tid);
     fb_sq_f32(w.Tm + cc, FP_C, RA, tid);
-    __syncthreads();
+    fb_rows_f32(w.Uu + cd, RB, tid);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const float g = gt_s[rm0 + 4 * l4 + r];
@@ -1138,8 +1124,6 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = rm0 + 4 * l4 + r, f = 64 * g2 + cn0 + 16 * y + li;
-                const float pu = g2 ? U1[0][y][r] : U0[0][y][r];
-                RB[t * FP_LK + f] = w.Uv[cd + t * FP_D + f] - pu;
                 RC[t * FP_LK + f] = g2 ? D1[0][y][r] : D0[0][y][r];
             }
     __syncthreads();
@@ -1291,7 +1275,16 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         wave_mm<1, 2, true, false, true, false>(Zx, 0, FP_D, RC, FP_LK, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
         wave_mm<1, 2, true, true, true, false>(Px, 0, FP_D, Ob, FB_LB, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
         __syncthreads();
-        fb_rows_f32(w.dSp + dd + 64 * hh * FP_D, RA, tid);
+        // dS' half over the S half, <S, dS'> on the way (each thread reads
+        // the S elements it then overwrites)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
+            const float4 gv = *reinterpret_cast<const float4*>(w.dSp + dd + (long)(64 * hh + r) * FP_D + f);
+            const float4 sv = *reinterpret_cast<const float4*>(RA + r * FP_LK + f);
+            fro += (sv.x * gv.x + sv.y * gv.y) + (sv.z * gv.z + sv.w * gv.w);
+            *reinterpret_cast<float4*>(RA + r * FP_LK + f) = gv;
+        }
         __syncthreads();
         wave_mm<1, 2, true, false, true, false>(Tx, 0, FP_D, RB, FP_LK, nullptr, RA, FP_LK, nullptr, rm0, cn0, lane);
 #pragma unroll
@@ -1463,6 +1456,7 @@ __global__ __launch_bounds__(FO_NT) void ck_E_k(const uint16_t* __restrict__ d_o
 // instead of G' = gamma_C I - Kt^T W and H = Kt^T Uv (Kt = diag(Gamma[C-1,:]) K):
 //   forward  (TR = false): X_0 = 0,       X_{c+1} = gamma_C X_c + Kt^T (Uv - W X_c)
 //   backward (TR = true):  X_{NC-1} = 0,  X_{c-1} = gamma_C X_c + E_c - W^T (Kt X_c)
+// The forward also stores U_c = Uv - W X_c of every chunk for the backward.
 // One block per (unit, 64-column half), 8 waves; per chunk two dependent
 // products, 64 x 64 x 128 (Z) and 128 x 64 x 64 (the update).  W and Kt of the
 // next chunk (and Uv or E at this lane's outputs) are prefetched into
@@ -1494,7 +1488,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
         Xt[nn * FP_LK + a] = 0.0f;
         Xu[(long)c_first * DD + (long)a * FP_D + col0 + nn] = 0.0f;
     }
-    if (NC < 2) return;
+    if (TR && NC < 2) return;  // the forward still stores U of a single chunk
 
     // chunk n's W, K rows and Gamma[C-1, :] of this thread, gamma_C, and the
     // additive term at this lane's outputs (Uv forward, E backward), held in
@@ -1539,7 +1533,8 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     } while (0)
     int c = c_first;
     S2_STAGE(u * NC + c);
-    for (int s = 0; s < NC - 1; ++s) {
+    // the forward also runs step 1 of the last chunk: its U goes to the backward
+    for (int s = 0; s < (TR ? NC - 1 : NC); ++s) {
         const int cn = TR ? c - 1 : c + 1;  // output slot
         __syncthreads();                     // the previous chunk's readers of Ws, Ks, Zs are done
         S2_PUT(0, w0, k0, g0);
@@ -1561,19 +1556,25 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
                     for (int r = 0; r < 4; ++r) z2[x][y][r] = r2[x][y][r];
         }
         __syncthreads();  // Ws, Ks and X^T ready
-        if (s + 1 < NC - 1) S2_STAGE(u * NC + cn);
+        if (s + 1 < (TR ? NC - 1 : NC)) S2_STAGE(u * NC + cn);
         // step 1: Z = R1 - A1 X  (forward: Uv - W X; backward: -Kt X)
         {
             f32x4 acc[1][2];
             acc_zero(acc);
             wave_mm<1, 2, true, false, true, false>(acc, 0, FP_D, A1s, FP_LK, nullptr, Xt, FP_LK, nullptr, m1, n1,
                                                     lane);
+            float* const Ug = w.Uu + (u * NC + c) * CD;
 #pragma unroll
             for (int y = 0; y < 2; ++y)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    Zs[(m1 + 4 * l4 + r) * FP_LC + n1 + 16 * y + li] = z1[y][r] - acc[0][y][r];
+                for (int r = 0; r < 4; ++r) {
+                    const int t = m1 + 4 * l4 + r, nn = n1 + 16 * y + li;
+                    const float z = z1[y][r] - acc[0][y][r];
+                    Zs[t * FP_LC + nn] = z;
+                    if (!TR) Ug[t * FP_D + col0 + nn] = z;  // U = Uv - W S of chunk c
+                }
         }
+        if (!TR && s == NC - 1) break;
         __syncthreads();  // Z ready
         // step 2: X' = gamma_C X + R2 + A2^T Z  (R2 = E in the backward); each
         // wave reads and then overwrites only its own elements of X^T
