@@ -75,7 +75,7 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     };
     const size_t N = d.N, CD = d.CD, CC = d.CC, DD = d.DD, C = d.C;
     // the fused C = 64, dh = 128 kernels need only the forward factors, the
-    // states, U and E; the decomposed path's other regions are left out
+    // states and U; the decomposed path's other regions are left out
     const bool fused = d.C == 64 && d.dh == 128;
     auto opt = [&](size_t n) -> float* { return fused ? nullptr : take(n); };
     w.Qu = take(N * CD);
@@ -104,7 +104,7 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     w.Ou = opt(N * CD);
     w.dOu = opt(N * CD);
     w.dOg = opt(N * CD);
-    w.E = take(N * DD);
+    w.E = opt(N * DD);
     w.dSp = take(N * DD);
     w.Uu = take(N * CD);
     w.dU = opt(N * CD);
@@ -1360,12 +1360,11 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------- outputs and E
-// O = Qp S + M Uv for one chunk (C = 64, dh = 128), written token-major; and
-// E = Qp^T dO for the reverse scan, reading the bf16 dO directly.  256 threads,
-// 51 KB of LDS (three blocks per CU).
+// O = Qp S + M Uv for one chunk (C = 64, dh = 128), written token-major.  256
+// threads, 51 KB of LDS (three blocks per CU).
 constexpr int FO_NT = 256;
 constexpr int FO_LDS_F = FP_C * FP_LC + FP_C * FP_LK;
-static_assert(FO_LDS_F * 4 <= 65536 && FP_C * FP_LK + FP_C * FB_LB / 2 <= FO_LDS_F, "LDS of the out / E kernels");
+static_assert(FO_LDS_F * 4 <= 65536, "LDS of the output kernel");
 
 __global__ __launch_bounds__(FO_NT) void ck_out_fused_k(int T, int H, int NC, ChunkWs w, float* __restrict__ o) {
     extern __shared__ float4 fo_lds4[];
@@ -1415,55 +1414,19 @@ __global__ __launch_bounds__(FO_NT) void ck_out_fused_k(int T, int H, int NC, Ch
             }
 }
 
-__global__ __launch_bounds__(FO_NT) void ck_E_k(const uint16_t* __restrict__ d_o, int T, int H, int NC, ChunkWs w) {
-    extern __shared__ float4 fo_lds4[];
-    float* const Qs = reinterpret_cast<float*>(fo_lds4);                 // Qp [t][a] (stride FP_LK)
-    uint16_t* const Ob = reinterpret_cast<uint16_t*>(Qs + FP_C * FP_LK);  // dO bf16 [t][f] (stride FB_LB)
-    const long n = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int li = lane & 15, l4 = lane >> 4;
-    const long u = n / NC;
-    const int c = (int)(n - u * NC);
-    const int b = (int)(u / H), h = (int)(u - (long)b * H);
-    const int t0 = c * FP_C;
-    const int valid = min(FP_C, T - t0);
-    const long rowbase = ((long)b * T + t0) * H * FP_D + (long)h * FP_D;
-    const long rowstride = (long)H * FP_D;
-    const long cd = n * FP_C * FP_D, dd = n * FP_D * FP_D;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int e = tid + i * FO_NT, r = e >> 5, f = 4 * (e & 31);
-        *reinterpret_cast<float4*>(Qs + r * FP_LK + f) = *reinterpret_cast<const float4*>(w.Qp + cd + r * FP_D + f);
-        uint2 x = make_uint2(0u, 0u);
-        if (r < valid) x = *reinterpret_cast<const uint2*>(d_o + rowbase + (long)r * rowstride + f);
-        *reinterpret_cast<uint2*>(Ob + r * FB_LB + f) = x;
-    }
-    __syncthreads();
-    const int m0 = 64 * (wv >> 1), n0 = 64 * (wv & 1);
-    f32x4 acc[4][4];
-    acc_zero(acc);
-    wave_mm<4, 4, false, false, false, true>(acc, 0, FP_C, Qs, FP_LK, nullptr, Ob, FB_LB, nullptr, m0, n0, lane);
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                w.E[dd + (m0 + 16 * x + 4 * l4 + r) * FP_D + n0 + 16 * y + li] = acc[x][y][r];
-}
 
-// State scan of the fused C = 64, dh = 128 path, from the per-chunk factors
-// instead of G' = gamma_C I - Kt^T W and H = Kt^T Uv (Kt = diag(Gamma[C-1,:]) K):
-//   forward  (TR = false): X_0 = 0,       X_{c+1} = gamma_C X_c + Kt^T (Uv - W X_c)
-//   backward (TR = true):  X_{NC-1} = 0,  X_{c-1} = gamma_C X_c + E_c - W^T (Kt X_c)
-// The forward also stores U_c = Uv - W X_c of every chunk for the backward.
+// Forward state scan of the fused C = 64, dh = 128 path, from the per-chunk
+// factors instead of G' = gamma_C I - Kt^T W and H = Kt^T Uv
+// (Kt = diag(Gamma[C-1,:]) K):
+//   X_0 = 0,  X_{c+1} = gamma_C X_c + Kt^T (Uv - W X_c)
+// It also stores U_c = Uv - W X_c of every chunk (the last included) for the
+// backward.
 // One block per (unit, 64-column half), 8 waves; per chunk two dependent
 // products, 64 x 64 x 128 (Z) and 128 x 64 x 64 (the update).  W and Kt of the
 // next chunk (and Uv or E at this lane's outputs) are prefetched into
 // registers during the products.  LDS: W, Kt [64][132], X^T [64][132], Z [64][68].
 constexpr int S2_LDS_F = 3 * FP_C * FP_LK + FP_C * FP_LC;
 
-template <bool TR>
 __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict__ X, int NC) {
     extern __shared__ float4 s2_lds4[];
     float* const Ws = reinterpret_cast<float*>(s2_lds4);  // W_c   [t][a]
@@ -1478,24 +1441,23 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     float* const Xu = X + u * NC * DD;
     const int m1 = 16 * (wv >> 1), n1 = 32 * (wv & 1);  // step 1 tile: t x n
     const int m2 = 32 * (wv >> 1), n2 = 32 * (wv & 1);  // step 2 tile: a x n
-    const float* const A1s = TR ? Ks : Ws;
-    const float* const A2s = TR ? Ws : Ks;
+    const float* const A1s = Ws;
+    const float* const A2s = Ks;
 
     // the starting slot is zero
-    const int c_first = TR ? NC - 1 : 0;
+    const int c_first = 0;
     for (int e = tid; e < 64 * FP_D; e += FP_NT) {
         const int nn = e & 63, a = e >> 6;
         Xt[nn * FP_LK + a] = 0.0f;
         Xu[(long)c_first * DD + (long)a * FP_D + col0 + nn] = 0.0f;
     }
-    if (TR && NC < 2) return;  // the forward still stores U of a single chunk
 
-    // chunk n's W, K rows and Gamma[C-1, :] of this thread, gamma_C, and the
-    // additive term at this lane's outputs (Uv forward, E backward), held in
-    // named registers (arrays carried across the chunk loop go to scratch)
+    // chunk n's W, K rows and Gamma[C-1, :] of this thread, gamma_C and Uv at
+    // this lane's step-1 outputs, held in named registers (arrays carried
+    // across the chunk loop go to scratch)
     float4 w0, w1, w2, w3, k0, k1, k2, k3;
     float g0, g1, g2, g3, gC = 0.0f;
-    float r1[2][4], r2[2][2][4];
+    float r1[2][4];
 #define S2_ROW(i) ((tid + (i) * FP_NT) >> 5)
 #define S2_COL(i) (4 * ((tid + (i) * FP_NT) & 31))
 #define S2_STAGE(nn)                                                                                   \
@@ -1516,14 +1478,8 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
         g2 = w.gt[n_ * FP_C + S2_ROW(2)];                                                              \
         g3 = w.gt[n_ * FP_C + S2_ROW(3)];                                                              \
         gC = w.gC[n_];                                                                                 \
-        if (!TR) {                                                                                     \
-            _Pragma("unroll") for (int y = 0; y < 2; ++y) _Pragma("unroll") for (int r = 0; r < 4; ++r) \
-                r1[y][r] = w.Uv[n_ * CD + (m1 + 4 * l4 + r) * FP_D + col0 + n1 + 16 * y + li];         \
-        } else {                                                                                       \
-            _Pragma("unroll") for (int x = 0; x < 2; ++x) _Pragma("unroll") for (int y = 0; y < 2; ++y) \
-                _Pragma("unroll") for (int r = 0; r < 4; ++r) r2[x][y][r] =                            \
-                    w.E[n_ * DD + (m2 + 16 * x + 4 * l4 + r) * FP_D + col0 + n2 + 16 * y + li];        \
-        }                                                                                              \
+        _Pragma("unroll") for (int y = 0; y < 2; ++y) _Pragma("unroll") for (int r = 0; r < 4; ++r)     \
+            r1[y][r] = w.Uv[n_ * CD + (m1 + 4 * l4 + r) * FP_D + col0 + n1 + 16 * y + li];             \
     } while (0)
 #define S2_PUT(i, wi, ki, gi)                                                                          \
     do {                                                                                               \
@@ -1533,31 +1489,23 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     } while (0)
     int c = c_first;
     S2_STAGE(u * NC + c);
-    // the forward also runs step 1 of the last chunk: its U goes to the backward
-    for (int s = 0; s < (TR ? NC - 1 : NC); ++s) {
-        const int cn = TR ? c - 1 : c + 1;  // output slot
+    // step 1 of the last chunk runs too: its U goes to the backward
+    for (int s = 0; s < NC; ++s) {
+        const int cn = c + 1;  // output slot
         __syncthreads();                     // the previous chunk's readers of Ws, Ks, Zs are done
         S2_PUT(0, w0, k0, g0);
         S2_PUT(1, w1, k1, g1);
         S2_PUT(2, w2, k2, g2);
         S2_PUT(3, w3, k3, g3);
         const float gCc = gC;
-        float z1[2][4], z2[2][2][4];
+        float z1[2][4];
 #pragma unroll
         for (int y = 0; y < 2; ++y)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) z1[y][r] = TR ? 0.0f : r1[y][r];
-        if constexpr (TR) {
-#pragma unroll
-            for (int x = 0; x < 2; ++x)
-#pragma unroll
-                for (int y = 0; y < 2; ++y)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) z2[x][y][r] = r2[x][y][r];
-        }
+            for (int r = 0; r < 4; ++r) z1[y][r] = r1[y][r];
         __syncthreads();  // Ws, Ks and X^T ready
-        if (s + 1 < (TR ? NC - 1 : NC)) S2_STAGE(u * NC + cn);
-        // step 1: Z = R1 - A1 X  (forward: Uv - W X; backward: -Kt X)
+        if (s + 1 < NC) S2_STAGE(u * NC + cn);
+        // step 1: Z = U = Uv - W X
         {
             f32x4 acc[1][2];
             acc_zero(acc);
@@ -1571,13 +1519,13 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
                     const int t = m1 + 4 * l4 + r, nn = n1 + 16 * y + li;
                     const float z = z1[y][r] - acc[0][y][r];
                     Zs[t * FP_LC + nn] = z;
-                    if (!TR) Ug[t * FP_D + col0 + nn] = z;  // U = Uv - W S of chunk c
+                    Ug[t * FP_D + col0 + nn] = z;  // U = Uv - W S of chunk c
                 }
         }
-        if (!TR && s == NC - 1) break;
+        if (s == NC - 1) break;
         __syncthreads();  // Z ready
-        // step 2: X' = gamma_C X + R2 + A2^T Z  (R2 = E in the backward); each
-        // wave reads and then overwrites only its own elements of X^T
+        // step 2: X' = gamma_C X + Kt^T Z; each wave reads and then overwrites
+        // only its own elements of X^T
         {
             f32x4 acc[2][2];
 #pragma unroll
@@ -1587,7 +1535,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float xv = Xt[(n2 + 16 * y + li) * FP_LK + m2 + 16 * x + 4 * l4 + r];
-                        acc[x][y][r] = TR ? gCc * xv + z2[x][y][r] : gCc * xv;
+                        acc[x][y][r] = gCc * xv;
                     }
             wave_mm<2, 2, false, false, false, false>(acc, 0, FP_C, A2s, FP_LK, nullptr, Zs, FP_LC, nullptr, m2, n2,
                                                       lane);
@@ -1609,6 +1557,158 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
 #undef S2_COL
 #undef S2_STAGE
 #undef S2_PUT
+}
+
+// Reverse scan of the fused path with E_c = Qp_c^T dO_c formed in place:
+//   X_{NC-1} = 0,  X_{c-1} = gamma_C X_c + Qp_c^T dO_c - W_c^T diag(Gamma[C-1,:]) K_c X_c
+// E is the same 128 x 64 x 64 shape as the update product, so it goes into
+// the same accumulators.  K is staged as bf16 (exact: a bf16 input) and
+// Gamma[C-1, :] is applied to the rows of K X; the block's 64 columns of dO
+// come straight from the bf16 input (zero past T).  LDS: W, Qp, X^T f32
+// [64][132], Z [64][68], K bf16 [64][136], dO bf16 [64][72], Gamma[C-1, :].
+constexpr int S3_LB = 64 + 8;
+constexpr int S3_LDS_F = 3 * FP_C * FP_LK + FP_C * FP_LC + FP_C * FB_LB / 2 + FP_C * S3_LB / 2 + FP_C;
+
+__global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_t* __restrict__ d_o, int T, int H,
+                                                        int NC) {
+    extern __shared__ float4 s3_lds4[];
+    float* const Ws = reinterpret_cast<float*>(s3_lds4);                // W_c   [t][a]
+    float* const Qs = Ws + FP_C * FP_LK;                                // Qp_c  [t][a]
+    float* const Xt = Qs + FP_C * FP_LK;                                // X^T   [n][a]
+    float* const Zs = Xt + FP_C * FP_LK;                                // Z     [t][n]
+    uint16_t* const Kb = reinterpret_cast<uint16_t*>(Zs + FP_C * FP_LC);  // K_c   [t][a]
+    uint16_t* const Ob = Kb + FP_C * FB_LB;                             // dO_c  [t][n]
+    float* const gts = reinterpret_cast<float*>(Ob + FP_C * S3_LB);     // Gamma[C-1, :]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 15, l4 = lane >> 4;
+    const long u = blockIdx.x >> 1;
+    const int col0 = (blockIdx.x & 1) * 64;
+    const int b = (int)(u / H), h = (int)(u - (long)b * H);
+    const long DD = (long)FP_D * FP_D, CD = (long)FP_C * FP_D;
+    float* const Xu = w.dSp + u * NC * DD;
+    const int m1 = 16 * (wv >> 1), n1 = 32 * (wv & 1);  // step 1 tile: t x n
+    const int m2 = 32 * (wv >> 1), n2 = 32 * (wv & 1);  // step 2 tile: a x n
+
+    for (int e = tid; e < 64 * FP_D; e += FP_NT) {
+        const int nn = e & 63, a = e >> 6;
+        Xt[nn * FP_LK + a] = 0.0f;
+        Xu[(long)(NC - 1) * DD + (long)a * FP_D + col0 + nn] = 0.0f;
+    }
+    if (NC < 2) return;
+
+    // chunk c's W, Qp, K rows of this thread, its two quarter-rows of dO,
+    // Gamma[C-1, :] (first wave) and gamma_C, in named registers
+    float4 w0, w1, w2, w3, q0, q1, q2, q3, k0, k1, k2, k3;
+    uint2 o0, o1;
+    float gtv = 0.0f, gC = 0.0f;
+#define S3_ROW(i) ((tid + (i) * FP_NT) >> 5)
+#define S3_COL(i) (4 * ((tid + (i) * FP_NT) & 31))
+#define S3_OROW(i) ((tid + (i) * FP_NT) >> 4)
+#define S3_OCOL(i) (4 * ((tid + (i) * FP_NT) & 15))
+#define S3_LD4(dst, base, i) dst = *reinterpret_cast<const float4*>((base) + S3_ROW(i) * FP_D + S3_COL(i))
+#define S3_LDO(dst, i)                                                                                    \
+    do {                                                                                                  \
+        const int t_ = S3_OROW(i);                                                                        \
+        dst = make_uint2(0u, 0u);                                                                         \
+        if (t_ < valid_)                                                                                  \
+            dst = *reinterpret_cast<const uint2*>(d_o + ((long)(b * T + t0_ + t_) * H + h) * FP_D + col0 + \
+                                                  S3_OCOL(i));                                            \
+    } while (0)
+#define S3_STAGE(cc)                                                                   \
+    do {                                                                               \
+        const long n_ = u * NC + (cc);                                                 \
+        const int t0_ = (cc) * FP_C, valid_ = min(FP_C, T - t0_);                      \
+        S3_LD4(w0, w.W + n_ * CD, 0);                                                  \
+        S3_LD4(w1, w.W + n_ * CD, 1);                                                  \
+        S3_LD4(w2, w.W + n_ * CD, 2);                                                  \
+        S3_LD4(w3, w.W + n_ * CD, 3);                                                  \
+        S3_LD4(q0, w.Qp + n_ * CD, 0);                                                 \
+        S3_LD4(q1, w.Qp + n_ * CD, 1);                                                 \
+        S3_LD4(q2, w.Qp + n_ * CD, 2);                                                 \
+        S3_LD4(q3, w.Qp + n_ * CD, 3);                                                 \
+        S3_LD4(k0, w.Ku + n_ * CD, 0);                                                 \
+        S3_LD4(k1, w.Ku + n_ * CD, 1);                                                 \
+        S3_LD4(k2, w.Ku + n_ * CD, 2);                                                 \
+        S3_LD4(k3, w.Ku + n_ * CD, 3);                                                 \
+        S3_LDO(o0, 0);                                                                 \
+        S3_LDO(o1, 1);                                                                 \
+        if (tid < FP_C) gtv = w.gt[n_ * FP_C + tid];                                   \
+        gC = w.gC[n_];                                                                 \
+    } while (0)
+#define S3_PUT(i, wi, qi, ki)                                                                                  \
+    do {                                                                                                       \
+        *reinterpret_cast<float4*>(Ws + S3_ROW(i) * FP_LK + S3_COL(i)) = (wi);                                 \
+        *reinterpret_cast<float4*>(Qs + S3_ROW(i) * FP_LK + S3_COL(i)) = (qi);                                 \
+        *reinterpret_cast<uint2*>(Kb + S3_ROW(i) * FB_LB + S3_COL(i)) =                                        \
+            make_uint2((__float_as_uint((ki).x) >> 16) | (__float_as_uint((ki).y) & 0xffff0000u),              \
+                       (__float_as_uint((ki).z) >> 16) | (__float_as_uint((ki).w) & 0xffff0000u));             \
+    } while (0)
+    int c = NC - 1;
+    S3_STAGE(c);
+    for (int s = 0; s < NC - 1; ++s) {
+        const int cn = c - 1;  // output slot
+        __syncthreads();       // the previous chunk's readers of the staged operands are done
+        S3_PUT(0, w0, q0, k0);
+        S3_PUT(1, w1, q1, k1);
+        S3_PUT(2, w2, q2, k2);
+        S3_PUT(3, w3, q3, k3);
+        *reinterpret_cast<uint2*>(Ob + S3_OROW(0) * S3_LB + S3_OCOL(0)) = o0;
+        *reinterpret_cast<uint2*>(Ob + S3_OROW(1) * S3_LB + S3_OCOL(1)) = o1;
+        if (tid < FP_C) gts[tid] = gtv;
+        const float gCc = gC;
+        __syncthreads();  // staged operands and X^T ready
+        if (s + 1 < NC - 1) S3_STAGE(cn);
+        // step 1: Z = -diag(Gamma[C-1,:]) K X
+        {
+            f32x4 acc[1][2];
+            acc_zero(acc);
+            wave_mm<1, 2, true, true, true, false>(acc, 0, FP_D, Kb, FB_LB, nullptr, Xt, FP_LK, nullptr, m1, n1, lane);
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = m1 + 4 * l4 + r;
+                    Zs[t * FP_LC + n1 + 16 * y + li] = -(gts[t] * acc[0][y][r]);
+                }
+        }
+        __syncthreads();  // Z ready
+        // step 2: X' = gamma_C X + Qp^T dO + W^T Z; each wave reads and then
+        // overwrites only its own elements of X^T
+        {
+            f32x4 acc[2][2];
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[x][y][r] = gCc * Xt[(n2 + 16 * y + li) * FP_LK + m2 + 16 * x + 4 * l4 + r];
+            wave_mm<2, 2, false, false, false, true>(acc, 0, FP_C, Qs, FP_LK, nullptr, Ob, S3_LB, nullptr, m2, n2,
+                                                     lane);
+            wave_mm<2, 2, false, false, false, false>(acc, 0, FP_C, Ws, FP_LK, nullptr, Zs, FP_LC, nullptr, m2, n2,
+                                                      lane);
+            float* const Xn = Xu + (long)cn * DD;
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int a = m2 + 16 * x + 4 * l4 + r, nn = n2 + 16 * y + li;
+                        Xt[nn * FP_LK + a] = acc[x][y][r];
+                        Xn[(long)a * FP_D + col0 + nn] = acc[x][y][r];
+                    }
+        }
+        c = cn;
+    }
+#undef S3_ROW
+#undef S3_COL
+#undef S3_OROW
+#undef S3_OCOL
+#undef S3_LD4
+#undef S3_LDO
+#undef S3_STAGE
+#undef S3_PUT
 }
 
 // The state scan over chunks: the persistent kernel for dh = 128, else one
@@ -1647,23 +1747,19 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
     return ASCA_OK;
 }
 
-// The factorised state scan of the fused C = 64, dh = 128 path.
-static int scan2(bool tr, const ChunkDims& d, const ChunkWs& w, float* X, hipStream_t st) {
+// The factorised forward state scan of the fused C = 64, dh = 128 path.
+static int scan2(const ChunkDims& d, const ChunkWs& w, hipStream_t st) {
     constexpr size_t lds = (size_t)S2_LDS_F * sizeof(float);
-    static bool attr[2] = {false, false};
-    const void* fn = tr ? reinterpret_cast<const void*>(&ck_scan2_k<true>)
-                        : reinterpret_cast<const void*>(&ck_scan2_k<false>);
-    if (!attr[tr]) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_scan2_k),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr[tr] = true;
+        attr = true;
     }
     int rc = pre_launch("chunk_scan2");
     if (rc) return rc;
-    if (tr)
-        hipLaunchKernelGGL(ck_scan2_k<true>, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, X, d.NC);
-    else
-        hipLaunchKernelGGL(ck_scan2_k<false>, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, X, d.NC);
+    hipLaunchKernelGGL(ck_scan2_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, w.S, d.NC);
     return post_launch("chunk_scan2");
 }
 
@@ -1672,7 +1768,7 @@ static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, float* o, hipStr
     const int C = d.C, dh = d.dh;
     int rc;
     if (C == FP_C && dh == FP_D) {
-        if ((rc = scan2(false, d, w, w.S, st))) return rc;
+        if ((rc = scan2(d, w, st))) return rc;
         CK_LAUNCH_LDS("chunk_out_fused", ck_out_fused_k, dim3((unsigned)d.N), dim3(FO_NT),
                   (size_t)FO_LDS_F * sizeof(float), d.T, d.H, d.NC, w, o);
         return ASCA_OK;
@@ -1772,9 +1868,19 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
     const hipStream_t st = as_stream(stream);
     if (C == FP_C && dh == FP_D) {
         // E, the reverse scan, then one fused kernel for all per-chunk gradients
-        CK_LAUNCH_LDS("chunk_E", ck_E_k, dim3((unsigned)d.N), dim3(FO_NT), (size_t)FO_LDS_F * sizeof(float), d_o, T, H,
-                  d.NC, w);
-        if ((rc = scan2(true, d, w, w.dSp, st))) return rc;
+        {
+            constexpr size_t lds = (size_t)S3_LDS_F * sizeof(float);
+            static bool attr = false;
+            if (!attr) {
+                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_scan2_bwd_k),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+                attr = true;
+            }
+            if ((rc = pre_launch("chunk_scan2_bwd"))) return rc;
+            hipLaunchKernelGGL(ck_scan2_bwd_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, d_o, T, H, d.NC);
+            if ((rc = post_launch("chunk_scan2_bwd"))) return rc;
+        }
         constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
         static bool attr = false;
         if (!attr) {
