@@ -26,6 +26,23 @@ ASCA_DEV float dpp(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
+// DPP move that leaves `old` in lanes whose source lane lies outside the row.
+template <int CTRL>
+ASCA_DEV float dpp_or(float old, float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Inclusive prefix product over the lanes of each 16-lane row, correct for the
+// first N lanes of the row (N in 1, 2, 4, 8, 16): row_shr by 1, 2, 4, 8.
+template <int N>
+ASCA_DEV float prefix_prod(float x) {
+    if constexpr (N > 1) x *= dpp_or<0x111>(1.0f, x);
+    if constexpr (N > 2) x *= dpp_or<0x112>(1.0f, x);
+    if constexpr (N > 4) x *= dpp_or<0x114>(1.0f, x);
+    if constexpr (N > 8) x *= dpp_or<0x118>(1.0f, x);
+    return x;
+}
+
 // x from lane (lane ^ 32) added to x: every lane receives the pair sum.
 ASCA_DEV float add_xor32(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -177,6 +177,61 @@ ASCA_DEV void fwd_rd(float (&kk)[DH / 8], float (&qq)[DH / 8], float& vv, const 
     vv = buf[2 * L::KQ_F + (w * L::CK + jj) * 8 + c];
 }
 
+// The CK steps of one chunk for this lane's slice s of its column
+// (rust/src/delta.rs:289-314 per step).  Lane p of the column group returns
+// the raw o and S^T k of step p in hold_o / hold_s.
+//   SC = false: s is the state; S <- alpha S + k u^T (two operations per element).
+//   SC = true:  s is S / G_j, G_j = alpha_0 ... alpha_{j-1} of the chunk, so the
+//     update is s <- s + k (u / G_{j+1})^T, one FMA per element; with x = s^T k,
+//     u / G_{j+1} = beta (v / G_{j+1} - x), and the caller scales hold_s by G_j
+//     and hold_o by G_{j+1}.  rl (lane j) = 1 / G_{j+1}.
+template <int DH, bool SC>
+ASCA_DEV void fwd_steps(float (&s)[DH / 8], const float* __restrict__ buf, float gcur, float rl, int w, int row0,
+                        int c, int p, float& hold_o, float& hold_s) {
+    using L = FS<DH>;
+    constexpr int R = L::R, CK = L::CK;
+    static_assert(L::G == CK, "one batched store per chunk");
+    float kk[2][R], qq[2][R], vv[2];
+    fwd_rd<DH>(kk[0], qq[0], vv[0], buf, 0, w, row0, c);
+#pragma unroll
+    for (int jj = 0; jj < CK; ++jj) {
+        if (jj + 1 < CK) fwd_rd<DH>(kk[(jj + 1) & 1], qq[(jj + 1) & 1], vv[(jj + 1) & 1], buf, jj + 1, w, row0, c);
+        const int cs = jj & 1;
+        const float bt = readlane_f(gcur, CK + jj);
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < R; j += 2) {
+            a0 = fmaf(s[j], kk[cs][j], a0);
+            a1 = fmaf(s[j + 1], kk[cs][j + 1], a1);
+        }
+        const float x = group_sum<8>(a0 + a1);
+        float o0 = 0.0f, o1 = 0.0f;
+        if constexpr (SC) {
+            const float ut = bt * fmaf(vv[cs], readlane_f(rl, jj), -x);
+#pragma unroll
+            for (int j = 0; j < R; j += 2) {
+                s[j] = fmaf(kk[cs][j], ut, s[j]);
+                s[j + 1] = fmaf(kk[cs][j + 1], ut, s[j + 1]);
+                o0 = fmaf(s[j], qq[cs][j], o0);
+                o1 = fmaf(s[j + 1], qq[cs][j + 1], o1);
+            }
+        } else {
+            const float a = readlane_f(gcur, jj);
+            const float u = bt * (vv[cs] - a * x);
+#pragma unroll
+            for (int j = 0; j < R; j += 2) {
+                s[j] = a * s[j] + kk[cs][j] * u;
+                s[j + 1] = a * s[j + 1] + kk[cs][j + 1] * u;
+                o0 = fmaf(s[j], qq[cs][j], o0);
+                o1 = fmaf(s[j + 1], qq[cs][j + 1], o1);
+            }
+        }
+        const float oo = group_sum<8>(o0 + o1);
+        hold_o = (p == jj) ? oo : hold_o;
+        hold_s = (p == jj) ? x : hold_s;
+    }
+}
+
 // One block per (sequence, head) unit, unit = h*B + b (the reference's s_pre
 // order, rust/src/delta.rs:54-56).  ckpt: nslots = ceil(T/CK) states per unit,
 // slot j = S^T before step j*CK (element (a, i) of S at [i*dh + a]).
@@ -186,8 +241,8 @@ __global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
     const float* __restrict__ alpha, const float* __restrict__ beta, float* __restrict__ o,
     float* __restrict__ sk_out, float* __restrict__ ckpt, int B, int T, int H, int dh, int nslots) {
     using L = FS<DH, CS>;
-    constexpr int R = L::R, CK = L::CK, G = L::G;
-    static_assert(2 * CK <= 64 && CK % G == 0, "chunk layout");
+    constexpr int R = L::R, CK = L::CK;
+    static_assert(2 * CK <= 16, "chunk layout: the gates of a chunk fit one 16-lane row");
     __shared__ float4 lds4[2 * L::BUF_F / 4];
     float* const lds = reinterpret_cast<float*>(lds4);
 
@@ -241,42 +296,31 @@ __global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
                 for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr + j) = s[j];
             }
         }
-        float kk[2][R], qq[2][R], vv[2];
-        fwd_rd<DH>(kk[0], qq[0], vv[0], buf, 0, w, row0, c);
-        float hold_o = 0.0f, hold_s = 0.0f;
+        // Lanes j < CK of gcur hold the chunk's alpha; when all of them lie in
+        // [2^-8, 2^8] the chunk runs on the scaled state (fwd_steps).
+        const bool bad = lane < CK && !(gcur >= 0x1p-8f && gcur <= 0x1p8f);
+        float hold_o = 0.0f, hold_s = 0.0f, fo = 1.0f, fs = 1.0f;
+        if (__ballot(bad) == 0) {
+            // G_{j+1} = alpha_0 ... alpha_j in lane j (and in lane j of every 2CK group)
+            const float pr = prefix_prod<CK>((lane & (2 * CK - 1)) < CK ? gcur : 1.0f);
+            const float rl = __builtin_amdgcn_rcpf(pr);
+            // both permutes run on every lane: a permute reads 0 from lanes that
+            // are switched off
+            fo = __shfl(pr, p & (CK - 1));
+            const float fprev = __shfl(pr, (p + CK - 1) & (CK - 1));
+            fs = p == 0 ? 1.0f : fprev;
+            fwd_steps<DH, true>(s, buf, gcur, rl, w, row0, c, p, hold_o, hold_s);
+            const float gend = readlane_f(pr, CK - 1);
 #pragma unroll
-        for (int jj = 0; jj < CK; ++jj) {
-            if (jj + 1 < CK) fwd_rd<DH>(kk[(jj + 1) & 1], qq[(jj + 1) & 1], vv[(jj + 1) & 1], buf, jj + 1, w, row0, c);
-            const int cs = jj & 1;
-            const float a = readlane_f(gcur, jj);
-            const float bt = readlane_f(gcur, CK + jj);
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int j = 0; j < R; j += 2) {
-                a0 = fmaf(s[j], kk[cs][j], a0);
-                a1 = fmaf(s[j + 1], kk[cs][j + 1], a1);
-            }
-            const float sk = group_sum<8>(a0 + a1);
-            const float u = bt * (vv[cs] - a * sk);
-            float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll
-            for (int j = 0; j < R; j += 2) {
-                s[j] = a * s[j] + kk[cs][j] * u;
-                s[j + 1] = a * s[j + 1] + kk[cs][j + 1] * u;
-                o0 = fmaf(s[j], qq[cs][j], o0);
-                o1 = fmaf(s[j + 1], qq[cs][j + 1], o1);
-            }
-            const float oo = group_sum<8>(o0 + o1);
-            // lane p of the column group keeps the results of step t0 + G*m + p and
-            // writes them once every G steps
-            hold_o = (p == jj % G) ? oo : hold_o;
-            hold_s = (p == jj % G) ? sk : hold_s;
-            if (jj % G == G - 1) {
-                const int ts = t0 + jj - (G - 1) + p;
-                const bool ok = p < G && ts < T && col_ok;
-                *(ok ? ob + (long)ts * d + col : tr) = hold_o;
-                *(ok ? skb + (long)ts * d + col : tr + 1) = hold_s;
-            }
+            for (int j = 0; j < R; ++j) s[j] *= gend;
+        } else {
+            fwd_steps<DH, false>(s, buf, gcur, 0.0f, w, row0, c, p, hold_o, hold_s);
+        }
+        {   // lane p of the column group holds the results of step t0 + p
+            const int ts = t0 + p;
+            const bool ok = p < CK && ts < T && col_ok;
+            *(ok ? ob + (long)ts * d + col : tr) = hold_o * fo;
+            *(ok ? skb + (long)ts * d + col : tr + 1) = hold_s * fs;
         }
         fwd_stage_store<DH, CS>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
         __syncthreads();
@@ -357,9 +401,15 @@ struct BS {
     static constexpr int RAB_F = CK * W * 2;     // dalpha / dbeta per wave
     static constexpr int STQK_F = CK * DH;       // staged q (and k) rows
     static constexpr int STW_F = W * CK * 24;    // staged dO, v, sk (8 columns each) per wave
-    static constexpr int STAB_F = 2 * CK;        // staged alpha, beta
-    static constexpr int BUF_F = 2 * RED_F + RAB_F + 2 * STQK_F + STW_F + STAB_F;
-    static constexpr size_t LDS = 2 * (size_t)BUF_F * 4;
+    static constexpr int STAB_F = 8 * CK + 8;    // gate table (8 floats per step), flag, sink float4
+    static constexpr int RV_F = CK * DH;          // dv rows
+    static constexpr int ST_OFF = 2 * RED_F + RAB_F + RV_F;   // start of the staged operands
+    static constexpr int BUF_F = ST_OFF + 2 * STQK_F + STW_F + STAB_F;
+    // The next segment's checkpoint tile goes through LDS (per lane, [m][thread]
+    // float2), so no wait on global memory sits at a segment's start.
+    static constexpr int CKS_F = NT * M * 2;
+    static constexpr size_t LDS = 2 * (size_t)BUF_F * 4 + (size_t)CKS_F * 4;
+    static_assert(LDS <= 160 * 1024, "backward LDS");
     // staging registers
     static constexpr int QK4 = CK * DH / 4;             // float4 per staged tensor (q or k)
     static constexpr int NQ = (2 * QK4 + NT - 1) / NT;  // staged q/k float4 per thread
@@ -370,16 +420,18 @@ struct BS {
 template <int DH, int CS>
 struct BStage {
     float4 rq[BS<DH, CS>::NQ], rw[BS<DH, CS>::NW];
-    float rab;
+    float rab;                    // lanes j < CK: alpha of step j, CK <= j < 2CK: beta
+    float rqk;                    // the same lanes: the saved q / k norms (fused backward)
     float rck[2][BS<DH, CS>::M];  // checkpoint tile: column colb+n, rows rowb..rowb+M-1
 };
 
 // wg: the wave's index among all waves of the unit (its value columns)
-template <int DH, int CS, bool EXACT>
+template <int DH, int CS, bool EXACT, bool FUSED>
 ASCA_DEV void bstage_load(BStage<DH, CS>& st, int g, const float* __restrict__ q, const float* __restrict__ k,
                           const float* __restrict__ v, const float* __restrict__ d_o,
                           const float* __restrict__ skv, const float* __restrict__ alpha,
-                          const float* __restrict__ beta, const float* __restrict__ ckb, long ubase, long gbase,
+                          const float* __restrict__ beta, const float* __restrict__ qnorm,
+                          const float* __restrict__ knorm, const float* __restrict__ ckb, long ubase, long gbase,
                           long d, long dh2, int T, int H, int dh, int wg, int lane, int rowb, int colb) {
     using S = BS<DH, CS>;
     constexpr int CK = S::CK, M = S::M;
@@ -403,14 +455,13 @@ ASCA_DEV void bstage_load(BStage<DH, CS>& st, int g, const float* __restrict__ q
         const int j = rem / 2, half = rem % 2;
         const long t = min(t0 + j, T - 1);
         const float* src = tsr == 0 ? d_o : (tsr == 1 ? v : skv);
-        float4 x = ld4m<EXACT>(src + ubase + t * d, wg * 8 + half * 4, dh);
-        if (tsr == 0 && t0 + j >= T) x = make_float4(0.f, 0.f, 0.f, 0.f);   // padded steps carry dO = 0
-        st.rw[i] = x;
+        st.rw[i] = ld4m<EXACT>(src + ubase + t * d, wg * 8 + half * 4, dh);
     }
     {
         const int gl = lane & (2 * CK - 1);
         const long t = min(t0 + gl % CK, T - 1);
         st.rab = (gl < CK ? alpha : beta)[gbase + t * H];
+        st.rqk = FUSED ? (gl < CK ? qnorm : knorm)[gbase + t * H] : 0.0f;
     }
     const float* cks = ckb + (long)g * dh2;
 #pragma unroll
@@ -433,32 +484,60 @@ ASCA_DEV void bstage_load(BStage<DH, CS>& st, int g, const float* __restrict__ q
     }
 }
 
+// Registers -> the LDS buffer of segment g (q, k rows, the waves' dO / v / sk
+// columns, the gate table) and this thread's checkpoint slot cks.  Every lane
+// stores, lanes without an element into the buffer's sink slot: a store that
+// only some lanes make lets the compiler move the matching load down to it,
+// which turns the prefetch into a wait.  Padded steps (t >= T) get dO = 0 here.
 template <int DH, int CS>
-ASCA_DEV void bstage_store(const BStage<DH, CS>& st, float* __restrict__ st_q, float* __restrict__ st_k,
-                           float* __restrict__ st_w, float* __restrict__ st_ab, int w, int lane) {
+ASCA_DEV void bstage_store(const BStage<DH, CS>& st, int g, int T, float* __restrict__ st_q,
+                           float* __restrict__ st_k, float* __restrict__ st_w, float* __restrict__ st_ab,
+                           float2* __restrict__ cks, int w, int lane) {
     using S = BS<DH, CS>;
     constexpr int CK = S::CK;
+    float* const sink = st_ab + 8 * CK + 4;
+#pragma unroll
+    for (int m = 0; m < S::M; ++m) cks[m * S::NT] = make_float2(st.rck[0][m], st.rck[1][m]);
 #pragma unroll
     for (int i = 0; i < S::NQ; ++i) {
-        const int f = (int)threadIdx.x + i * S::NT;
-        if (f < 2 * S::QK4) {
-            const int tsr = f >= S::QK4;
-            const int fl = f - tsr * S::QK4;
-            const int j = fl / (DH / 4), c4 = fl % (DH / 4);
-            *reinterpret_cast<float4*>((tsr ? st_k : st_q) + j * DH + 4 * c4) = st.rq[i];
-        }
+        const int f0 = (int)threadIdx.x + i * S::NT;
+        const bool ok = f0 < 2 * S::QK4;
+        const int f = ok ? f0 : 0;
+        const int tsr = f >= S::QK4;
+        const int fl = f - tsr * S::QK4;
+        const int j = fl / (DH / 4), c4 = fl % (DH / 4);
+        *reinterpret_cast<float4*>(ok ? (tsr ? st_k : st_q) + j * DH + 4 * c4 : sink) = st.rq[i];
     }
 #pragma unroll
     for (int i = 0; i < S::NW; ++i) {
-        const int f = lane + 64 * i;
-        if (f < S::W4) {
-            const int tsr = f / (CK * 2);
-            const int rem = f % (CK * 2);
-            const int j = rem / 2, half = rem % 2;
-            *reinterpret_cast<float4*>(st_w + (w * CK + j) * 24 + tsr * 8 + half * 4) = st.rw[i];
-        }
+        const int f0 = lane + 64 * i;
+        const bool ok = f0 < S::W4;
+        const int f = ok ? f0 : 0;
+        const int tsr = f / (CK * 2);
+        const int rem = f % (CK * 2);
+        const int j = rem / 2, half = rem % 2;
+        float4 x = st.rw[i];
+        if (tsr == 0 && g * CK + j >= T) x = make_float4(0.f, 0.f, 0.f, 0.f);   // padded steps carry dO = 0
+        *reinterpret_cast<float4*>(ok ? st_w + (w * CK + j) * 24 + tsr * 8 + half * 4 : sink) = x;
     }
-    if (w == 0 && lane < 2 * CK) st_ab[lane] = st.rab;
+    // Gate table, row j: alpha_j, beta_j, G_{j+1}, 1/G_{j+1}, 1/alpha_j, |q_j|,
+    // |k_j| with G_{j+1} = alpha_0 ... alpha_j of the segment; st_ab[8 CK] = 1
+    // when every alpha of the segment lies in [2^-8, 2^8] (the range of the
+    // scaled form).  Wave 0 writes it; the other waves compute it into the sink.
+    const bool w0 = w == 0;
+    const bool ga = lane < CK;
+    const int row = ga ? lane : lane - CK;
+    const bool gl = w0 && lane < 2 * CK;
+    *(gl ? st_ab + row * 8 + (ga ? 0 : 1) : sink) = st.rab;
+    *(gl ? st_ab + row * 8 + (ga ? 5 : 6) : sink + 1) = st.rqk;
+    const float pr = prefix_prod<CK>(ga ? st.rab : 1.0f);
+    const bool wa = w0 && ga;
+    *(wa ? st_ab + lane * 8 + 2 : sink) = pr;
+    *(wa ? st_ab + lane * 8 + 3 : sink + 1) = __builtin_amdgcn_rcpf(pr);
+    *(wa ? st_ab + lane * 8 + 4 : sink + 2) = __builtin_amdgcn_rcpf(st.rab);
+    const bool bad = ga && !(st.rab >= 0x1p-8f && st.rab <= 0x1p8f);
+    const bool in_range = __ballot(bad) == 0;
+    *(w0 && lane == 0 ? st_ab + 8 * CK : sink + 3) = in_range ? 1.0f : 0.0f;
 }
 
 // LDS operands of reverse step j: q, k rows and the dO, v, sk column pairs.
@@ -466,7 +545,7 @@ template <int M>
 struct BOps {
     float q[M], k[M];
     float2 dO, v, sk;
-    float a, b;
+    float a, b, g1, r1, ia;   // gate table row of the step
 };
 
 template <int DH>
@@ -493,24 +572,39 @@ ASCA_DEV void bops_read(BOps<DH / 16>& o, const float* __restrict__ st_q, const 
     o.dO = *reinterpret_cast<const float2*>(sw);
     o.v = *reinterpret_cast<const float2*>(sw + 8);
     o.sk = *reinterpret_cast<const float2*>(sw + 16);
-    o.a = st_ab[j];
-    o.b = st_ab[CK + j];
+    const float4 gt = *reinterpret_cast<const float4*>(st_ab + 8 * j);
+    o.a = gt.x;
+    o.b = gt.y;
+    o.g1 = gt.z;
+    o.r1 = gt.w;
+    o.ia = st_ab[8 * j + 4];
 }
 
 // One reverse step of the BPTT for this lane's tile (rust/src/delta.rs:485-572
-// reorganised per value column).  sm: S_{t-1} tile from the register stash.
-// Updates ds in place, stores dv, and leaves the dq / dk row sums and the
-// dalpha / dbeta totals of this wave in LDS for the epilogue.
-template <int DH, bool EXACT>
-ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], float (&ds)[DH / 16][2],
-                       float* __restrict__ rq, float* __restrict__ rk, float& pa_out, float& pb_out,
-                       float* __restrict__ dv_dst, float* __restrict__ tr, bool tvalid, int rg, int cg, int rowb,
-                       int colb, int dh) {
+// reorganised per value column).  sm / sa: tiles of S before / after the step
+// from the register stash.  Updates ds in place, stores dv, and leaves the dq /
+// dk row sums and the dalpha / dbeta totals of this wave in LDS for the epilogue.
+//   SC = false: ds is dS, sm / sa are S.
+//   SC = true: with G_j = alpha_0 ... alpha_{j-1} of the segment, ds holds
+//     G_{j+1} dS, sm = S_before / G_j and sa = S_after / G_{j+1}; then
+//     dS <- alpha dS + k dsk^T becomes ds <- ds + k (-beta du~)^T with
+//     du~ = ds^T k = G_{j+1} du (one FMA per element), and every output term
+//     takes its scale from the step's gate-table row (g1 = G_{j+1}, r1 = 1/G_{j+1},
+//     ia = 1/alpha = G_j / G_{j+1}).
+template <int DH, bool EXACT, bool SC>
+ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], const float (&sa)[DH / 16][2],
+                       float (&ds)[DH / 16][2], float* __restrict__ rq, float* __restrict__ rk, float& pab_out,
+                       float* __restrict__ rv, int rg, int cg,
+                       int rowb, int colb, int dh) {
     constexpr int M = DH / 16;
     const float a = in.a, bb = in.b;
-    const float dO[2] = {in.dO.x, in.dO.y};
     const float vv[2] = {in.v.x, in.v.y};
     const float sk[2] = {in.sk.x, in.sk.y};
+    float dO[2] = {in.dO.x, in.dO.y};
+    if constexpr (SC) {
+        dO[0] *= in.g1;
+        dO[1] *= in.g1;
+    }
 
     // dS += q dO^T  (delta.rs:508-511)
 #pragma unroll
@@ -518,64 +612,58 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], f
 #pragma unroll
         for (int n = 0; n < 2; ++n) ds[m][n] = fmaf(in.q[m], dO[n], ds[m][n]);
     // du = dS^T k  (delta.rs:536-542): 16-lane butterfly over row groups
-    float du[2];
+    float dut[2];
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
         float acc = 0.0f;
 #pragma unroll
         for (int m = 0; m < M; ++m) acc = fmaf(ds[m][n], in.k[m], acc);
-        du[n] = group_sum<16>(acc);
+        dut[n] = group_sum<16>(acc);
     }
-    float wv[2], u[2], dsk[2];
-    const float c1 = -bb * a;
+    // du: true du; uh: the u that multiplies ds; sh: the dsk that multiplies sm
+    // and updates ds
+    float du[2], wv[2], uh[2], sh[2];
+    const float cu = SC ? bb * in.r1 : bb;
+    const float cs = SC ? -bb : -bb * a;
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
+        du[n] = SC ? dut[n] * in.r1 : dut[n];
         wv[n] = vv[n] - a * sk[n];
-        u[n] = bb * wv[n];
-        dsk[n] = c1 * du[n];
+        uh[n] = cu * wv[n];
+        sh[n] = cs * dut[n];
     }
-    // dv = beta du  (delta.rs:550), stored by the lanes of row group 0
-    if constexpr (EXACT) {
-        *(rg == 0 && tvalid ? reinterpret_cast<float2*>(dv_dst) : reinterpret_cast<float2*>(tr)) =
-            make_float2(bb * du[0], bb * du[1]);
-    } else {
-#pragma unroll
-        for (int n = 0; n < 2; ++n) *((rg == 0 && tvalid && colb + n < dh) ? dv_dst + n : tr + n) = bb * du[n];
-    }
+    // dv = beta du  (delta.rs:550): the lanes of row group 0 put it in the
+    // step's LDS row; the epilogue stores whole rows
+    if (rg == 0) *reinterpret_cast<float2*>(rv + colb) = make_float2(bb * du[0], bb * du[1]);
 
     // Off-critical-path partial sums over this lane's 2 columns.
-    //   dq = S_t dO = alpha S_{t-1} dO + k (u.dO)          (delta.rs:504-507)
+    //   dq = S_t dO                                       (delta.rs:504-507)
     //   dk = dS u + S_{t-1} dsk                           (delta.rs:532-534, 556-558)
     //   dalpha = <dS, S_{t-1}> - beta du.sk               (delta.rs:530, 552)
     //   dbeta = du.(v - alpha sk)                         (delta.rs:549)
-    const float y = fmaf(dO[1], u[1], dO[0] * u[0]);
-    const float adO[2] = {a * dO[0], a * dO[1]};
     float pq[M], pk[M];
     float pa0 = 0.0f, pa1 = 0.0f;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        float xq = in.k[m] * y;
-        xq = fmaf(sm[m][0], adO[0], xq);
-        xq = fmaf(sm[m][1], adO[1], xq);
-        float xk = u[0] * ds[m][0];
-        xk = fmaf(u[1], ds[m][1], xk);
-        xk = fmaf(dsk[0], sm[m][0], xk);
-        xk = fmaf(dsk[1], sm[m][1], xk);
-        pq[m] = xq;
-        pk[m] = xk;
+        pq[m] = fmaf(sa[m][1], dO[1], sa[m][0] * dO[0]);
+        float xk = uh[0] * ds[m][0];
+        xk = fmaf(uh[1], ds[m][1], xk);
+        xk = fmaf(sh[0], sm[m][0], xk);
+        pk[m] = fmaf(sh[1], sm[m][1], xk);
         pa0 = fmaf(ds[m][0], sm[m][0], pa0);
         pa1 = fmaf(ds[m][1], sm[m][1], pa1);
     }
     const float ea = fmaf(-bb * du[1], sk[1], -bb * du[0] * sk[0]);
     const float eb = fmaf(du[1], wv[1], du[0] * wv[0]);
-    float pa = pa0 + pa1 + (rg == 0 ? ea : 0.0f);
+    const float pab = SC ? (pa0 + pa1) * in.ia : pa0 + pa1;
+    float pa = pab + (rg == 0 ? ea : 0.0f);
     float pb = rg == 0 ? eb : 0.0f;
 
     // dS <- alpha dS + k dsk^T  (delta.rs:543-545, 559-563)
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int n = 0; n < 2; ++n) ds[m][n] = a * ds[m][n] + in.k[m] * dsk[n];
+        for (int n = 0; n < 2; ++n) ds[m][n] = SC ? fmaf(in.k[m], sh[n], ds[m][n]) : a * ds[m][n] + in.k[m] * sh[n];
 
     // Column sums of pq, pk over the 4 column groups (lane bits 4,5),
     // transposed so each lane keeps whole-row sums.
@@ -603,20 +691,19 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], f
         rk[rowb + 2 * cg] = tsum16(yk[0], yk[2]);
         rk[rowb + 2 * cg + 1] = tsum16(yk[1], yk[3]);
     }
-    pa_out = pa;
-    pb_out = pb;
+    // first level of the cross-step reduction of (dalpha, dbeta): lanes < 32
+    // keep the dalpha pair sum, lanes >= 32 the dbeta one
+    pab_out = tsum32(pa, pb);
 }
 
-// Sum of the 2*CK per-lane partials x[j] over all 64 lanes, transposed so that
-// the totals end up spread over lanes (three swap/DPP levels on halving value
-// sets, then a butterfly over the lanes left), and written to red_ab:
-// x[j] (j < CK) is dalpha of step j, x[CK + j] dbeta of step j.
+// Sum of the 2*CK per-step partials (dalpha of step j, dbeta of step j) over
+// all 64 lanes, given y[j] = their first transposed level (tsum32: lanes < 32
+// hold the dalpha pair sum of step j, lanes >= 32 the dbeta one); two more
+// swap/DPP levels on halving value sets, then a butterfly over the lanes left;
+// the totals go to red_ab[(j*W + w)*2 + {0: dalpha, 1: dbeta}].
 template <int CK, int W>
-ASCA_DEV void cross_step_sum(float (&x)[2 * CK], float* __restrict__ red_ab, int w, int lane) {
+ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, int w, int lane) {
     constexpr int K = 2 * CK;
-    float y[K / 2];
-#pragma unroll
-    for (int i = 0; i < K / 2; ++i) y[i] = tsum32(x[i], x[i + K / 2]);
     // lane holds y[i] = total over lane bit 5 of x[i + (bit5 ? K/2 : 0)]
     if constexpr (K / 2 >= 2) {
         float z[K / 4];
@@ -649,6 +736,88 @@ ASCA_DEV void cross_step_sum(float (&x)[2 * CK], float* __restrict__ red_ab, int
     }
 }
 
+// One segment of CK steps (t0 .. t0+CK-1): recompute the states from the
+// checkpoint s0 into the register stash (phase A), then run the steps in
+// reverse (phase B), storing the next segment's staged operands (stg) into its
+// LDS buffer nbuf halfway, and reduce the per-step dalpha / dbeta partials.  With SC
+// the stash holds S / G_j and ds is carried as G_{j+1} dS inside the segment
+// (see bwd_step); ds enters and leaves unscaled.
+template <int DH, int CS, bool EXACT, bool SC>
+ASCA_DEV void bwd_segment(const float (&s0)[DH / 16][2], float (&ds)[DH / 16][2], const BStage<DH, CS>& stg,
+                          float* __restrict__ nbuf, float2* __restrict__ cks, const float* __restrict__ st_q,
+                          const float* __restrict__ st_k, const float* __restrict__ st_w,
+                          const float* __restrict__ st_ab, float* __restrict__ red_q, float* __restrict__ red_k,
+                          float* __restrict__ red_ab, float* __restrict__ red_v, int t0,
+                          int T, int w, int lane, int rg, int cg, int rowb, int colb, int dh) {
+    using S = BS<DH, CS>;
+    constexpr int M = S::M, CK = S::CK, W = S::W;
+    // stash[j] = S before step t0 + j, stash[CK] = S after the segment's last step
+    float stash[CK + 1][M][2];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        stash[0][m][0] = s0[m][0];
+        stash[0][m][1] = s0[m][1];
+    }
+    // ---- phase A: S_{t0+1} .. S_{t0+CK}
+#pragma unroll
+    for (int j = 1; j <= CK; ++j) {
+        const int jp = j - 1;
+        float km[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) km[m] = st_k[jp * DH + rowb + m];
+        const float* sw = st_w + (w * CK + jp) * 24 + cg * 2;
+        const float2 vv = *reinterpret_cast<const float2*>(sw + 8);
+        const float2 sk = *reinterpret_cast<const float2*>(sw + 16);
+        const float4 gt = *reinterpret_cast<const float4*>(st_ab + 8 * jp);
+        const float a = gt.x, bt = gt.y;
+        float u0 = bt * (vv.x - a * sk.x), u1 = bt * (vv.y - a * sk.y);
+        if constexpr (SC) {
+            u0 *= gt.w;
+            u1 *= gt.w;
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if constexpr (SC) {
+                stash[j][m][0] = fmaf(km[m], u0, stash[jp][m][0]);
+                stash[j][m][1] = fmaf(km[m], u1, stash[jp][m][1]);
+            } else {
+                stash[j][m][0] = a * stash[jp][m][0] + km[m] * u0;
+                stash[j][m][1] = a * stash[jp][m][1] + km[m] * u1;
+            }
+        }
+    }
+    if constexpr (SC) {
+        const float gend = st_ab[8 * (CK - 1) + 2];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            ds[m][0] *= gend;
+            ds[m][1] *= gend;
+        }
+    }
+
+    // ---- phase B: steps t0+CK-1 .. t0 in reverse, LDS operands one step ahead
+    BOps<M> op[2];
+    float pab[CK];
+    bops_read<DH>(op[(CK - 1) & 1], st_q, st_k, st_w, st_ab, CK - 1, w, rowb, cg);
+#pragma unroll
+    for (int jj = CK - 1; jj >= 0; --jj) {
+        if (jj > 0) bops_read<DH>(op[(jj - 1) & 1], st_q, st_k, st_w, st_ab, jj - 1, w, rowb, cg);
+        bwd_step<DH, EXACT, SC>(op[jj & 1], stash[jj], stash[jj + 1], ds, red_q + (jj * W + w) * DH,
+                                red_k + (jj * W + w) * DH, pab[jj], red_v + jj * DH, rg, cg, rowb, colb, dh);
+        if (jj == CK / 2) {
+            // the staged operands of the next segment (loads issued at the
+            // segment's start) go to its buffer; the fence keeps the scheduler
+            // from hoisting the stores, and their wait, to the segment's start
+            __builtin_amdgcn_sched_barrier(0);
+            float* const n_q = nbuf + S::ST_OFF;
+            float* const n_k = n_q + S::STQK_F;
+            float* const n_w = n_k + S::STQK_F;
+            bstage_store<DH, CS>(stg, t0 > 0 ? t0 / CK - 1 : 0, T, n_q, n_k, n_w, n_w + S::STW_F, cks, w, lane);
+        }
+    }
+    cross_step_sum<CK, W>(pab, red_ab, w, lane);
+}
+
 // Backward of one unit per block (CS = 1), or of half of its value columns
 // per block (CS = 2).  Output pointers are already offset to the head-0 column
 // of their quantity; element (r, h*dh + i) is at ptr[r*ldx + h*dh + i] and the
@@ -669,6 +838,7 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
     constexpr int M = S::M, W = S::W, CK = S::CK;
     extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
+    float2* const cks = reinterpret_cast<float2*>(lds4 + 2 * S::BUF_F / 4) + threadIdx.x;   // checkpoint slot
 
     const int unit = blockIdx.x / CS, part = blockIdx.x - unit * CS;
     const int h = unit / B, b = unit - h * B;
@@ -684,72 +854,49 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
     const long hoff = (long)h * dh;
     const float* ckb = ckpt + (long)unit * nslots * dh2;
     const int nseg = (T + CK - 1) / CK;
-    float* const tr = trash_f(threadIdx.x * 2);
 
     float ds[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) ds[m][0] = ds[m][1] = 0.0f;
 
     BStage<DH, CS> stg;
-    bstage_load<DH, CS, EXACT>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2, T, H, dh,
-                               wg, lane, rowb, colb);
+    bstage_load<DH, CS, EXACT, FUSED>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase,
+                                      gbase, d, dh2, T, H, dh, wg, lane, rowb, colb);
+    {
+        float* const b0 = lds + ((nseg - 1) & 1) * S::BUF_F + S::ST_OFF;
+        bstage_store<DH, CS>(stg, nseg - 1, T, b0, b0 + S::STQK_F, b0 + 2 * S::STQK_F,
+                             b0 + 2 * S::STQK_F + S::STW_F, cks, w, lane);
+    }
     for (int g = nseg - 1; g >= 0; --g) {
         const int t0 = g * CK;
         float* const buf = lds + (g & 1) * S::BUF_F;
+        float* const nbuf = lds + ((g + 1) & 1) * S::BUF_F;   // the next segment's (g - 1)
         float* const red_q = buf;                        // [CK][W][DH]
         float* const red_k = red_q + S::RED_F;           // [CK][W][DH]
         float* const red_ab = red_k + S::RED_F;          // [CK][W][2]
-        float* const st_q = red_ab + S::RAB_F;           // [CK][DH]
+        float* const red_v = red_ab + S::RAB_F;          // [CK][DH]
+        float* const st_q = buf + S::ST_OFF;             // [CK][DH]
         float* const st_k = st_q + S::STQK_F;            // [CK][DH]
         float* const st_w = st_k + S::STQK_F;            // [W][CK][24]
-        float* const st_ab = st_w + S::STW_F;            // [2][CK]
+        float* const st_ab = st_w + S::STW_F;            // [CK][8] gate table + flag
 
-        // stash[j] = S before step t0 + j (tile of this lane)
-        float stash[CK][M][2];
+        float s0[M][2];   // checkpoint: S before step t0 (this thread's slot)
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            stash[0][m][0] = stg.rck[0][m];
-            stash[0][m][1] = stg.rck[1][m];
+            const float2 x = cks[m * S::NT];
+            s0[m][0] = x.x;
+            s0[m][1] = x.y;
         }
-        bstage_store<DH, CS>(stg, st_q, st_k, st_w, st_ab, w, lane);
-        bstage_load<DH, CS, EXACT>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, ckb, ubase, gbase, d, dh2,
-                                   T, H, dh, wg, lane, rowb, colb);
+        bstage_load<DH, CS, EXACT, FUSED>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb,
+                                          ubase, gbase, d, dh2, T, H, dh, wg, lane, rowb, colb);
         __syncthreads();  // staging of this segment visible to all waves
 
-        // ---- phase A: recompute S_{t0+1} .. S_{t0+CK-1} into the stash
-#pragma unroll
-        for (int j = 1; j < CK; ++j) {
-            const int jp = j - 1;
-            float km[M];
-#pragma unroll
-            for (int m = 0; m < M; ++m) km[m] = st_k[jp * DH + rowb + m];
-            const float* sw = st_w + (w * CK + jp) * 24 + cg * 2;
-            const float2 vv = *reinterpret_cast<const float2*>(sw + 8);
-            const float2 sk = *reinterpret_cast<const float2*>(sw + 16);
-            const float a = st_ab[jp], bt = st_ab[CK + jp];
-            const float u0 = bt * (vv.x - a * sk.x), u1 = bt * (vv.y - a * sk.y);
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                stash[j][m][0] = a * stash[jp][m][0] + km[m] * u0;
-                stash[j][m][1] = a * stash[jp][m][1] + km[m] * u1;
-            }
-        }
-
-        // ---- phase B: steps t0+CK-1 .. t0 in reverse, LDS operands one step ahead
-        {
-            BOps<M> op[2];
-            float pab[2 * CK];
-            bops_read<DH>(op[(CK - 1) & 1], st_q, st_k, st_w, st_ab, CK - 1, w, rowb, cg);
-#pragma unroll
-            for (int jj = CK - 1; jj >= 0; --jj) {
-                if (jj > 0) bops_read<DH>(op[(jj - 1) & 1], st_q, st_k, st_w, st_ab, jj - 1, w, rowb, cg);
-                const int t = t0 + jj;
-                bwd_step<DH, EXACT>(op[jj & 1], stash[jj], ds, red_q + (jj * W + w) * DH, red_k + (jj * W + w) * DH,
-                                    pab[jj], pab[CK + jj], gv + ((long)b * T + t) * ldx + hoff + colb, tr, t < T, rg,
-                                    cg, rowb, colb, dh);
-            }
-            cross_step_sum<CK, W>(pab, red_ab, w, lane);
-        }
+        if (__builtin_amdgcn_readfirstlane(__float_as_int(st_ab[8 * CK])) == __float_as_int(1.0f))
+            bwd_segment<DH, CS, EXACT, true>(s0, ds, stg, nbuf, cks, st_q, st_k, st_w, st_ab, red_q, red_k,
+                                             red_ab, red_v, t0, T, w, lane, rg, cg, rowb, colb, dh);
+        else
+            bwd_segment<DH, CS, EXACT, false>(s0, ds, stg, nbuf, cks, st_q, st_k, st_w, st_ab, red_q, red_k,
+                                              red_ab, red_v, t0, T, w, lane, rg, cg, rowb, colb, dh);
         __syncthreads();  // red_* of this segment complete
 
         // ---- phase C: cross-wave sums, optional norm/sigmoid backward, stores
@@ -786,6 +933,13 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
                 dA += x.x;
                 dB += x.y;
             }
+            // dv: complete per column; this block's columns are [part DH/CS, (part+1) DH/CS)
+#pragma unroll
+            for (int ia = 0; ia < NA; ++ia) {
+                const int a = lane + 64 * ia;
+                if (a < DH / CS && part * (DH / CS) + a < dh)
+                    gv[r * ldx + hoff + part * (DH / CS) + a] = red_v[jj * DH + part * (DH / CS) + a];
+            }
             if constexpr (CS > 1) {
                 float* const px = part_x + ((long)part * B * T + r) * d + hoff;
 #pragma unroll
@@ -804,7 +958,7 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
             } else if constexpr (FUSED) {
                 dotq = wave_sum(dotq);
                 dotk = wave_sum(dotk);
-                const float qn = qnorm[r * H + h], kn = knorm[r * H + h];
+                const float qn = st_ab[8 * jj + 5], kn = st_ab[8 * jj + 6];
 #pragma unroll
                 for (int ia = 0; ia < NA; ++ia) {
                     const int a = lane + 64 * ia;
@@ -814,7 +968,7 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
                     }
                 }
                 if (lane == 0) {
-                    const float al = st_ab[jj], be = st_ab[CK + jj];
+                    const float al = st_ab[8 * jj], be = st_ab[8 * jj + 1];
                     ga[r * ldg + h] = dA * al * (1.0f - al);
                     gb[r * ldg + h] = dB * be * (1.0f - be);
                 }

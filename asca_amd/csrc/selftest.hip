@@ -1,6 +1,6 @@
 // In-bounds check of the wave-level primitives the kernels rely on: DPP
 // quad_perm / row_half_mirror / row_mirror / row_ror:8 and the gfx950
-// permlane16/32 swaps, and the operand/result lane layout of
+// permlane16/32 swaps, the row_shr prefix product, and the operand/result lane layout of
 // v_mfma_f32_16x16x4_f32 that the GEMM kernels assume.  One wave, lane-indexed
 // input, results copied back.
 #include "common.h"
@@ -8,7 +8,7 @@
 
 namespace asca {
 
-constexpr int SELFTEST_COLS = 14;
+constexpr int SELFTEST_COLS = 16;
 
 __global__ __launch_bounds__(64) void selftest_wave_k(float* __restrict__ out) {
     const int l = threadIdx.x;
@@ -41,6 +41,12 @@ __global__ __launch_bounds__(64) void selftest_wave_k(float* __restrict__ out) {
         r[11] = d[1];
         r[12] = d[2];
         r[13] = d[3];
+    }
+    {
+        // powers of two: the products are exact
+        const float z = __int_as_float((127 + (l * 3) % 5 - 2) << 23);
+        r[14] = prefix_prod<8>(z);
+        r[15] = prefix_prod<2>(z);
     }
 #pragma unroll
     for (int c = 0; c < SELFTEST_COLS; ++c) out[c * 64 + l] = r[c];

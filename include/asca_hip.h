@@ -108,8 +108,9 @@ ASCA_API int asca_event_elapsed_ms(float* ms, void* start, void* stop);
  * permlane32_swap, permlane16_swap, full-wave sum) on x[lane] = lane and
  * y[lane] = 100 + lane, then one v_mfma_f32_16x16x4_f32 on small-integer
  * operands a[lane] = (7 lane) % 13 - 6, b[lane] = (5 lane) % 11 - 5 (rows 10-13:
- * its four result registers), and copies 14 x 64 floats to host_out (row c =
- * result c per lane).  No reference counterpart. */
+ * its four result registers), then the row_shr prefix products over 8 and 2
+ * lanes of z[lane] = 2^((3 lane) % 5 - 2) (rows 14, 15), and copies 16 x 64
+ * floats to host_out (row c = result c per lane).  No reference counterpart. */
 ASCA_API int asca_selftest_wave(float* host_out);
 
 /* Plain streaming device copy of n floats (n % 4 == 0, 16-byte aligned

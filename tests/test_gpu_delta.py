@@ -37,7 +37,7 @@ def test_wave_primitives_lane_semantics(g):
     import ctypes as C
     from asca_amd import _lib
 
-    out = np.zeros((14, 64), dtype=np.float32)  # rows 10-13: MFMA probe (test_gpu_ops)
+    out = np.zeros((16, 64), dtype=np.float32)  # rows 10-13: MFMA probe (test_gpu_ops)
     _lib.call("asca_selftest_wave", out.ctypes.data_as(C.c_void_p))
     lane = np.arange(64)
     np.testing.assert_array_equal(out[0], lane ^ 1)
@@ -54,6 +54,14 @@ def test_wave_primitives_lane_semantics(g):
     np.testing.assert_array_equal(out[7], np.where(odd == 0, lane, 100 + lane - 16))
     np.testing.assert_array_equal(out[8], np.where(odd == 0, lane + 16, 100 + lane))
     np.testing.assert_array_equal(out[9], np.full(64, 2016.0))
+    # row_shr prefix products of z = 2^e: the first n lanes of each 16-lane row
+    # hold the product of the row's lanes up to their own
+    e = (lane * 3) % 5 - 2
+    for row, n in ((14, 8), (15, 2)):
+        pos = lane & 15
+        want = np.array([2.0 ** e[l - min(pos[l], n - 1): l + 1].sum() for l in lane])
+        sel = pos < n
+        np.testing.assert_array_equal(out[row][sel], want[sel])
 
 
 def test_config0_b4_t128_h4_dh32(orc, g):
@@ -79,6 +87,24 @@ def test_config1_b32_t512_h8_dh64(orc, g):
 ])
 def test_edge_shapes(orc, g, B, T, H, dh):
     _check_all(orc, g, orc.DeltaInputs(100 + B * T + dh, B, T, H, dh), B, T, H, dh, "edge")
+
+
+@pytest.mark.parametrize("B,T,H,dh", [(2, 75, 2, 16), (2, 75, 3, 32), (2, 75, 2, 64), (1, 75, 2, 128), (2, 60, 2, 48)])
+def test_extreme_gates(orc, g, B, T, H, dh):
+    # Inside a checkpoint segment the kernels keep the state divided by the
+    # running product of alpha when every alpha of the segment lies in
+    # [2^-8, 2^8], and run the plain recurrence otherwise.  Cover both, and the
+    # switch between them: exact zeros and 1e-6 (plain), a stretch of 0.005
+    # (scaled, products down to 4e-19), exact ones and 1.5 (scaled, growing).
+    x = orc.DeltaInputs(7 + dh, B, T, H, dh)
+    t = np.arange(B * T) % T
+    a = x.alpha.reshape(B * T, H)
+    a[(t >= 16) & (t < 32)] = 0.005
+    a[(t >= 40) & (t < 44), 0] = 1.0
+    a[(t >= 44) & (t < 48)] = 1.5
+    a[t % 37 == 5] = 0.0
+    a[t % 11 == 3, -1] = 1e-6
+    _check_all(orc, g, x, B, T, H, dh, "extreme gates")
 
 
 def test_states_download_matches_cpu_history(orc, g):

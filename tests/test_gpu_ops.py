@@ -21,7 +21,7 @@ GRAD_TOL = 1e-4
 def test_mfma_16x16x4_lane_layout(g):
     from asca_amd import _lib
 
-    out = np.zeros((14, 64), dtype=np.float32)
+    out = np.zeros((16, 64), dtype=np.float32)
     _lib.call("asca_selftest_wave", out.ctypes.data_as(C.c_void_p))
     lane = np.arange(64)
     a = ((lane * 7) % 13 - 6).astype(np.float64)
