@@ -913,8 +913,10 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
                 qa[ia] = 0.0f;
                 ka[ia] = 0.0f;
                 if (a < DH) {
+                    dq[ia] = red_q[jj * W * DH + a];
+                    dk[ia] = red_k[jj * W * DH + a];
 #pragma unroll
-                    for (int w2 = 0; w2 < W; ++w2) {
+                    for (int w2 = 1; w2 < W; ++w2) {
                         dq[ia] += red_q[(jj * W + w2) * DH + a];
                         dk[ia] += red_k[(jj * W + w2) * DH + a];
                     }
@@ -926,9 +928,14 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
                 dotq = fmaf(qa[ia], dq[ia], dotq);
                 dotk = fmaf(ka[ia], dk[ia], dotk);
             }
-            float dA = 0.0f, dB = 0.0f;
+            float dA, dB;
+            {
+                const float2 x = *reinterpret_cast<const float2*>(red_ab + jj * W * 2);
+                dA = x.x;
+                dB = x.y;
+            }
 #pragma unroll
-            for (int w2 = 0; w2 < W; ++w2) {
+            for (int w2 = 1; w2 < W; ++w2) {
                 const float2 x = *reinterpret_cast<const float2*>(red_ab + (jj * W + w2) * 2);
                 dA += x.x;
                 dB += x.y;
@@ -958,13 +965,15 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
             } else if constexpr (FUSED) {
                 dotq = wave_sum(dotq);
                 dotk = wave_sum(dotk);
-                const float qn = st_ab[8 * jj + 5], kn = st_ab[8 * jj + 6];
+                // 1/|q|, 1/|k| by the hardware reciprocal (within 1 ulp)
+                const float iqn = __builtin_amdgcn_rcpf(st_ab[8 * jj + 5]);
+                const float ikn = __builtin_amdgcn_rcpf(st_ab[8 * jj + 6]);
 #pragma unroll
                 for (int ia = 0; ia < NA; ++ia) {
                     const int a = lane + 64 * ia;
                     if (a < dh) {
-                        gq[r * ldx + hoff + a] = (dq[ia] - qa[ia] * dotq) / qn;
-                        gk[r * ldx + hoff + a] = (dk[ia] - ka[ia] * dotk) / kn;
+                        gq[r * ldx + hoff + a] = (dq[ia] - qa[ia] * dotq) * iqn;
+                        gk[r * ldx + hoff + a] = (dk[ia] - ka[ia] * dotk) * ikn;
                     }
                 }
                 if (lane == 0) {
