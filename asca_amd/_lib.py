@@ -86,6 +86,8 @@ SIGNATURES: dict[str, tuple] = {
     "asca_model_forward_backward": (_i, [_p, _p, _p, _i, _i, _p, _p]),
     "asca_model_adamw": (_i, [_p, _p]),
     "asca_model_train_step": (_i, [_p, _p, _p, _i, _i, _p, _p]),
+    "asca_model_decode_state_floats": (_i, [_p, C.POINTER(_sz)]),
+    "asca_model_decode_step": (_i, [_p, _p, _i, _p, _p, _p]),
 }
 
 ERRORS = {

@@ -18,6 +18,7 @@
 // delta.rs:96-105, model.rs:103-105).
 #include <cstdio>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -165,6 +166,15 @@ struct MActs {  // per-layer activations kept for the backward
     void* dws;
 };
 
+struct MDecode {  // decode activations, sized for n sequences
+    int n = 0;
+    std::vector<void*> allocs;
+    float *xa = nullptr, *xb = nullptr, *qkv = nullptr, *gate = nullptr, *o = nullptr, *mid = nullptr,
+          *xn = nullptr, *pre = nullptr, *hid = nullptr, *hf = nullptr;
+    int32_t *route = nullptr, *perm = nullptr, *off = nullptr;
+    void* rws = nullptr;
+};
+
 }  // namespace asca
 
 using namespace asca;
@@ -190,6 +200,7 @@ struct asca_model {
             *emb_off = nullptr;
     void *route_ws = nullptr, *emb_ws = nullptr;
     bool fwd_done = false;
+    MDecode dec;
 };
 
 static void free_acts(asca_model* M) {
@@ -429,8 +440,123 @@ static int model_adamw(asca_model* M, hipStream_t st) {
     return ASCA_OK;
 }
 
+static void free_decode(asca_model* M) {
+    if (!M->dec.allocs.empty()) (void)hipDeviceSynchronize();
+    for (void* a : M->dec.allocs) (void)hipFree(a);
+    M->dec = MDecode();
+}
+
+// Decode workspace for n sequences (one row each).
+static int ensure_decode(asca_model* M, int n) {
+    MDecode& D = M->dec;
+    if (D.n == n) return ASCA_OK;
+    free_decode(M);
+    size_t rws = 0;
+    int rc = asca_hash_route_ws_bytes(n, M->E, &rws);
+    if (rc) return rc;
+    const size_t d = M->d, N = n;
+    auto take = [&](auto** out, size_t count, size_t elem) {
+        void* p = nullptr;
+        const size_t bytes = (count ? count : 1) * elem;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return fail(ASCA_ERR_OOM, "decode: hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        D.allocs.push_back(p);
+        *out = reinterpret_cast<std::remove_pointer_t<decltype(out)>>(p);
+        return (int)ASCA_OK;
+    };
+    if ((rc = take(&D.xa, N * d, 4)) || (rc = take(&D.xb, N * d, 4)) || (rc = take(&D.qkv, N * 3 * d, 4)) ||
+        (rc = take(&D.gate, N * 2 * M->H, 4)) || (rc = take(&D.o, N * d, 4)) || (rc = take(&D.mid, N * d, 4)) ||
+        (rc = take(&D.xn, N * d, 4)) || (rc = take(&D.pre, N * M->dff, 4)) || (rc = take(&D.hid, N * M->dff, 4)) ||
+        (rc = take(&D.hf, N * d, 4)) || (rc = take(&D.route, N, 4)) || (rc = take(&D.perm, N, 4)) ||
+        (rc = take(&D.off, (size_t)M->E + 1, 4)) || (rc = take(&D.rws, rws, 1))) {
+        free_decode(M);
+        return rc;
+    }
+    D.n = n;
+    return ASCA_OK;
+}
+
+// Model::step for n sequences, one token each (model.rs:631-649): embedding,
+// per layer x_mid = x + DeltaBlock::step(x) (delta.rs:341-411, the layer's
+// states) and x = x_mid + HashMoe::step(x_mid) (model.rs:308-337: RMSNorm, the
+// token's hashed expert, SiLU, shared b2), then RMSNorm and the head.  The same
+// launches as the training forward at one row per sequence, with the delta
+// recurrence replaced by the decode step on the carried states.
+static int model_decode(asca_model* M, const uint32_t* ids, int n, float* states, float* logits, hipStream_t st) {
+    MDecode& D = M->dec;
+    const int d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V;
+    const size_t sl = (size_t)n * H * dh * dh;  // one layer's states
+    int rc;
+    if ((rc = bucket_launch(true, ids, n, E, D.route, D.perm, D.off, D.rws, st))) return rc;
+    if ((rc = pre_launch("embed"))) return rc;
+    hipLaunchKernelGGL(embed_k, dim3((n + 3) / 4), dim3(256), 0, st, M->p + M->t[0].off, ids, (long)n, d, V, D.xa);
+    if ((rc = post_launch("embed"))) return rc;
+    float* x = D.xa;
+    float* nx = D.xb;
+    for (int l = 0; l < M->L; ++l) {
+        const MLayer& P = M->lay[l];
+        GemmArgs q = gemm_plain(x, d, M->p + P.w_qkv, 3 * d, D.qkv, 3 * d, n, 3 * d, d);
+        q.bias = M->p + P.b_qkv;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, q, n, st, "dec_qkv_proj"))) return rc;
+        GemmArgs gg = gemm_plain(x, d, M->p + P.w_gate, 2 * H, D.gate, 2 * H, n, 2 * H, d);
+        gg.bias = M->p + P.b_gate;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, gg, n, st, "dec_gate_proj"))) return rc;
+        if ((rc = asca_delta_decode_step(states + l * sl, D.qkv, D.gate, D.o, n, H, dh, st))) return rc;
+        GemmArgs yo = gemm_plain(D.o, d, M->p + P.w_o, d, D.mid, d, n, d, d);
+        yo.bias = M->p + P.b_o;
+        yo.resid = x;
+        yo.ld_resid = d;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, yo, n, st, "dec_out_proj"))) return rc;
+        if ((rc = asca_rmsnorm(D.mid, D.xn, nullptr, n, d, MODEL_EPS, st))) return rc;
+        GemmArgs w1 = gemm_args();
+        w1.A = D.xn;
+        w1.lda = d;
+        w1.a_rows = D.perm;
+        w1.B = M->p + P.w1;
+        w1.ldb = (long)E * dff;
+        w1.b_gs = dff;
+        w1.C = D.pre;
+        w1.ldc = dff;
+        w1.bias = M->p + P.b1;
+        w1.bias_gs = dff;
+        w1.aux_out = D.hid;
+        w1.ld_aux = dff;
+        w1.M = n;
+        w1.N = dff;
+        w1.K = d;
+        w1.goff = D.off;
+        w1.ngroups = E;
+        w1.gmode = 1;
+        if ((rc = gemm_launch(0, 0, EPI_SILU, w1, n, st, "dec_moe_w1"))) return rc;
+        GemmArgs w2 = gemm_args();
+        w2.A = D.hid;
+        w2.lda = dff;
+        w2.B = M->p + P.w2;
+        w2.ldb = d;
+        w2.b_gs = (long)dff * d;
+        w2.C = nx;
+        w2.ldc = d;
+        w2.c_rows = D.perm;
+        w2.bias = M->p + P.b2;
+        w2.resid = D.mid;
+        w2.ld_resid = d;
+        w2.M = n;
+        w2.N = d;
+        w2.K = dff;
+        w2.goff = D.off;
+        w2.ngroups = E;
+        w2.gmode = 1;
+        if ((rc = gemm_launch(0, 0, EPI_STORE, w2, n, st, "dec_moe_w2"))) return rc;
+        std::swap(x, nx);
+    }
+    if ((rc = asca_rmsnorm(x, D.hf, nullptr, n, d, MODEL_EPS, st))) return rc;
+    GemmArgs hd = gemm_plain(D.hf, d, M->p + M->t[1].off, V, logits, V, n, V, d);
+    return gemm_launch(0, 0, EPI_STORE, hd, n, st, "dec_head");
+}
+
 static void destroy_model(asca_model* M) {
     free_acts(M);
+    free_decode(M);
     (void)hipDeviceSynchronize();
     for (void* q : {(void*)M->p, (void*)M->g, (void*)M->m, (void*)M->v, (void*)M->chunks})
         if (q) (void)hipFree(q);
@@ -577,6 +703,21 @@ int asca_model_train_step(asca_model* M, const uint32_t* ids, const uint32_t* ta
     int rc = asca_model_forward_backward(M, ids, targets, batch, seq, loss, stream);
     if (rc) return rc;
     return model_adamw(M, as_stream(stream));
+}
+
+int asca_model_decode_state_floats(const asca_model* M, size_t* per_seq) {
+    if (!M || !per_seq) return fail(ASCA_ERR_INVALID, "null pointer");
+    *per_seq = (size_t)M->L * M->H * M->dh * M->dh;
+    return ASCA_OK;
+}
+
+int asca_model_decode_step(asca_model* M, const uint32_t* ids, int n_seq, float* states, float* logits,
+                           void* stream) {
+    if (!M || !ids || !states || !logits) return fail(ASCA_ERR_INVALID, "null pointer");
+    if (n_seq < 1 || (long)n_seq * M->H > 0x7fffffffL) return fail(ASCA_ERR_INVALID, "bad n_seq %d", n_seq);
+    int rc = ensure_decode(M, n_seq);
+    if (rc) return rc;
+    return model_decode(M, ids, n_seq, states, logits, as_stream(stream));
 }
 
 }  // extern "C"

@@ -3,7 +3,8 @@
 The host-side shape of the reference's Model (rust/src/model.rs:528-802) and
 training step (rust/src/train.rs:176-186): `forward_backward` is zero_grads +
 forward + backward, `adamw` is the optimiser step over every tensor, and
-`train_step` both.  Parameters, gradients and AdamW moments stay on the device;
+`train_step` both; `new_decode_state` / `step` are Model::new_decode_state /
+Model::step (model.rs:619-649) for many sequences at once.  Parameters, gradients and AdamW moments stay on the device;
 `params()` / `grads()` / `set_params()` move them as host arrays in the
 reference's params() order for initialisation, checkpoints and parity checks.
 """
@@ -140,6 +141,38 @@ class DeviceModel:
         lb = self._loss_buf()
         _lib.call("asca_model_train_step", self._h, _vp(ids), _vp(targets), batch, seq, _vp(lb), stream)
         return self._read_loss() if sync else None
+
+    # -- decode (Model::new_decode_state / Model::step, model.rs:619-649) -----
+    def decode_state_floats(self) -> int:
+        """Floats of carried state per sequence: n_layers * n_heads * dh * dh."""
+        n = C.c_size_t()
+        _lib.call("asca_model_decode_state_floats", self._h, C.byref(n))
+        return n.value
+
+    def new_decode_state(self, n_seq: int = 1) -> DevBuf:
+        """Zero states for n_seq new sequences, layout (L, n_seq, H, dh, dh)."""
+        buf = DevBuf(4 * n_seq * self.decode_state_floats())
+        _lib.call("asca_memset32", _vp(buf), 0, n_seq * self.decode_state_floats(), None)
+        return buf
+
+    def step(self, ids, states: DevBuf, sync: bool = True):
+        """One token per sequence (ids: n_seq ints) through the model on the
+        carried states; returns the (n_seq, V) logits (None with sync=False:
+        they stay in the device buffer `decode_logits`)."""
+        ids = np.ascontiguousarray(np.atleast_1d(ids), dtype=np.uint32)
+        n = len(ids)
+        if states.nbytes < 4 * n * self.decode_state_floats():
+            raise ValueError("states buffer too small for %d sequences" % n)
+        di = self._ids("dec_ids", ids)
+        lb = self._bufs.get("decode_logits")
+        if lb is None or lb.nbytes < 4 * n * self.vocab:
+            lb = DevBuf(4 * n * self.vocab)
+            self._bufs["decode_logits"] = lb
+        _lib.call("asca_model_decode_step", self._h, _vp(di), n, _vp(states), _vp(lb), None)
+        if not sync:
+            return None
+        _lib.call("asca_sync")
+        return lb.to_host((n, self.vocab))
 
     def _read_loss(self) -> float:
         _lib.call("asca_sync")

@@ -391,6 +391,19 @@ ASCA_API int asca_model_adamw(asca_model* model, void* stream);
 ASCA_API int asca_model_train_step(asca_model* model, const uint32_t* ids, const uint32_t* targets, int batch,
                                    int seq, float* loss, void* stream);
 
+/* Model::step for n_seq sequences at once, one token each (rust/src/model.rs:
+ * 631-649; DeltaBlock::step delta.rs:341-411, HashMoe::step model.rs:308-337):
+ * ids[s] (device u32) goes through the embedding, every layer's delta step on
+ * the carried states and hashed-expert MoE, the final RMSNorm and the head.
+ * The reference decodes on the CPU only, one sequence at a time.
+ *   states : device f32, n_seq * asca_model_decode_state_floats() floats,
+ *            layout (L, n_seq, H, dh, dh) row-major S[a][i] (zero for a new
+ *            sequence), updated in place
+ *   logits : device f32 (n_seq, V) */
+ASCA_API int asca_model_decode_state_floats(const asca_model* model, size_t* per_seq);
+ASCA_API int asca_model_decode_step(asca_model* model, const uint32_t* ids, int n_seq, float* states,
+                                   float* logits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

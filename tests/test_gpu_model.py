@@ -125,3 +125,33 @@ def test_config3_full_step_runs_deterministically():
     for a, b in zip(g1, g2):
         np.testing.assert_array_equal(a, b)
     dm.close()
+
+
+@pytest.mark.parametrize("cfg,batch,seq", [
+    ((256, 64, 4, 2, 8, 128), 1, 24),       # the reference's decode gate: Config::tiny, 24 tokens
+    ((256, 64, 4, 2, 8, 128), 5, 13),       # several sequences per step
+    ((256, 512, 8, 1, 16, 1024), 3, 9),     # configs[3] widths (dh 64)
+    ((200, 48, 3, 2, 5, 40), 2, 11),        # odd widths, dh 16
+])
+def test_decode_steps_match_forward(cfg, batch, seq):
+    # rust/tests/decode_parity.rs: decoding token by token on carried states
+    # gives the logits of one full forward over the sequence, within 1e-4 of
+    # the largest logit (decode_parity.rs:36); here against the oracle forward.
+    V = cfg[0]
+    dm, om = _models(cfg, 17)
+    rng = np.random.default_rng(3 + batch * seq)
+    ids = rng.integers(0, V, (batch, seq)).astype(np.uint32)
+    print(f"[decode] cfg={cfg} batch={batch} seq={seq}", flush=True)
+    ref, _ = om.forward(ids.reshape(-1), batch)
+    ref = ref.reshape(batch, seq, V)
+    st = dm.new_decode_state(batch)
+    worst = 0.0
+    for t in range(seq):
+        got = dm.step(ids[:, t], st)
+        worst = max(worst, float(np.max(np.abs(got - ref[:, t]))))
+    rel = worst / float(np.max(np.abs(ref)))
+    print(f"[decode]   worst |dlogit| {worst:.3e}, relative {rel:.3e}", flush=True)
+    assert rel <= 1e-4
+    # the states hold exactly L * H * dh^2 floats per sequence, whatever the length
+    assert dm.decode_state_floats() == cfg[3] * cfg[1] * (cfg[1] // cfg[2])
+    dm.close()
