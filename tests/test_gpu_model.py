@@ -155,3 +155,44 @@ def test_decode_steps_match_forward(cfg, batch, seq):
     # the states hold exactly L * H * dh^2 floats per sequence, whatever the length
     assert dm.decode_state_floats() == cfg[3] * cfg[1] * (cfg[1] // cfg[2])
     dm.close()
+
+
+def test_checkpoint_resume_round_trip(tmp_path):
+    # train.rs:303-455 on the device-resident model: save_resume writes the
+    # weights and the moments held in HBM; load_resume restores them bit for
+    # bit with the AdamW counter at the saved step, and training continues
+    # exactly as on the original model given the same counter.
+    from asca_amd import checkpoint as ck
+
+    cfg = (256, 64, 4, 2, 8, 128)
+    dm, _ = _models(cfg, 9)
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, 256, 48).astype(np.uint32)
+    tgt = rng.integers(0, 256, 48).astype(np.uint32)
+    dm.train_step(ids, tgt, 2)
+    dm.train_step(ids, tgt, 2)
+    path = str(tmp_path / "resume.ck")
+    ck.save_resume(path, dm, 2)
+    assert ck.peek_resume(path) == (cfg, 2)
+    dm2, step = ck.load_resume(path)
+    assert step == 2 and dm2.adamw_step_count() == 2
+    for a, b in zip(dm.params(), dm2.params()):
+        np.testing.assert_array_equal(a, b)
+    for x, y in zip(dm.moments(), dm2.moments()):
+        for a, b in zip(x, y):
+            np.testing.assert_array_equal(a, b)
+    dm.set_adamw(step=2)
+    l1 = dm.train_step(ids, tgt, 2)
+    l2 = dm2.train_step(ids, tgt, 2)
+    assert l1 == l2
+    for a, b in zip(dm.params(), dm2.params()):
+        np.testing.assert_array_equal(a, b)
+    # weights-only file: same weights, zero moments
+    wpath = str(tmp_path / "weights.ck")
+    ck.save(wpath, dm)
+    dm3 = ck.load(wpath)
+    for a, b in zip(dm.params(), dm3.params()):
+        np.testing.assert_array_equal(a, b)
+    assert all(not a.any() for a in dm3.moments()[0])
+    for x in (dm, dm2, dm3):
+        x.close()
