@@ -78,9 +78,10 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     // states and U; the decomposed path's other regions are left out
     const bool fused = d.C == 64 && d.dh == 128;
     auto opt = [&](size_t n) -> float* { return fused ? nullptr : take(n); };
-    w.Qu = take(N * CD);
-    w.Ku = take(N * CD);
-    w.Vu = take(N * CD);
+    // f32 copies of q, k, v: the fused kernels read the bf16 inputs instead
+    w.Qu = opt(N * CD);
+    w.Ku = opt(N * CD);
+    w.Vu = opt(N * CD);
     w.al = take(N * C);
     w.be = take(N * C);
     w.gam = take(N * C);
@@ -802,8 +803,8 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         w.al[n * FP_C + tid] = a_s[tid];
         w.be[n * FP_C + tid] = b_s[tid];
     }
-    fp_load_rows(k, Ks, w.Ku + cd, rowbase, rowstride, valid, tid, FP_NT);
-    fp_load_rows(q, X, w.Qu + cd, rowbase, rowstride, valid, tid, FP_NT);
+    fp_load_rows(k, Ks, nullptr, rowbase, rowstride, valid, tid, FP_NT);
+    fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
     __syncthreads();
     // gamma: inclusive product scan over the first wave.  Gamma[t][i] =
     // prod_{i < s <= t} alpha_s (t >= i), never by division (gamma can
@@ -898,7 +899,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
             const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
             Ts[(16 * bi + ((e >> 4) & 15)) * FP_LC + 16 * bj + (e & 15)] = 0.0f;
         }
-        fp_load_rows(v, X, w.Vu + cd, rowbase, rowstride, valid, t2, FP_NT - 64);
+        fp_load_rows(v, X, nullptr, rowbase, rowstride, valid, t2, FP_NT - 64);
     }
     __syncthreads();
     // the blocks below the diagonal, one block diagonal at a time
@@ -1022,19 +1023,9 @@ ASCA_DEV void fb_sq_f32(const float* __restrict__ src, int ld_src, float* dst, i
     }
 }
 
-// 64 x 128 f32 holding bf16 values -> bf16 LDS (row stride FB_LB).
-ASCA_DEV void fb_rows_bf16(const float* __restrict__ src, uint16_t* dst, int tid) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
-        const float4 x = *reinterpret_cast<const float4*>(src + r * FP_D + f);
-        *reinterpret_cast<uint2*>(dst + r * FB_LB + f) =
-            make_uint2((__float_as_uint(x.x) >> 16) | (__float_as_uint(x.y) & 0xffff0000u),
-                       (__float_as_uint(x.z) >> 16) | (__float_as_uint(x.w) & 0xffff0000u));
-    }
-}
-
-__global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restrict__ d_o, int T, int H, int NC,
+__global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                        const uint16_t* __restrict__ v,
+                                                        const uint16_t* __restrict__ d_o, int T, int H, int NC,
                                                         ChunkWs w, float* __restrict__ dq, float* __restrict__ dk,
                                                         float* __restrict__ dv, float* __restrict__ dalpha,
                                                         float* __restrict__ dbeta) {
@@ -1078,7 +1069,13 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         g_s[tid] = w.gam[n * FP_C + tid];
         gt_s[tid] = w.gt[n * FP_C + tid];
     }
-    fb_rows_bf16(w.Ku + cd, Kb, tid);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // K rows (bf16, exact), zero past T
+        const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
+        uint2 x = make_uint2(0u, 0u);
+        if (t < valid) x = *reinterpret_cast<const uint2*>(k + rowbase + t * rowstride + f);
+        *reinterpret_cast<uint2*>(Kb + t * FB_LB + f) = x;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
@@ -1137,7 +1134,11 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
             for (int y = 0; y < 2; ++y)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    pV[g2][y][r] = w.Vu[cd + (rm0 + 4 * l4 + r) * FP_D + 64 * g2 + cn0 + 16 * y + li];
+                {
+                    const int t = rm0 + 4 * l4 + r;
+                    const uint16_t x = t < valid ? v[rowbase + t * rowstride + 64 * g2 + cn0 + 16 * y + li] : 0;
+                    pV[g2][y][r] = __uint_as_float((uint32_t)x << 16);
+                }
         f32x4 Y0[1][2], Y1[1][2];
         acc_zero(Y0);
         acc_zero(Y1);
@@ -1209,9 +1210,7 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
-        const float4 x = *reinterpret_cast<const float4*>(w.Qu + cd + r * FP_D + f);
-        qst[i] = make_uint2((__float_as_uint(x.x) >> 16) | (__float_as_uint(x.y) & 0xffff0000u),
-                            (__float_as_uint(x.z) >> 16) | (__float_as_uint(x.w) & 0xffff0000u));
+        qst[i] = r < valid ? *reinterpret_cast<const uint2*>(q + rowbase + r * rowstride + f) : make_uint2(0u, 0u);
     }
     __syncthreads();
     // R term of d log alpha_m: sum_{t >= m} sum_{i < m} R[t][i]; wave w takes rows 8w .. 8w+7
@@ -1427,7 +1426,8 @@ __global__ __launch_bounds__(FO_NT) void ck_out_fused_k(int T, int H, int NC, Ch
 // registers during the products.  LDS: W, Kt [64][132], X^T [64][132], Z [64][68].
 constexpr int S2_LDS_F = 3 * FP_C * FP_LK + FP_C * FP_LC;
 
-__global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict__ X, int NC) {
+__global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, const uint16_t* __restrict__ kin, int T, int H,
+                                                    float* __restrict__ X, int NC) {
     extern __shared__ float4 s2_lds4[];
     float* const Ws = reinterpret_cast<float*>(s2_lds4);  // W_c   [t][a]
     float* const Ks = Ws + FP_C * FP_LK;                  // Kt_c  [t][a]
@@ -1437,6 +1437,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     const int li = lane & 15, l4 = lane >> 4;
     const long u = blockIdx.x >> 1;
     const int col0 = (blockIdx.x & 1) * 64;
+    const int ub = (int)(u / H), uh = (int)(u - (long)ub * H);
     const long DD = (long)FP_D * FP_D, CD = (long)FP_C * FP_D;
     float* const Xu = X + u * NC * DD;
     const int m1 = 16 * (wv >> 1), n1 = 32 * (wv & 1);  // step 1 tile: t x n
@@ -1455,24 +1456,33 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     // chunk n's W, K rows and Gamma[C-1, :] of this thread, gamma_C and Uv at
     // this lane's step-1 outputs, held in named registers (arrays carried
     // across the chunk loop go to scratch)
-    float4 w0, w1, w2, w3, k0, k1, k2, k3;
+    float4 w0, w1, w2, w3;
+    uint2 k0, k1, k2, k3;  // 4 bf16 each
     float g0, g1, g2, g3, gC = 0.0f;
     float r1[2][4];
 #define S2_ROW(i) ((tid + (i) * FP_NT) >> 5)
 #define S2_COL(i) (4 * ((tid + (i) * FP_NT) & 31))
-#define S2_STAGE(nn)                                                                                   \
+#define S2_LDK(dst, i)                                                                                 \
     do {                                                                                               \
-        const long n_ = (nn);                                                                          \
+        const int t_ = S2_ROW(i);                                                                      \
+        dst = make_uint2(0u, 0u);                                                                      \
+        if (t_ < valid_)                                                                               \
+            dst = *reinterpret_cast<const uint2*>(kin + ((long)(ub * T + t0_ + t_) * H + uh) * FP_D +  \
+                                                  S2_COL(i));                                          \
+    } while (0)
+#define S2_STAGE(cc)                                                                                   \
+    do {                                                                                               \
+        const long n_ = u * NC + (cc);                                                                 \
+        const int t0_ = (cc) * FP_C, valid_ = min(FP_C, T - t0_);                                      \
         const float* W_ = w.W + n_ * CD;                                                               \
-        const float* K_ = w.Ku + n_ * CD;                                                              \
         w0 = *reinterpret_cast<const float4*>(W_ + S2_ROW(0) * FP_D + S2_COL(0));                      \
         w1 = *reinterpret_cast<const float4*>(W_ + S2_ROW(1) * FP_D + S2_COL(1));                      \
         w2 = *reinterpret_cast<const float4*>(W_ + S2_ROW(2) * FP_D + S2_COL(2));                      \
         w3 = *reinterpret_cast<const float4*>(W_ + S2_ROW(3) * FP_D + S2_COL(3));                      \
-        k0 = *reinterpret_cast<const float4*>(K_ + S2_ROW(0) * FP_D + S2_COL(0));                      \
-        k1 = *reinterpret_cast<const float4*>(K_ + S2_ROW(1) * FP_D + S2_COL(1));                      \
-        k2 = *reinterpret_cast<const float4*>(K_ + S2_ROW(2) * FP_D + S2_COL(2));                      \
-        k3 = *reinterpret_cast<const float4*>(K_ + S2_ROW(3) * FP_D + S2_COL(3));                      \
+        S2_LDK(k0, 0);                                                                                 \
+        S2_LDK(k1, 1);                                                                                 \
+        S2_LDK(k2, 2);                                                                                 \
+        S2_LDK(k3, 3);                                                                                 \
         g0 = w.gt[n_ * FP_C + S2_ROW(0)];                                                              \
         g1 = w.gt[n_ * FP_C + S2_ROW(1)];                                                              \
         g2 = w.gt[n_ * FP_C + S2_ROW(2)];                                                              \
@@ -1485,10 +1495,11 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
     do {                                                                                               \
         *reinterpret_cast<float4*>(Ws + S2_ROW(i) * FP_LK + S2_COL(i)) = (wi);                         \
         *reinterpret_cast<float4*>(Ks + S2_ROW(i) * FP_LK + S2_COL(i)) =                               \
-            make_float4((gi) * (ki).x, (gi) * (ki).y, (gi) * (ki).z, (gi) * (ki).w);                   \
+            make_float4((gi) * __uint_as_float((ki).x << 16), (gi) * __uint_as_float((ki).x & 0xffff0000u), \
+                        (gi) * __uint_as_float((ki).y << 16), (gi) * __uint_as_float((ki).y & 0xffff0000u)); \
     } while (0)
     int c = c_first;
-    S2_STAGE(u * NC + c);
+    S2_STAGE(c);
     // step 1 of the last chunk runs too: its U goes to the backward
     for (int s = 0; s < NC; ++s) {
         const int cn = c + 1;  // output slot
@@ -1504,7 +1515,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
 #pragma unroll
             for (int r = 0; r < 4; ++r) z1[y][r] = r1[y][r];
         __syncthreads();  // Ws, Ks and X^T ready
-        if (s + 1 < NC) S2_STAGE(u * NC + cn);
+        if (s + 1 < NC) S2_STAGE(cn);
         // step 1: Z = U = Uv - W X
         {
             f32x4 acc[1][2];
@@ -1556,6 +1567,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
 #undef S2_ROW
 #undef S2_COL
 #undef S2_STAGE
+#undef S2_LDK
 #undef S2_PUT
 }
 
@@ -1569,8 +1581,8 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_k(ChunkWs w, float* __restrict
 constexpr int S3_LB = 64 + 8;
 constexpr int S3_LDS_F = 3 * FP_C * FP_LK + FP_C * FP_LC + FP_C * FB_LB / 2 + FP_C * S3_LB / 2 + FP_C;
 
-__global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_t* __restrict__ d_o, int T, int H,
-                                                        int NC) {
+__global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_t* __restrict__ kin,
+                                                        const uint16_t* __restrict__ d_o, int T, int H, int NC) {
     extern __shared__ float4 s3_lds4[];
     float* const Ws = reinterpret_cast<float*>(s3_lds4);                // W_c   [t][a]
     float* const Qs = Ws + FP_C * FP_LK;                                // Qp_c  [t][a]
@@ -1598,8 +1610,8 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_
 
     // chunk c's W, Qp, K rows of this thread, its two quarter-rows of dO,
     // Gamma[C-1, :] (first wave) and gamma_C, in named registers
-    float4 w0, w1, w2, w3, q0, q1, q2, q3, k0, k1, k2, k3;
-    uint2 o0, o1;
+    float4 w0, w1, w2, w3, q0, q1, q2, q3;
+    uint2 k0, k1, k2, k3, o0, o1;
     float gtv = 0.0f, gC = 0.0f;
 #define S3_ROW(i) ((tid + (i) * FP_NT) >> 5)
 #define S3_COL(i) (4 * ((tid + (i) * FP_NT) & 31))
@@ -1614,6 +1626,13 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_
             dst = *reinterpret_cast<const uint2*>(d_o + ((long)(b * T + t0_ + t_) * H + h) * FP_D + col0 + \
                                                   S3_OCOL(i));                                            \
     } while (0)
+#define S3_LDK(dst, i)                                                                                    \
+    do {                                                                                                  \
+        const int t_ = S3_ROW(i);                                                                         \
+        dst = make_uint2(0u, 0u);                                                                         \
+        if (t_ < valid_)                                                                                  \
+            dst = *reinterpret_cast<const uint2*>(kin + ((long)(b * T + t0_ + t_) * H + h) * FP_D + S3_COL(i)); \
+    } while (0)
 #define S3_STAGE(cc)                                                                   \
     do {                                                                               \
         const long n_ = u * NC + (cc);                                                 \
@@ -1626,10 +1645,10 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_
         S3_LD4(q1, w.Qp + n_ * CD, 1);                                                 \
         S3_LD4(q2, w.Qp + n_ * CD, 2);                                                 \
         S3_LD4(q3, w.Qp + n_ * CD, 3);                                                 \
-        S3_LD4(k0, w.Ku + n_ * CD, 0);                                                 \
-        S3_LD4(k1, w.Ku + n_ * CD, 1);                                                 \
-        S3_LD4(k2, w.Ku + n_ * CD, 2);                                                 \
-        S3_LD4(k3, w.Ku + n_ * CD, 3);                                                 \
+        S3_LDK(k0, 0);                                                                 \
+        S3_LDK(k1, 1);                                                                 \
+        S3_LDK(k2, 2);                                                                 \
+        S3_LDK(k3, 3);                                                                 \
         S3_LDO(o0, 0);                                                                 \
         S3_LDO(o1, 1);                                                                 \
         if (tid < FP_C) gtv = w.gt[n_ * FP_C + tid];                                   \
@@ -1639,9 +1658,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_
     do {                                                                                                       \
         *reinterpret_cast<float4*>(Ws + S3_ROW(i) * FP_LK + S3_COL(i)) = (wi);                                 \
         *reinterpret_cast<float4*>(Qs + S3_ROW(i) * FP_LK + S3_COL(i)) = (qi);                                 \
-        *reinterpret_cast<uint2*>(Kb + S3_ROW(i) * FB_LB + S3_COL(i)) =                                        \
-            make_uint2((__float_as_uint((ki).x) >> 16) | (__float_as_uint((ki).y) & 0xffff0000u),              \
-                       (__float_as_uint((ki).z) >> 16) | (__float_as_uint((ki).w) & 0xffff0000u));             \
+        *reinterpret_cast<uint2*>(Kb + S3_ROW(i) * FB_LB + S3_COL(i)) = (ki);                                  \
     } while (0)
     int c = NC - 1;
     S3_STAGE(c);
@@ -1708,6 +1725,7 @@ __global__ __launch_bounds__(FP_NT) void ck_scan2_bwd_k(ChunkWs w, const uint16_
 #undef S3_LD4
 #undef S3_LDO
 #undef S3_STAGE
+#undef S3_LDK
 #undef S3_PUT
 }
 
@@ -1748,7 +1766,7 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
 }
 
 // The factorised forward state scan of the fused C = 64, dh = 128 path.
-static int scan2(const ChunkDims& d, const ChunkWs& w, hipStream_t st) {
+static int scan2(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, hipStream_t st) {
     constexpr size_t lds = (size_t)S2_LDS_F * sizeof(float);
     static bool attr = false;
     if (!attr) {
@@ -1759,16 +1777,16 @@ static int scan2(const ChunkDims& d, const ChunkWs& w, hipStream_t st) {
     }
     int rc = pre_launch("chunk_scan2");
     if (rc) return rc;
-    hipLaunchKernelGGL(ck_scan2_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, w.S, d.NC);
+    hipLaunchKernelGGL(ck_scan2_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, k, d.T, d.H, w.S, d.NC);
     return post_launch("chunk_scan2");
 }
 
 // The state scan and the outputs O = Qp S + M Uv.
-static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, float* o, hipStream_t st) {
+static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, float* o, hipStream_t st) {
     const int C = d.C, dh = d.dh;
     int rc;
     if (C == FP_C && dh == FP_D) {
-        if ((rc = scan2(d, w, st))) return rc;
+        if ((rc = scan2(d, w, k, st))) return rc;
         CK_LAUNCH_LDS("chunk_out_fused", ck_out_fused_k, dim3((unsigned)d.N), dim3(FO_NT),
                   (size_t)FO_LDS_F * sizeof(float), d.T, d.H, d.NC, w, o);
         return ASCA_OK;
@@ -1823,7 +1841,7 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
         hipLaunchKernelGGL(ck_fwd_prep_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, alpha, beta, T, H,
                            d.NC, w);
         if ((rc = post_launch("chunk_fwd_prep"))) return rc;
-        return chunk_fwd_tail(d, w, o, st);
+        return chunk_fwd_tail(d, w, k, o, st);
     }
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), q, w.Qu, T, H, dh, d.Tp, tot_in4);
@@ -1853,15 +1871,16 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
                     "chunk_H")))
         return rc;
     CK_LAUNCH("chunk_diag", ck_diag_k, dim3(nblk(d.N * dh)), dim3(256), w.Gp, w.gC, dh, d.N * dh);
-    return chunk_fwd_tail(d, w, o, st);
+    return chunk_fwd_tail(d, w, k, o, st);
 }
 
-int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha, float* dbeta, int B,
-                   int T, int H, int dh, int C, void* stream) {
+int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* d_o, void* ws, float* dq,
+                   float* dk, float* dv, float* dalpha, float* dbeta, int B, int T, int H, int dh, int C,
+                   void* stream) {
     int rc = chunk_check(B, T, H, dh, C);
     if (rc) return rc;
     if ((long)B * T * H == 0) return ASCA_OK;
-    if (!d_o || !ws || !dq || !dk || !dv || !dalpha || !dbeta)
+    if (!q || !k || !v || !d_o || !ws || !dq || !dk || !dv || !dalpha || !dbeta)
         return fail(ASCA_ERR_INVALID, "asca_chunk_bwd: null pointer");
     const ChunkDims d = chunk_dims(B, T, H, dh, C);
     const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws));
@@ -1878,7 +1897,8 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
                 attr = true;
             }
             if ((rc = pre_launch("chunk_scan2_bwd"))) return rc;
-            hipLaunchKernelGGL(ck_scan2_bwd_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, d_o, T, H, d.NC);
+            hipLaunchKernelGGL(ck_scan2_bwd_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, k, d_o, T, H,
+                               d.NC);
             if ((rc = post_launch("chunk_scan2_bwd"))) return rc;
         }
         constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
@@ -1890,8 +1910,8 @@ int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* d
             attr = true;
         }
         if ((rc = pre_launch("chunk_bwd_fused"))) return rc;
-        hipLaunchKernelGGL(ck_bwd_fused_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, d_o, T, H, d.NC, w, dq, dk, dv,
-                           dalpha, dbeta);
+        hipLaunchKernelGGL(ck_bwd_fused_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, d_o, T, H, d.NC, w,
+                           dq, dk, dv, dalpha, dbeta);
         return post_launch("chunk_bwd_fused");
     }
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);

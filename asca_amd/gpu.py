@@ -243,12 +243,20 @@ def from_bf16(x: np.ndarray) -> np.ndarray:
 
 
 class ChunkDev:
-    """Chunked-form forward state on the device: the workspace holding the
-    unit-major inputs and every per-chunk intermediate the backward reads."""
+    """Chunked-form forward state on the device: the bf16 q, k, v and the
+    workspace holding every per-chunk intermediate the backward reads (the
+    inputs stay resident for the backward, as DeltaDev keeps them,
+    rust/src/cuda/mod.rs:1386-1397)."""
 
-    def __init__(self, ws, batch, seq, n_heads, dh, chunk):
+    def __init__(self, ws, inputs, batch, seq, n_heads, dh, chunk):
         self.ws = ws
+        self.inputs = inputs
         self.batch, self.seq, self.n_heads, self.dh, self.chunk = batch, seq, n_heads, dh, chunk
+
+    def free(self) -> None:
+        for b in (self.ws, *self.inputs):
+            b.free()
+        self.inputs = ()
 
 
 # --------------------------------------------------------------------- Gpu
@@ -575,10 +583,14 @@ class Gpu:
                       n_heads, dh, chunk, None)
             _lib.call("asca_sync")
             o = out.to_host((t_len, d))
-        finally:
-            for x in (*ins, ga, gb, out):
+        except Exception:
+            for x in (*ins, ws):
                 x.free()
-        return o, ChunkDev(ws, batch, seq, n_heads, dh, chunk)
+            raise
+        finally:
+            for x in (ga, gb, out):
+                x.free()
+        return o, ChunkDev(ws, tuple(ins), batch, seq, n_heads, dh, chunk)
 
     def delta_chunked_bwd(self, dev: ChunkDev, d_o):
         """Raw gradients (dq, dk, dv, dalpha, dbeta) of the chunked form given
@@ -589,7 +601,8 @@ class Gpu:
         bdo = DevBuf.from_array(x)
         outs = [DevBuf(t_len * d * 4) for _ in range(3)] + [DevBuf(t_len * H * 4) for _ in range(2)]
         try:
-            _lib.call("asca_chunk_bwd", _vp(bdo), _vp(dev.ws), *[_vp(o) for o in outs], B, T, H, dh, Cc, None)
+            _lib.call("asca_chunk_bwd", *[_vp(x) for x in dev.inputs], _vp(bdo), _vp(dev.ws),
+                      *[_vp(o) for o in outs], B, T, H, dh, Cc, None)
             _lib.call("asca_sync")
             return tuple([o.to_host((t_len, d)) for o in outs[:3]] + [o.to_host((t_len, H)) for o in outs[3:]])
         finally:

@@ -273,7 +273,8 @@ def bench_chunk(args):
                   C.c_void_p(da.ptr), C.c_void_p(db.ptr), C.c_void_p(o.ptr), C.c_void_p(ws.ptr), B, T, H, dh, Cc, sp)
 
     def bwd():
-        _lib.call("asca_chunk_bwd", C.c_void_p(dev["d_o"].ptr), C.c_void_p(ws.ptr),
+        _lib.call("asca_chunk_bwd", C.c_void_p(dev["q"].ptr), C.c_void_p(dev["k"].ptr), C.c_void_p(dev["v"].ptr),
+                  C.c_void_p(dev["d_o"].ptr), C.c_void_p(ws.ptr),
                   *[C.c_void_p(b.ptr) for b in grads], B, T, H, dh, Cc, sp)
 
     K = args.steps or 10

@@ -342,13 +342,16 @@ ASCA_API int asca_moe_bwd(const float* xn, const float* w1, const float* w2, con
  *   o, dq, dk, dv : (B*T, H*dh) f32; dalpha, dbeta : (B*T, H) f32 (raw, not logits)
  *   1 <= C <= 64; dh a multiple of 4, at most 256.
  *   ws : asca_chunk_ws_bytes bytes; the forward leaves in it what the backward
- *   needs (call asca_chunk_bwd with the forward's ws). */
+ *   needs: call asca_chunk_bwd with the forward's ws and the same q, k, v (the
+ *   backward reads the bf16 inputs, as the reference's backward keeps q, k, v
+ *   resident in DeltaDev, rust/src/cuda/mod.rs:1386-1397). */
 ASCA_API int asca_chunk_ws_bytes(int B, int T, int H, int dh, int C, size_t* bytes);
 ASCA_API int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* alpha,
                             const float* beta, float* o, void* ws, int B, int T, int H, int dh, int C,
                             void* stream);
-ASCA_API int asca_chunk_bwd(const uint16_t* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha,
-                            float* dbeta, int B, int T, int H, int dh, int C, void* stream);
+ASCA_API int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* d_o, void* ws,
+                            float* dq, float* dk, float* dv, float* dalpha, float* dbeta, int B, int T, int H,
+                            int dh, int C, void* stream);
 
 /* ----------------------------------------------------- training step -- */
 
