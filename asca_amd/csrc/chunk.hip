@@ -731,18 +731,36 @@ ASCA_DEV void st_nt4(float* p, float4 v) {
 // 64 x 128 bf16 rows of one chunk -> LDS f32 [t][f] (stride FP_LK) and, if
 // gdst is set, the unit-major f32 copy; rows past T are zero.  tid counts from
 // 0 over the nthr threads taking part.
-ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, float* __restrict__ gdst, long rowbase,
-                           long rowstride, int valid_rows, int tid, int nthr) {
-    for (int e = tid; e < FP_C * FP_D / 4; e += nthr) {
-        const int t = e >> 5, f = 4 * (e & 31);
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t < valid_rows) {
-            const uint2 r = *reinterpret_cast<const uint2*>(src + rowbase + (long)t * rowstride + f);
-            x = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
-                            __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
-        }
-        *reinterpret_cast<float4*>(lds + t * FP_LK + f) = x;
-        if (gdst) st_nt4(gdst + t * FP_D + f, x);
+// 4 bf16 of chunk row t at column f, 0 for rows past the sequence (t >=
+// valid, valid >= 1).  The load itself is unconditional (row clamped): a load
+// under a branch is waited for inside the branch, which serialises the loads.
+ASCA_DEV uint2 ld_row4(const uint16_t* __restrict__ src, long rowbase, long rowstride, int t, int valid, int f) {
+    const uint2 x = *reinterpret_cast<const uint2*>(src + rowbase + (long)min(t, valid - 1) * rowstride + f);
+    return t < valid ? x : make_uint2(0u, 0u);
+}
+
+ASCA_DEV float4 bf4_f32(uint2 r) {
+    return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                       __uint_as_float(r.y & 0xffff0000u));
+}
+
+// The chunk's 64 rows x 128 bf16 (rows past the sequence as 0) into LDS as
+// f32 [64][FP_LK], by NTHR threads: all of a thread's loads are issued before
+// the first is used.
+template <int NTHR>
+ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, long rowbase, long rowstride, int valid_rows,
+                           int tid) {
+    constexpr int NE = FP_C * FP_D / 4, NPER = (NE + NTHR - 1) / NTHR;
+    uint2 r[NPER];
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = min(tid + i * NTHR, NE - 1);
+        r[i] = ld_row4(src, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
+    }
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = tid + i * NTHR;
+        if (NE % NTHR == 0 || e < NE) *reinterpret_cast<float4*>(lds + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r[i]);
     }
 }
 
@@ -797,14 +815,15 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     // gates (padding steps are identities), K and Q
     if (tid < FP_C) {
         const bool in = tid < valid;
-        const long gi = ((long)b * T + t0 + tid) * H + h;
-        a_s[tid] = in ? alpha[gi] : 1.0f;
-        b_s[tid] = in ? beta[gi] : 0.0f;
-        w.al[n * FP_C + tid] = a_s[tid];
-        w.be[n * FP_C + tid] = b_s[tid];
+        const long gi = ((long)b * T + t0 + min(tid, valid - 1)) * H + h;
+        const float av = alpha[gi], bv = beta[gi];
+        a_s[tid] = in ? av : 1.0f;
+        b_s[tid] = in ? bv : 0.0f;
+        w.al[n * FP_C + tid] = in ? av : 1.0f;
+        w.be[n * FP_C + tid] = in ? bv : 0.0f;
     }
-    fp_load_rows(k, Ks, nullptr, rowbase, rowstride, valid, tid, FP_NT);
-    fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
+    fp_load_rows<FP_NT>(k, Ks, rowbase, rowstride, valid, tid);
+    fp_load_rows<FP_NT>(q, X, rowbase, rowstride, valid, tid);
     __syncthreads();
     // gamma: inclusive product scan over the first wave.  Gamma[t][i] =
     // prod_{i < s <= t} alpha_s (t >= i), never by division (gamma can
@@ -899,7 +918,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
             const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
             Ts[(16 * bi + ((e >> 4) & 15)) * FP_LC + 16 * bj + (e & 15)] = 0.0f;
         }
-        fp_load_rows(v, X, nullptr, rowbase, rowstride, valid, t2, FP_NT - 64);
+        fp_load_rows<FP_NT - 64>(v, X, rowbase, rowstride, valid, t2);
     }
     __syncthreads();
     // the blocks below the diagonal, one block diagonal at a time
@@ -948,7 +967,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
                     Y[t * FP_LK + f] = acc[x][y][r];
                     st_nt(w.W + cd + t * FP_D + f, acc[x][y][r]);
                 }
-        fp_load_rows(q, X, nullptr, rowbase, rowstride, valid, tid, FP_NT);
+        fp_load_rows<FP_NT>(q, X, rowbase, rowstride, valid, tid);
     }
     __syncthreads();
     // Qp = diag(gamma) Q - M W
@@ -1069,19 +1088,20 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         g_s[tid] = w.gam[n * FP_C + tid];
         gt_s[tid] = w.gt[n * FP_C + tid];
     }
+    {   // K and dO rows (bf16, exact), zero past T; every load issued first
+        uint2 xk[4], xo[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {   // K rows (bf16, exact), zero past T
-        const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
-        uint2 x = make_uint2(0u, 0u);
-        if (t < valid) x = *reinterpret_cast<const uint2*>(k + rowbase + t * rowstride + f);
-        *reinterpret_cast<uint2*>(Kb + t * FB_LB + f) = x;
-    }
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
+            xk[i] = ld_row4(k, rowbase, rowstride, t, valid, f);
+            xo[i] = ld_row4(d_o, rowbase, rowstride, t, valid, f);
+        }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
-        uint2 x = make_uint2(0u, 0u);
-        if (t < valid) x = *reinterpret_cast<const uint2*>(d_o + rowbase + (long)t * rowstride + f);
-        *reinterpret_cast<uint2*>(Ob + t * FB_LB + f) = x;
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * FP_NT, t = e >> 5, f = 4 * (e & 31);
+            *reinterpret_cast<uint2*>(Kb + t * FB_LB + f) = xk[i];
+            *reinterpret_cast<uint2*>(Ob + t * FB_LB + f) = xo[i];
+        }
     }
 
     // ---- dU = diag(gt) K dS' + M^T dO over the two row halves of dS'; U = Uv - W S
@@ -1127,18 +1147,34 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 
     // ---- Y = T^T dU; dv = beta Y
     {
+        // V at this lane's Y positions; a whole chunk (every chunk but a ragged
+        // last one) takes the branch without a per-row condition, so its 16
+        // loads are all in flight together
         float pV[2][2][4];
+        if (valid == FP_C) {
 #pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2)
+            for (int g2 = 0; g2 < 2; ++g2)
 #pragma unroll
-            for (int y = 0; y < 2; ++y)
+                for (int y = 0; y < 2; ++y)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                {
-                    const int t = rm0 + 4 * l4 + r;
-                    const uint16_t x = t < valid ? v[rowbase + t * rowstride + 64 * g2 + cn0 + 16 * y + li] : 0;
-                    pV[g2][y][r] = __uint_as_float((uint32_t)x << 16);
-                }
+                    for (int r = 0; r < 4; ++r)
+                        pV[g2][y][r] = __uint_as_float(
+                            (uint32_t)v[rowbase + (long)(rm0 + 4 * l4 + r) * rowstride + 64 * g2 + cn0 + 16 * y + li]
+                            << 16);
+        } else {
+#pragma unroll
+            for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+                for (int y = 0; y < 2; ++y)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = rm0 + 4 * l4 + r;
+                        pV[g2][y][r] = t < valid ? __uint_as_float((uint32_t)v[rowbase + (long)t * rowstride + 64 * g2 +
+                                                                               cn0 + 16 * y + li]
+                                                                   << 16)
+                                                 : 0.0f;
+                    }
+        }
         f32x4 Y0[1][2], Y1[1][2];
         acc_zero(Y0);
         acc_zero(Y1);
@@ -1210,7 +1246,7 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = tid + i * FP_NT, r = e >> 5, f = 4 * (e & 31);
-        qst[i] = r < valid ? *reinterpret_cast<const uint2*>(q + rowbase + r * rowstride + f) : make_uint2(0u, 0u);
+        qst[i] = ld_row4(q, rowbase, rowstride, r, valid, f);
     }
     __syncthreads();
     // R term of d log alpha_m: sum_{t >= m} sum_{i < m} R[t][i]; wave w takes rows 8w .. 8w+7
