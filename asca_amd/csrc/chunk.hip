@@ -764,6 +764,27 @@ ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, long ro
     }
 }
 
+// Two such tensors, with all loads of both in flight together.
+template <int NTHR>
+ASCA_DEV void fp_load_rows2(const uint16_t* __restrict__ s0, float* l0, const uint16_t* __restrict__ s1, float* l1,
+                            long rowbase, long rowstride, int valid_rows, int tid) {
+    constexpr int NE = FP_C * FP_D / 4, NPER = (NE + NTHR - 1) / NTHR;
+    static_assert(NE % NTHR == 0, "whole passes");
+    uint2 r0[NPER], r1[NPER];
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = tid + i * NTHR;
+        r0[i] = ld_row4(s0, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
+        r1[i] = ld_row4(s1, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
+    }
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+        const int e = tid + i * NTHR;
+        *reinterpret_cast<float4*>(l0 + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r0[i]);
+        *reinterpret_cast<float4*>(l1 + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r1[i]);
+    }
+}
+
 // Off-diagonal 16 x 16 block (i, j), i > j, of T = (I + L)^-1 from the blocks
 // already known: T_ij = -T_ii (L[i, j..i) T[j..i, j]), one wave.  Ls holds L,
 // Ts holds T (both stride FP_LC).  The product's accumulator feeds the second
@@ -813,6 +834,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     const long cd = n * FP_C * FP_D, cc = n * FP_C * FP_C, dd = n * FP_D * FP_D;
 
     // gates (padding steps are identities), K and Q
+    fp_load_rows2<FP_NT>(k, Ks, q, X, rowbase, rowstride, valid, tid);
     if (tid < FP_C) {
         const bool in = tid < valid;
         const long gi = ((long)b * T + t0 + min(tid, valid - 1)) * H + h;
@@ -822,8 +844,6 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
         w.al[n * FP_C + tid] = in ? av : 1.0f;
         w.be[n * FP_C + tid] = in ? bv : 0.0f;
     }
-    fp_load_rows<FP_NT>(k, Ks, rowbase, rowstride, valid, tid);
-    fp_load_rows<FP_NT>(q, X, rowbase, rowstride, valid, tid);
     __syncthreads();
     // gamma: inclusive product scan over the first wave.  Gamma[t][i] =
     // prod_{i < s <= t} alpha_s (t >= i), never by division (gamma can
