@@ -320,80 +320,103 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_k(GemmArgs p) {
     }
 
     // epilogue: result register r of tile (x, y) sits at tile row 4 (lane / 16) + r,
-    // tile column lane % 16
+    // tile column lane % 16.  Element y of a lane's row is column nc0 + NS y.
+    // Every load the epilogue needs is unconditional (indices clamped into the
+    // operand) and issued ahead of its use: the bias once per thread, the scatter
+    // indices, residual, C and pre of four rows at a time.  A load under a
+    // per-element condition is waited for on its own, one latency per element.
+    constexpr int NS = B_KC ? 16 : 1;
+    const int nc0 = B_KC ? n0 + wn + (lane & 15) : n0 + wn + TNW * (lane & 15);
+    const int nmax = p.N - 1;
+    float bv[TNW];
+    if (bias) {
+#pragma unroll
+        for (int y = 0; y < TNW; ++y) bv[y] = bias[min(nc0 + NS * y, nmax)];
+    }
+    const bool add_c = EPI == EPI_STORE && p.beta != 0.0f;
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
+        long srt[4], crow[4];
+        bool rok[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int tr = 4 * (lane >> 4) + r;
             const int m = m0 + wm + (A_KC ? 16 * x + tr : 4 * tr + x);
-            if (m >= Mg) continue;
-            const long sorted = (p.gmode == 1 ? goff_g : 0) + m;
-            const long crow = p.c_rows ? (long)p.c_rows[sorted] : sorted;
-            float* Cr = C + crow * p.ldc;
-            float v[TNW];
+            rok[r] = m < Mg;
+            srt[r] = (p.gmode == 1 ? goff_g : 0) + min(m, Mg - 1);
+        }
 #pragma unroll
-            for (int y = 0; y < TNW; ++y) v[y] = acc[x][y][r];
-            if constexpr (!B_KC) {
-                // columns n .. n + TNW - 1 of one row
-                const int n = n0 + wn + TNW * (lane & 15);
-                if (n >= p.N) continue;
-                const int cnt = min(p.N - n, TNW);
-                float o[TNW], hb[TNW];
+        for (int r = 0; r < 4; ++r) crow[r] = p.c_rows ? (long)p.c_rows[srt[r]] : srt[r];
+        float lr[4][TNW], lc[4][TNW], la[4][TNW];
+        if constexpr (EPI == EPI_STORE) {
+            if (resid) {
 #pragma unroll
-                for (int y = 0; y < TNW; ++y) {
-                    float a = p.alpha * v[y];
-                    if (y < cnt) {
-                        if (bias) a += bias[n + y];
-                        if constexpr (EPI == EPI_STORE) {
-                            if (p.beta != 0.0f) a += p.beta * Cr[n + y];
-                            if (resid) a += resid[crow * p.ld_resid + n + y];
-                        } else if constexpr (EPI == EPI_SILU) {
-                            hb[y] = silu_ref(a);
-                        } else {
-                            const float pr = p.aux[sorted * p.ld_aux + n + y];
-                            const float sg = 1.0f / (1.0f + expf(-pr));
-                            a = v[y] * (sg * (1.0f + pr * (1.0f - sg)));
-                        }
-                    }
-                    o[y] = a;
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int y = 0; y < TNW; ++y) lr[r][y] = resid[crow[r] * p.ld_resid + min(nc0 + NS * y, nmax)];
+            }
+            if (add_c) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int y = 0; y < TNW; ++y) lc[r][y] = C[crow[r] * p.ldc + min(nc0 + NS * y, nmax)];
+            }
+        } else if constexpr (EPI == EPI_SILU_BWD) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int y = 0; y < TNW; ++y) la[r][y] = p.aux[srt[r] * p.ld_aux + min(nc0 + NS * y, nmax)];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (!rok[r]) continue;
+            float* Cr = C + crow[r] * p.ldc;
+            float o[TNW], hb[TNW];
+#pragma unroll
+            for (int y = 0; y < TNW; ++y) {
+                float a = p.alpha * acc[x][y][r];
+                if (bias) a += bv[y];
+                if constexpr (EPI == EPI_STORE) {
+                    if (add_c) a += p.beta * lc[r][y];
+                    if (resid) a += lr[r][y];
+                } else if constexpr (EPI == EPI_SILU) {
+                    hb[y] = silu_ref(a);
+                } else {
+                    const float pr = la[r][y];
+                    const float sg = 1.0f / (1.0f + expf(-pr));
+                    a = acc[x][y][r] * (sg * (1.0f + pr * (1.0f - sg)));
                 }
+                o[y] = a;
+            }
+            if constexpr (!B_KC) {
+                // columns nc0 .. nc0 + TNW - 1 of one row
+                if (nc0 >= p.N) continue;
+                const int cnt = min(p.N - nc0, TNW);
+                const long ao = srt[r] * p.ld_aux + nc0;
                 if (VEC && cnt == TNW && TNW == 4) {
-                    *reinterpret_cast<float4*>(Cr + n) = make_float4(o[0], o[1], o[TNW - 2], o[TNW - 1]);
+                    *reinterpret_cast<float4*>(Cr + nc0) = make_float4(o[0], o[1], o[TNW - 2], o[TNW - 1]);
                     if constexpr (EPI == EPI_SILU)
-                        *reinterpret_cast<float4*>(p.aux_out + sorted * p.ld_aux + n) =
+                        *reinterpret_cast<float4*>(p.aux_out + ao) =
                             make_float4(hb[0], hb[1], hb[TNW - 2], hb[TNW - 1]);
                 } else if (VEC && cnt == TNW && TNW == 2) {
-                    *reinterpret_cast<float2*>(Cr + n) = make_float2(o[0], o[TNW - 1]);
+                    *reinterpret_cast<float2*>(Cr + nc0) = make_float2(o[0], o[TNW - 1]);
                     if constexpr (EPI == EPI_SILU)
-                        *reinterpret_cast<float2*>(p.aux_out + sorted * p.ld_aux + n) = make_float2(hb[0], hb[TNW - 1]);
+                        *reinterpret_cast<float2*>(p.aux_out + ao) = make_float2(hb[0], hb[TNW - 1]);
                 } else {
 #pragma unroll
                     for (int y = 0; y < TNW; ++y)
                         if (y < cnt) {
-                            Cr[n + y] = o[y];
-                            if constexpr (EPI == EPI_SILU) p.aux_out[sorted * p.ld_aux + n + y] = hb[y];
+                            Cr[nc0 + y] = o[y];
+                            if constexpr (EPI == EPI_SILU) p.aux_out[ao + y] = hb[y];
                         }
                 }
             } else {
 #pragma unroll
                 for (int y = 0; y < TNW; ++y) {
-                    const int n = n0 + wn + 16 * y + (lane & 15);
+                    const int n = nc0 + 16 * y;
                     if (n >= p.N) continue;
-                    float a = p.alpha * v[y];
-                    if (bias) a += bias[n];
-                    if constexpr (EPI == EPI_STORE) {
-                        if (p.beta != 0.0f) a += p.beta * Cr[n];
-                        if (resid) a += resid[crow * p.ld_resid + n];
-                        Cr[n] = a;
-                    } else if constexpr (EPI == EPI_SILU) {
-                        Cr[n] = a;
-                        p.aux_out[sorted * p.ld_aux + n] = silu_ref(a);
-                    } else {
-                        const float pr = p.aux[sorted * p.ld_aux + n];
-                        const float sg = 1.0f / (1.0f + expf(-pr));
-                        Cr[n] = v[y] * (sg * (1.0f + pr * (1.0f - sg)));
-                    }
+                    Cr[n] = o[y];
+                    if constexpr (EPI == EPI_SILU) p.aux_out[srt[r] * p.ld_aux + n] = hb[y];
                 }
             }
         }
