@@ -29,7 +29,10 @@ struct Dec {
     static constexpr int W = NT / 64;
 };
 
-template <bool VEC, int RPT, bool NTMP>
+// FULL: dh is exactly 128 (every row and column of the tile exists), so no
+// load carries a condition and the loads of a thread are all in flight
+// together (a load under a condition is waited for on its own).
+template <bool VEC, int RPT, bool NTMP, bool FULL = false>
 __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict__ states,
                                                                const float* __restrict__ qkv,
                                                                const float* __restrict__ gate, float* __restrict__ o,
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict
     for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
         if constexpr (VEC) {
-            if (a < dh && c0 < dh) {
+            if (FULL || (a < dh && c0 < dh)) {
                 const f32x4* src = reinterpret_cast<const f32x4*>(S + (long)a * dh + c0);
                 const f32x4 x = NTMP ? __builtin_nontemporal_load(src) : *src;
                 s[j] = make_float4(x[0], x[1], x[2], x[3]);
@@ -73,8 +76,8 @@ __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
         const int i = lane + 64 * x;
-        const float qv = i < dh ? qh[i] : 0.0f;
-        const float kv = i < dh ? kh[i] : 0.0f;
+        const float qv = FULL || i < dh ? qh[i] : 0.0f;
+        const float kv = FULL || i < dh ? kh[i] : 0.0f;
         qq = fmaf(qv, qv, qq);
         kk = fmaf(kv, kv, kk);
     }
@@ -88,12 +91,12 @@ __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
-        kr[j] = a < dh ? kh[a] * ki : 0.0f;
-        qr[j] = a < dh ? qh[a] * qi : 0.0f;
+        kr[j] = FULL || a < dh ? kh[a] * ki : 0.0f;
+        qr[j] = FULL || a < dh ? qh[a] * qi : 0.0f;
     }
     float vv[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) vv[x] = c0 + x < dh ? vh[c0 + x] : 0.0f;
+    for (int x = 0; x < 4; ++x) vv[x] = FULL || c0 + x < dh ? vh[c0 + x] : 0.0f;
 
     // sk = S^T k over this thread's rows, then the row groups
     float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict
     for (int j = 0; j < RPT; ++j) {
         const int a = r0 + j;
         if constexpr (VEC) {
-            if (a < dh && c0 < dh) {
+            if (FULL || (a < dh && c0 < dh)) {
                 f32x4* dst = reinterpret_cast<f32x4*>(S + (long)a * dh + c0);
                 const f32x4 x = {s[j].x, s[j].y, s[j].z, s[j].w};
                 if (NTMP)
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(Dec<RPT>::NT) void delta_decode_k(float* __restrict
         const float* e = reinterpret_cast<const float*>(&t);
 #pragma unroll
         for (int x = 0; x < 4; ++x)
-            if (c + x < dh) oh[c + x] = e[x];
+            if (FULL || c + x < dh) oh[c + x] = e[x];
     }
 }
 
@@ -194,7 +197,10 @@ extern "C" int asca_delta_decode_step(float* states, const float* qkv, const flo
     if (rc) return rc;
     const bool vec = dh % 4 == 0 && (reinterpret_cast<uintptr_t>(states) & 15) == 0;
     const hipStream_t st = as_stream(stream);
-    if (vec)
+    if (vec && dh == 128)
+        hipLaunchKernelGGL((delta_decode_k<true, 8, true, true>), dim3(n_seq * H), dim3(Dec<8>::NT), 0, st, states,
+                           qkv, gate, o, H, dh);
+    else if (vec)
         hipLaunchKernelGGL((delta_decode_k<true, 8, true>), dim3(n_seq * H), dim3(Dec<8>::NT), 0, st, states, qkv,
                            gate, o, H, dh);
     else
