@@ -1102,10 +1102,12 @@ struct DeltaWs {
 
 // Units (sequence, head) at or below which each unit's value columns run on two
 // blocks: half of MI355X's 256 CUs, so that a small batch still fills the chip.
-// A function of the shape only, so the workspace size never depends on the
-// device state.
+// dh = 128 always splits: one block of 16 waves would cap the backward at 128
+// VGPRs (1024 threads per block) and spill about 140 of them, where two
+// blocks of 8 waves hold their ~215 without spilling.  A function of the shape
+// only, so the workspace size never depends on the device state.
 constexpr long SPLIT_UNITS = 128;
-static int col_split(int B, int H) { return (long)B * H <= SPLIT_UNITS ? 2 : 1; }
+static int col_split(int B, int H, int dhc) { return (long)B * H <= SPLIT_UNITS || dhc == 128 ? 2 : 1; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1116,7 +1118,7 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     w.nslots = (T + w.ck - 1) / w.ck;
     const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
-    w.cs = col_split(B, H);
+    w.cs = col_split(B, H, dhc);
     const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
     const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
@@ -1142,10 +1144,10 @@ static int launch_fwd_t(const float* q, const float* k, const float* v, const fl
                         float* o, const DeltaWs& ws, int B, int T, int H, int dh, hipStream_t st) {
     int rc = pre_launch("delta_fwd");
     if (rc) return rc;
-    if (ws.cs > 1)
+    if (DH == 128 || ws.cs > 1)
         hipLaunchKernelGGL((delta_fwd_k<DH, 2, EXACT>), dim3(B * H * 2), dim3(FS<DH, 2>::NT), 0, st, q, k, v, alpha,
                            beta, o, ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
-    else
+    else if constexpr (DH < 128)  // dh = 128 always splits its columns
         hipLaunchKernelGGL((delta_fwd_k<DH, 1, EXACT>), dim3(B * H), dim3(FS<DH, 1>::NT), 0, st, q, k, v, alpha,
                            beta, o, ws.sk, ws.ckpt, B, T, H, dh, ws.nslots);
     return post_launch("delta_fwd");
@@ -1209,10 +1211,11 @@ static int launch_bwd_t(const float* q, const float* k, const float* v, const fl
                         const float* d_o, const DeltaWs& ws, const float* qn, const float* kn, float* gq, float* gk,
                         float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
                         hipStream_t st) {
-    if (ws.cs > 1)
+    if (DH == 128 || ws.cs > 1)
         return launch_bwd_cs<DH, 2, EXACT, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg,
                                                   B, T, H, dh, st);
-    return launch_bwd_cs<DH, 1, EXACT, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B,
+    if constexpr (DH == 128) return fail(ASCA_ERR_UNSUPPORTED, "dh=128 without column split");
+    else return launch_bwd_cs<DH, 1, EXACT, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B,
                                               T, H, dh, st);
 }
 

@@ -81,6 +81,8 @@ def test_config1_b32_t512_h8_dh64(orc, g):
     (2, 33, 2, 24),     # masked dh, T not a multiple of the checkpoint interval
     (2, 70, 2, 48),
     (1, 45, 2, 128),
+    (9, 20, 16, 128),   # 144 units: dh = 128 splits its columns at any unit count
+    (9, 13, 16, 100),
     (2, 17, 6, 32),     # dh of the reference's delta-grad gate (main.rs:1106), ragged T
     (5, 64, 1, 64),
     (1, 9, 2, 5),       # odd dh
