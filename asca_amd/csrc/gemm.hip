@@ -201,7 +201,7 @@ ASCA_DEV void mfma_4xn(f32x4 (&acc)[4][TN], const float (&fa)[4][4], const float
 // 16 TNW columns (TNW = 4, or 2 for the narrower tile that lets three blocks
 // share a CU).
 template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN, int TNW = 4>
-__global__ __launch_bounds__(64 * WM * WN, 1) void gemm_k(GemmArgs p) {
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN >= 4 ? 2 : 1))) void gemm_k(GemmArgs p) {
     constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 16 * TNW * WN;
     constexpr bool A_KC = !TA, B_KC = TB;
     constexpr int A_F = tile_floats<A_KC, BM>();
@@ -280,43 +280,45 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void gemm_k(GemmArgs p) {
             tile_load<B_KC, VEC, BN, NT>(rb, B, p.ldb, p.b_rows, b_off, n0, lim_n, k0, K_hi - k0, tid);
         }
     };
-    // Pipeline per k-tile kt (fragments of both 16-k halves of kt already in
-    // registers): issue the global loads of kt+1; MFMAs of half 0; store kt+1
-    // to the other LDS buffer; barrier; read half 0 of kt+1 while the MFMAs of
-    // half 1 run, then half 1 of kt+1.  A buffer is rewritten only after the
-    // barrier that follows the last read of its previous tile.
+    // Two halves per k-tile kt, split by one barrier.  Each half multiplies
+    // fragments that are already in registers while the other half's
+    // fragments are read:
+    //   A(kt): MFMAs of 16-k group 0 of kt | read group 1 of kt; store the
+    //          registers holding k-tile kt+1 to the other LDS buffer
+    //   B(kt): MFMAs of group 1 of kt | read group 0 of kt+1; issue the
+    //          global loads of k-tile kt+2 into the registers
+    // so a global load has a whole half plus most of the next to arrive.  The
+    // buffer written in A(kt) was last read in A(kt-1), before the barrier of
+    // kt-1.  Near the end the k-tile loaded is clamped to the last one (a
+    // repeated load that is never stored).
     float fa0[4][4], fb0[4][TNW], fa1[4][4], fb1[4][TNW];
     if (nk > 0) {
         load(K_lo);
         tile_store<A_KC, BM, NT>(ra, lds, tid);
         tile_store<B_KC, BN, NT>(rb, lds + A_F, tid);
-    }
-    __syncthreads();
-    if (nk > 0) {
+        load(K_lo + (nk > 1 ? GM_BK : 0));
+        __syncthreads();
         frag_read<A_KC, BM>(fa0, lds, wm, 0, lane);
         frag_read_n<B_KC, BN, TNW>(fb0, lds + A_F, wn, 0, lane);
-        frag_read<A_KC, BM>(fa1, lds, wm, 1, lane);
-        frag_read_n<B_KC, BN, TNW>(fb1, lds + A_F, wn, 1, lane);
-    }
-    for (long kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        float* const Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
-        if (more) load(K_lo + (kt + 1) * GM_BK);
-        mfma_4xn<TNW>(acc, fa0, fb0);
-        if (more) {
+        for (long kt = 0; kt < nk - 1; ++kt) {
+            float* const Cs = lds + (kt & 1) * (A_F + B_F);
+            float* const Ns = lds + ((kt + 1) & 1) * (A_F + B_F);
+            frag_read<A_KC, BM>(fa1, Cs, wm, 1, lane);
+            frag_read_n<B_KC, BN, TNW>(fb1, Cs + A_F, wn, 1, lane);
+            mfma_4xn<TNW>(acc, fa0, fb0);
             tile_store<A_KC, BM, NT>(ra, Ns, tid);
             tile_store<B_KC, BN, NT>(rb, Ns + A_F, tid);
-        }
-        __syncthreads();
-        if (more) {
+            __syncthreads();
             frag_read<A_KC, BM>(fa0, Ns, wm, 0, lane);
             frag_read_n<B_KC, BN, TNW>(fb0, Ns + A_F, wn, 0, lane);
+            load(K_lo + min(kt + 2, nk - 1) * GM_BK);
+            mfma_4xn<TNW>(acc, fa1, fb1);
         }
+        float* const Ls = lds + ((nk - 1) & 1) * (A_F + B_F);
+        frag_read<A_KC, BM>(fa1, Ls, wm, 1, lane);
+        frag_read_n<B_KC, BN, TNW>(fb1, Ls + A_F, wn, 1, lane);
+        mfma_4xn<TNW>(acc, fa0, fb0);
         mfma_4xn<TNW>(acc, fa1, fb1);
-        if (more) {
-            frag_read<A_KC, BM>(fa1, Ns, wm, 1, lane);
-            frag_read_n<B_KC, BN, TNW>(fb1, Ns + A_F, wn, 1, lane);
-        }
     }
 
     // epilogue: result register r of tile (x, y) sits at tile row 4 (lane / 16) + r,
