@@ -98,9 +98,23 @@ ASCA_DEV void tile_rows(long (&ro)[8 * R / NT], long ld, const int* rows, long r
     }
 }
 
+// Row offsets (source row * ld) of this thread's k-rows of an mn-contiguous
+// tile whose storage rows are gathered (rows != null): read one k-tile ahead
+// of its loads, so no load waits on the index read before it.  Rows past the
+// valid extent are clamped to the last valid one.
+template <int R, int NT>
+ASCA_DEV void tile_krows(long (&ro)[8 * R / NT], long ld, const int* rows, long row_off, long k0, long lim_k,
+                         int tid) {
+#pragma unroll
+    for (int j = 0; j < 8 * R / NT; ++j) {
+        const int kr = (tid + NT * j) / (R / 4);
+        ro[j] = (long)rows[row_off + k0 + min((long)kr, lim_k - 1)] * ld;
+    }
+}
+
 // As tile_load for a tile that lies wholly inside the operand (aligned, no
 // edge): unconditional 16-byte loads; a k-contiguous tile takes its row
-// offsets from tile_rows.
+// offsets from tile_rows, a gathered mn-contiguous one from tile_krows.
 template <bool KC, int R, int NT>
 ASCA_DEV void tile_load_full(float4 (&r)[8 * R / NT], const float* base, long ld, const int* rows, long row_off,
                              const long (&ro)[8 * R / NT], int mn0, long k0, int tid) {
@@ -112,7 +126,8 @@ ASCA_DEV void tile_load_full(float4 (&r)[8 * R / NT], const float* base, long ld
             r[j] = *reinterpret_cast<const float4*>(base + ro[j] + k0 + kk);
         } else {
             const int kr = sl / (R / 4), mm = 4 * (sl % (R / 4));
-            r[j] = *reinterpret_cast<const float4*>(base + srow(rows, row_off, k0 + kr) * ld + mn0 + mm);
+            const long off = rows ? ro[j] : (row_off + k0 + kr) * ld;
+            r[j] = *reinterpret_cast<const float4*>(base + off + mn0 + mm);
         }
     }
 }
@@ -271,6 +286,12 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     long roa[8 * BM / NT], rob[8 * BN / NT];
     if (A_KC) tile_rows<BM, NT>(roa, p.lda, p.a_rows, a_off, m0, lim_m, tid);
     if (B_KC) tile_rows<BN, NT>(rob, p.ldb, p.b_rows, b_off, n0, lim_n, tid);
+    // gathered mn-contiguous operands: the row offsets of k-tile kt
+    auto krows = [&](long kt) {
+        const long k0 = K_lo + min(kt, nk - 1) * GM_BK;
+        if (!A_KC && p.a_rows) tile_krows<BM, NT>(roa, p.lda, p.a_rows, a_off, k0, K_hi - k0, tid);
+        if (!B_KC && p.b_rows) tile_krows<BN, NT>(rob, p.ldb, p.b_rows, b_off, k0, K_hi - k0, tid);
+    };
     auto load = [&](long k0) {
         if (interior && K_hi - k0 >= GM_BK) {
             tile_load_full<A_KC, BM, NT>(ra, A, p.lda, p.a_rows, a_off, roa, m0, k0, tid);
@@ -293,10 +314,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     // repeated load that is never stored).
     float fa0[4][4], fb0[4][TNW], fa1[4][4], fb1[4][TNW];
     if (nk > 0) {
+        krows(0);
         load(K_lo);
+        krows(1);
         tile_store<A_KC, BM, NT>(ra, lds, tid);
         tile_store<B_KC, BN, NT>(rb, lds + A_F, tid);
         load(K_lo + (nk > 1 ? GM_BK : 0));
+        krows(2);
         __syncthreads();
         frag_read<A_KC, BM>(fa0, lds, wm, 0, lane);
         frag_read_n<B_KC, BN, TNW>(fb0, lds + A_F, wn, 0, lane);
@@ -312,6 +336,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
             frag_read<A_KC, BM>(fa0, Ns, wm, 0, lane);
             frag_read_n<B_KC, BN, TNW>(fb0, Ns + A_F, wn, 0, lane);
             load(K_lo + min(kt + 2, nk - 1) * GM_BK);
+            krows(kt + 3);
             mfma_4xn<TNW>(acc, fa1, fb1);
         }
         float* const Ls = lds + ((nk - 1) & 1) * (A_F + B_F);
