@@ -137,16 +137,62 @@ __global__ __launch_bounds__(256) void adamw_multi_k(float* __restrict__ p, cons
     const float eps_t = eps * sqrtf(bc2);
     const float wd = lr0 * wd0;
     const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
-    for (long i = c.start + threadIdx.x; i < c.start + c.len; i += 256) {
-        const float gi = g[i];
-        const float mi = b1 * m[i] + omb1 * gi;
-        const float vi = b2 * v[i] + omb2 * gi * gi;
-        m[i] = mi;
-        v[i] = vi;
+    auto one = [&](float& pi, float gi, float& mi, float& vi) {
+#pragma clang fp contract(off)
+        mi = b1 * mi + omb1 * gi;
+        vi = b2 * vi + omb2 * gi * gi;
         const float upd = mi / (sqrtf(vi) + eps_t);
-        float pi = p[i];
         pi -= wd * pi;
         pi -= lr * upd;
+    };
+    long i0 = c.start;
+    if (((c.start | c.len) & 3) == 0) {
+        // 16-byte accesses, four float4 of each array in flight per thread
+        // (unconditional loads in the unrolled part, the rest one at a time)
+        constexpr int U = 4;
+        const long n4 = c.len >> 2;
+        float4* p4 = reinterpret_cast<float4*>(p + c.start);
+        const float4* g4 = reinterpret_cast<const float4*>(g + c.start);
+        float4* m4 = reinterpret_cast<float4*>(m + c.start);
+        float4* v4 = reinterpret_cast<float4*>(v + c.start);
+        long i = threadIdx.x;
+        for (; i + 256 * (U - 1) < n4; i += 256 * U) {
+            float4 pr[U], gr[U], mr[U], vr[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                gr[u] = g4[i + 256 * u];
+                mr[u] = m4[i + 256 * u];
+                vr[u] = v4[i + 256 * u];
+                pr[u] = p4[i + 256 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                one(pr[u].x, gr[u].x, mr[u].x, vr[u].x);
+                one(pr[u].y, gr[u].y, mr[u].y, vr[u].y);
+                one(pr[u].z, gr[u].z, mr[u].z, vr[u].z);
+                one(pr[u].w, gr[u].w, mr[u].w, vr[u].w);
+                m4[i + 256 * u] = mr[u];
+                v4[i + 256 * u] = vr[u];
+                p4[i + 256 * u] = pr[u];
+            }
+        }
+        for (; i < n4; i += 256) {
+            float4 pr = p4[i], gr = g4[i], mr = m4[i], vr = v4[i];
+            one(pr.x, gr.x, mr.x, vr.x);
+            one(pr.y, gr.y, mr.y, vr.y);
+            one(pr.z, gr.z, mr.z, vr.z);
+            one(pr.w, gr.w, mr.w, vr.w);
+            m4[i] = mr;
+            v4[i] = vr;
+            p4[i] = pr;
+        }
+        i0 = c.start + c.len;  // nothing left
+    }
+    for (long i = i0 + threadIdx.x; i < c.start + c.len; i += 256) {
+        float pi = p[i], mi = m[i], vi = v[i];
+        one(pi, g[i], mi, vi);
+        m[i] = mi;
+        v[i] = vi;
         p[i] = pi;
     }
 }

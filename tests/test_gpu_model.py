@@ -55,8 +55,11 @@ def test_train_step_grads_match_oracle(cfg, batch, seq):
     dm.close()
 
 
-def test_adamw_over_all_tensors_bit_exact():
-    cfg = (256, 64, 4, 2, 8, 128)
+@pytest.mark.parametrize("cfg", [
+    (256, 64, 4, 2, 8, 128),
+    (255, 48, 3, 1, 3, 40),   # tensors whose sizes are not multiples of 4 (b_gate: 6)
+])
+def test_adamw_over_all_tensors_bit_exact(cfg):
     dm, om = _models(cfg, 5)
     rng = np.random.default_rng(2)
     grads = [rng.standard_normal(a.shape).astype(np.float32) for a in om.p]
