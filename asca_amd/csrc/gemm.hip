@@ -26,7 +26,11 @@
 // fragment read is one 16-byte ds_read: a [mn][k] read yields four k-steps of
 // one 16-row tile, a [k][mn] read yields one k-step of four tiles whose rows
 // are interleaved by 4.  The epilogue maps rows/columns back accordingly.
+// Plain products whose grid fills whole rounds of the CUs, and the grouped-K
+// expert weight gradients, take a 128 x 256 variant on 8 waves whose operand
+// tiles go from global memory straight into LDS (described at dma_mainloop).
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "gemm.h"
@@ -212,10 +216,193 @@ ASCA_DEV void mfma_4xn(f32x4 (&acc)[4][TN], const float (&fa)[4][4], const float
                 acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][x], fb[s][y], acc[x][y], 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS main loop (128 x 256 block tile, 8 waves of 64 x 64).
+//
+// The operand tiles go from global memory straight into LDS with
+// global_load_lds_dwordx4 (no register staging, no ds_write): each instruction
+// writes 64 lanes x 16 bytes contiguously at M0, and the lane -> global address
+// map is free, so every 1 KB chunk of a stage is laid out exactly as the MFMA
+// fragment reads want it: lane l reads the 16 bytes at chunk + 16 l (linear,
+// no bank conflict, no padding).  A stage is one k-tile of 16:
+//   k-contiguous operand ([mn][k] in memory): chunk c holds mn = 16 c + l % 16,
+//     k = 4 (l / 16) .. +3, i.e. the four k-steps of one 16-row tile;
+//   mn-contiguous operand ([k][mn]): chunk c holds k = 4 (l / 16) + c % 4,
+//     mn = 64 (c / 4) + 4 (l % 16) .. +3, i.e. one k-step of four tiles whose
+//     rows are interleaved by 4 (the same fragment semantics as the register
+//     path, so the epilogue is shared).
+// A (128 mn) has 8 chunks, B (256 mn) 16: wave w loads A chunk w and B chunks
+// 2w, 2w+1.  Three stages: step t waits for its own loads of tile t+1, passes
+// a barrier (every wave's part landed, every wave done reading tile t-1),
+// issues tile t+2 into the stage of tile t-1, reads the fragments of tile t+1
+// and multiplies tile t from registers.  Lanes whose k lies past the K range
+// load from a zero block instead (k tails, grouped K); rows past M or N are
+// clamped into the tile (their results are never stored).
+//
+// The loads are written as inline assembly: the compiler's own tracking of
+// LDS DMA makes every LDS read wait for all outstanding loads.  The loop waits
+// for them itself (s_waitcnt vmcnt(0) before each barrier), and waits for all
+// of them before the kernel ends, so no load lands in LDS after the block.
+constexpr int DMA_STAGES = 3, DMA_BK = 16, DMA_CH = 24;  // chunks per stage
+constexpr int DMA_STAGE_B = DMA_CH * 1024;
+
+__device__ float4 g_dma_zero = {0.f, 0.f, 0.f, 0.f};  // read-only source for k past the range
+
+ASCA_DEV void dma16(const float* g, unsigned lds_byte) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_byte), "v"(g) : "memory", "m0");
+}
+ASCA_DEV void dma_wait_all() { __builtin_amdgcn_s_waitcnt(0xF70); }  // vmcnt(0)
+
+// One lane's share of one chunk of an operand: source of the next k-tile.
+struct DmaSrc {
+    const float* p;  // k-contiguous, or mn-contiguous without row gather: source at the next k-tile
+    long step;       // advance per k-tile (floats)
+    long col;        // mn-contiguous: column of the lane's float4
+    int kofs;        // the lane's k within a k-tile
+    int idx;         // mn-contiguous with row gather: storage row of the next k-tile
+};
+
+template <bool KC>
+ASCA_DEV DmaSrc dma_src(int c, int lane, const float* base, long ld, const int* rows, long row_off, int mn0,
+                        int lim_mn, long K_lo, long K_hi) {
+    DmaSrc d;
+    if constexpr (KC) {
+        int mn = 16 * c + (lane & 15);
+        if (mn >= lim_mn) mn = 0;
+        d.kofs = 4 * (lane >> 4);
+        d.p = base + srow(rows, row_off, mn0 + mn) * ld + K_lo + d.kofs;
+        d.step = DMA_BK;
+        d.col = 0;
+        d.idx = 0;
+    } else {
+        d.kofs = 4 * (lane >> 4) + (c & 3);
+        const int mm = min(64 * (c >> 2) + 4 * (lane & 15), lim_mn - 4);
+        d.col = mn0 + mm;
+        d.p = base + (row_off + K_lo + d.kofs) * ld + d.col;
+        d.step = (long)DMA_BK * ld;
+        d.idx = rows ? rows[row_off + min(K_lo + d.kofs, K_hi - 1)] : 0;
+    }
+    return d;
+}
+
+// Issue k-tile t of one chunk into LDS byte address `dst`, then advance.  In
+// a k-tile that reaches past K_hi (`tail`, the last one at most) a lane whose
+// k is past K_hi reads the zero block.
+template <bool KC>
+ASCA_DEV void dma_issue(DmaSrc& d, long t, const float* base, long ld, const int* rows, long row_off, long K_lo,
+                        long K_hi, bool tail, unsigned dst) {
+    const long k = K_lo + t * DMA_BK + d.kofs;
+    const float* src = d.p;
+    if constexpr (!KC) {
+        if (rows) {  // uniform
+            src = base + (long)d.idx * ld + d.col;
+            d.idx = rows[row_off + min(k + DMA_BK, K_hi - 1)];  // next k-tile's storage row
+        }
+    }
+    if (tail && k >= K_hi) src = reinterpret_cast<const float*>(&g_dma_zero);  // tail: uniform
+    d.p += d.step;
+    dma16(src, dst);
+}
+
+template <bool TA, bool TB>
+ASCA_DEV void dma_mainloop(f32x4 (&acc)[4][4], const float* A, const float* B, const GemmArgs& p, long a_off,
+                           long b_off, int m0, int n0, int lim_m, int lim_n, long K_lo, long K_hi, int w, int lane,
+                           int wm, int wn) {
+    constexpr bool A_KC = !TA, B_KC = TB;
+    extern __shared__ float4 lds4[];
+    const float4* lds = lds4;
+    const unsigned lds_b = (unsigned)(unsigned long)((__attribute__((address_space(3))) float4*)lds4);
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    DmaSrc sa = dma_src<A_KC>(wu, lane, A, p.lda, p.a_rows, a_off, m0, lim_m, K_lo, K_hi);
+    DmaSrc sb0 = dma_src<B_KC>(2 * wu, lane, B, p.ldb, p.b_rows, b_off, n0, lim_n, K_lo, K_hi);
+    DmaSrc sb1 = dma_src<B_KC>(2 * wu + 1, lane, B, p.ldb, p.b_rows, b_off, n0, lim_n, K_lo, K_hi);
+    const unsigned ca = lds_b + (unsigned)wu * 1024u, cb = lds_b + (unsigned)(8 + 2 * wu) * 1024u;
+    // tile t into stage S (compile-time)
+    const long t_tail = (K_hi - K_lo) / DMA_BK;  // first k-tile not wholly inside the K range
+    auto issue = [&](long t, auto S) {
+        constexpr unsigned so = (unsigned)decltype(S)::value * DMA_STAGE_B;
+        const bool tail = t >= t_tail;
+        dma_issue<A_KC>(sa, t, A, p.lda, p.a_rows, a_off, K_lo, K_hi, tail, ca + so);
+        dma_issue<B_KC>(sb0, t, B, p.ldb, p.b_rows, b_off, K_lo, K_hi, tail, cb + so);
+        dma_issue<B_KC>(sb1, t, B, p.ldb, p.b_rows, b_off, K_lo, K_hi, tail, cb + 1024u + so);
+    };
+    float fa[2][4][4], fb[2][4][4];
+    // fragments of stage S into buffer BUF (both compile-time): 16-byte reads
+    // at chunk + 16 lane
+    const float4* rb = lds + lane;
+    const int ax = A_KC ? (wm >> 4) : (wm >> 6) * 4, bx = 8 + (B_KC ? (wn >> 4) : (wn >> 6) * 4);
+    auto rd = [&](auto S, auto BUF) {
+        constexpr int st = decltype(S)::value * (DMA_STAGE_B / 16), buf = decltype(BUF)::value;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = rb[st + (ax + i) * 64];
+            if constexpr (A_KC) {
+                fa[buf][0][i] = v.x; fa[buf][1][i] = v.y; fa[buf][2][i] = v.z; fa[buf][3][i] = v.w;
+            } else {
+                fa[buf][i][0] = v.x; fa[buf][i][1] = v.y; fa[buf][i][2] = v.z; fa[buf][i][3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = rb[st + (bx + i) * 64];
+            if constexpr (B_KC) {
+                fb[buf][0][i] = v.x; fb[buf][1][i] = v.y; fb[buf][2][i] = v.z; fb[buf][3][i] = v.w;
+            } else {
+                fb[buf][i][0] = v.x; fb[buf][i][1] = v.y; fb[buf][i][2] = v.z; fb[buf][i][3] = v.w;
+            }
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    const long nk = (K_hi - K_lo + DMA_BK - 1) / DMA_BK;  // > 0
+    issue(0, I0{});
+    if (nk > 1) issue(1, I1{});
+    dma_wait_all();
+    __syncthreads();
+    rd(I0{}, I0{});
+    // Step t at phase P = t % 6: tile t in buffer P % 2 and stage P % 3.
+    auto step = [&](long t, auto P) {
+        constexpr int ph = decltype(P)::value;
+        dma_wait_all();
+        __syncthreads();
+        if (t + 2 < nk) issue(t + 2, std::integral_constant<int, (ph + 2) % 3>{});
+        rd(std::integral_constant<int, (ph + 1) % 3>{}, std::integral_constant<int, (ph + 1) % 2>{});
+        mfma_4xn<4>(acc, fa[ph % 2], fb[ph % 2]);
+    };
+    using P3 = std::integral_constant<int, 3>;
+    using P4 = std::integral_constant<int, 4>;
+    using P5 = std::integral_constant<int, 5>;
+    long t = 0;
+    for (; t + 6 < nk; t += 6) {
+        step(t, I0{});
+        step(t + 1, I1{});
+        step(t + 2, I2{});
+        step(t + 3, P3{});
+        step(t + 4, P4{});
+        step(t + 5, P5{});
+    }
+    // the last 1..6 steps (the fragments read past the last tile are unused)
+    do {
+        step(t, I0{});
+        if (t + 1 >= nk) break;
+        step(t + 1, I1{});
+        if (t + 2 >= nk) break;
+        step(t + 2, I2{});
+        if (t + 3 >= nk) break;
+        step(t + 3, P3{});
+        if (t + 4 >= nk) break;
+        step(t + 4, P4{});
+        if (t + 5 >= nk) break;
+        step(t + 5, P5{});
+    } while (false);
+    dma_wait_all();
+}
+
 // Block tile (64 WM) x (16 TNW WN) on WM x WN waves; a wave owns 64 rows x
 // 16 TNW columns (TNW = 4, or 2 for the narrower tile that lets three blocks
 // share a CU).
-template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN, int TNW = 4>
+template <bool TA, bool TB, int EPI, bool VEC, int WM, int WN, int TNW = 4, bool DMA = false>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN >= 4 ? 2 : 1))) void gemm_k(GemmArgs p) {
     constexpr int NT = 64 * WM * WN, BM = 64 * WM, BN = 16 * TNW * WN;
     constexpr bool A_KC = !TA, B_KC = TB;
@@ -278,6 +465,11 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
         for (int y = 0; y < TNW; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    if constexpr (DMA) {
+        static_assert(WM == 2 && WN == 4 && TNW == 4 && VEC, "direct-to-LDS tile");
+        if (K_hi > K_lo)
+            dma_mainloop<TA, TB>(acc, A, B, p, a_off, b_off, m0, n0, lim_m, lim_n, K_lo, K_hi, w, lane, wm, wn);
+    } else {
     const long nk = (K_hi - K_lo + GM_BK - 1) / GM_BK;
     float4 ra[8 * BM / NT], rb[8 * BN / NT];
     // interior blocks (whole tiles in M and N) load without edge checks,
@@ -344,6 +536,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
         frag_read_n<B_KC, BN, TNW>(fb1, Ls + A_F, wn, 1, lane);
         mfma_4xn<TNW>(acc, fa0, fb0);
         mfma_4xn<TNW>(acc, fa1, fb1);
+    }
     }
 
     // epilogue: result register r of tile (x, y) sits at tile row 4 (lane / 16) + r,
@@ -698,18 +891,19 @@ static int scratch_get(size_t bytes, float** out) {
     return ASCA_OK;
 }
 
-template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2, int TNW = 4>
+template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2, int TNW = 4, bool DMA = false>
 static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds =
-        2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 16 * TNW * WN>()) * sizeof(float);
+        DMA ? (size_t)DMA_STAGES * DMA_STAGE_B
+            : 2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 16 * TNW * WN>()) * sizeof(float);
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN, TNW>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN, TNW, DMA>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
         attr = true;
     }
-    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN, TNW>), grid, dim3(64 * WM * WN), lds, st, a);
+    hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN, TNW, DMA>), grid, dim3(64 * WM * WN), lds, st, a);
     return ASCA_OK;
 }
 
@@ -779,7 +973,23 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     const bool narrow =
         vec && wm == 2 && a.gmode != 3 &&
         round_fill(count(64), per_cu64) * (per_cu64 >= 3 ? 0.95 : 0.8) > round_fill(count(128), 2);
-    const int bn = narrow ? 64 : 128;
+    // Direct-to-LDS 128 x 256 tiles (one 8-wave block per CU) where every
+    // operand float4 is whole (k-contiguous operands need K in multiples of 4,
+    // mn-contiguous ones M or N) and the grid fills whole rounds of the CUs.
+    // Measured against the 128 x 128 register-staged tile: 5-9% faster on
+    // plain products with full rounds (16384 x {1536, 512} x 512 NN and NT,
+    // 4096^3) and on the grouped-K expert weight gradients; slower with a
+    // partly empty last round and on the grouped-row products (left on the
+    // register path).
+    const bool kc_any = !ta || tb;
+    const bool dma_ok = vec && (!kc_any || a.K % 4 == 0) && (!ta || a.M % 4 == 0) && (tb || a.N % 4 == 0) &&
+                        a.N >= 4 && (!ta || a.M >= 4) && ((a.gmode == 0 && a.k_per_split <= 0) || a.gmode == 2);
+    auto count_dma = [&]() -> long {
+        const long tn = (a.N + 255) / 256, tm = (a.M + 127) / 128;
+        return a.gmode == 2 ? (long)a.ngroups * tm * tn : tm * tn;
+    };
+    const bool dma = dma_ok && wm == 2 && round_fill(count_dma(), 1) >= 0.9;
+    const int bn = dma ? 256 : narrow ? 64 : 128;
     a.tiles_n = (a.N + bn - 1) / bn;
     a.tiles_m = (a.M + 64 * wm - 1) / (64 * wm);
     long blocks;
@@ -798,6 +1008,7 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
 #define ASCA_GEMM_CASE(TA_, TB_, EPI_)                                                                  \
     if (ta == TA_ && tb == TB_ && epi == EPI_)                                                          \
         rc = !vec ? launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st)                                   \
+             : dma    ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 4, 4, true>(a, grid, st)                 \
              : narrow ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 2, 2>(a, grid, st)                       \
                       : launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st);                                \
     else

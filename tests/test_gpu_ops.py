@@ -50,7 +50,8 @@ def _ref_gemm(a, b, ta, tb, alpha, beta, c, bias):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 32), (1, 1, 1), (300, 257, 77), (64, 1536, 512),
-                                   (513, 16, 512), (130, 200, 4096), (7, 9, 0)])
+                                   (513, 16, 512), (130, 200, 4096), (7, 9, 0),
+                                   (300, 260, 84), (129, 516, 36)])  # partial tiles and k-tails, N % 4 == 0
 def test_gemm_variants(orc, g, ta, tb, M, N, K):
     rng = np.random.default_rng(M * 7 + N * 3 + K + 10 * ta + tb)
     a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
