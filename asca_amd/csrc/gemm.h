@@ -41,6 +41,13 @@ struct GemmArgs {
 GemmArgs gemm_args();
 // m_total: for gmode 1, the total rows over all groups (bounds the grid).
 int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t st, const char* name);
+// Skinny products with n <= 16 columns (the gate projection): Y (T x n, ld n)
+// = X W + b, and G (K x n, ld n) = X^T D with db = column sums of D (db may be
+// null).  Shapes the 16-wide kernels do not take go to the general GEMM.
+int skinny_fwd_launch(const float* X, long ldx, const float* W, const float* b, float* Y, long T, int K, int n,
+                      hipStream_t st);
+int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, float* db, long T, int K, int n,
+                        hipStream_t st);
 // out[g*N + c] (+)= column sums of X over the rows of group g (or all rows).
 int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, int ngroups, float* out,
                   int accumulate, hipStream_t st);

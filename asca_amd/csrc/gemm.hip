@@ -1085,6 +1085,175 @@ int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, i
     return post_launch("colsum_fin");
 }
 
+// ---------------------------------------------------------------------------
+// Skinny products with n <= 16 output columns (the gate projection, n = 2H):
+// the 16-wide MFMA output tile matches them, where a 128-wide block tile of
+// the general kernel would multiply mostly padding.
+//
+// Forward Y (T x n) = X (T x K) W (K x n) + b: one wave per 16 rows.  Lane
+// (i = l % 16, q = l / 16) supplies A = X[row i][16 j + 4 q + e] from one
+// 16-byte load per 16-k group j (e = 0..3 are four MFMA k-steps: the k index
+// is permuted inside each group of 16, which the sum does not see) and keeps
+// the matching B = W[16 j + 4 q + e][i] for the whole K in registers.
+template <int KT>  // K = 16 KT
+__global__ __launch_bounds__(256) void skinny_fwd_k(const float* __restrict__ X, long ldx, const float* __restrict__ W,
+                                                    const float* __restrict__ b, float* __restrict__ Y, long T, int n) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const long r0 = ((long)blockIdx.x * 4 + w) * 16;
+    if (r0 >= T) return;  // whole wave
+    const int i = lane & 15, q = lane >> 4;
+    const int ic = min(i, n - 1);
+    float wb[4 * KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = W[(long)(16 * j + 4 * q + e) * n + ic];
+            wb[4 * j + e] = i < n ? v : 0.0f;
+        }
+    const float* xr = X + min(r0 + i, T - 1) * ldx + 4 * q;
+    float4 xv[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) xv[j] = *reinterpret_cast<const float4*>(xr + 16 * j);
+    // every load above is in flight before the first product (the scheduler
+    // would otherwise interleave them with the products, one wait each)
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].x, wb[4 * j + 0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].y, wb[4 * j + 1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].z, wb[4 * j + 2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].w, wb[4 * j + 3], acc, 0, 0, 0);
+    }
+    const float bi = b ? b[ic] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const long row = r0 + 4 * q + r;
+        if (i < n && row < T) Y[row * n + i] = acc[r] + bi;
+    }
+}
+
+// Weight gradient G (K x n) = X^T D and bias gradient db = column sums of D,
+// over T rows.  Wave (tile it, chunk s) reduces rows s*SK_T .. +SK_T into a
+// 16 x 16 partial of G (i = 16 it + lane % 16): per MFMA k-step the four lane
+// groups q take rows t = 4 m + q, lane (i, q) supplies X[t][16 it + i] and
+// D[t][i].  Waves of tile 0 also sum their D values for db.  Partials go to
+// part[s][K + 1][16] (row K: db) and skinny_reduce_k adds them in chunk order.
+constexpr int SK_T = 256;  // rows per wave
+__global__ __launch_bounds__(256) void skinny_wgrad_k(const float* __restrict__ X, long ldx,
+                                                      const float* __restrict__ D, long T, int K, int n,
+                                                      float* __restrict__ part) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int it = blockIdx.x;
+    const long s = (long)blockIdx.y * 4 + w;
+    const long nch = (T + SK_T - 1) / SK_T;
+    if (s >= nch) return;  // whole wave
+    const int i = lane & 15, q = lane >> 4;
+    const int ic = min(i, n - 1);
+    const long t0 = s * SK_T;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float dsum = 0.0f;
+    constexpr int NM = SK_T / 4;
+    constexpr int G = 16;  // k-steps whose loads are issued together
+#pragma unroll 1
+    for (int m0 = 0; m0 < NM; m0 += G) {
+        float av[G], bv[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const long t = t0 + 4 * (m0 + u) + q;
+            const long tc = min(t, T - 1);
+            const float xa = X[tc * ldx + 16 * it + i];
+            const float db = D[tc * n + ic];
+            av[u] = t < T ? xa : 0.0f;
+            bv[u] = (t < T && i < n) ? db : 0.0f;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the group's loads go out together
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+            dsum += bv[u];
+        }
+    }
+    float* ps = part + s * (long)(K + 1) * 16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ps[(16 * it + 4 * q + r) * 16 + i] = acc[r];
+    if (it == 0) {
+        dsum += __shfl_xor(dsum, 16);
+        dsum += __shfl_xor(dsum, 32);
+        if (q == 0) ps[K * 16 + i] = dsum;
+    }
+}
+
+__global__ __launch_bounds__(256) void skinny_reduce_k(const float* __restrict__ part, long nch, int K, int n,
+                                                       float* __restrict__ G, float* __restrict__ db) {
+    const long e = (long)blockIdx.x * 256 + threadIdx.x;  // output (row, col) of the (K + 1) x n result
+    if (e >= (long)(K + 1) * n) return;
+    const int row = (int)(e / n), col = (int)(e - (long)row * n);
+    float acc = 0.0f;
+    for (long s = 0; s < nch; ++s) acc += part[(s * (K + 1) + row) * 16 + col];
+    if (row < K)
+        G[(long)row * n + col] = acc;
+    else if (db)
+        db[col] = acc;
+}
+
+static bool skinny_ok(const float* X, long ldx, int K, int n) {
+    return n >= 1 && n <= 16 && (K == 128 || K == 256 || K == 512) && ldx % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+}
+
+int skinny_fwd_launch(const float* X, long ldx, const float* W, const float* b, float* Y, long T, int K, int n,
+                      hipStream_t st) {
+    if (T <= 0 || n <= 0) return ASCA_OK;
+    if (!skinny_ok(X, ldx, K, n)) {
+        GemmArgs a = gemm_args();
+        a.A = X;
+        a.lda = ldx;
+        a.B = W;
+        a.ldb = n;
+        a.C = Y;
+        a.ldc = n;
+        a.M = (int)T;
+        a.N = n;
+        a.K = K;
+        a.bias = b;
+        return gemm_launch(0, 0, EPI_STORE, a, T, st, "skinny_fwd");
+    }
+    int rc = pre_launch("skinny_fwd");
+    if (rc) return rc;
+    const dim3 grid((unsigned)((T + 63) / 64));
+    if (K == 512)
+        hipLaunchKernelGGL(skinny_fwd_k<32>, grid, dim3(256), 0, st, X, ldx, W, b, Y, T, n);
+    else if (K == 256)
+        hipLaunchKernelGGL(skinny_fwd_k<16>, grid, dim3(256), 0, st, X, ldx, W, b, Y, T, n);
+    else
+        hipLaunchKernelGGL(skinny_fwd_k<8>, grid, dim3(256), 0, st, X, ldx, W, b, Y, T, n);
+    return post_launch("skinny_fwd");
+}
+
+int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, float* db, long T, int K, int n,
+                        hipStream_t st) {
+    if (n <= 0 || K <= 0) return ASCA_OK;
+    if (T <= 0 || !skinny_ok(X, ldx, K, n) || K % 16) {
+        int rc = asca_gemm(1, 0, K, n, (int)T, 1.0f, X, (int)ldx, D, n, 0.0f, G, n, nullptr, st);
+        if (rc || !db) return rc;
+        return colsum_launch(D, T, n, n, nullptr, 0, db, 0, st);
+    }
+    const long nch = (T + SK_T - 1) / SK_T;
+    float* part = nullptr;
+    int rc = scratch_get((size_t)nch * (K + 1) * 16 * sizeof(float), &part);
+    if (rc) return rc;
+    if ((rc = pre_launch("skinny_wgrad"))) return rc;
+    hipLaunchKernelGGL(skinny_wgrad_k, dim3((unsigned)(K / 16), (unsigned)((nch + 3) / 4)), dim3(256), 0, st, X, ldx,
+                       D, T, K, n, part);
+    if ((rc = post_launch("skinny_wgrad"))) return rc;
+    if ((rc = pre_launch("skinny_reduce"))) return rc;
+    hipLaunchKernelGGL(skinny_reduce_k, dim3((unsigned)(((long)(K + 1) * n + 255) / 256)), dim3(256), 0, st, part,
+                       nch, K, n, G, db);
+    return post_launch("skinny_reduce");
+}
+
 }  // namespace asca
 
 using namespace asca;

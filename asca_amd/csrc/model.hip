@@ -353,9 +353,7 @@ static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* tar
         GemmArgs q = gemm_plain(x, d, M->p + P.w_qkv, 3 * d, M->qkv_t, 3 * d, T, 3 * d, d);
         q.bias = M->p + P.b_qkv;
         if ((rc = gemm_launch(0, 0, EPI_STORE, q, T, st, "qkv_proj"))) return rc;
-        GemmArgs gg = gemm_plain(x, d, M->p + P.w_gate, 2 * H, M->gate_t, 2 * H, T, 2 * H, d);
-        gg.bias = M->p + P.b_gate;
-        if ((rc = gemm_launch(0, 0, EPI_STORE, gg, T, st, "gate_proj"))) return rc;
+        if ((rc = skinny_fwd_launch(x, d, M->p + P.w_gate, M->p + P.b_gate, M->gate_t, T, d, 2 * H, st))) return rc;
         if ((rc = pre_launch("qkv_prep"))) return rc;
         hipLaunchKernelGGL(qkv_prep_k, dim3(T), dim3(256), 0, st, M->qkv_t, M->gate_t, H, dh, a.q, a.k, a.v, a.qn,
                            a.kn, a.al, a.be);
@@ -458,8 +456,7 @@ static int model_backward(asca_model* M, hipStream_t st) {
             return rc;
         if ((rc = gemm_wgrad(x_in, d, M->dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, st))) return rc;
         if ((rc = asca_colsum(M->dqkv, T, 3 * d, G + P.b_qkv, 0, st))) return rc;
-        if ((rc = gemm_wgrad(x_in, d, M->dgate, 2 * H, G + P.w_gate, d, 2 * H, T, st))) return rc;
-        if ((rc = asca_colsum(M->dgate, T, 2 * H, G + P.b_gate, 0, st))) return rc;
+        if ((rc = skinny_wgrad_launch(x_in, d, M->dgate, G + P.w_gate, G + P.b_gate, T, d, 2 * H, st))) return rc;
         // dx = d_mid + d_qkv W_qkv^T + d_gate W_gate^T
         GemmArgs dq = gemm_plain(M->dqkv, 3 * d, M->p + P.w_qkv, 3 * d, M->dx, d, T, d, 3 * d);
         dq.resid = M->dmid;
@@ -544,9 +541,7 @@ static int model_decode(asca_model* M, const uint32_t* ids, int n, float* states
         GemmArgs q = gemm_plain(x, d, M->p + P.w_qkv, 3 * d, D.qkv, 3 * d, n, 3 * d, d);
         q.bias = M->p + P.b_qkv;
         if ((rc = gemm_launch(0, 0, EPI_STORE, q, n, st, "dec_qkv_proj"))) return rc;
-        GemmArgs gg = gemm_plain(x, d, M->p + P.w_gate, 2 * H, D.gate, 2 * H, n, 2 * H, d);
-        gg.bias = M->p + P.b_gate;
-        if ((rc = gemm_launch(0, 0, EPI_STORE, gg, n, st, "dec_gate_proj"))) return rc;
+        if ((rc = skinny_fwd_launch(x, d, M->p + P.w_gate, M->p + P.b_gate, D.gate, n, d, 2 * H, st))) return rc;
         if ((rc = asca_delta_decode_step(states + l * sl, D.qkv, D.gate, D.o, n, H, dh, st))) return rc;
         GemmArgs yo = gemm_plain(D.o, d, M->p + P.w_o, d, D.mid, d, n, d, d);
         yo.bias = M->p + P.b_o;

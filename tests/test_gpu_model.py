@@ -32,6 +32,8 @@ def _models(cfg, seed):
     ((256, 64, 4, 2, 8, 128), 2, 32),
     ((256, 512, 8, 1, 16, 1024), 2, 64),    # configs[3] widths, 128 tokens
     ((200, 48, 3, 2, 5, 40), 3, 17),        # ragged: odd widths, dh 16, T not a multiple of 8
+    ((256, 128, 4, 1, 4, 64), 3, 100),      # gate projection on the 16-column kernels with K = 128, 300 rows
+    ((256, 256, 16, 1, 4, 64), 2, 20),      # 2H = 32 gate columns: the general GEMM
 ])
 def test_train_step_grads_match_oracle(cfg, batch, seq):
     dm, om = _models(cfg, 21)
