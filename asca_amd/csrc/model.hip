@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "gemm.h"
+#include "moe.h"
 #include "ops.h"
 #include "runtime.h"
 
@@ -240,8 +241,15 @@ struct asca_model {
     std::vector<void*> allocs;
     std::vector<MActs> acts;
     float *x0 = nullptr, *qkv_t = nullptr, *gate_t = nullptr, *h_final = nullptr, *logits = nullptr;
-    float *dlogits = nullptr, *losses = nullptr, *loss = nullptr, *dx = nullptr, *dmid = nullptr;
-    float *dxn = nullptr, *dtmp = nullptr, *dqkv = nullptr, *dgate = nullptr, *dpre = nullptr;
+    float *dlogits = nullptr, *losses = nullptr, *loss = nullptr;
+    float *dxn = nullptr, *dtmp = nullptr;
+    // two sets, alternating by layer, of the gradients the weight-gradient
+    // stream reads while the next layer's backward runs
+    float *dx[2] = {nullptr, nullptr}, *dmid[2] = {nullptr, nullptr}, *dqkv[2] = {nullptr, nullptr},
+          *dgate[2] = {nullptr, nullptr}, *dpre[2] = {nullptr, nullptr};
+    // weight-gradient stream (default priority, non-blocking) and its events
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> evs;
     int32_t *route_e = nullptr, *perm = nullptr, *off = nullptr, *emb_b = nullptr, *emb_perm = nullptr,
             *emb_off = nullptr;
     void *route_ws = nullptr, *emb_ws = nullptr;
@@ -296,10 +304,8 @@ static int ensure_acts(asca_model* M, int batch, int seq) {
         if ((rc = dalloc(M, &M->x0, T * d)) || (rc = dalloc(M, &M->qkv_t, T * 3 * d)) ||
             (rc = dalloc(M, &M->gate_t, T * 2 * H)) || (rc = dalloc(M, &M->h_final, T * d)) ||
             (rc = dalloc(M, &M->logits, T * V)) || (rc = dalloc(M, &M->dlogits, T * V)) ||
-            (rc = dalloc(M, &M->losses, T)) || (rc = dalloc(M, &M->loss, 1)) || (rc = dalloc(M, &M->dx, T * d)) ||
-            (rc = dalloc(M, &M->dmid, T * d)) || (rc = dalloc(M, &M->dxn, T * d)) ||
-            (rc = dalloc(M, &M->dtmp, T * d)) || (rc = dalloc(M, &M->dqkv, T * 3 * d)) ||
-            (rc = dalloc(M, &M->dgate, T * 2 * H)) || (rc = dalloc(M, &M->dpre, T * dff)) ||
+            (rc = dalloc(M, &M->losses, T)) || (rc = dalloc(M, &M->loss, 1)) || (rc = dalloc(M, &M->dxn, T * d)) ||
+            (rc = dalloc(M, &M->dtmp, T * d)) ||
             (rc = dalloc(M, &M->route_e, T)) || (rc = dalloc(M, &M->perm, T)) ||
             (rc = dalloc(M, &M->off, (size_t)M->E + 1)) || (rc = dalloc(M, &M->emb_b, T)) ||
             (rc = dalloc(M, &M->emb_perm, T)) || (rc = dalloc(M, &M->emb_off, V + 1)) ||
@@ -307,6 +313,11 @@ static int ensure_acts(asca_model* M, int batch, int seq) {
             goto oom;
         M->route_ws = rw;
         M->emb_ws = ew;
+        for (int k = 0; k < 2; ++k)
+            if ((rc = dalloc(M, &M->dx[k], T * d)) || (rc = dalloc(M, &M->dmid[k], T * d)) ||
+                (rc = dalloc(M, &M->dqkv[k], T * 3 * d)) || (rc = dalloc(M, &M->dgate[k], T * 2 * H)) ||
+                (rc = dalloc(M, &M->dpre[k], T * dff)))
+                goto oom;
     }
     M->batch = batch;
     M->seq = seq;
@@ -426,50 +437,107 @@ static int gemm_wgrad(const float* X, int ldx, const float* D, int ldd, float* G
     return asca_gemm(1, 0, M_, N_, T, 1.0f, X, ldx, D, ldd, 0.0f, G, N_, nullptr, st);
 }
 
+// Weight-gradient stream and its events, created on first use.  Events per
+// layer l: 4l + {0: dpre written, 1: d_mid written, 2: d_qkv written, 3: the
+// layer's weight gradients done}; then fork and join.
+static int ensure_side(asca_model* M) {
+    if (M->side) return ASCA_OK;
+    hipError_t e = hipStreamCreateWithFlags(&M->side, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        M->side = nullptr;
+        return fail(ASCA_ERR_HIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
+    }
+    M->evs.assign((size_t)4 * M->L + 2, nullptr);
+    for (auto& ev : M->evs)
+        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
+            return fail(ASCA_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
+    return ASCA_OK;
+}
+
+// `from` records event ev, `to` waits for it.
+static int hand_over(hipStream_t from, hipStream_t to, hipEvent_t ev) {
+    hipError_t e = hipEventRecord(ev, from);
+    if (e == hipSuccess) e = hipStreamWaitEvent(to, ev, 0);
+    return e == hipSuccess ? (int)ASCA_OK : fail(ASCA_ERR_HIP, "stream hand-over: %s", hipGetErrorString(e));
+}
+
 // Backward of the whole model into the gradient buffer (overwritten).
+//
+// The chain of data gradients (dx through each layer) runs on the caller's
+// stream `st`.  The weight and bias gradients, which nothing later in the
+// backward reads, run on the model's second stream as soon as their inputs
+// are written, so they overlap the next layer's chain (above all the
+// VALU-bound recurrence backward, which leaves the matrix cores idle).  The
+// gradients they read alternate between two buffer sets by layer parity;
+// before the chain overwrites a set it waits for the weight gradients that
+// read it (layer l + 2, and layer l + 1 for dx), and `st` joins the second
+// stream at the end, so work queued on `st` afterwards sees every gradient.
 static int model_backward(asca_model* M, hipStream_t st) {
-    const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V;
-    int rc;
+    const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V, L = M->L;
+    int rc = ensure_side(M);
+    if (rc) return rc;
+    hipStream_t sd = M->side;
+    auto ev = [&](int l, int k) { return M->evs[(size_t)4 * l + k]; };
+    hipEvent_t ev_fork = M->evs[(size_t)4 * L], ev_join = M->evs[(size_t)4 * L + 1];
     float* G = M->g;
-    const float* x_last = M->acts[M->L - 1].x_out;
-    // head: d_head = h^T dlogits ; dh = dlogits W_head^T ; dx = rmsnorm_bwd(x_L, dh)
-    if ((rc = gemm_wgrad(M->h_final, d, M->dlogits, V, G + M->t[1].off, d, V, T, st))) return rc;
+    const float* x_last = M->acts[L - 1].x_out;
+    if ((rc = hand_over(st, sd, ev_fork))) return rc;
+    // head: d_head = h^T dlogits (second stream) ; dh = dlogits W_head^T ; dx = rmsnorm_bwd(x_L, dh)
+    if ((rc = gemm_wgrad(M->h_final, d, M->dlogits, V, G + M->t[1].off, d, V, T, sd))) return rc;
     GemmArgs dhh = gemm_plain(M->dlogits, V, M->p + M->t[1].off, V, M->dtmp, d, T, d, V);
     if ((rc = gemm_launch(0, 1, EPI_STORE, dhh, T, st, "head_dx"))) return rc;
-    if ((rc = rmsnorm_bwd_launch(x_last, M->dtmp, nullptr, M->dx, T, d, MODEL_EPS, st))) return rc;
-    for (int l = M->L - 1; l >= 0; --l) {
+    if ((rc = rmsnorm_bwd_launch(x_last, M->dtmp, nullptr, M->dx[(L - 1) & 1], T, d, MODEL_EPS, st))) return rc;
+    for (int l = L - 1; l >= 0; --l) {
         const MLayer& P = M->lay[l];
         MActs& a = M->acts[l];
         const float* x_in = l ? M->acts[l - 1].x_out : M->x0;
-        // MoE backward from dout = dx; d_mid = dx + rmsnorm_bwd(x_mid, dxn)
-        if ((rc = asca_moe_bwd(a.xn, M->p + P.w1, M->p + P.w2, a.pre, a.hid, M->perm, M->off, M->dx, T, d, dff, E,
-                               M->dxn, G + P.w1, G + P.b1, G + P.w2, G + P.b2, M->dpre, 0, st)))
+        const int b = l & 1;
+        float *din = M->dx[b], *dout = M->dx[b ^ 1], *dmid = M->dmid[b], *dqkv = M->dqkv[b], *dgate = M->dgate[b],
+              *dpre = M->dpre[b];
+        // set b was last read by the weight gradients of layer l + 2
+        if (l + 2 < L && hipStreamWaitEvent(st, ev(l + 2, 3), 0) != hipSuccess)
+            return fail(ASCA_ERR_HIP, "hipStreamWaitEvent failed");
+        // MoE backward from dout = din; d_mid = din + rmsnorm_bwd(x_mid, dxn)
+        if ((rc = moe_bwd_data(M->p + P.w1, M->p + P.w2, a.pre, M->perm, M->off, din, T, d, dff, E, M->dxn, dpre,
+                               st)))
             return rc;
-        if ((rc = rmsnorm_bwd_launch(a.x_mid, M->dxn, M->dx, M->dmid, T, d, MODEL_EPS, st))) return rc;
+        if ((rc = hand_over(st, sd, ev(l, 0)))) return rc;
+        if ((rc = moe_bwd_weights(a.xn, a.hid, M->perm, M->off, din, dpre, T, d, dff, E, G + P.w1, G + P.b1,
+                                  G + P.w2, G + P.b2, 0, sd)))
+            return rc;
+        if ((rc = rmsnorm_bwd_launch(a.x_mid, M->dxn, din, dmid, T, d, MODEL_EPS, st))) return rc;
+        if ((rc = hand_over(st, sd, ev(l, 1)))) return rc;
+        if ((rc = gemm_wgrad(a.o, d, dmid, d, G + P.w_o, d, d, T, sd))) return rc;
+        if ((rc = asca_colsum(dmid, T, d, G + P.b_o, 0, sd))) return rc;
         // delta block backward (delta.rs:615-674) from dy = d_mid
-        GemmArgs dov = gemm_plain(M->dmid, d, M->p + P.w_o, d, M->dtmp, d, T, d, d);
+        GemmArgs dov = gemm_plain(dmid, d, M->p + P.w_o, d, M->dtmp, d, T, d, d);
         if ((rc = gemm_launch(0, 1, EPI_STORE, dov, T, st, "out_proj_dx"))) return rc;
-        if ((rc = gemm_wgrad(a.o, d, M->dmid, d, G + P.w_o, d, d, T, st))) return rc;
-        if ((rc = asca_colsum(M->dmid, T, d, G + P.b_o, 0, st))) return rc;
-        if ((rc = asca_delta_bwd_fused(a.q, a.k, a.v, a.al, a.be, a.qn, a.kn, M->dtmp, a.dws, M->dqkv, M->dgate,
-                                       M->batch, M->seq, H, dh, st)))
+        if ((rc = asca_delta_bwd_fused(a.q, a.k, a.v, a.al, a.be, a.qn, a.kn, M->dtmp, a.dws, dqkv, dgate, M->batch,
+                                       M->seq, H, dh, st)))
             return rc;
-        if ((rc = gemm_wgrad(x_in, d, M->dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, st))) return rc;
-        if ((rc = asca_colsum(M->dqkv, T, 3 * d, G + P.b_qkv, 0, st))) return rc;
-        if ((rc = skinny_wgrad_launch(x_in, d, M->dgate, G + P.w_gate, G + P.b_gate, T, d, 2 * H, st))) return rc;
+        if ((rc = hand_over(st, sd, ev(l, 2)))) return rc;
+        if ((rc = gemm_wgrad(x_in, d, dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, sd))) return rc;
+        if ((rc = asca_colsum(dqkv, T, 3 * d, G + P.b_qkv, 0, sd))) return rc;
+        if ((rc = skinny_wgrad_launch(x_in, d, dgate, G + P.w_gate, G + P.b_gate, T, d, 2 * H, sd))) return rc;
+        if (hipEventRecord(ev(l, 3), sd) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
+        // dout (the layer below's din) was last read by the weight gradients of layer l + 1
+        if (l + 1 < L && hipStreamWaitEvent(st, ev(l + 1, 3), 0) != hipSuccess)
+            return fail(ASCA_ERR_HIP, "hipStreamWaitEvent failed");
         // dx = d_mid + d_qkv W_qkv^T + d_gate W_gate^T
-        GemmArgs dq = gemm_plain(M->dqkv, 3 * d, M->p + P.w_qkv, 3 * d, M->dx, d, T, d, 3 * d);
-        dq.resid = M->dmid;
+        GemmArgs dq = gemm_plain(dqkv, 3 * d, M->p + P.w_qkv, 3 * d, dout, d, T, d, 3 * d);
+        dq.resid = dmid;
         dq.ld_resid = d;
         if ((rc = gemm_launch(0, 1, EPI_STORE, dq, T, st, "qkv_proj_dx"))) return rc;
-        GemmArgs dg = gemm_plain(M->dgate, 2 * H, M->p + P.w_gate, 2 * H, M->dx, d, T, d, 2 * H);
+        GemmArgs dg = gemm_plain(dgate, 2 * H, M->p + P.w_gate, 2 * H, dout, d, T, d, 2 * H);
         dg.beta = 1.0f;
         if ((rc = gemm_launch(0, 1, EPI_STORE, dg, T, st, "gate_proj_dx"))) return rc;
     }
     // embedding gradient
     if ((rc = pre_launch("embed_grad"))) return rc;
-    hipLaunchKernelGGL(embed_grad_k, dim3(V), dim3(256), 0, st, M->dx, M->emb_perm, M->emb_off, d, G + M->t[0].off);
-    return post_launch("embed_grad");
+    hipLaunchKernelGGL(embed_grad_k, dim3(V), dim3(256), 0, st, M->dx[1], M->emb_perm, M->emb_off, d,
+                       G + M->t[0].off);
+    if ((rc = post_launch("embed_grad"))) return rc;
+    return hand_over(sd, st, ev_join);
 }
 
 static int model_adamw(asca_model* M, hipStream_t st) {
@@ -599,6 +667,9 @@ static void destroy_model(asca_model* M) {
     free_acts(M);
     free_decode(M);
     (void)hipDeviceSynchronize();
+    for (hipEvent_t e : M->evs)
+        if (e) (void)hipEventDestroy(e);
+    if (M->side) (void)hipStreamDestroy(M->side);
     for (void* q : {(void*)M->p, (void*)M->g, (void*)M->m, (void*)M->v, (void*)M->chunks})
         if (q) (void)hipFree(q);
     delete M;
