@@ -234,6 +234,7 @@ struct asca_model {
     std::vector<MLayer> lay;
     AdamChunk* chunks = nullptr;
     int n_chunks = 0;
+    std::vector<int> chunk0;  // first AdamW chunk of tensor j (size tensors + 1)
     float lr = 3e-4f, b1 = 0.9f, b2 = 0.95f, eps = 1e-8f, wd = 0.01f;
     uint32_t adam_step = 0;
     // activation workspace, sized for one (batch, seq)
@@ -438,8 +439,9 @@ static int gemm_wgrad(const float* X, int ldx, const float* D, int ldd, float* G
 }
 
 // Weight-gradient stream and its events, created on first use.  Events per
-// layer l: 4l + {0: dpre written, 1: d_mid written, 2: d_qkv written, 3: the
-// layer's weight gradients done}; then fork and join.
+// layer l: 5l + {0: dpre written, 1: d_mid written, 2: d_qkv written, 3: the
+// layer's weight gradients done, 4: the chain done with the layer's weights};
+// then fork, join, head weights done, embedding gradient done.
 static int ensure_side(asca_model* M) {
     if (M->side) return ASCA_OK;
     hipError_t e = hipStreamCreateWithFlags(&M->side, hipStreamNonBlocking);
@@ -447,7 +449,7 @@ static int ensure_side(asca_model* M) {
         M->side = nullptr;
         return fail(ASCA_ERR_HIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
     }
-    M->evs.assign((size_t)4 * M->L + 2, nullptr);
+    M->evs.assign((size_t)5 * M->L + 4, nullptr);
     for (auto& ev : M->evs)
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
             return fail(ASCA_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
@@ -472,13 +474,20 @@ static int hand_over(hipStream_t from, hipStream_t to, hipEvent_t ev) {
 // before the chain overwrites a set it waits for the weight gradients that
 // read it (layer l + 2, and layer l + 1 for dx), and `st` joins the second
 // stream at the end, so work queued on `st` afterwards sees every gradient.
-static int model_backward(asca_model* M, hipStream_t st) {
+static int adamw_range(asca_model* M, size_t j0, size_t j1, hipStream_t st);
+
+// with_adamw: also apply AdamW on the second stream, each layer's tensors as
+// soon as their gradients are final and the chain no longer reads their
+// weights (the update is elementwise per tensor, so the result is the same as
+// one launch after the backward); the caller advances the step counter.
+static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false) {
     const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V, L = M->L;
     int rc = ensure_side(M);
     if (rc) return rc;
     hipStream_t sd = M->side;
-    auto ev = [&](int l, int k) { return M->evs[(size_t)4 * l + k]; };
-    hipEvent_t ev_fork = M->evs[(size_t)4 * L], ev_join = M->evs[(size_t)4 * L + 1];
+    auto ev = [&](int l, int k) { return M->evs[(size_t)5 * l + k]; };
+    hipEvent_t ev_fork = M->evs[(size_t)5 * L], ev_join = M->evs[(size_t)5 * L + 1];
+    hipEvent_t ev_head = M->evs[(size_t)5 * L + 2], ev_emb = M->evs[(size_t)5 * L + 3];
     float* G = M->g;
     const float* x_last = M->acts[L - 1].x_out;
     if ((rc = hand_over(st, sd, ev_fork))) return rc;
@@ -487,6 +496,9 @@ static int model_backward(asca_model* M, hipStream_t st) {
     GemmArgs dhh = gemm_plain(M->dlogits, V, M->p + M->t[1].off, V, M->dtmp, d, T, d, V);
     if ((rc = gemm_launch(0, 1, EPI_STORE, dhh, T, st, "head_dx"))) return rc;
     if ((rc = rmsnorm_bwd_launch(x_last, M->dtmp, nullptr, M->dx[(L - 1) & 1], T, d, MODEL_EPS, st))) return rc;
+    if (with_adamw) {  // head (tensor 1): its gradient is queued on the second stream, its weights read above
+        if ((rc = hand_over(st, sd, ev_head)) || (rc = adamw_range(M, 1, 2, sd))) return rc;
+    }
     for (int l = L - 1; l >= 0; --l) {
         const MLayer& P = M->lay[l];
         MActs& a = M->acts[l];
@@ -531,21 +543,36 @@ static int model_backward(asca_model* M, hipStream_t st) {
         GemmArgs dg = gemm_plain(dgate, 2 * H, M->p + P.w_gate, 2 * H, dout, d, T, d, 2 * H);
         dg.beta = 1.0f;
         if ((rc = gemm_launch(0, 1, EPI_STORE, dg, T, st, "gate_proj_dx"))) return rc;
+        if (with_adamw) {  // layer l's tensors: 2 + 10 l .. 2 + 10 l + 9
+            if ((rc = hand_over(st, sd, ev(l, 4))) || (rc = adamw_range(M, 2 + 10 * (size_t)l, 12 + 10 * (size_t)l, sd)))
+                return rc;
+        }
     }
     // embedding gradient
     if ((rc = pre_launch("embed_grad"))) return rc;
     hipLaunchKernelGGL(embed_grad_k, dim3(V), dim3(256), 0, st, M->dx[1], M->emb_perm, M->emb_off, d,
                        G + M->t[0].off);
     if ((rc = post_launch("embed_grad"))) return rc;
+    if (with_adamw) {  // embedding (tensor 0)
+        if ((rc = hand_over(st, sd, ev_emb)) || (rc = adamw_range(M, 0, 1, sd))) return rc;
+    }
     return hand_over(sd, st, ev_join);
 }
 
-static int model_adamw(asca_model* M, hipStream_t st) {
+// AdamW over tensors j0 .. j1-1 with the step counter base M->adam_step (the
+// caller advances it once all tensors are updated).
+static int adamw_range(asca_model* M, size_t j0, size_t j1, hipStream_t st) {
+    const int c0 = M->chunk0[j0], c1 = M->chunk0[j1];
+    if (c1 <= c0) return ASCA_OK;
     int rc = pre_launch("adamw_multi");
     if (rc) return rc;
-    hipLaunchKernelGGL(adamw_multi_k, dim3(M->n_chunks), dim3(256), 0, st, M->p, M->g, M->m, M->v, M->chunks,
+    hipLaunchKernelGGL(adamw_multi_k, dim3(c1 - c0), dim3(256), 0, st, M->p, M->g, M->m, M->v, M->chunks + c0,
                        M->adam_step, M->lr, M->b1, M->b2, M->eps, M->wd);
-    rc = post_launch("adamw_multi");
+    return post_launch("adamw_multi");
+}
+
+static int model_adamw(asca_model* M, hipStream_t st) {
+    int rc = adamw_range(M, 0, M->t.size(), st);
     if (rc) return rc;
     M->adam_step += (uint32_t)M->t.size();
     return ASCA_OK;
@@ -725,6 +752,11 @@ int asca_model_create(int vocab, int d_model, int n_heads, int n_layers, int n_e
         for (long s = 0; s < (long)M->t[j].n; s += CH)
             ch.push_back({(int)j, 0, (long)M->t[j].off + s, std::min(CH, (long)M->t[j].n - s)});
     M->n_chunks = (int)ch.size();
+    M->chunk0.assign(M->t.size() + 1, 0);
+    for (size_t j = 0, c = 0; j <= M->t.size(); ++j) {
+        while (c < ch.size() && (size_t)ch[c].tensor < j) ++c;
+        M->chunk0[j] = (int)c;
+    }
     const size_t bytes = M->n_params * sizeof(float);
     hipError_t e = hipSuccess;
     for (float** q : {&M->p, &M->g, &M->m, &M->v}) {
@@ -812,9 +844,16 @@ int asca_model_adamw(asca_model* M, void* stream) {
 
 int asca_model_train_step(asca_model* M, const uint32_t* ids, const uint32_t* targets, int batch, int seq,
                           float* loss, void* stream) {
-    int rc = asca_model_forward_backward(M, ids, targets, batch, seq, loss, stream);
+    if (!M || !ids || !targets) return fail(ASCA_ERR_INVALID, "null pointer");
+    if (batch < 1 || seq < 1 || (long)batch * seq > 0x7fffffffL) return fail(ASCA_ERR_INVALID, "bad batch/seq");
+    int rc = ensure_acts(M, batch, seq);
     if (rc) return rc;
-    return model_adamw(M, as_stream(stream));
+    const hipStream_t st = as_stream(stream);
+    if ((rc = model_forward(M, ids, targets, st))) return rc;
+    if ((rc = model_backward(M, st, true))) return rc;
+    M->adam_step += (uint32_t)M->t.size();
+    if (loss) return d2d(loss, M->loss, sizeof(float), st);
+    return ASCA_OK;
 }
 
 int asca_model_decode_state_floats(const asca_model* M, size_t* per_seq) {

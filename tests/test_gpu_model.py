@@ -107,6 +107,33 @@ def test_two_train_steps_follow_the_oracle():
     dm.close()
 
 
+def test_train_step_equals_backward_then_adamw():
+    """asca_model_train_step applies AdamW per layer during the backward (on the
+    model's second stream); the parameters and moments must be bit-identical to
+    a forward_backward followed by one AdamW launch over all tensors."""
+    cfg = (256, 512, 8, 2, 16, 1024)
+    a, _ = _models(cfg, 31)
+    b, _ = _models(cfg, 31)
+    rng = np.random.default_rng(4)
+    for dm in (a, b):
+        dm.set_adamw(step=5)
+    for it in range(2):
+        ids = rng.integers(0, 256, 3 * 40).astype(np.uint32)
+        tgts = rng.integers(0, 256, 3 * 40).astype(np.uint32)
+        la = a.train_step(ids, tgts, 3)
+        lb = b.forward_backward(ids, tgts, 3)
+        b.adamw()
+        assert la == lb
+    assert a.adamw_step_count() == b.adamw_step_count() == 5 + 2 * len(a.params())
+    for x, y in zip(a.params(), b.params()):
+        np.testing.assert_array_equal(x, y)
+    for ma, mb in zip(a.moments(), b.moments()):
+        for x, y in zip(ma, mb):
+            np.testing.assert_array_equal(x, y)
+    a.close()
+    b.close()
+
+
 def test_config3_full_step_runs_deterministically():
     """configs[3] at full size (V=256, d=512, 8 layers, H=8, E=16, d_ff=1024,
     B=16, T=1024): a forward+backward from N(0, 0.02) weights gives a finite
