@@ -385,12 +385,17 @@ ASCA_API int asca_model_adamw_step_count(const asca_model* model, uint32_t* step
 /* Model::forward + Model::backward after zero_grads (rust/src/train.rs:176-186):
  * ids, targets are device u32 arrays of batch*seq tokens (sequence b is rows
  * b*seq..); gradients are written into the grads buffer; *loss (device, may
- * be NULL) receives the mean cross-entropy. */
+ * be NULL) receives the mean cross-entropy.  The weight gradients run on a
+ * second stream owned by the model (default priority, non-blocking), which
+ * `stream` waits for before the call's last work: anything queued on `stream`
+ * afterwards (or a synchronisation of it) sees every gradient. */
 ASCA_API int asca_model_forward_backward(asca_model* model, const uint32_t* ids, const uint32_t* targets,
                                          int batch, int seq, float* loss, void* stream);
 /* The optimiser step over every tensor (model.rs:797-802 / AdamW::update). */
 ASCA_API int asca_model_adamw(asca_model* model, void* stream);
-/* forward_backward followed by asca_model_adamw: one training step. */
+/* forward_backward followed by asca_model_adamw: one training step (the
+ * update of each layer's tensors starts on the model's second stream once
+ * their gradients are final; the result is bit-identical). */
 ASCA_API int asca_model_train_step(asca_model* model, const uint32_t* ids, const uint32_t* targets, int batch,
                                    int seq, float* loss, void* stream);
 
