@@ -243,8 +243,10 @@ ASCA_DEV void mfma_4xn(f32x4 (&acc)[4][TN], const float (&fa)[4][4], const float
 // LDS DMA makes every LDS read wait for all outstanding loads.  The loop waits
 // for them itself (s_waitcnt vmcnt(0) before each barrier), and waits for all
 // of them before the kernel ends, so no load lands in LDS after the block.
-constexpr int DMA_STAGES = 3, DMA_BK = 16, DMA_CH = 24;  // chunks per stage
-constexpr int DMA_STAGE_B = DMA_CH * 1024;
+constexpr int DMA_STAGES = 3, DMA_BK = 16;
+// bytes of one stage: 8 chunks of A (128 rows) and 4 WN of B (64 WN columns)
+template <int WN>
+constexpr int dma_stage_bytes() { return (8 + 4 * WN) * 1024; }
 
 __device__ float4 g_dma_zero = {0.f, 0.f, 0.f, 0.f};  // read-only source for k past the range
 
@@ -304,25 +306,32 @@ ASCA_DEV void dma_issue(DmaSrc& d, long t, const float* base, long ld, const int
     dma16(src, dst);
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int WN>
 ASCA_DEV void dma_mainloop(f32x4 (&acc)[4][4], const float* A, const float* B, const GemmArgs& p, long a_off,
                            long b_off, int m0, int n0, int lim_m, int lim_n, long K_lo, long K_hi, int w, int lane,
                            int wm, int wn) {
     constexpr bool A_KC = !TA, B_KC = TB;
+    constexpr int STAGE_B = dma_stage_bytes<WN>();
+    constexpr int APW = 4 / WN;  // A chunks per wave (8 chunks over 2 WN waves); B chunks: 2 per wave
     extern __shared__ float4 lds4[];
     const float4* lds = lds4;
     const unsigned lds_b = (unsigned)(unsigned long)((__attribute__((address_space(3))) float4*)lds4);
     const int wu = __builtin_amdgcn_readfirstlane(w);
-    DmaSrc sa = dma_src<A_KC>(wu, lane, A, p.lda, p.a_rows, a_off, m0, lim_m, K_lo, K_hi);
+    DmaSrc sa[APW];
+#pragma unroll
+    for (int j = 0; j < APW; ++j)
+        sa[j] = dma_src<A_KC>(APW * wu + j, lane, A, p.lda, p.a_rows, a_off, m0, lim_m, K_lo, K_hi);
     DmaSrc sb0 = dma_src<B_KC>(2 * wu, lane, B, p.ldb, p.b_rows, b_off, n0, lim_n, K_lo, K_hi);
     DmaSrc sb1 = dma_src<B_KC>(2 * wu + 1, lane, B, p.ldb, p.b_rows, b_off, n0, lim_n, K_lo, K_hi);
-    const unsigned ca = lds_b + (unsigned)wu * 1024u, cb = lds_b + (unsigned)(8 + 2 * wu) * 1024u;
+    const unsigned ca = lds_b + (unsigned)(APW * wu) * 1024u, cb = lds_b + (unsigned)(8 + 2 * wu) * 1024u;
     // tile t into stage S (compile-time)
     const long t_tail = (K_hi - K_lo) / DMA_BK;  // first k-tile not wholly inside the K range
     auto issue = [&](long t, auto S) {
-        constexpr unsigned so = (unsigned)decltype(S)::value * DMA_STAGE_B;
+        constexpr unsigned so = (unsigned)decltype(S)::value * STAGE_B;
         const bool tail = t >= t_tail;
-        dma_issue<A_KC>(sa, t, A, p.lda, p.a_rows, a_off, K_lo, K_hi, tail, ca + so);
+#pragma unroll
+        for (int j = 0; j < APW; ++j)
+            dma_issue<A_KC>(sa[j], t, A, p.lda, p.a_rows, a_off, K_lo, K_hi, tail, ca + 1024u * j + so);
         dma_issue<B_KC>(sb0, t, B, p.ldb, p.b_rows, b_off, K_lo, K_hi, tail, cb + so);
         dma_issue<B_KC>(sb1, t, B, p.ldb, p.b_rows, b_off, K_lo, K_hi, tail, cb + 1024u + so);
     };
@@ -332,7 +341,7 @@ ASCA_DEV void dma_mainloop(f32x4 (&acc)[4][4], const float* A, const float* B, c
     const float4* rb = lds + lane;
     const int ax = A_KC ? (wm >> 4) : (wm >> 6) * 4, bx = 8 + (B_KC ? (wn >> 4) : (wn >> 6) * 4);
     auto rd = [&](auto S, auto BUF) {
-        constexpr int st = decltype(S)::value * (DMA_STAGE_B / 16), buf = decltype(BUF)::value;
+        constexpr int st = decltype(S)::value * (STAGE_B / 16), buf = decltype(BUF)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 v = rb[st + (ax + i) * 64];
@@ -466,9 +475,9 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
         for (int y = 0; y < TNW; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if constexpr (DMA) {
-        static_assert(WM == 2 && WN == 4 && TNW == 4 && VEC, "direct-to-LDS tile");
+        static_assert(WM == 2 && (WN == 4 || WN == 2) && TNW == 4 && VEC, "direct-to-LDS tile");
         if (K_hi > K_lo)
-            dma_mainloop<TA, TB>(acc, A, B, p, a_off, b_off, m0, n0, lim_m, lim_n, K_lo, K_hi, w, lane, wm, wn);
+            dma_mainloop<TA, TB, WN>(acc, A, B, p, a_off, b_off, m0, n0, lim_m, lim_n, K_lo, K_hi, w, lane, wm, wn);
     } else {
     const long nk = (K_hi - K_lo + GM_BK - 1) / GM_BK;
     float4 ra[8 * BM / NT], rb[8 * BN / NT];
@@ -894,7 +903,7 @@ static int scratch_get(size_t bytes, float** out) {
 template <bool TA, bool TB, int EPI, bool VEC, int WM = 2, int WN = 2, int TNW = 4, bool DMA = false>
 static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds =
-        DMA ? (size_t)DMA_STAGES * DMA_STAGE_B
+        DMA ? (size_t)DMA_STAGES * dma_stage_bytes<WN>()
             : 2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 16 * TNW * WN>()) * sizeof(float);
     static bool attr = false;
     if (!attr) {
@@ -979,17 +988,23 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     // Measured against the 128 x 128 register-staged tile: 5-9% faster on
     // plain products with full rounds (16384 x {1536, 512} x 512 NN and NT,
     // 4096^3) and on the grouped-K expert weight gradients; slower with a
-    // partly empty last round and on the grouped-row products (left on the
-    // register path).
+    // partly empty last round and on the grouped-row products.
     const bool kc_any = !ta || tb;
-    const bool dma_ok = vec && (!kc_any || a.K % 4 == 0) && (!ta || a.M % 4 == 0) && (tb || a.N % 4 == 0) &&
-                        a.N >= 4 && (!ta || a.M >= 4) && ((a.gmode == 0 && a.k_per_split <= 0) || a.gmode == 2);
+    const bool dma_ops = vec && (!kc_any || a.K % 4 == 0) && (!ta || a.M % 4 == 0) && (tb || a.N % 4 == 0) &&
+                         a.N >= 4 && (!ta || a.M >= 4);
+    const bool dma_ok = dma_ops && ((a.gmode == 0 && a.k_per_split <= 0) || a.gmode == 2);
     auto count_dma = [&]() -> long {
         const long tn = (a.N + 255) / 256, tm = (a.M + 127) / 128;
         return a.gmode == 2 ? (long)a.ngroups * tm * tn : tm * tn;
     };
     const bool dma = dma_ok && wm == 2 && round_fill(count_dma(), 1) >= 0.9;
-    const int bn = dma ? 256 : narrow ? 64 : 128;
+    // otherwise the same loads on a 128 x 128 tile (4 waves, two blocks per CU)
+    // for the grouped-row expert products and plain products without split-K
+    // (measured: MoE forward 466 -> 439 us, backward 903 -> 840 us, the
+    // 16384x256x512 head 52 -> 48 us; the split-K weight gradients stay on the
+    // register path, 312 against 337 us)
+    const bool dma128 = !dma && dma_ops && wm == 2 && (a.gmode == 1 || (a.gmode == 0 && a.k_per_split <= 0));
+    const int bn = dma ? 256 : dma128 ? 128 : narrow ? 64 : 128;
     a.tiles_n = (a.N + bn - 1) / bn;
     a.tiles_m = (a.M + 64 * wm - 1) / (64 * wm);
     long blocks;
@@ -1009,6 +1024,7 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
     if (ta == TA_ && tb == TB_ && epi == EPI_)                                                          \
         rc = !vec ? launch_gemm_t<TA_, TB_, EPI_, false>(a, grid, st)                                   \
              : dma    ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 4, 4, true>(a, grid, st)                 \
+             : dma128 ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 2, 4, true>(a, grid, st)                 \
              : narrow ? launch_gemm_t<TA_, TB_, EPI_, true, 2, 2, 2>(a, grid, st)                       \
                       : launch_gemm_t<TA_, TB_, EPI_, true>(a, grid, st);                                \
     else
