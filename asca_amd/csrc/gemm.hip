@@ -1155,7 +1155,7 @@ __global__ __launch_bounds__(256) void skinny_fwd_k(const float* __restrict__ X,
 // 16 x 16 partial of G (i = 16 it + lane % 16): per MFMA k-step the four lane
 // groups q take rows t = 4 m + q, lane (i, q) supplies X[t][16 it + i] and
 // D[t][i].  Waves of tile 0 also sum their D values for db.  Partials go to
-// part[s][K + 1][16] (row K: db) and skinny_reduce_k adds them in chunk order.
+// part[s][K + 1][16] (row K: db) and skinny_reduce_k adds them in a fixed order.
 constexpr int SK_T = 256;  // rows per wave
 __global__ __launch_bounds__(256) void skinny_wgrad_k(const float* __restrict__ X, long ldx,
                                                       const float* __restrict__ D, long T, int K, int n,
@@ -1201,17 +1201,25 @@ __global__ __launch_bounds__(256) void skinny_wgrad_k(const float* __restrict__ 
     }
 }
 
+// One wave per output row of the (K + 1) x n result: lane (c = l % 16,
+// g = l / 16) adds chunks g, g + 4, ... (independent loads, all in flight),
+// then the four lane groups are added (a fixed order).
 __global__ __launch_bounds__(256) void skinny_reduce_k(const float* __restrict__ part, long nch, int K, int n,
                                                        float* __restrict__ G, float* __restrict__ db) {
-    const long e = (long)blockIdx.x * 256 + threadIdx.x;  // output (row, col) of the (K + 1) x n result
-    if (e >= (long)(K + 1) * n) return;
-    const int row = (int)(e / n), col = (int)(e - (long)row * n);
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row > K) return;  // whole wave
+    const int c = lane & 15, g = lane >> 4;
     float acc = 0.0f;
-    for (long s = 0; s < nch; ++s) acc += part[(s * (K + 1) + row) * 16 + col];
-    if (row < K)
-        G[(long)row * n + col] = acc;
-    else if (db)
-        db[col] = acc;
+    for (long s = g; s < nch; s += 4) acc += part[(s * (K + 1) + row) * 16 + c];
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (g == 0 && c < n) {
+        if (row < K)
+            G[row * n + c] = acc;
+        else if (db)
+            db[c] = acc;
+    }
 }
 
 static bool skinny_ok(const float* X, long ldx, int K, int n) {
@@ -1265,8 +1273,7 @@ int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, floa
                        D, T, K, n, part);
     if ((rc = post_launch("skinny_wgrad"))) return rc;
     if ((rc = pre_launch("skinny_reduce"))) return rc;
-    hipLaunchKernelGGL(skinny_reduce_k, dim3((unsigned)(((long)(K + 1) * n + 255) / 256)), dim3(256), 0, st, part,
-                       nch, K, n, G, db);
+    hipLaunchKernelGGL(skinny_reduce_k, dim3((unsigned)((K + 1 + 3) / 4)), dim3(256), 0, st, part, nch, K, n, G, db);
     return post_launch("skinny_reduce");
 }
 
