@@ -43,23 +43,43 @@ __global__ __launch_bounds__(256) void qkv_prep_k(const float* __restrict__ qkv,
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int d = H * dh;
     const float* src = qkv + r * 3 * d;
+    // dh <= 128: two elements per lane; every load of a head is issued before
+    // its reductions (clamped indices, unconditional), then the stores
     for (int h = w; h < H; h += 4) {
+        float xq[2], xk[2], xv[2];
 #pragma unroll
-        for (int which = 0; which < 2; ++which) {
-            const float* s = src + which * d + h * dh;
-            float ss = 0.0f;
-            for (int j = lane; j < dh; j += 64) ss += s[j] * s[j];
-            ss = wave_sum(ss);
-            const float n = fmaxf(sqrtf(ss), 1e-8f);
-            float* dst = (which ? k : q) + r * d + h * dh;
-            for (int j = lane; j < dh; j += 64) dst[j] = s[j] / n;
-            if (lane == 0) (which ? kn : qn)[r * H + h] = n;
+        for (int e = 0; e < 2; ++e) {
+            const int j = min(lane + 64 * e, dh - 1);
+            xq[e] = src[h * dh + j];
+            xk[e] = src[d + h * dh + j];
+            xv[e] = src[2 * d + h * dh + j];
         }
-        const float* s = src + 2 * d + h * dh;
-        for (int j = lane; j < dh; j += 64) v[r * d + h * dh + j] = s[j];
+        const float ga = gate[r * 2 * H + h], gb = gate[r * 2 * H + H + h];
+        float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (lane + 64 * e < dh) {
+                sq += xq[e] * xq[e];
+                sk += xk[e] * xk[e];
+            }
+        sq = wave_sum(sq);
+        sk = wave_sum(sk);
+        const float nq = fmaxf(sqrtf(sq), 1e-8f), nk = fmaxf(sqrtf(sk), 1e-8f);
+        const long o = r * d + h * dh;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int j = lane + 64 * e;
+            if (j < dh) {
+                q[o + j] = xq[e] / nq;
+                k[o + j] = xk[e] / nk;
+                v[o + j] = xv[e];
+            }
+        }
         if (lane == 0) {
-            alpha[r * H + h] = 1.0f / (1.0f + expf(-gate[r * 2 * H + h]));
-            beta[r * H + h] = 1.0f / (1.0f + expf(-gate[r * 2 * H + H + h]));
+            qn[r * H + h] = nq;
+            kn[r * H + h] = nk;
+            alpha[r * H + h] = 1.0f / (1.0f + expf(-ga));
+            beta[r * H + h] = 1.0f / (1.0f + expf(-gb));
         }
     }
 }
