@@ -1016,30 +1016,50 @@ __global__ __launch_bounds__(256) void delta_combine_k(
     const int h = (int)(id - r * H);
     const long d = (long)H * dh, n = rows * d;
     const long o = r * d + (long)h * dh;
-    float dq[2], dk[2], qa[2], ka[2];
+    // every load issued first (indices clamped into the head, lanes past dh
+    // masked afterwards): a load under a per-lane condition is waited for on
+    // its own
+    float x0[2], x1[2], x2[2], x3[2], qa[2], ka[2];
+#pragma unroll
+    for (int ia = 0; ia < 2; ++ia) {
+        const long a = o + min(lane + 64 * ia, dh - 1);
+        x0[ia] = part_x[a];
+        x1[ia] = part_x[n + a];
+        x2[ia] = part_x[2 * n + a];
+        x3[ia] = part_x[3 * n + a];
+        if constexpr (FUSED) {
+            qa[ia] = q[a];
+            ka[ia] = k[a];
+        }
+    }
+    const long og = r * 2 * H + h, ng = rows * 2 * H;
+    const float g0 = part_g[og], g1 = part_g[ng + og], g2 = part_g[og + H], g3 = part_g[ng + og + H];
+    float qn = 1.0f, kn = 1.0f, al = 0.0f, be = 0.0f;
+    if constexpr (FUSED) {
+        qn = qnorm[r * H + h];
+        kn = knorm[r * H + h];
+        al = alpha[r * H + h];
+        be = beta[r * H + h];
+    }
+    float dq[2], dk[2];
     float dotq = 0.0f, dotk = 0.0f;
 #pragma unroll
     for (int ia = 0; ia < 2; ++ia) {
-        const int a = lane + 64 * ia;
-        dq[ia] = dk[ia] = qa[ia] = ka[ia] = 0.0f;
-        if (a < dh) {
-            dq[ia] = part_x[o + a] + part_x[n + o + a];
-            dk[ia] = part_x[2 * n + o + a] + part_x[3 * n + o + a];
-            if (FUSED) {
-                qa[ia] = q[o + a];
-                ka[ia] = k[o + a];
-            }
+        const bool ok = lane + 64 * ia < dh;
+        dq[ia] = ok ? x0[ia] + x1[ia] : 0.0f;
+        dk[ia] = ok ? x2[ia] + x3[ia] : 0.0f;
+        if constexpr (FUSED) {
+            qa[ia] = ok ? qa[ia] : 0.0f;
+            ka[ia] = ok ? ka[ia] : 0.0f;
+            dotq = fmaf(qa[ia], dq[ia], dotq);
+            dotk = fmaf(ka[ia], dk[ia], dotk);
         }
-        dotq = fmaf(qa[ia], dq[ia], dotq);
-        dotk = fmaf(ka[ia], dk[ia], dotk);
     }
-    const long og = r * 2 * H + h, ng = rows * 2 * H;
-    const float dA = part_g[og] + part_g[ng + og];
-    const float dB = part_g[og + H] + part_g[ng + og + H];
+    const float dA = g0 + g1;
+    const float dB = g2 + g3;
     if constexpr (FUSED) {
         dotq = wave_sum(dotq);
         dotk = wave_sum(dotk);
-        const float qn = qnorm[r * H + h], kn = knorm[r * H + h];
 #pragma unroll
         for (int ia = 0; ia < 2; ++ia) {
             const int a = lane + 64 * ia;
@@ -1049,7 +1069,6 @@ __global__ __launch_bounds__(256) void delta_combine_k(
             }
         }
         if (lane == 0) {
-            const float al = alpha[r * H + h], be = beta[r * H + h];
             ga[r * ldg + h] = dA * al * (1.0f - al);
             gb[r * ldg + h] = dB * be * (1.0f - be);
         }
