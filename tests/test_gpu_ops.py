@@ -65,6 +65,22 @@ def test_gemm_variants(orc, g, ta, tb, M, N, K):
     assert orc.rel_err(got, _ref_gemm(a, b, ta, tb, 0.5, 1.0, c, bias)) <= FWD_TOL
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_direct_to_lds_tiles_with_edges(orc, g, ta, tb):
+    # 8100 x 1020 output: 64 x 4 blocks of 128 x 256 fill one round of the
+    # CUs, so the direct-to-LDS 128 x 256 tile runs, with a partial last row
+    # tile, a partial last column tile and a k-tail (84 = 5 x 16 + 4)
+    M, N, K = 8100, 1020, 84
+    rng = np.random.default_rng(40 + 2 * ta + tb)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    c = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    print(f"[gemm] direct-to-LDS ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    got = g.gemm(a, b, trans_a=bool(ta), trans_b=bool(tb), alpha=0.5, beta=1.0, c=c, bias=bias)
+    assert orc.rel_err(got, _ref_gemm(a, b, ta, tb, 0.5, 1.0, c, bias)) <= FWD_TOL
+
+
 def test_gemm_split_k_projection_weight_grad(orc, g):
     # dW_qkv = x^T d_qkv at config[3]: 512 x 1536 output, K = 16384 tokens
     rng = np.random.default_rng(11)
