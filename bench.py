@@ -443,14 +443,72 @@ def bench_train(args):
     print(json.dumps(result), flush=True)
 
 
+GEMM_SHAPES = [  # (name, trans_a, trans_b, M, N, K): the f32 products of configs[3] and a square one
+    ("qkv projection 16384x1536x512 NN", 0, 0, 16384, 1536, 512),
+    ("out projection 16384x512x512 NN", 0, 0, 16384, 512, 512),
+    ("qkv input gradient 16384x512x1536 NT", 0, 1, 16384, 512, 1536),
+    ("qkv weight gradient 512x1536x16384 TN (split-K)", 1, 0, 512, 1536, 16384),
+    ("head 16384x256x512 NN", 0, 0, 16384, 256, 512),
+    ("square 4096x4096x4096 NN", 0, 0, 4096, 4096, 4096),
+]
+
+
+def bench_gemm(args):
+    """The f32 MFMA GEMM (asca_gemm) on the configs[3] product shapes and
+    4096^3, operands resident in HBM, HIP events around K launches each;
+    value = TFLOP/s of the 4096^3 product (the MFMA-bound reference point)."""
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf
+
+    if gpu.gpu() is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    K_rep = args.steps or 20
+    W = args.warmup
+    rng = np.random.default_rng(0)
+    tm = Timer()
+    out = {}
+    for name, ta, tb, M, N, K in GEMM_SHAPES:
+        a = DevBuf.from_host(rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+        b = DevBuf.from_host(rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32))
+        c = DevBuf(M * N * 4)
+        lda, ldb = (M if ta else K), (K if tb else N)
+        args_c = (ta, tb, M, N, K, C.c_float(1.0), C.c_void_p(a.ptr), lda, C.c_void_p(b.ptr), ldb, C.c_float(0.0),
+                  C.c_void_p(c.ptr), N, None, C.c_void_p(tm.stream))
+        for _ in range(W):
+            _lib.call("asca_gemm", *args_c)
+        tm.sync()
+        e0, e1 = tm.event(), tm.event()
+        tm.record(e0)
+        for _ in range(K_rep):
+            _lib.call("asca_gemm", *args_c)
+        tm.record(e1)
+        tm.sync()
+        ms = tm.elapsed(e0, e1) / K_rep
+        tm.destroy(e0, e1)
+        out[name] = {"us": round(ms * 1e3, 1), "tflops": round(2.0 * M * N * K / ms / 1e9, 1)}
+        print(f"bench gemm: {name}: {ms * 1e3:.1f} us, {out[name]['tflops']} TFLOP/s", file=sys.stderr, flush=True)
+        a.free(), b.free(), c.free()
+    sq = out["square 4096x4096x4096 NN"]
+    result = {
+        "metric": "f32 GEMM TFLOP/s (asca_gemm, 4096^3 NN; configs[3] product shapes alongside)",
+        "value": sq["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": K_rep, "warmup": W,
+        "ms_per_step": round(sq["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic N(0,1) operands",
+        "config": {"workload": "asca_gemm (MFMA f32)", "shapes": out},
+        "roofline": {"bound": "mfma", "achieved": sq["tflops"], "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(sq["tflops"] / 157.3, 4), "traffic": None, "kernel": "gemm_k 4096^3"},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train", "chunk"],
+    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train", "chunk", "gemm"],
                     help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]; train: configs[3]; "
-                         "chunk: configs[2]")
+                         "chunk: configs[2]; gemm: the f32 GEMM on the configs[3] product shapes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib", action="store_true",
                     help="also run the known-size copy kernel (for counter calibration)")
@@ -468,6 +526,9 @@ def main():
         return
     if args.workload == "chunk":
         bench_chunk(args)
+        return
+    if args.workload == "gemm":
+        bench_gemm(args)
         return
     if args.steps is None:
         args.steps = 100
