@@ -471,8 +471,15 @@ static int ensure_side(asca_model* M) {
     }
     M->evs.assign((size_t)5 * M->L + 4, nullptr);
     for (auto& ev : M->evs)
-        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
+        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
+            // leave no half-made set behind: the next call starts again
+            for (hipEvent_t x : M->evs)
+                if (x) (void)hipEventDestroy(x);
+            M->evs.clear();
+            (void)hipStreamDestroy(M->side);
+            M->side = nullptr;
             return fail(ASCA_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
+        }
     return ASCA_OK;
 }
 
