@@ -516,7 +516,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         sys.stderr.write("bench.py: this build runs on exactly one GPU (the delta-rule units are independent "
-                         "per (sequence, head); see DESIGN.md for how the path shards). Use --gpus 1.\n")
+                         "per (sequence, head), so the path would shard over B or H with no exchange). "
+                         "Use --gpus 1.\n")
         sys.exit(2)
     if args.workload == "decode":
         bench_decode(args)
