@@ -87,4 +87,14 @@ ASCA_DEV float wave_sum(float x) {
 
 ASCA_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load and store of the wave (s_waitcnt vmcnt(0)), which
+// turns a prefetch issued before it into a stall; kernels whose waves share
+// nothing but LDS use this instead (s_waitcnt lgkmcnt(0); s_barrier).
+ASCA_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace asca

@@ -31,6 +31,7 @@
 //    plus a per-segment cross-wave sum through LDS, where the L2-norm and
 //    sigmoid backward of the drop-in variant also run.
 #include "common.h"
+#include "delta.h"
 #include "runtime.h"
 
 namespace asca {
@@ -232,9 +233,26 @@ ASCA_DEV void fwd_steps(float (&s)[DH / 8], const float* __restrict__ buf, float
     }
 }
 
+// A lane's rows row0 .. row0+R-1 of column col into a checkpoint slot (S^T,
+// contiguous per column); masked elements go to the trash.
+template <int R, bool EXACT>
+ASCA_DEV void store_ckpt(float* __restrict__ dst, const float (&s)[R], bool col_ok, int row0, int dh,
+                         float* __restrict__ tr) {
+    if constexpr (EXACT && R % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < R; j += 4)
+            *reinterpret_cast<float4*>(dst + j) = make_float4(s[j], s[j + 1], s[j + 2], s[j + 3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr + j) = s[j];
+    }
+}
+
 // One block per (sequence, head) unit, unit = h*B + b (the reference's s_pre
-// order, rust/src/delta.rs:54-56).  ckpt: nslots = ceil(T/CK) states per unit,
-// slot j = S^T before step j*CK (element (a, i) of S at [i*dh + a]).
+// order, rust/src/delta.rs:54-56).  ckpt: nslots = ceil(T/CK) + 1 states per
+// unit, slot j = S^T before step j*CK (element (a, i) of S at [i*dh + a]), the
+// last slot S^T after step T-1.  Steps past T (the tail of the last chunk) run
+// with alpha = 1, beta = 0, which leaves the state unchanged.
 template <int DH, int CS, bool EXACT>
 __global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -275,27 +293,23 @@ __global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
 
     FwdStage<DH, CS> stg;
     fwd_stage_load<DH, CS, EXACT>(stg, 0, q, k, v, ubase, d, T, dh, wg, lane);
-    float gnext = gsrc[(long)min(gstep, T - 1) * H];
+    // a gate of step t (lane-dependent: alpha or beta); past T, alpha = 1 and beta = 0
+    const float gpad = gl < CK ? 1.0f : 0.0f;
+    auto gate = [&](int t) {
+        const float x = gsrc[(long)min(t, T - 1) * H];
+        return t < T ? x : gpad;
+    };
+    float gnext = gate(gstep);
     fwd_stage_store<DH, CS>(stg, lds, w, lane);
-    __syncthreads();
+    lds_barrier();
 
     for (int ci = 0; ci < nchunk; ++ci) {
         const int t0 = ci * CK;
         const float* buf = lds + (ci & 1) * L::BUF_F;
         const float gcur = gnext;
-        gnext = gsrc[(long)min(t0 + CK + gstep, T - 1) * H];
+        gnext = gate(t0 + CK + gstep);
         fwd_stage_load<DH, CS, EXACT>(stg, min(ci + 1, nchunk - 1), q, k, v, ubase, d, T, dh, wg, lane);
-        {   // checkpoint: S before step t0, as S^T
-            float* dst = ckb + (long)ci * dh2 + (long)col * dh + row0;
-            if constexpr (EXACT && R % 4 == 0) {
-#pragma unroll
-                for (int j = 0; j < R; j += 4)
-                    *reinterpret_cast<float4*>(dst + j) = make_float4(s[j], s[j + 1], s[j + 2], s[j + 3]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < R; ++j) *((col_ok && row0 + j < dh) ? dst + j : tr + j) = s[j];
-            }
-        }
+        store_ckpt<R, EXACT>(ckb + (long)ci * dh2 + (long)col * dh + row0, s, col_ok, row0, dh, tr);
         // Lanes j < CK of gcur hold the chunk's alpha; when all of them lie in
         // [2^-8, 2^8] the chunk runs on the scaled state (fwd_steps).
         const bool bad = lane < CK && !(gcur >= 0x1p-8f && gcur <= 0x1p8f);
@@ -323,8 +337,9 @@ __global__ __launch_bounds__((FS<DH, CS>::NT)) void delta_fwd_k(
             *(ok ? skb + (long)ts * d + col : tr + 1) = hold_s * fs;
         }
         fwd_stage_store<DH, CS>(stg, lds + ((ci + 1) & 1) * L::BUF_F, w, lane);
-        __syncthreads();
+        lds_barrier();
     }
+    store_ckpt<R, EXACT>(ckb + (long)nchunk * dh2 + (long)col * dh + row0, s, col_ok, row0, dh, tr);
 }
 
 // Full state history for download_states: S before every step then the final
@@ -696,46 +711,6 @@ ASCA_DEV void bwd_step(const BOps<DH / 16>& in, const float (&sm)[DH / 16][2], c
     pab_out = tsum32(pa, pb);
 }
 
-// Sum of the 2*CK per-step partials (dalpha of step j, dbeta of step j) over
-// all 64 lanes, given y[j] = their first transposed level (tsum32: lanes < 32
-// hold the dalpha pair sum of step j, lanes >= 32 the dbeta one); two more
-// swap/DPP levels on halving value sets, then a butterfly over the lanes left;
-// the totals go to red_ab[(j*W + w)*2 + {0: dalpha, 1: dbeta}].
-template <int CK, int W>
-ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, int w, int lane) {
-    constexpr int K = 2 * CK;
-    // lane holds y[i] = total over lane bit 5 of x[i + (bit5 ? K/2 : 0)]
-    if constexpr (K / 2 >= 2) {
-        float z[K / 4];
-#pragma unroll
-        for (int i = 0; i < K / 4; ++i) z[i] = tsum16(y[i], y[i + K / 4]);
-        if constexpr (K / 4 >= 2) {
-            const bool b3 = (lane & 8) != 0;
-            float u[K / 8];
-#pragma unroll
-            for (int i = 0; i < K / 8; ++i) {
-                const float keep = b3 ? z[i + K / 8] : z[i];
-                const float send = b3 ? z[i] : z[i + K / 8];
-                u[i] = keep + dpp<DPP_ROW_ROR8>(send);
-            }
-#pragma unroll
-            for (int i = 0; i < K / 8; ++i) {
-                const float tot = group_sum<8>(u[i]);
-                const int idx = i + (b3 ? K / 8 : 0) + ((lane & 16) ? K / 4 : 0) + ((lane & 32) ? K / 2 : 0);
-                if ((lane & 7) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
-            }
-        } else {
-            const float tot = group_sum<16>(z[0]);
-            const int idx = ((lane & 16) ? K / 4 : 0) + ((lane & 32) ? K / 2 : 0);
-            if ((lane & 15) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
-        }
-    } else {
-        const float tot = add_xor16(group_sum<16>(y[0]));
-        const int idx = (lane & 32) ? K / 2 : 0;
-        if ((lane & 31) == 0) red_ab[((idx % CK) * W + w) * 2 + idx / CK] = tot;
-    }
-}
-
 // One segment of CK steps (t0 .. t0+CK-1): recompute the states from the
 // checkpoint s0 into the register stash (phase A), then run the steps in
 // reverse (phase B), storing the next segment's staged operands (stg) into its
@@ -889,7 +864,7 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
         }
         bstage_load<DH, CS, EXACT, FUSED>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb,
                                           ubase, gbase, d, dh2, T, H, dh, wg, lane, rowb, colb);
-        __syncthreads();  // staging of this segment visible to all waves
+        lds_barrier();  // staging of this segment visible to all waves
 
         if (__builtin_amdgcn_readfirstlane(__float_as_int(st_ab[8 * CK])) == __float_as_int(1.0f))
             bwd_segment<DH, CS, EXACT, true>(s0, ds, stg, nbuf, cks, st_q, st_k, st_w, st_ab, red_q, red_k,
@@ -897,7 +872,7 @@ __global__ __launch_bounds__((BS<DH, CS>::NT)) void delta_bwd_k(
         else
             bwd_segment<DH, CS, EXACT, false>(s0, ds, stg, nbuf, cks, st_q, st_k, st_w, st_ab, red_q, red_k,
                                               red_ab, red_v, t0, T, w, lane, rg, cg, rowb, colb, dh);
-        __syncthreads();  // red_* of this segment complete
+        lds_barrier();  // red_* of this segment complete
 
         // ---- phase C: cross-wave sums, optional norm/sigmoid backward, stores
         constexpr int NA = (DH + 63) / 64;
@@ -1108,16 +1083,6 @@ static int ck_for(int dhc) {
     }
 }
 
-struct DeltaWs {
-    float* sk;
-    float* ckpt;
-    float* part_x;  // column split: partial dq, dk  [2][CS][B*T][H*dh]
-    float* part_g;  // column split: partial dalpha, dbeta  [CS][B*T][2H]
-    int ck;
-    int nslots;
-    int cs;
-    size_t bytes;
-};
 
 // Units (sequence, head) at or below which each unit's value columns run on two
 // blocks: half of MI355X's 256 CUs, so that a small batch still fills the chip.
@@ -1128,16 +1093,19 @@ struct DeltaWs {
 constexpr long SPLIT_UNITS = 128;
 static int col_split(int B, int H, int dhc) { return (long)B * H <= SPLIT_UNITS || dhc == 128 ? 2 : 1; }
 
+// dh = 64 with a block per unit runs on the four-wave kernels of delta64.hip.
+static bool four_wave(int dh, int cs) { return dh == 64 && cs == 1; }
+
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     DeltaWs w;
     const int dhc = dh_class(dh);
-    w.ck = ck_for(dhc);
-    w.nslots = (T + w.ck - 1) / w.ck;
+    w.cs = col_split(B, H, dhc);
+    w.ck = four_wave(dh, w.cs) ? D64_CK : ck_for(dhc);
+    w.nslots = (T + w.ck - 1) / w.ck + 1;   // the state before every chunk, then the final state
     const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
-    w.cs = col_split(B, H, dhc);
     const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
     const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
@@ -1176,6 +1144,7 @@ static int launch_fwd(const float* q, const float* k, const float* v, const floa
                       float* o, const DeltaWs& ws, int B, int T, int H, int dh, hipStream_t st) {
     const int dhc = dh_class(dh);
     const bool exact = dh == dhc && aligned16(q) && aligned16(k);
+    if (four_wave(dh, ws.cs)) return launch_fwd64(q, k, v, alpha, beta, o, ws, B, T, H, st);
 #define ASCA_FWD(DHC)                                                                                    \
     if (dhc == DHC)                                                                                      \
         return exact ? launch_fwd_t<DHC, true>(q, k, v, alpha, beta, o, ws, B, T, H, dh, st)             \
@@ -1246,6 +1215,8 @@ static int launch_bwd(const float* q, const float* k, const float* v, const floa
     const int dhc = dh_class(dh);
     const bool exact = dh == dhc && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(d_o) &&
                        aligned16(gv) && ((ldx * 4) % 16 == 0);
+    if (four_wave(dh, ws.cs))
+        return launch_bwd64(FUSED, q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, st);
 #define ASCA_BWD(DHC)                                                                                            \
     if (dhc == DHC)                                                                                              \
         return exact ? launch_bwd_t<DHC, true, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, \

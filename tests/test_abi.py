@@ -33,17 +33,19 @@ def test_workspace_bytes_layout():
     out = C.c_size_t()
     _lib.call("asca_delta_ws_bytes", 32, 512, 8, 64, C.byref(out))
     sk = 32 * 512 * 8 * 64 * 4
-    ckpt = 32 * 8 * (512 // 8) * 64 * 64 * 4
+    # dh = 64 on a block per unit (the four-wave kernels): a checkpoint before
+    # every 16-step chunk plus the state after the last step
+    ckpt = 32 * 8 * (512 // 16 + 1) * 64 * 64 * 4
     assert out.value == sk + ckpt
     # at most 128 (sequence, head) units: each unit's columns run on two blocks,
     # and the workspace adds the two blocks' partial dq, dk and dalpha, dbeta
     _lib.call("asca_delta_ws_bytes", 4, 128, 4, 32, C.byref(out))
-    base = 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 8) * 32 * 32 * 4
+    base = 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 8 + 1) * 32 * 32 * 4
     part_x = 2 * 2 * 4 * 128 * 4 * 32 * 4
     part_g = 2 * 4 * 128 * 2 * 4 * 4
     assert out.value == base + part_x + part_g
     _lib.call("asca_delta_ws_bytes", 16, 1024, 8, 64, C.byref(out))
-    base = 16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 8) * 64 * 64 * 4
+    base = 16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 8 + 1) * 64 * 64 * 4
     assert out.value == base + 2 * 2 * 16 * 1024 * 8 * 64 * 4 + 2 * 16 * 1024 * 2 * 8 * 4
     with pytest.raises(_lib.AscaError) as ei:
         _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))

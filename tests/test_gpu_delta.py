@@ -181,3 +181,98 @@ def test_empty_and_invalid_shapes(g):
     with pytest.raises(AscaError) as ei:
         g.delta_scan(x, x, x, xg, xg, 1, 4, 1, 129)
     assert ei.value.code == 3
+
+
+# dh = 64 with more than 128 (sequence, head) units runs on the four-wave
+# kernels (16 state elements per lane, 16-step chunks; the backward steps its
+# scaled state back from the checkpoint after each segment).  Ragged tails, a single step, fewer
+# steps than a segment, and the extreme gate patterns of test_extreme_gates.
+@pytest.mark.parametrize("B,T,H", [(129, 1, 1), (17, 5, 8), (20, 16, 8), (17, 29, 8), (33, 67, 4), (3, 40, 48)])
+def test_four_wave_dh64_shapes(orc, g, B, T, H):
+    dh = 64
+    _check_all(orc, g, orc.DeltaInputs(300 + B * T + H, B, T, H, dh), B, T, H, dh, "dh64 four-wave")
+
+
+def test_four_wave_dh64_extreme_gates(orc, g):
+    B, T, H, dh = 17, 75, 8, 64
+    x = orc.DeltaInputs(77, B, T, H, dh)
+    t = np.arange(B * T) % T
+    a = x.alpha.reshape(B * T, H)
+    a[(t >= 16) & (t < 32)] = 0.005
+    a[(t >= 40) & (t < 44), 0] = 1.0
+    a[(t >= 44) & (t < 48)] = 1.5
+    a[t % 37 == 5] = 0.0
+    a[t % 11 == 3, -1] = 1e-6
+    _check_all(orc, g, x, B, T, H, dh, "dh64 four-wave extreme gates")
+
+
+def test_four_wave_dh64_batch_isolation(orc, g):
+    # 136 units together, then each sequence alone (8 units: the eight-lane
+    # column-split kernels); forward and fused backward agree to the bar
+    B, T, H, dh = 17, 24, 8, 64
+    x = orc.DeltaInputs(31, B, T, H, dh)
+    o, dev = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
+    d_qkv, d_gate = g.delta_bwd_dev(dev, x.d_o, x.qn, x.kn)
+    for b in (0, 7, 16):
+        rs = slice(b * T, (b + 1) * T)
+        sub = [np.ascontiguousarray(a[rs]) for a in (x.q, x.k, x.v, x.alpha, x.beta)]
+        o1, dev1 = g.delta_scan(*sub, 1, T, H, dh)
+        q1, g1 = g.delta_bwd_dev(dev1, np.ascontiguousarray(x.d_o[rs]), np.ascontiguousarray(x.qn[rs]),
+                                 np.ascontiguousarray(x.kn[rs]))
+        assert orc.rel_err(o[rs], o1) <= FWD_TOL
+        assert orc.rel_err(d_qkv[rs], q1) <= GRAD_TOL
+        assert orc.rel_err(d_gate[rs], g1) <= GRAD_TOL
+
+
+@pytest.mark.parametrize("a", [0.5, 0.6, 0.7, 0.72, 0.75, 0.8, 0.9, 0.99])
+def test_four_wave_dh64_constant_gates(orc, g, a):
+    # Every alpha equal: each 16-step segment has gate product a^16, which puts
+    # a <= 0.70 on the forward recompute and a >= 0.71 on the backward walk of
+    # the scaled state (rounding magnified by up to 1/a^16 <= 256).
+    B, T, H, dh = 17, 80, 8, 64
+    x = orc.DeltaInputs(500, B, T, H, dh)
+    x.alpha[:] = np.float32(a)
+    _check_all(orc, g, x, B, T, H, dh, f"dh64 alpha={a}")
+
+
+def test_four_wave_dh64_unaligned_pointers(orc, g):
+    # q, k, v and dO one float past a 16-byte boundary: the four-wave kernels
+    # load them with scalar accesses and give the aligned results' parity.
+    import ctypes as C
+    from asca_amd import _lib
+    from asca_amd.gpu import DevBuf, _vp
+
+    B, T, H, dh = 17, 21, 8, 64
+    x = orc.DeltaInputs(41, B, T, H, dh)
+    o_ref, dq, dk, dv, da, db = orc.delta_fwd_bwd(x.q, x.k, x.v, x.alpha, x.beta, x.d_o, B, T, H, dh)
+    rows, d = B * T, H * dh
+
+    def shifted(a):
+        buf = DevBuf((a.size + 1) * 4)
+        flat = np.concatenate([np.zeros(1, np.float32), a.ravel()])
+        buf.upload(flat)
+        return buf, buf.ptr + 4
+
+    bufs = []
+    ptr = {}
+    for name in ("q", "k", "v", "d_o"):
+        bf, p = shifted(getattr(x, name))
+        bufs.append(bf)
+        ptr[name] = p
+    al, be = DevBuf.from_host(x.alpha), DevBuf.from_host(x.beta)
+    wsb = C.c_size_t()
+    _lib.call("asca_delta_ws_bytes", B, T, H, dh, C.byref(wsb))
+    ws = DevBuf(wsb.value)
+    o = DevBuf(rows * d * 4)
+    outs = [DevBuf(rows * d * 4) for _ in range(3)] + [DevBuf(rows * H * 4) for _ in range(2)]
+    _lib.call("asca_delta_fwd", _vp(ptr["q"]), _vp(ptr["k"]), _vp(ptr["v"]), _vp(al), _vp(be), _vp(o), _vp(ws),
+              B, T, H, dh, None)
+    _lib.call("asca_delta_bwd_raw", _vp(ptr["q"]), _vp(ptr["k"]), _vp(ptr["v"]), _vp(al), _vp(be),
+              _vp(ptr["d_o"]), _vp(ws), *[_vp(t) for t in outs], B, T, H, dh, None)
+    _lib.call("asca_sync")
+    got = [o.to_host((rows, d))] + [t.to_host((rows, d)) for t in outs[:3]] + [t.to_host((rows, H)) for t in outs[3:]]
+    errs = [orc.rel_err(a, r) for a, r in zip(got, (o_ref, dq, dk, dv, da, db))]
+    print(f"[delta parity] dh64 unaligned rel errors {errs}", flush=True)
+    assert errs[0] <= FWD_TOL and max(errs[1:]) <= GRAD_TOL, errs
+    for b in [*bufs, al, be, ws, o, *outs]:
+        b.free()
