@@ -65,12 +65,16 @@ SIGNATURES: dict[str, tuple] = {
     "asca_gather_rows": (_i, [_p, _p, _l, _i, _p, _p]),
     "asca_scatter_rows": (_i, [_p, _p, _l, _i, _p, _p]),
     "asca_colsum": (_i, [_p, _l, _i, _p, _i, _p]),
+    "asca_colsum_ws_bytes": (_i, [_l, _i, C.POINTER(_sz)]),
+    "asca_colsum_ws": (_i, [_p, _l, _i, _p, _i, _p, _sz, _p]),
     "asca_adamw_scalars": (_i, [_f, _f, _f, _f, _f, C.c_uint32, _fp]),
     "asca_adamw": (_i, [_p, _p, _p, _p, _l, _f, _f, _f, _f, _f, _p]),
     "asca_hash_route_ws_bytes": (_i, [_i, _i, C.POINTER(_sz)]),
     "asca_hash_route": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
     "asca_bucket_keys": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
     "asca_gemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p]),
+    "asca_gemm_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
+    "asca_gemm_ws": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p, _sz, _p]),
     "asca_moe_fwd": (_i, [_p] * 7 + [_i] * 4 + [_p] * 4),
     "asca_moe_bwd": (_i, [_p] * 8 + [_i] * 4 + [_p] * 6 + [_i, _p]),
     "asca_chunk_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
@@ -98,6 +102,7 @@ ERRORS = {
     5: "injected failure",
     6: "out of device memory",
     7: "no device",
+    8: "optimiser step partially applied",
 }
 
 

@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "runtime.h"
+
 namespace asca {
 
 enum : int { EPI_STORE = 0, EPI_SILU = 1, EPI_SILU_BWD = 2 };
@@ -47,9 +49,20 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
 int skinny_fwd_launch(const float* X, long ldx, const float* W, const float* b, float* Y, long T, int K, int n,
                       hipStream_t st);
 int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, float* db, long T, int K, int n,
-                        hipStream_t st);
-// out[g*N + c] (+)= column sums of X over the rows of group g (or all rows).
+                        Ws ws, hipStream_t st);
+size_t skinny_wgrad_ws_floats(long T, int K, int n);
+// out[g*N + c] (+)= column sums of X over the rows of group g (or all rows);
+// ws holds the row-slice partials (colsum_ws_floats).
 int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, int ngroups, float* out,
-                  int accumulate, hipStream_t st);
+                  int accumulate, Ws ws, hipStream_t st);
+size_t colsum_ws_floats(long rows, int N, bool grouped, int ngroups);
+// Plain product C = alpha op(A) op(B) + beta C (+ bias per column), the
+// arithmetic of asca_gemm; split-K partials go to ws (gemm_ws_floats of the
+// shape; 0 when the product does not split).
+int gemm_run(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
+             long ldb, float beta, float* C, long ldc, const float* bias, Ws ws, hipStream_t st);
+size_t gemm_ws_floats(int M, int N, int K);
+int gemm_check(int trans_a, int trans_b, int M, int N, int K, const float* A, long lda, const float* B, long ldb,
+               const float* C, long ldc);
 
 }  // namespace asca

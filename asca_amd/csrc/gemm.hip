@@ -868,35 +868,10 @@ __global__ __launch_bounds__(256) void colsum_fin_k(const float* __restrict__ pa
 
 // ---------------------------------------------------------------- host side
 
-// Per-device scratch for split-K partials and column-sum slices; grown on
-// demand (growth waits for the device so in-flight kernels never see a freed
-// buffer).
-struct Scratch {
-    std::mutex mu;
-    void* ptr[16] = {};
-    size_t bytes[16] = {};
-};
-static Scratch g_scratch;
-
-static int scratch_get(size_t bytes, float** out) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return fail(ASCA_ERR_HIP, "hipGetDevice failed");
-    std::lock_guard<std::mutex> lk(g_scratch.mu);
-    if (g_scratch.bytes[dev] < bytes) {
-        size_t nb = g_scratch.bytes[dev] ? g_scratch.bytes[dev] : (size_t)1 << 20;
-        while (nb < bytes) nb *= 2;
-        if (g_scratch.ptr[dev]) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(g_scratch.ptr[dev]);
-            g_scratch.ptr[dev] = nullptr;
-            g_scratch.bytes[dev] = 0;
-        }
-        void* p = nullptr;
-        if (hipMalloc(&p, nb) != hipSuccess) return fail(ASCA_ERR_OOM, "scratch hipMalloc(%zu) failed", nb);
-        g_scratch.ptr[dev] = p;
-        g_scratch.bytes[dev] = nb;
-    }
-    *out = reinterpret_cast<float*>(g_scratch.ptr[dev]);
+static int ws_check(const Ws& ws, size_t floats, const char* name) {
+    if (floats == 0) return ASCA_OK;
+    if (!ws.p || ws.floats < floats)
+        return fail(ASCA_ERR_INVALID, "%s: workspace of %zu floats, %zu needed", name, ws.floats, floats);
     return ASCA_OK;
 }
 
@@ -1076,20 +1051,31 @@ GemmArgs gemm_args() {
     return a;
 }
 
+// Slices of a column sum: about CS_SLICE rows each (twice as many per group:
+// group sizes vary).
+static int colsum_slices(long rows, int G, bool grouped) {
+    const long avg = grouped ? (2 * rows) / G + 1 : rows;
+    const int ns = (int)min((avg + CS_SLICE - 1) / CS_SLICE, 1024L);
+    return ns < 1 ? 1 : ns;
+}
+
+size_t colsum_ws_floats(long rows, int N, bool grouped, int ngroups) {
+    const int G = grouped ? ngroups : 1;
+    if (N <= 0 || G <= 0) return 0;
+    return (size_t)G * colsum_slices(rows, G, grouped) * N;
+}
+
 // Column sums of X (rows x N, ld ldx), per group when goff is given.
 int colsum_launch(const float* X, long rows, int N, long ldx, const int* goff, int ngroups, float* out,
-                  int accumulate, hipStream_t st) {
+                  int accumulate, Ws ws, hipStream_t st) {
     if (N == 0) return ASCA_OK;
     const int G = goff ? ngroups : 1;
     if (G == 0) return ASCA_OK;
     const int cb = (N + 63) / 64;
-    // slices of about CS_SLICE rows (twice as many per group: group sizes vary)
-    const long avg = goff ? (2 * rows) / G + 1 : rows;
-    int ns = (int)min((avg + CS_SLICE - 1) / CS_SLICE, 1024L);
-    if (ns < 1) ns = 1;
-    float* part = nullptr;
-    int rc = scratch_get((size_t)G * ns * N * sizeof(float), &part);
+    const int ns = colsum_slices(rows, G, goff != nullptr);
+    int rc = ws_check(ws, (size_t)G * ns * N, "colsum");
     if (rc) return rc;
+    float* const part = ws.p;
     rc = pre_launch("colsum");
     if (rc) return rc;
     hipLaunchKernelGGL(colsum_part_k, dim3(cb, ns, G), dim3(256), 0, st, X, rows, N, ldx, goff, part, ns);
@@ -1256,18 +1242,25 @@ int skinny_fwd_launch(const float* X, long ldx, const float* W, const float* b, 
     return post_launch("skinny_fwd");
 }
 
+size_t skinny_wgrad_ws_floats(long T, int K, int n) {
+    if (n <= 0 || K <= 0) return 0;
+    const size_t fallback = max(gemm_ws_floats(K, n, (int)min(T, 0x7fffffffL)), colsum_ws_floats(T, n, false, 0));
+    const long nch = (max(T, 0L) + SK_T - 1) / SK_T;
+    return max(fallback, (size_t)nch * (K + 1) * 16);
+}
+
 int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, float* db, long T, int K, int n,
-                        hipStream_t st) {
+                        Ws ws, hipStream_t st) {
     if (n <= 0 || K <= 0) return ASCA_OK;
     if (T <= 0 || !skinny_ok(X, ldx, K, n) || K % 16) {
-        int rc = asca_gemm(1, 0, K, n, (int)T, 1.0f, X, (int)ldx, D, n, 0.0f, G, n, nullptr, st);
+        int rc = gemm_run(1, 0, K, n, (int)T, 1.0f, X, ldx, D, n, 0.0f, G, n, nullptr, ws, st);
         if (rc || !db) return rc;
-        return colsum_launch(D, T, n, n, nullptr, 0, db, 0, st);
+        return colsum_launch(D, T, n, n, nullptr, 0, db, 0, ws, st);
     }
     const long nch = (T + SK_T - 1) / SK_T;
-    float* part = nullptr;
-    int rc = scratch_get((size_t)nch * (K + 1) * 16 * sizeof(float), &part);
+    int rc = ws_check(ws, (size_t)nch * (K + 1) * 16, "skinny_wgrad");
     if (rc) return rc;
+    float* const part = ws.p;
     if ((rc = pre_launch("skinny_wgrad"))) return rc;
     hipLaunchKernelGGL(skinny_wgrad_k, dim3((unsigned)(K / 16), (unsigned)((nch + 3) / 4)), dim3(256), 0, st, X, ldx,
                        D, T, K, n, part);
@@ -1277,20 +1270,46 @@ int skinny_wgrad_launch(const float* X, long ldx, const float* D, float* G, floa
     return post_launch("skinny_reduce");
 }
 
-}  // namespace asca
+// Split-K decision of a plain product: split K when the output has too few
+// tiles to fill the chip.  Returns the split count and the K range per split.
+static int gemm_splits(int M, int N, int K, long* kps_out) {
+    const long tiles = (long)((M + GM_BM - 1) / GM_BM) * ((N + GM_BN - 1) / GM_BN);
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    int splits = 1;
+    if (tiles < cus && K >= 1024) {
+        splits = (int)min((long)K / 512, (2L * cus + tiles - 1) / tiles);
+        if (splits < 1) splits = 1;
+    }
+    long kps = K;
+    if (splits > 1) {
+        kps = ((K + splits - 1) / splits + GM_BK - 1) / GM_BK * GM_BK;
+        splits = (int)((K + kps - 1) / kps);
+    }
+    *kps_out = kps;
+    return splits;
+}
 
-using namespace asca;
+size_t gemm_ws_floats(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    long kps = 0;
+    const int splits = gemm_splits(M, N, K, &kps);
+    return splits > 1 ? (size_t)splits * M * N : 0;
+}
 
-extern "C" {
-
-int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
-              long ldb, float beta, float* C, long ldc, const float* bias, void* stream) {
+int gemm_check(int trans_a, int trans_b, int M, int N, int K, const float* A, long lda, const float* B, long ldb,
+               const float* C, long ldc) {
     if (M < 0 || N < 0 || K < 0) return fail(ASCA_ERR_INVALID, "asca_gemm: negative shape");
     if (M == 0 || N == 0) return ASCA_OK;
     if (!C || (K > 0 && (!A || !B))) return fail(ASCA_ERR_INVALID, "asca_gemm: null pointer");
     const long a_cols = trans_a ? M : K, b_cols = trans_b ? K : N;
     if (lda < a_cols || ldb < b_cols || ldc < N) return fail(ASCA_ERR_INVALID, "asca_gemm: leading dimension too small");
-    const hipStream_t st = as_stream(stream);
+    return ASCA_OK;
+}
+
+// C = alpha op(A) op(B) + beta C (+ bias), split-K partials in ws.
+int gemm_run(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
+             long ldb, float beta, float* C, long ldc, const float* bias, Ws ws, hipStream_t st) {
+    if (M == 0 || N == 0) return ASCA_OK;
     GemmArgs a = gemm_args();
     a.A = A;
     a.B = B;
@@ -1304,21 +1323,13 @@ int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const 
     a.alpha = alpha;
     a.beta = beta;
     a.bias = bias;
-    // split K when the output has too few tiles to fill the chip
-    const long tiles = (long)((M + GM_BM - 1) / GM_BM) * ((N + GM_BN - 1) / GM_BN);
-    const int cus = cu_count() > 0 ? cu_count() : 256;
-    int splits = 1;
-    if (tiles < cus && K >= 1024) {
-        splits = (int)min((long)K / 512, (2L * cus + tiles - 1) / tiles);
-        if (splits < 1) splits = 1;
-    }
+    long kps = 0;
+    const int splits = K > 0 ? gemm_splits(M, N, K, &kps) : 1;
     if (splits == 1) return gemm_launch(trans_a, trans_b, EPI_STORE, a, M, st, "gemm");
-    long kps = ((K + splits - 1) / splits + GM_BK - 1) / GM_BK * GM_BK;
-    splits = (int)((K + kps - 1) / kps);
     const long MN = (long)M * N;
-    float* part = nullptr;
-    int rc = scratch_get((size_t)splits * MN * sizeof(float), &part);
+    int rc = ws_check(ws, (size_t)splits * MN, "gemm split-K");
     if (rc) return rc;
+    float* const part = ws.p;
     GemmArgs s = a;
     s.C = part;
     s.ldc = N;
@@ -1331,6 +1342,7 @@ int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const 
     if (rc) return rc;
     rc = pre_launch("splitk_reduce");
     if (rc) return rc;
+    const int cus = cu_count() > 0 ? cu_count() : 256;
     long blocks = (MN + 255) / 256;
     if (blocks > 4L * cus * 8) blocks = 4L * cus * 8;
     hipLaunchKernelGGL(splitk_reduce_k, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, MN, N, C, ldc, alpha,
@@ -1338,11 +1350,73 @@ int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const 
     return post_launch("splitk_reduce");
 }
 
+}  // namespace asca
+
+using namespace asca;
+
+extern "C" {
+
+int asca_gemm_ws_bytes(int trans_a, int trans_b, int M, int N, int K, size_t* bytes) {
+    (void)trans_a;
+    (void)trans_b;
+    if (!bytes) return fail(ASCA_ERR_INVALID, "null output pointer");
+    if (M < 0 || N < 0 || K < 0) return fail(ASCA_ERR_INVALID, "asca_gemm_ws_bytes: negative shape");
+    *bytes = gemm_ws_floats(M, N, K) * sizeof(float);
+    return ASCA_OK;
+}
+
+int asca_gemm_ws(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
+                 long ldb, float beta, float* C, long ldc, const float* bias, void* ws, size_t ws_bytes,
+                 void* stream) {
+    int rc = gemm_check(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc);
+    if (rc || M == 0 || N == 0) return rc;
+    return gemm_run(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias,
+                    Ws{reinterpret_cast<float*>(ws), ws_bytes / sizeof(float)}, as_stream(stream));
+}
+
+// The reference's matmul takes no workspace: split-K partials come from the
+// stream-ordered allocator on the call's stream and go back to it behind the
+// reduction, so calls on different streams never share them.
+int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda, const float* B,
+              long ldb, float beta, float* C, long ldc, const float* bias, void* stream) {
+    int rc = gemm_check(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc);
+    if (rc || M == 0 || N == 0) return rc;
+    const hipStream_t st = as_stream(stream);
+    const size_t need = gemm_ws_floats(M, N, K);
+    StreamScratch sc;
+    if ((rc = sc.get(need, st))) return rc;
+    rc = gemm_run(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, sc.ws, st);
+    const int rf = sc.release(st);
+    return rc ? rc : rf;
+}
+
+int asca_colsum_ws_bytes(long rows, int cols, size_t* bytes) {
+    if (!bytes) return fail(ASCA_ERR_INVALID, "null output pointer");
+    if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "asca_colsum_ws_bytes: negative shape");
+    *bytes = colsum_ws_floats(rows, cols, false, 0) * sizeof(float);
+    return ASCA_OK;
+}
+
+int asca_colsum_ws(const float* X, long rows, int cols, float* out, int accumulate, void* ws, size_t ws_bytes,
+                   void* stream) {
+    if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "asca_colsum: negative shape");
+    if (cols == 0) return ASCA_OK;
+    if (!out || (rows > 0 && !X)) return fail(ASCA_ERR_INVALID, "asca_colsum: null pointer");
+    return colsum_launch(X, rows, cols, cols, nullptr, 0, out, accumulate,
+                         Ws{reinterpret_cast<float*>(ws), ws_bytes / sizeof(float)}, as_stream(stream));
+}
+
 int asca_colsum(const float* X, long rows, int cols, float* out, int accumulate, void* stream) {
     if (rows < 0 || cols < 0) return fail(ASCA_ERR_INVALID, "asca_colsum: negative shape");
     if (cols == 0) return ASCA_OK;
     if (!out || (rows > 0 && !X)) return fail(ASCA_ERR_INVALID, "asca_colsum: null pointer");
-    return colsum_launch(X, rows, cols, cols, nullptr, 0, out, accumulate, as_stream(stream));
+    const hipStream_t st = as_stream(stream);
+    StreamScratch sc;
+    int rc = sc.get(colsum_ws_floats(rows, cols, false, 0), st);
+    if (rc) return rc;
+    rc = colsum_launch(X, rows, cols, cols, nullptr, 0, out, accumulate, sc.ws, st);
+    const int rf = sc.release(st);
+    return rc ? rc : rf;
 }
 
 }  // extern "C"

@@ -16,6 +16,7 @@
 // tensors in the reference's params() order: embed, head, then per layer
 // w_qkv, b_qkv, w_gate, b_gate, w_o, b_o, w1, b1, w2, b2 (model.rs:596-603,
 // delta.rs:96-105, model.rs:103-105).
+#include <algorithm>
 #include <cstdio>
 #include <string>
 #include <type_traits>
@@ -268,9 +269,13 @@ struct asca_model {
     // stream reads while the next layer's backward runs
     float *dx[2] = {nullptr, nullptr}, *dmid[2] = {nullptr, nullptr}, *dqkv[2] = {nullptr, nullptr},
           *dgate[2] = {nullptr, nullptr}, *dpre[2] = {nullptr, nullptr};
-    // weight-gradient stream (default priority, non-blocking) and its events
-    hipStream_t side = nullptr;
+    // weight-gradient stream and optimiser stream (default priority,
+    // non-blocking) and their events
+    hipStream_t side = nullptr, opt = nullptr;
     std::vector<hipEvent_t> evs;
+    // scratch of the weight-gradient stream: split-K partials and column-sum
+    // slices of every weight and bias gradient (they run there one at a time)
+    Ws wscratch{nullptr, 0};
     int32_t *route_e = nullptr, *perm = nullptr, *off = nullptr, *emb_b = nullptr, *emb_perm = nullptr,
             *emb_off = nullptr;
     void *route_ws = nullptr, *emb_ws = nullptr;
@@ -283,6 +288,7 @@ static void free_acts(asca_model* M) {
     for (void* a : M->allocs) (void)hipFree(a);
     M->allocs.clear();
     M->acts.clear();
+    M->wscratch = Ws{nullptr, 0};
     M->batch = M->seq = 0;
     M->fwd_done = false;
 }
@@ -334,6 +340,17 @@ static int ensure_acts(asca_model* M, int batch, int seq) {
             goto oom;
         M->route_ws = rw;
         M->emb_ws = ew;
+        // the weight-gradient stream's scratch, for its largest user
+        size_t ws = gemm_ws_floats(d, V, (int)T);
+        ws = std::max(ws, gemm_ws_floats(d, d, (int)T));
+        ws = std::max(ws, gemm_ws_floats(d, 3 * d, (int)T));
+        ws = std::max(ws, colsum_ws_floats((long)T, d, false, 0));
+        ws = std::max(ws, colsum_ws_floats((long)T, 3 * d, false, 0));
+        ws = std::max(ws, skinny_wgrad_ws_floats((long)T, d, 2 * H));
+        ws = std::max(ws, moe_bwd_weights_ws_floats((int)T, d, dff, M->E));
+        float* wsp = nullptr;
+        if ((rc = dalloc(M, &wsp, ws))) goto oom;
+        M->wscratch = Ws{wsp, ws};
         for (int k = 0; k < 2; ++k)
             if ((rc = dalloc(M, &M->dx[k], T * d)) || (rc = dalloc(M, &M->dmid[k], T * d)) ||
                 (rc = dalloc(M, &M->dqkv[k], T * 3 * d)) || (rc = dalloc(M, &M->dgate[k], T * 2 * H)) ||
@@ -452,32 +469,43 @@ static int model_forward(asca_model* M, const uint32_t* ids, const uint32_t* tar
     return ASCA_OK;
 }
 
-static int gemm_wgrad(const float* X, int ldx, const float* D, int ldd, float* G, int M_, int N_, int T,
+static int gemm_wgrad(const float* X, int ldx, const float* D, int ldd, float* G, int M_, int N_, int T, Ws ws,
                       hipStream_t st) {
     // G (M_ x N_) = X^T D over T rows; split K when the output is small
-    return asca_gemm(1, 0, M_, N_, T, 1.0f, X, ldx, D, ldd, 0.0f, G, N_, nullptr, st);
+    return gemm_run(1, 0, M_, N_, T, 1.0f, X, ldx, D, ldd, 0.0f, G, N_, nullptr, ws, st);
 }
 
-// Weight-gradient stream and its events, created on first use.  Events per
-// layer l: 5l + {0: dpre written, 1: d_mid written, 2: d_qkv written, 3: the
-// layer's weight gradients done, 4: the chain done with the layer's weights};
-// then fork, join, head weights done, embedding gradient done.
+// Weight-gradient and optimiser streams and their events, created on first
+// use.  Events per layer l: 5l + {0: dpre written, 1: d_mid written, 2: d_qkv
+// written, 3: the layer's weight gradients done, 4: the chain done with the
+// layer's weights}; then EV_FORK, EV_JOIN (weight-gradient stream done),
+// EV_HEAD_CHAIN (the chain done with the head weights), EV_HEAD_GRAD (head
+// weight gradient done), EV_EMB (embedding gradient done), EV_OPT (optimiser
+// stream done).
+enum { EV_FORK = 0, EV_JOIN, EV_HEAD_CHAIN, EV_HEAD_GRAD, EV_EMB, EV_OPT, EV_GLOBAL };
+
+static void drop_side(asca_model* M) {
+    for (hipEvent_t x : M->evs)
+        if (x) (void)hipEventDestroy(x);
+    M->evs.clear();
+    if (M->side) (void)hipStreamDestroy(M->side);
+    if (M->opt) (void)hipStreamDestroy(M->opt);
+    M->side = M->opt = nullptr;
+}
+
 static int ensure_side(asca_model* M) {
     if (M->side) return ASCA_OK;
     hipError_t e = hipStreamCreateWithFlags(&M->side, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&M->opt, hipStreamNonBlocking);
     if (e != hipSuccess) {
-        M->side = nullptr;
+        drop_side(M);
         return fail(ASCA_ERR_HIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
     }
-    M->evs.assign((size_t)5 * M->L + 4, nullptr);
+    M->evs.assign((size_t)5 * M->L + EV_GLOBAL, nullptr);
     for (auto& ev : M->evs)
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
             // leave no half-made set behind: the next call starts again
-            for (hipEvent_t x : M->evs)
-                if (x) (void)hipEventDestroy(x);
-            M->evs.clear();
-            (void)hipStreamDestroy(M->side);
-            M->side = nullptr;
+            drop_side(M);
             return fail(ASCA_ERR_HIP, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
         }
     return ASCA_OK;
@@ -488,6 +516,12 @@ static int hand_over(hipStream_t from, hipStream_t to, hipEvent_t ev) {
     hipError_t e = hipEventRecord(ev, from);
     if (e == hipSuccess) e = hipStreamWaitEvent(to, ev, 0);
     return e == hipSuccess ? (int)ASCA_OK : fail(ASCA_ERR_HIP, "stream hand-over: %s", hipGetErrorString(e));
+}
+
+// After a failure: `st` still waits for whatever was queued on `from`, so no
+// later work on `st` races it.  Keeps the failure's message.
+static void join_after_error(hipStream_t from, hipStream_t st, hipEvent_t ev) {
+    if (hipEventRecord(ev, from) == hipSuccess) (void)hipStreamWaitEvent(st, ev, 0);
 }
 
 // Backward of the whole model into the gradient buffer (overwritten).
@@ -501,31 +535,24 @@ static int hand_over(hipStream_t from, hipStream_t to, hipEvent_t ev) {
 // before the chain overwrites a set it waits for the weight gradients that
 // read it (layer l + 2, and layer l + 1 for dx), and `st` joins the second
 // stream at the end, so work queued on `st` afterwards sees every gradient.
+// On a failure `st` still joins what was queued on the second stream.
 static int adamw_range(asca_model* M, size_t j0, size_t j1, hipStream_t st);
 
-// with_adamw: also apply AdamW on the second stream, each layer's tensors as
-// soon as their gradients are final and the chain no longer reads their
-// weights (the update is elementwise per tensor, so the result is the same as
-// one launch after the backward); the caller advances the step counter.
-static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false) {
+static int backward_body(asca_model* M, hipStream_t st, hipStream_t sd) {
     const int T = M->batch * M->seq, d = M->d, H = M->H, dh = M->dh, E = M->E, dff = M->dff, V = M->V, L = M->L;
-    int rc = ensure_side(M);
-    if (rc) return rc;
-    hipStream_t sd = M->side;
     auto ev = [&](int l, int k) { return M->evs[(size_t)5 * l + k]; };
-    hipEvent_t ev_fork = M->evs[(size_t)5 * L], ev_join = M->evs[(size_t)5 * L + 1];
-    hipEvent_t ev_head = M->evs[(size_t)5 * L + 2], ev_emb = M->evs[(size_t)5 * L + 3];
+    auto gev = [&](int k) { return M->evs[(size_t)5 * L + k]; };
+    const Ws ws = M->wscratch;
     float* G = M->g;
     const float* x_last = M->acts[L - 1].x_out;
-    if ((rc = hand_over(st, sd, ev_fork))) return rc;
+    int rc;
     // head: d_head = h^T dlogits (second stream) ; dh = dlogits W_head^T ; dx = rmsnorm_bwd(x_L, dh)
-    if ((rc = gemm_wgrad(M->h_final, d, M->dlogits, V, G + M->t[1].off, d, V, T, sd))) return rc;
+    if ((rc = gemm_wgrad(M->h_final, d, M->dlogits, V, G + M->t[1].off, d, V, T, ws, sd))) return rc;
+    if (hipEventRecord(gev(EV_HEAD_GRAD), sd) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
     GemmArgs dhh = gemm_plain(M->dlogits, V, M->p + M->t[1].off, V, M->dtmp, d, T, d, V);
     if ((rc = gemm_launch(0, 1, EPI_STORE, dhh, T, st, "head_dx"))) return rc;
+    if (hipEventRecord(gev(EV_HEAD_CHAIN), st) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
     if ((rc = rmsnorm_bwd_launch(x_last, M->dtmp, nullptr, M->dx[(L - 1) & 1], T, d, MODEL_EPS, st))) return rc;
-    if (with_adamw) {  // head (tensor 1): its gradient is queued on the second stream, its weights read above
-        if ((rc = hand_over(st, sd, ev_head)) || (rc = adamw_range(M, 1, 2, sd))) return rc;
-    }
     for (int l = L - 1; l >= 0; --l) {
         const MLayer& P = M->lay[l];
         MActs& a = M->acts[l];
@@ -542,12 +569,12 @@ static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false
             return rc;
         if ((rc = hand_over(st, sd, ev(l, 0)))) return rc;
         if ((rc = moe_bwd_weights(a.xn, a.hid, M->perm, M->off, din, dpre, T, d, dff, E, G + P.w1, G + P.b1,
-                                  G + P.w2, G + P.b2, 0, sd)))
+                                  G + P.w2, G + P.b2, 0, ws, sd)))
             return rc;
         if ((rc = rmsnorm_bwd_launch(a.x_mid, M->dxn, din, dmid, T, d, MODEL_EPS, st))) return rc;
         if ((rc = hand_over(st, sd, ev(l, 1)))) return rc;
-        if ((rc = gemm_wgrad(a.o, d, dmid, d, G + P.w_o, d, d, T, sd))) return rc;
-        if ((rc = asca_colsum(dmid, T, d, G + P.b_o, 0, sd))) return rc;
+        if ((rc = gemm_wgrad(a.o, d, dmid, d, G + P.w_o, d, d, T, ws, sd))) return rc;
+        if ((rc = colsum_launch(dmid, T, d, d, nullptr, 0, G + P.b_o, 0, ws, sd))) return rc;
         // delta block backward (delta.rs:615-674) from dy = d_mid
         GemmArgs dov = gemm_plain(dmid, d, M->p + P.w_o, d, M->dtmp, d, T, d, d);
         if ((rc = gemm_launch(0, 1, EPI_STORE, dov, T, st, "out_proj_dx"))) return rc;
@@ -555,9 +582,9 @@ static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false
                                        M->seq, H, dh, st)))
             return rc;
         if ((rc = hand_over(st, sd, ev(l, 2)))) return rc;
-        if ((rc = gemm_wgrad(x_in, d, dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, sd))) return rc;
-        if ((rc = asca_colsum(dqkv, T, 3 * d, G + P.b_qkv, 0, sd))) return rc;
-        if ((rc = skinny_wgrad_launch(x_in, d, dgate, G + P.w_gate, G + P.b_gate, T, d, 2 * H, sd))) return rc;
+        if ((rc = gemm_wgrad(x_in, d, dqkv, 3 * d, G + P.w_qkv, d, 3 * d, T, ws, sd))) return rc;
+        if ((rc = colsum_launch(dqkv, T, 3 * d, 3 * d, nullptr, 0, G + P.b_qkv, 0, ws, sd))) return rc;
+        if ((rc = skinny_wgrad_launch(x_in, d, dgate, G + P.w_gate, G + P.b_gate, T, d, 2 * H, ws, sd))) return rc;
         if (hipEventRecord(ev(l, 3), sd) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
         // dout (the layer below's din) was last read by the weight gradients of layer l + 1
         if (l + 1 < L && hipStreamWaitEvent(st, ev(l + 1, 3), 0) != hipSuccess)
@@ -570,20 +597,77 @@ static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false
         GemmArgs dg = gemm_plain(dgate, 2 * H, M->p + P.w_gate, 2 * H, dout, d, T, d, 2 * H);
         dg.beta = 1.0f;
         if ((rc = gemm_launch(0, 1, EPI_STORE, dg, T, st, "gate_proj_dx"))) return rc;
-        if (with_adamw) {  // layer l's tensors: 2 + 10 l .. 2 + 10 l + 9
-            if ((rc = hand_over(st, sd, ev(l, 4))) || (rc = adamw_range(M, 2 + 10 * (size_t)l, 12 + 10 * (size_t)l, sd)))
-                return rc;
-        }
+        // the chain is done with layer l's weights
+        if (hipEventRecord(ev(l, 4), st) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
     }
     // embedding gradient
     if ((rc = pre_launch("embed_grad"))) return rc;
     hipLaunchKernelGGL(embed_grad_k, dim3(V), dim3(256), 0, st, M->dx[1], M->emb_perm, M->emb_off, d,
                        G + M->t[0].off);
     if ((rc = post_launch("embed_grad"))) return rc;
-    if (with_adamw) {  // embedding (tensor 0)
-        if ((rc = hand_over(st, sd, ev_emb)) || (rc = adamw_range(M, 0, 1, sd))) return rc;
+    if (hipEventRecord(gev(EV_EMB), st) != hipSuccess) return fail(ASCA_ERR_HIP, "hipEventRecord failed");
+    return ASCA_OK;
+}
+
+// The optimiser step of a training step on the model's third stream: each
+// group of tensors (head, layers from the top, embedding) starts once its
+// gradients are final and the chain no longer reads its weights, so the
+// updates overlap the rest of the backward (the update is elementwise per
+// tensor: the result equals one launch after the backward).  Issued only
+// after every backward launch was queued without error.
+static int optimiser_body(asca_model* M, hipStream_t st, hipStream_t sd, int* launched) {
+    const int L = M->L;
+    auto ev = [&](int l, int k) { return M->evs[(size_t)5 * l + k]; };
+    auto gev = [&](int k) { return M->evs[(size_t)5 * L + k]; };
+    const hipStream_t so = M->opt;
+    (void)sd;
+    (void)st;
+    auto group = [&](hipEvent_t a, hipEvent_t b, size_t j0, size_t j1) -> int {
+        if (hipStreamWaitEvent(so, a, 0) != hipSuccess || hipStreamWaitEvent(so, b, 0) != hipSuccess)
+            return fail(ASCA_ERR_HIP, "hipStreamWaitEvent failed");
+        int rc = adamw_range(M, j0, j1, so);
+        if (!rc) ++*launched;
+        return rc;
+    };
+    int rc = group(gev(EV_HEAD_GRAD), gev(EV_HEAD_CHAIN), 1, 2);   // head (tensor 1)
+    for (int l = L - 1; l >= 0 && !rc; --l)                         // layer l: tensors 2 + 10 l .. 2 + 10 l + 9
+        rc = group(ev(l, 3), ev(l, 4), 2 + 10 * (size_t)l, 12 + 10 * (size_t)l);
+    if (!rc) rc = group(gev(EV_EMB), gev(EV_EMB), 0, 1);             // embedding (tensor 0)
+    return rc;
+}
+
+// with_adamw: also apply AdamW (optimiser_body); the caller advances the step
+// counter on success.  A failure there after some tensors were updated is
+// reported as ASCA_ERR_PARTIAL_UPDATE; every other failure leaves the
+// parameters and moments untouched.
+static int model_backward(asca_model* M, hipStream_t st, bool with_adamw = false) {
+    int rc = ensure_side(M);
+    if (rc) return rc;
+    const hipStream_t sd = M->side;
+    auto gev = [&](int k) { return M->evs[(size_t)5 * M->L + k]; };
+    if ((rc = hand_over(st, sd, gev(EV_FORK)))) return rc;
+    if ((rc = backward_body(M, st, sd))) {
+        join_after_error(sd, st, gev(EV_JOIN));
+        return rc;
     }
-    return hand_over(sd, st, ev_join);
+    if (with_adamw) {
+        int launched = 0;
+        if ((rc = optimiser_body(M, st, sd, &launched))) {
+            join_after_error(sd, st, gev(EV_JOIN));
+            join_after_error(M->opt, st, gev(EV_OPT));
+            if (launched) {
+                const std::string why = asca_last_error();
+                return fail(ASCA_ERR_PARTIAL_UPDATE, "optimiser step failed after %d of its launches (%s)", launched,
+                            why.c_str());
+            }
+            return rc;
+        }
+        if ((rc = hand_over(M->opt, st, gev(EV_OPT)))) {
+            join_after_error(sd, st, gev(EV_JOIN));
+            return fail(ASCA_ERR_PARTIAL_UPDATE, "optimiser stream join failed");
+        }
+    }
+    return hand_over(sd, st, gev(EV_JOIN));
 }
 
 // AdamW over tensors j0 .. j1-1 with the step counter base M->adam_step (the
@@ -721,9 +805,7 @@ static void destroy_model(asca_model* M) {
     free_acts(M);
     free_decode(M);
     (void)hipDeviceSynchronize();
-    for (hipEvent_t e : M->evs)
-        if (e) (void)hipEventDestroy(e);
-    if (M->side) (void)hipStreamDestroy(M->side);
+    drop_side(M);
     for (void* q : {(void*)M->p, (void*)M->g, (void*)M->m, (void*)M->v, (void*)M->chunks})
         if (q) (void)hipFree(q);
     delete M;

@@ -15,6 +15,8 @@
 // row order: row i belongs to token perm[i].
 #include "common.h"
 #include "gemm.h"
+#include <algorithm>
+
 #include "moe.h"
 #include "runtime.h"
 
@@ -73,9 +75,13 @@ int asca::moe_bwd_data(const float* w1, const float* w2, const float* pre, const
     return gemm_launch(0, 1, EPI_STORE, dx, T, st, "moe_bwd_dxn");
 }
 
+size_t asca::moe_bwd_weights_ws_floats(int T, int d, int d_ff, int E) {
+    return std::max(colsum_ws_floats(T, d, false, 0), colsum_ws_floats(T, d_ff, true, E));
+}
+
 int asca::moe_bwd_weights(const float* xn, const float* hidden, const int32_t* perm, const int32_t* offsets,
                           const float* dout, const float* dpre_ws, int T, int d, int d_ff, int E, float* dw1,
-                          float* db1, float* dw2, float* db2, int accumulate, hipStream_t st) {
+                          float* db1, float* dw2, float* db2, int accumulate, Ws ws, hipStream_t st) {
     const float beta = accumulate ? 1.0f : 0.0f;
     // dW2[e] (+)= hidden_e^T dout[perm_e]
     GemmArgs g2 = gemm_args();
@@ -96,9 +102,9 @@ int asca::moe_bwd_weights(const float* xn, const float* hidden, const int32_t* p
     int rc = gemm_launch(1, 0, EPI_STORE, g2, 0, st, "moe_bwd_dw2");
     if (rc) return rc;
     // db2 (+)= colsum(dout)
-    if ((rc = colsum_launch(dout, T, d, d, nullptr, 0, db2, accumulate, st))) return rc;
+    if ((rc = colsum_launch(dout, T, d, d, nullptr, 0, db2, accumulate, ws, st))) return rc;
     // db1[e] (+)= colsum(dpre_e)
-    if ((rc = colsum_launch(dpre_ws, T, d_ff, d_ff, offsets, E, db1, accumulate, st))) return rc;
+    if ((rc = colsum_launch(dpre_ws, T, d_ff, d_ff, offsets, E, db1, accumulate, ws, st))) return rc;
     // dW1[:, e] (+)= xn[perm_e]^T dpre_e
     GemmArgs g1 = gemm_args();
     g1.A = xn;
@@ -181,8 +187,14 @@ int asca_moe_bwd(const float* xn, const float* w1, const float* w2, const float*
         return fail(ASCA_ERR_INVALID, "asca_moe_bwd: null pointer");
     const hipStream_t st = as_stream(stream);
     if ((rc = moe_bwd_data(w1, w2, pre, perm, offsets, dout, T, d, d_ff, n_experts, dxn, dpre_ws, st))) return rc;
-    return moe_bwd_weights(xn, hidden, perm, offsets, dout, dpre_ws, T, d, d_ff, n_experts, dw1, db1, dw2, db2,
-                           accumulate, st);
+    // the column sums' partials: stream-ordered scratch (the reference's
+    // moe_bwd_dev takes no workspace beyond dpre)
+    StreamScratch sc;
+    if ((rc = sc.get(moe_bwd_weights_ws_floats(T, d, d_ff, n_experts), st))) return rc;
+    rc = moe_bwd_weights(xn, hidden, perm, offsets, dout, dpre_ws, T, d, d_ff, n_experts, dw1, db1, dw2, db2,
+                         accumulate, sc.ws, st);
+    const int rf = sc.release(st);
+    return rc ? rc : rf;
 }
 
 }  // extern "C"

@@ -28,4 +28,21 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Number of compute units of the active device (0 before init).
 int cu_count();
 
+// A caller-provided device workspace of `floats` floats.
+struct Ws {
+    float* p;
+    size_t floats;
+};
+
+// Scratch for the entry points that take no workspace argument (as the
+// reference's operators take none): get() allocates from the stream-ordered
+// allocator on the call's stream (hipMallocAsync), release() returns it behind
+// the work queued so far (hipFreeAsync).  Calls on different streams never
+// share scratch and nothing waits for the device.
+struct StreamScratch {
+    Ws ws{nullptr, 0};
+    int get(size_t floats, hipStream_t st);
+    int release(hipStream_t st);
+};
+
 }  // namespace asca

@@ -73,6 +73,23 @@ int pre_launch(const char* kernel) {
     return ASCA_OK;
 }
 
+int StreamScratch::get(size_t floats, hipStream_t st) {
+    ws = Ws{nullptr, 0};
+    if (floats == 0) return ASCA_OK;
+    void* p = nullptr;
+    hipError_t e = hipMallocAsync(&p, floats * sizeof(float), st);
+    if (e != hipSuccess) return fail(ASCA_ERR_OOM, "hipMallocAsync(%zu): %s", floats * sizeof(float), hipGetErrorString(e));
+    ws = Ws{reinterpret_cast<float*>(p), floats};
+    return ASCA_OK;
+}
+
+int StreamScratch::release(hipStream_t st) {
+    if (!ws.p) return ASCA_OK;
+    hipError_t e = hipFreeAsync(ws.p, st);
+    ws = Ws{nullptr, 0};
+    return e == hipSuccess ? (int)ASCA_OK : fail(ASCA_ERR_HIP, "hipFreeAsync: %s", hipGetErrorString(e));
+}
+
 int post_launch(const char* kernel) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(ASCA_ERR_HIP, "launch of %s failed: %s", kernel, hipGetErrorString(e));
@@ -112,6 +129,13 @@ int asca_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(ASCA_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", device,
                     prop.gcnArchName);
+    // The stream-ordered allocator behind StreamScratch keeps what is freed for
+    // reuse instead of returning it to the driver at every synchronisation.
+    hipMemPool_t pool = nullptr;
+    if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess && pool) {
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
     g_device = device;
     g_cus = prop.multiProcessorCount;
     snprintf(g_name, sizeof g_name, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, g_cus);

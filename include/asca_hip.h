@@ -40,7 +40,9 @@ enum {
     ASCA_ERR_NOT_INIT = 4,     /* asca_init has not succeeded                      */
     ASCA_ERR_INJECTED = 5,     /* failure injected by asca_fail_after             */
     ASCA_ERR_OOM = 6,          /* device allocation failed                        */
-    ASCA_ERR_NO_DEVICE = 7     /* no HIP device present                           */
+    ASCA_ERR_NO_DEVICE = 7,    /* no HIP device present                           */
+    ASCA_ERR_PARTIAL_UPDATE = 8 /* asca_model_train_step: the optimiser step failed
+                                  after updating some tensors (see there)        */
 };
 
 /* ------------------------------------------------------------ runtime ---- */
@@ -234,8 +236,18 @@ ASCA_API int asca_scatter_rows(const float* src, const int32_t* idx, long n, int
                                void* stream);
 
 /* out[c] (+)= sum over rows of X[r][c] (accumulate != 0 adds to out): the bias
- * gradient, colsum_raw of rust/src/cuda/mod.rs:642-669.  Deterministic. */
+ * gradient, colsum_raw of rust/src/cuda/mod.rs:642-669.  Deterministic (row
+ * slices summed in a fixed order).  The slices' partial sums live in
+ * stream-ordered scratch on `stream` (hipMallocAsync / hipFreeAsync), so calls
+ * on different streams never share it. */
 ASCA_API int asca_colsum(const float* X, long rows, int cols, float* out, int accumulate, void* stream);
+/* asca_colsum with the partial sums in a caller workspace of at least
+ * asca_colsum_ws_bytes(rows, cols) bytes (no allocation; a workspace must not
+ * be shared by calls that overlap).  No reference counterpart: colsum_raw
+ * draws its scratch from the crate's pool. */
+ASCA_API int asca_colsum_ws_bytes(long rows, int cols, size_t* bytes);
+ASCA_API int asca_colsum_ws(const float* X, long rows, int cols, float* out, int accumulate, void* ws,
+                            size_t ws_bytes, void* stream);
 
 /* ----------------------------------------------------------------- AdamW -- */
 
@@ -290,12 +302,23 @@ ASCA_API int asca_bucket_keys(const uint32_t* keys, int n, int n_buckets, int32_
  * matmul_ld_raw / matmul_ta_ld_raw / matmul_tb_raw (rust/src/cuda/mod.rs:286-521,
  * 671-743) with kernels matmul_f32 / matmul_ta_f32 / matmul_ld_f32
  * (asca.cu:14-141); CPU semantics Mat::matmul / matmul_ta / matmul_t
- * (rust/src/tensor.rs:91-201).  Deterministic (split-K partials are summed in
- * a fixed order in a library-owned per-device scratch buffer; calls that
- * split K on different streams of one device must not overlap). */
+ * (rust/src/tensor.rs:91-201).  Deterministic: when the output has too few
+ * tiles to fill the device, K is split and the partial products are summed in
+ * a fixed order; the partials live in stream-ordered scratch on `stream`
+ * (hipMallocAsync / hipFreeAsync), so calls on different streams never share
+ * them. */
 ASCA_API int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda,
                        const float* B, long ldb, float beta, float* C, long ldc, const float* bias,
                        void* stream);
+/* asca_gemm with the split-K partials in a caller workspace of at least
+ * asca_gemm_ws_bytes(...) bytes (0 when the product does not split): no
+ * allocation and the same results bit for bit; a workspace must not be shared
+ * by calls that overlap.  No reference counterpart: matmul_raw draws its
+ * buffers from the crate's pool (rust/src/cuda/mod.rs:100-174). */
+ASCA_API int asca_gemm_ws_bytes(int trans_a, int trans_b, int M, int N, int K, size_t* bytes);
+ASCA_API int asca_gemm_ws(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda,
+                          const float* B, long ldb, float beta, float* C, long ldc, const float* bias, void* ws,
+                          size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------- MoE -- */
 
@@ -393,9 +416,15 @@ ASCA_API int asca_model_forward_backward(asca_model* model, const uint32_t* ids,
                                          int batch, int seq, float* loss, void* stream);
 /* The optimiser step over every tensor (model.rs:797-802 / AdamW::update). */
 ASCA_API int asca_model_adamw(asca_model* model, void* stream);
-/* forward_backward followed by asca_model_adamw: one training step (the
- * update of each layer's tensors starts on the model's second stream once
- * their gradients are final; the result is bit-identical). */
+/* forward_backward followed by asca_model_adamw: one training step.  The
+ * updates run on a third stream of the model, each group of tensors as soon as
+ * its gradients are final (bit-identical to one update after the backward);
+ * they are queued only after every launch of the backward was queued.  A
+ * failure before the updates leaves parameters, moments and the step count
+ * untouched (repeat the step); ASCA_ERR_PARTIAL_UPDATE means an update launch
+ * failed after others were queued: some tensors moved by one step, the step
+ * count did not (restore from a checkpoint).  Either way `stream` waits for
+ * everything the call queued on the model's streams. */
 ASCA_API int asca_model_train_step(asca_model* model, const uint32_t* ids, const uint32_t* targets, int batch,
                                    int seq, float* loss, void* stream);
 

@@ -228,3 +228,67 @@ def test_checkpoint_resume_round_trip(tmp_path):
     assert all(not a.any() for a in dm3.moments()[0])
     for x in (dm, dm2, dm3):
         x.close()
+
+
+def _launches():
+    import ctypes as C
+    from asca_amd import _lib
+
+    h2d, d2h, n = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    _lib.call("asca_stats", C.byref(h2d), C.byref(d2h), C.byref(n))
+    return n.value
+
+
+@pytest.mark.parametrize("where", ["forward", "mid-backward", "last backward launch", "optimiser"])
+def test_train_step_failure_leaves_parameters_untouched(where):
+    """A launch that fails inside the forward or backward makes
+    asca_model_train_step return the error with the parameters, AdamW moments
+    and step count exactly as before, and the caller's repeat of the step gives
+    what a model that never failed gets.  A failure among the optimiser's
+    launches (queued only after the whole backward) is ASCA_ERR_PARTIAL_UPDATE:
+    the groups queued before it moved, the step count did not."""
+    from asca_amd import gpu
+    from asca_amd._lib import AscaError
+
+    cfg = (256, 64, 4, 2, 4, 64)
+    L = cfg[3]
+    a, _ = _models(cfg, 41)
+    b, _ = _models(cfg, 41)
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, 256, 2 * 24).astype(np.uint32)
+    tgts = rng.integers(0, 256, 2 * 24).astype(np.uint32)
+    a.train_step(ids, tgts, 2)
+    n0 = _launches()
+    b.train_step(ids, tgts, 2)
+    per_step = _launches() - n0
+    n_opt = L + 2                       # head, each layer, embedding
+    fail_at = {"forward": 3, "mid-backward": (per_step - n_opt) * 3 // 4,
+               "last backward launch": per_step - n_opt - 1, "optimiser": per_step - 2}[where]
+    p0, m0, s0 = a.params(), a.moments(), a.adamw_step_count()
+    print(f"[model] {per_step} launches per step; injected failure at launch {fail_at} ({where})", flush=True)
+    gpu.fail_after(fail_at)
+    with pytest.raises(AscaError) as ei:
+        a.train_step(ids, tgts, 2)
+    gpu.fail_after(-1)
+    assert a.adamw_step_count() == s0
+    p1, m1 = a.params(), a.moments()
+    if where == "optimiser":
+        assert ei.value.code == 8, ei.value
+        # the groups before the failing one (all but the embedding, tensor 0) moved
+        assert np.array_equal(p1[0], p0[0]) and not np.array_equal(p1[1], p0[1])
+        a.close()
+        b.close()
+        return
+    assert ei.value.code == 5, ei.value
+    for x, y in zip(p1, p0):
+        np.testing.assert_array_equal(x, y)
+    for ma, mb in zip(m1, m0):
+        for x, y in zip(ma, mb):
+            np.testing.assert_array_equal(x, y)
+    la = a.train_step(ids, tgts, 2)
+    lb = b.train_step(ids, tgts, 2)
+    assert la == lb
+    for x, y in zip(a.params(), b.params()):
+        np.testing.assert_array_equal(x, y)
+    a.close()
+    b.close()

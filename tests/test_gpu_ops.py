@@ -93,6 +93,109 @@ def test_gemm_split_k_projection_weight_grad(orc, g):
     np.testing.assert_array_equal(got, g.gemm(x, d, trans_a=True))
 
 
+def _dev(a):
+    from asca_amd.gpu import DevBuf
+
+    return DevBuf.from_host(np.ascontiguousarray(a, dtype=np.float32))
+
+
+def test_gemm_and_colsum_workspace_variants_bit_identical(g):
+    # asca_gemm_ws / asca_colsum_ws (caller workspace) give the bits of
+    # asca_gemm / asca_colsum (stream-ordered scratch), split and unsplit
+    from asca_amd import _lib
+    from asca_amd.gpu import DevBuf, _vp
+
+    rng = np.random.default_rng(12)
+    for (M, N, K) in ((512, 1536, 16384), (512, 512, 8192), (96, 80, 700)):
+        x = rng.standard_normal((K, M)).astype(np.float32)
+        d = rng.standard_normal((K, N)).astype(np.float32)
+        bx, bd = _dev(x), _dev(d)
+        wsb = C.c_size_t()
+        _lib.call("asca_gemm_ws_bytes", 1, 0, M, N, K, C.byref(wsb))
+        print(f"[gemm] ws variant TN {M}x{N}x{K}: workspace {wsb.value} B", flush=True)
+        ws = DevBuf(max(wsb.value, 4))
+        c1, c2 = DevBuf(M * N * 4), DevBuf(M * N * 4)
+        _lib.call("asca_gemm", 1, 0, M, N, K, 1.0, _vp(bx), M, _vp(bd), N, 0.0, _vp(c1), N, None, None)
+        _lib.call("asca_gemm_ws", 1, 0, M, N, K, 1.0, _vp(bx), M, _vp(bd), N, 0.0, _vp(c2), N, None, _vp(ws),
+                  wsb.value, None)
+        s1, s2 = DevBuf(N * 4), DevBuf(N * 4)
+        _lib.call("asca_colsum_ws_bytes", K, N, C.byref(wsb))
+        ws2 = DevBuf(max(wsb.value, 4))
+        _lib.call("asca_colsum", _vp(bd), K, N, _vp(s1), 0, None)
+        _lib.call("asca_colsum_ws", _vp(bd), K, N, _vp(s2), 0, _vp(ws2), wsb.value, None)
+        _lib.call("asca_sync")
+        np.testing.assert_array_equal(c1.to_host((M, N)), c2.to_host((M, N)))
+        np.testing.assert_array_equal(s1.to_host((N,)), s2.to_host((N,)))
+        for b in (bx, bd, ws, c1, c2, s1, s2, ws2):
+            b.free()
+    # a workspace declared smaller than asked for is refused (every buffer is
+    # allocated at full size, so nothing could go out of bounds either way)
+    from asca_amd._lib import AscaError
+
+    M, N, K = 512, 512, 8192
+    _lib.call("asca_gemm_ws_bytes", 1, 0, M, N, K, C.byref(wsb))
+    assert wsb.value > 16
+    bx, bd, c, ws = DevBuf(K * M * 4), DevBuf(K * N * 4), DevBuf(M * N * 4), DevBuf(wsb.value)
+    with pytest.raises(AscaError) as ei:
+        _lib.call("asca_gemm_ws", 1, 0, M, N, K, 1.0, _vp(bx), M, _vp(bd), N, 0.0, _vp(c), N, None, _vp(ws), 16,
+                  None)
+    assert ei.value.code == 1
+    _lib.call("asca_sync")
+    for b in (bx, bd, c, ws):
+        b.free()
+
+
+def test_split_k_gemms_and_colsums_on_two_streams_concurrently(g):
+    # Split-K products and column sums queued on two streams at once, next to a
+    # model backward on a third, give the bits of the same calls run one after
+    # another: no scratch is shared between streams.
+    from asca_amd import _lib
+    from asca_amd.gpu import DevBuf, _vp
+    from asca_amd.model import DeviceModel
+    from oracle import model_oracle as mo
+
+    rng = np.random.default_rng(13)
+    shapes = [(512, 1536, 16384), (512, 512, 16384), (256, 768, 8192), (512, 1536, 12288)]
+    ins = []
+    for (M, N, K) in shapes:
+        ins.append((_dev(rng.standard_normal((K, M))), _dev(rng.standard_normal((K, N)))))
+    def run(streams):
+        outs = []
+        for i, ((M, N, K), (bx, bd)) in enumerate(zip(shapes, ins)):
+            st = streams[i % len(streams)]
+            c, s = DevBuf(M * N * 4), DevBuf(N * 4)
+            _lib.call("asca_gemm", 1, 0, M, N, K, 1.0, _vp(bx), M, _vp(bd), N, 0.0, _vp(c), N, None, st)
+            _lib.call("asca_colsum", _vp(bd), K, N, _vp(s), 0, st)
+            outs.append((c, s))
+        return outs
+
+    seq = run([None])
+    _lib.call("asca_sync")
+    ref = [(c.to_host((M, N)), s.to_host((N,))) for (c, s), (M, N, K) in zip(seq, shapes)]
+    cfg = (256, 512, 8, 2, 16, 1024)
+    dm = DeviceModel(*cfg)
+    dm.set_params(mo.init_params(3, *cfg))
+    ids = rng.integers(0, 256, 2 * 512).astype(np.uint32)
+    tgts = rng.integers(0, 256, 2 * 512).astype(np.uint32)
+    st = [C.c_void_p(), C.c_void_p(), C.c_void_p()]
+    for x in st:
+        _lib.call("asca_stream_create", C.byref(x))
+    bi, bt = dm.upload_batch(ids, tgts)
+    for rep in range(2):
+        print(f"[gemm] two streams + model backward, repetition {rep}", flush=True)
+        dm.forward_backward_dev(bi, bt, 2, 512, sync=False, stream=st[2])
+        par = run([st[0], st[1]])
+        _lib.call("asca_sync")
+        for (c, s), (rc_, rs_), (M, N, K) in zip(par, ref, shapes):
+            np.testing.assert_array_equal(c.to_host((M, N)), rc_)
+            np.testing.assert_array_equal(s.to_host((N,)), rs_)
+            c.free()
+            s.free()
+    for x in st:
+        _lib.call("asca_stream_destroy", x)
+    dm.close()
+
+
 def test_gemm_unaligned_leading_dimensions(orc, g):
     from asca_amd import _lib
     from asca_amd.gpu import DevBuf, _vp
