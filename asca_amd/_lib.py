@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple] = {
     "asca_bucket_keys": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
     "asca_gemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p]),
     "asca_gemm_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
+    "asca_gemm_noalloc": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p]),
     "asca_gemm_ws": (_i, [_i, _i, _i, _i, _i, _f, _p, _l, _p, _l, _f, _p, _l, _p, _p, _sz, _p]),
     "asca_moe_fwd": (_i, [_p] * 7 + [_i] * 4 + [_p] * 4),
     "asca_moe_bwd": (_i, [_p] * 8 + [_i] * 4 + [_p] * 6 + [_i, _p]),

@@ -1350,6 +1350,27 @@ int gemm_run(int trans_a, int trans_b, int M, int N, int K, float alpha, const f
     return post_launch("splitk_reduce");
 }
 
+// Scratch of asca_gemm_noalloc, the entry point for callers that cannot
+// allocate: a static device array of SCRATCH_FLOATS floats (64 MiB), which
+// every device the library runs on holds until the process ends.  In host code
+// `scratch` names a host-side stand-in, never the device memory: its device
+// address comes from hipGetSymbolAddress, once per device at asca_init (with
+// that device current), and only that address is used.
+constexpr size_t SCRATCH_FLOATS = (size_t)16 << 20;
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+static float* g_scratch_dev[64] = {};
+
+int noalloc_scratch_init(int device) {
+    if (device < 0 || device >= 64) return fail(ASCA_ERR_INVALID, "device %d out of range", device);
+    if (g_scratch_dev[device]) return ASCA_OK;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return fail(ASCA_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_dev[device] = reinterpret_cast<float*>(p);
+    return ASCA_OK;
+}
+
 }  // namespace asca
 
 using namespace asca;
@@ -1388,6 +1409,26 @@ int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const 
     rc = gemm_run(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, sc.ws, st);
     const int rf = sc.release(st);
     return rc ? rc : rf;
+}
+
+// asca_gemm whose split-K partials live in the static scratch: allocates
+// nothing.  Calls that overlap on one device share that scratch and race.
+int asca_gemm_noalloc(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda,
+                      const float* B, long ldb, float beta, float* C, long ldc, const float* bias, void* stream) {
+    int rc = gemm_check(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc);
+    if (rc || M == 0 || N == 0) return rc;
+    if ((rc = ensure_device())) return rc;
+    const size_t need = gemm_ws_floats(M, N, K);
+    if (need > SCRATCH_FLOATS)
+        return fail(ASCA_ERR_INVALID,
+                    "asca_gemm_noalloc: the split-K partials of %dx%dx%d need %zu bytes, the static scratch holds "
+                    "%zu (use asca_gemm_ws)",
+                    M, N, K, need * sizeof(float), SCRATCH_FLOATS * sizeof(float));
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !g_scratch_dev[dev])
+        return fail(ASCA_ERR_NOT_INIT, "asca_gemm_noalloc: no static scratch address for device %d", dev);
+    return gemm_run(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias,
+                    Ws{g_scratch_dev[dev], SCRATCH_FLOATS}, as_stream(stream));
 }
 
 int asca_colsum_ws_bytes(long rows, int cols, size_t* bytes) {

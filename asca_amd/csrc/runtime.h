@@ -28,6 +28,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Number of compute units of the active device (0 before init).
 int cu_count();
 
+// Device address of the static scratch of asca_gemm_noalloc on `device` (the
+// current device), taken once at asca_init (gemm.hip).
+int noalloc_scratch_init(int device);
+
 // A caller-provided device workspace of `floats` floats.
 struct Ws {
     float* p;

@@ -136,6 +136,7 @@ int asca_init(int device) {
         uint64_t keep = UINT64_MAX;
         (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
     }
+    if (int rc = noalloc_scratch_init(device)) return rc;
     g_device = device;
     g_cus = prop.multiProcessorCount;
     snprintf(g_name, sizeof g_name, "%s (%s, %d CUs)", prop.name, prop.gcnArchName, g_cus);

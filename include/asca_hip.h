@@ -316,6 +316,18 @@ ASCA_API int asca_gemm(int trans_a, int trans_b, int M, int N, int K, float alph
  * by calls that overlap.  No reference counterpart: matmul_raw draws its
  * buffers from the crate's pool (rust/src/cuda/mod.rs:100-174). */
 ASCA_API int asca_gemm_ws_bytes(int trans_a, int trans_b, int M, int N, int K, size_t* bytes);
+/* asca_gemm that allocates nothing, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart.  The split-K partials live in a
+ * static 64 MiB device array that every device the library runs on holds
+ * until the process ends; a product whose partials need more is refused with
+ * ASCA_ERR_INVALID (asca_gemm_ws takes any size).  The partials are written in
+ * full before they are read (nothing needs clearing), and the results are the
+ * bits of asca_gemm.  All calls on one device share the array: calls that
+ * overlap on one device (concurrent streams or threads) race. */
+ASCA_API int asca_gemm_noalloc(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                               long lda, const float* B, long ldb, float beta, float* C, long ldc,
+                               const float* bias, void* stream);
 ASCA_API int asca_gemm_ws(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, long lda,
                           const float* B, long ldb, float beta, float* C, long ldc, const float* bias, void* ws,
                           size_t ws_bytes, void* stream);
