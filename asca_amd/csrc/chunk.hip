@@ -301,7 +301,11 @@ __global__ __launch_bounds__(256) void ck_rowscale_k(const float* __restrict__ i
 //   dAs = dA + dA^T;  dbeta_j = Y_j.V_j + gamma_j Z_j.K_j + sum_i dL Gamma A;
 //   dgamma_t = beta_t Z_t.K_t + dO_t.(QS)_t (+ <dS', S> at t = C-1);
 //   dGamma = dMr o B (tril) + dL beta A (+ K_i.dKt_i on row C-1);
-//   dalpha_m = (sum_{t>=m} dgamma_t gamma_t + sum_{t>=m>i} dGamma Gamma) / alpha_m.
+//   dalpha_m = gamma_{m-1} s(m) + sum_{t>=m} Gamma[t][m] c_t(m), the derivative
+//   of every running product with alpha_m left out (no division: exact for
+//   alpha_m = 0), where s(m) = sum_{t>=m} Gamma[t][m] dgamma_t and
+//   c_t(m) = sum_{i<m} dGamma[t][i] Gamma[m-1][i], i.e. c_t(0) = 0,
+//   c_t(m+1) = alpha_m c_t(m) + dGamma[t][m].
 __global__ __launch_bounds__(256) void ck_bwd_scalars_k(
     const float* __restrict__ dMr, const float* __restrict__ dLs, const float* __restrict__ Gam,
     const float* __restrict__ Am, const float* __restrict__ Bm, const float* __restrict__ al,
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(256) void ck_bwd_scalars_k(
                 dAl[j][i] = dl * bj * g;
                 float dG = dm * Bm[o] + dl * bj * a;
                 if (j == C - 1) dG += kk[i];
-                R[j][i] = i < j ? dG * g : 0.0f;
+                R[j][i] = i < j ? dG : 0.0f;   // dGamma, strictly lower
                 Pb[j][i] = dl * g * a;  // dbeta row terms
             }
         }
@@ -378,21 +382,27 @@ __global__ __launch_bounds__(256) void ck_bwd_scalars_k(
         dbe[n * C + j] = yv[j] + gj * zk[j] + s;
         float dgam = be[n * C + j] * zk[j] + op[j];
         if (j == C - 1) dgam += fro;
-        dg[j] = dgam * gj;
-        // row j of R becomes its exclusive prefix along i: R[j][m] = sum_{i<m} R[j][i]
-        float run = 0.0f;
-        for (int i2 = 0; i2 < C; ++i2) {
-            const float x = R[j][i2];
-            R[j][i2] = run;
-            run += x;
+        dg[j] = dgam;
+    }
+    __syncthreads();
+    // dAl is free again: row t of X[t][m] = Gamma[t][m] c_t(m), one thread per row
+    if (tid < C) {
+        const int t = tid;
+        float cm = 0.0f;   // c_t(m)
+        for (int m = 0; m < C; ++m) {
+            dAl[t][m] = m <= t ? Gam[cc + (long)t * C + m] * cm : 0.0f;
+            cm = fmaf(al[n * C + m], cm, R[t][m]);
         }
     }
     __syncthreads();
     if (tid < C) {
         const int m = tid;
-        float s = 0.0f;
-        for (int t = m; t < C; ++t) s += dg[t] + R[t][m];
-        dal[n * C + m] = s / al[n * C + m];
+        float sm = 0.0f, x = 0.0f;
+        for (int t = m; t < C; ++t) {
+            sm = fmaf(Gam[cc + (long)t * C + m], dg[t], sm);
+            x += dAl[t][m];
+        }
+        dal[n * C + m] = fmaf(m ? gam[n * C + m - 1] : 1.0f, sm, x);
     }
 }
 
@@ -1256,7 +1266,7 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
                 RA[j * FP_LK + i] = g * dm;
                 RA[j * FP_LK + 64 + i] = dl * bj * g;
                 const float dG = dm * pBm[y][r] + dl * bj * am;
-                RE[j * FP_LC + i] = i < j ? dG * g : 0.0f;
+                RE[j * FP_LC + i] = i < j ? dG : 0.0f;   // dGamma, strictly lower
                 pb[r] += dl * g * am;
             }
         rows_out(pb, ppb + 64 * (wv & 1), rm0, lane);
@@ -1269,19 +1279,38 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         qst[i] = ld_row4(q, rowbase, rowstride, r, valid, f);
     }
     __syncthreads();
-    // R term of d log alpha_m: sum_{t >= m} sum_{i < m} R[t][i]; wave w takes rows 8w .. 8w+7
+    // dGamma term of dalpha_m (no division, exact at alpha_m = 0):
+    //   sum_{t >= m} Gamma[t][m] c_t(m),  c_t(m) = sum_{i < m} dGamma[t][i] Gamma[m-1][i],
+    // c_t(m+1) = alpha_m c_t(m) + dGamma[t][m] as an affine scan over the lanes;
+    // wave w takes rows 8w .. 8w+7
     {
-        float acc = 0.0f;
-        for (int t = 8 * wv; t < 8 * wv + 8; ++t) {
-            float sc = RE[t * FP_LC + lane];
+        float gr[8];
 #pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const float y = __shfl_up(sc, o);
-                if (lane >= o) sc += y;
+        for (int r = 0; r < 8; ++r) gr[r] = w.Gam[cc + (long)(8 * wv + r) * FP_C + lane];
+        // the scan's multipliers (products of alpha over the lanes' windows) are the same for every row
+        float am[6];
+        {
+            float a = a_s[lane];
+#pragma unroll
+            for (int lv = 0, o = 1; o < 64; o <<= 1, ++lv) {
+                am[lv] = a;
+                const float ap = __shfl_up(a, o);
+                if (lane >= o) a *= ap;
             }
-            float ex = __shfl_up(sc, 1);
-            if (lane == 0) ex = 0.0f;
-            if (t >= lane) acc += ex;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int t = 8 * wv + r;
+            float x = RE[t * FP_LC + lane];
+#pragma unroll
+            for (int lv = 0, o = 1; o < 64; o <<= 1, ++lv) {
+                const float xp = __shfl_up(x, o);
+                if (lane >= o) x = fmaf(am[lv], xp, x);
+            }
+            float cm = __shfl_up(x, 1);   // x = c_t(lane + 1)
+            if (lane == 0) cm = 0.0f;
+            if (t >= lane) acc = fmaf(gr[r], cm, acc);
         }
         pr[wv * 64 + lane] = acc;
     }
@@ -1391,24 +1420,33 @@ __global__ __launch_bounds__(FP_NT) void ck_bwd_fused_k(const uint16_t* __restri
         const float dbt = (pyv[t] + pyv[64 + t]) + gm * zkt + (ppb[t] + ppb[64 + t]);
         float dgam = b_s[t] * zkt + qdt;
         if (t == FP_C - 1) dgam += ((fr[0] + fr[1]) + (fr[2] + fr[3])) + ((fr[4] + fr[5]) + (fr[6] + fr[7]));
-        // suffix sum over t >= m of dgamma_t gamma_t; exclusive prefix over i < m of gt_i (K.dKt)_i
-        float suf = dgam * gm;
+        // s(m) = sum_{t >= m} Gamma[t][m] dgamma_t = dgamma_m + alpha_{m+1} s(m+1): a suffix affine scan
+        float sb = dgam, sa = lane + 1 < FP_C ? a_s[lane + 1] : 0.0f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_down(suf, o);
-            if (lane + o < 64) suf += y;
+            const float bn = __shfl_down(sb, o), an = __shfl_down(sa, o);
+            if (lane + o < 64) {
+                sb = fmaf(sa, bn, sb);
+                sa *= an;
+            }
         }
-        float pre = gt_s[t] * kkt;
+        // row C-1's K.dKt term of dGamma: e(m) = sum_{i < m} (K.dKt)_i Gamma[m-1][i],
+        // e(m+1) = alpha_m e(m) + (K.dKt)_m, weighted by Gamma[C-1][m]
+        float eb = kkt, ea = a_s[t];
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_up(pre, o);
-            if (lane >= o) pre += y;
+            const float bp = __shfl_up(eb, o), ap = __shfl_up(ea, o);
+            if (lane >= o) {
+                eb = fmaf(ea, bp, eb);
+                ea *= ap;
+            }
         }
-        float ex = __shfl_up(pre, 1);
-        if (lane == 0) ex = 0.0f;
+        float em = __shfl_up(eb, 1);
+        if (lane == 0) em = 0.0f;
+        const float gprev = lane ? g_s[lane - 1] : 1.0f;   // gamma_{m-1}
         if (t < valid) {
             const long gi = ((long)b * T + t0 + t) * H + h;
-            dalpha[gi] = (suf + dlr[t] + ex) / a_s[t];
+            dalpha[gi] = fmaf(gprev, sb, fmaf(gt_s[t], em, dlr[t]));
             dbeta[gi] = dbt;
         }
     }

@@ -144,11 +144,14 @@ def chunk_bwd(P, q, k, v, alpha, beta, dO, dSn):
     dgamma[C - 1] += np.sum(dSn * S)
     dGam = dM * (q @ k.T) + dL * beta[:, None] * A
     dGam[C - 1, :] += np.sum(k * dKt, 1)
-    R = np.tril(dGam * Gam, -1)
-    # d log alpha_m = sum_{t>=m} dgamma_t gamma_t + sum_{t>=m>i} R[t, i]
-    dlog = np.zeros(C)
-    suf = np.cumsum((dgamma * gamma)[::-1])[::-1]
+    # dalpha_m: the derivative of every running product with alpha_m left out,
+    #   d gamma_t / d alpha_m = gamma_{m-1} Gam[t, m]             (t >= m)
+    #   d Gam[t, i] / d alpha_m = Gam[m-1, i] Gam[t, m]          (i < m <= t)
+    # (no division by alpha: exact at alpha_m = 0)
+    dGs = np.tril(dGam, -1)
+    gprev = np.concatenate([[1.0], gamma[:-1]])
+    dalpha = np.zeros(C)
     for m in range(C):
-        dlog[m] = suf[m] + R[m:, :m].sum()
-    dalpha = dlog / alpha
+        r_m = np.sum(Gam[m:, m] * (dGs[m:, :m] @ Gam[m - 1, :m])) if m else 0.0
+        dalpha[m] = gprev[m] * np.sum(Gam[m:, m] * dgamma[m:]) + r_m
     return dq, dk, dv, dalpha, dbeta, dS

@@ -14,11 +14,25 @@ FWD_TOL = 2e-5
 GRAD_TOL = 1e-4
 
 
-def _check(orc, g, seed, B, T, H, dh, C, tag):
+def _extreme_gates(x, B, T):
+    # the gate patterns of test_gpu_delta.test_extreme_gates: exact zeros and
+    # 1e-6, a stretch of 0.005 (running products underflow), ones and 1.5
+    t = np.arange(B * T) % T
+    a = x.alpha.reshape(B * T, -1)
+    a[(t >= 16) & (t < 32)] = 0.005
+    a[(t >= 40) & (t < 44), 0] = 1.0
+    a[(t >= 44) & (t < 48)] = 1.5
+    a[t % 37 == 5] = 0.0
+    a[t % 11 == 3, -1] = 1e-6
+
+
+def _check(orc, g, seed, B, T, H, dh, C, tag, gates=None):
     from asca_amd.gpu import from_bf16, to_bf16
 
     print(f"[chunk] {tag} B={B} T={T} H={H} dh={dh} C={C}", flush=True)
     x = orc.DeltaInputs(seed, B, T, H, dh)
+    if gates is not None:
+        gates(x, B, T)
     qb, kb, vb, db_ = (to_bf16(a) for a in (x.q, x.k, x.v, x.d_o))
     q, k, v, d_o = (np.ascontiguousarray(from_bf16(a)) for a in (qb, kb, vb, db_))
     o_ref, dq, dk, dv, da, dbt = orc.delta_fwd_bwd(q, k, v, x.alpha, x.beta, d_o, B, T, H, dh)
@@ -50,3 +64,14 @@ def test_chunked_matches_recurrent(orc, g, B, T, H, dh, C):
 def test_chunked_config2_full_size(orc, g):
     # B=8, T=4096, H=16, dh=128, chunk 64, bf16 inputs, seed 0
     _check(orc, g, 0, 8, 4096, 16, 128, 64, "configs[2]")
+
+
+@pytest.mark.parametrize("B,T,H,dh,C", [
+    (2, 150, 2, 128, 64),   # fused C = 64, dh = 128 kernels, ragged last chunk
+    (2, 75, 3, 32, 16),     # decomposed path
+    (1, 100, 2, 64, 64),
+])
+def test_chunked_extreme_gates(orc, g, B, T, H, dh, C):
+    # dalpha takes every running product with alpha_m left out instead of
+    # dividing by alpha_m: finite and at the bar for alpha = 0 and 1e-6
+    _check(orc, g, 7 + dh, B, T, H, dh, C, "extreme gates", gates=_extreme_gates)

@@ -73,3 +73,23 @@ def test_chunked_against_the_c_oracle(orc):
     assert orc.rel_err(o, o_ref) <= 2e-6
     for g, ref in zip(co.bwd(cache, x.d_o), (dq, dk, dv, da, db)):
         assert orc.rel_err(g, ref) <= 1e-5
+
+
+def test_chunked_dalpha_at_zero_and_tiny_gates():
+    # dalpha from products with alpha_m left out (no division): finite at
+    # alpha = 0 and equal to autograd of the recurrence there
+    B, T, H, dh, C = 1, 48, 2, 8, 16
+    q, k, v, a, b, d_o = _inputs(5, B, T, H, dh)
+    t = np.arange(T)
+    a[t % 7 == 3] = 0.0
+    a[(t >= 20) & (t < 30), 0] = 1e-6
+    a[(t >= 32) & (t < 36), 1] = 1.5
+    o, cache = co.fwd(q, k, v, a, b, B, T, H, dh, C)
+    tt = [torch.tensor(x, requires_grad=True) for x in (q, k, v, a, b)]
+    o_ref = _recurrent_torch(*tt, B, T, H, dh)
+    (o_ref * torch.tensor(d_o)).sum().backward()
+    grads = co.bwd(cache, d_o)
+    assert all(np.isfinite(gr).all() for gr in grads)
+    for name, gr, ref in zip(("dq", "dk", "dv", "dalpha", "dbeta"), grads, tt):
+        r = ref.grad.numpy()
+        assert np.max(np.abs(gr - r)) <= 1e-10 * np.max(np.abs(r)), name
