@@ -141,19 +141,30 @@ ASCA_DEV void rd16(float (&x)[FR], const float* __restrict__ p) {
 }
 
 // The CK steps of a chunk for this lane's 16 rows (rust/src/delta.rs:289-314
-// per step).  Lane p of a column's quad keeps the raw o and S^T k of steps p,
-// p + 4, p + 8 and p + 12 in ho / hs.
+// per step), with the chunk's global stores spread over its steps: at the
+// checkpoint-wide rate of every wave a chunk's stores issued at once queue the
+// next chunk's loads behind them.  Steps 0..3 each store a quarter of the
+// checkpoint ck (the state before the chunk, as S^T) to ckdst; lane p of a
+// column's quad keeps the o and S^T k of step p + 4h and stores them after
+// step 4h + 3 (rows past nvalid go to the trash), except the last group's,
+// which it returns in last_o / last_sk (already rescaled) for the caller to
+// store once the next chunk's loads are queued: loads and stores complete in
+// order, and a load queued behind a fresh store waits for it.
 //   SC = false: s is the state; S <- alpha S + k u^T.
 //   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta (v / G_{j+1} - x) and
-//     s <- s + k (u / G_{j+1})^T (one FMA per element); o and S^T k leave scaled
-//     by 1/G_{j+1} and 1/G_j, and the caller rescales them.
+//     s <- s + k (u / G_{j+1})^T (one FMA per element); o and S^T k are
+//     rescaled by G_{j+1} and G_j at their store.
 template <bool SC>
 ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float* __restrict__ gt,
-                     const float (&vv)[CK], int p, float (&ho)[CK / 4], float (&hs)[CK / 4]) {
+                     const float (&vv)[CK], int p, const float (&ck)[FR], float* __restrict__ ckdst,
+                     float* __restrict__ od, float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr,
+                     float& last_o, float& last_sk) {
     const float* const kr = buf + F_K + fpad(16 * p);
     const float* const qr = buf + F_Q + fpad(16 * p);
     float kk[2][FR], qq[2][FR];
     float4 gg[2];
+    float2 gs = make_float2(1.0f, 1.0f);   // G_{jj+1}, G_jj of this lane's step jj = p + 4h
+    float ho = 0.0f, hs = 0.0f;
     rd16(kk[0], kr);
     rd16(qq[0], qr);
     gg[0] = *reinterpret_cast<const float4*>(gt);
@@ -165,6 +176,9 @@ ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float*
             rd16(qq[cs ^ 1], qr + (j + 1) * FROW);
             gg[cs ^ 1] = *reinterpret_cast<const float4*>(gt + (j + 1) * 8);
         }
+        if (SC && (j & 3) == 0) gs = *reinterpret_cast<const float2*>(gt + (p + j) * 8 + 4);
+        if (j < FR / 4)
+            *reinterpret_cast<float4*>(ckdst + 4 * j) = make_float4(ck[4 * j], ck[4 * j + 1], ck[4 * j + 2], ck[4 * j + 3]);
         // one wave per SIMD: nothing else hides LDS latency, so the reads of
         // step j + 1 stay at the top of step j, a whole step ahead of their use
         __builtin_amdgcn_sched_barrier(0);
@@ -199,8 +213,18 @@ ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float*
         }
         const float oo = group_sum<4>(o0 + o1);
         const bool mine = p == (j & 3);
-        ho[j >> 2] = mine ? oo : ho[j >> 2];
-        hs[j >> 2] = mine ? x : hs[j >> 2];
+        ho = mine ? oo : ho;
+        hs = mine ? x : hs;
+        if ((j & 3) == 3 && j + 1 < CK) {
+            const int jj = p + (j & ~3);
+            const bool ok = jj < nvalid;
+            *(ok ? od + jj * d : tr) = SC ? ho * gs.x : ho;
+            *(ok ? skd + jj * d : tr + 1) = SC ? hs * gs.y : hs;
+        }
+        if (j + 1 == CK) {
+            last_o = SC ? ho * gs.x : ho;
+            last_sk = SC ? hs * gs.y : hs;
+        }
     }
 }
 
@@ -236,44 +260,60 @@ __global__ __launch_bounds__(NT) void delta_fwd64_k(const float* __restrict__ q,
 #pragma unroll
     for (int m = 0; m < FR; ++m) s[m] = 0.0f;
 
-    FStage stg;
-    fstage_load<AL>(stg, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
-    bool sc_next = fstage_store(stg, lds, w, lane);
+    // Staged loads run two chunks ahead (the loads of chunk ci + 2 are queued
+    // at the start of chunk ci, into the register set that chunk ci + 1's data
+    // has just left for LDS), so each has two chunks of compute to arrive.
+    FStage sa, sb;
+    fstage_load<AL>(sa, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
+    bool sc_next = fstage_store(sa, lds, w, lane);
+    fstage_load<AL>(sa, min(1, nchunk - 1), q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
     lds_barrier();
 
-    for (int ci = 0; ci < nchunk; ++ci) {
+    // the last output group of the previous chunk, stored after this chunk's loads
+    float* pend_o = tr;
+    float* pend_sk = tr + 1;
+    float last_o = 0.0f, last_sk = 0.0f;
+    // chunk ci: `cur` holds chunk ci + 1 (stored to LDS at the end), `nxt` is
+    // loaded with chunk ci + 2
+    auto chunk = [&](int ci, FStage& cur, FStage& nxt) {
         const int t0 = ci * CK;
         const float* const buf = lds + (ci & 1) * F_BUF;
         const float* const gt = buf + F_G + w * CK * 8;
         const bool sc = sc_next;
-        fstage_load<AL>(stg, min(ci + 1, nchunk - 1), q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
-        store_state(ckb + (long)ci * DH2, s);   // checkpoint: S before step t0, as S^T
+        fstage_load<AL>(nxt, min(ci + 2, nchunk - 1), q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
+        *pend_o = last_o;
+        *pend_sk = last_sk;
         float vv[CK];
 #pragma unroll
         for (int j = 0; j < CK; ++j) vv[j] = buf[F_V + j * DH + col];
-        float ho[CK / 4], hs[CK / 4];
+        float ck[FR];   // the checkpoint: S before step t0
 #pragma unroll
-        for (int i = 0; i < CK / 4; ++i) ho[i] = hs[i] = 0.0f;
+        for (int m = 0; m < FR; ++m) ck[m] = s[m];
+        float* const od = o + ubase + (long)t0 * d + col;
+        float* const skd = sk_out + ubase + (long)t0 * d + col;
         if (sc) {
-            fsteps<true>(s, buf, gt, vv, p, ho, hs);
+            fsteps<true>(s, buf, gt, vv, p, ck, ckb + (long)ci * DH2, od, skd, d, T - t0, tr, last_o, last_sk);
             const float ge = gt[(CK - 1) * 8 + 4];
 #pragma unroll
             for (int m = 0; m < FR; ++m) s[m] *= ge;
         } else {
-            fsteps<false>(s, buf, gt, vv, p, ho, hs);
+            fsteps<false>(s, buf, gt, vv, p, ck, ckb + (long)ci * DH2, od, skd, d, T - t0, tr, last_o, last_sk);
         }
-#pragma unroll
-        for (int hh = 0; hh < CK / 4; ++hh) {
-            const int jj = p + 4 * hh;
-            const long t = t0 + jj;
-            const float2 gg = *reinterpret_cast<const float2*>(gt + jj * 8 + 4);   // G_{jj+1}, G_jj
-            const bool ok = t < T;
-            *(ok ? o + ubase + t * d + col : tr + 2 * hh) = ho[hh] * (sc ? gg.x : 1.0f);
-            *(ok ? sk_out + ubase + t * d + col : tr + 2 * hh + 1) = hs[hh] * (sc ? gg.y : 1.0f);
+        {
+            const int jj = p + CK - 4;
+            const bool ok = jj < T - t0;
+            pend_o = ok ? od + jj * d : tr;
+            pend_sk = ok ? skd + jj * d : tr + 1;
         }
-        sc_next = fstage_store(stg, lds + ((ci + 1) & 1) * F_BUF, w, lane);
+        sc_next = fstage_store(cur, lds + ((ci + 1) & 1) * F_BUF, w, lane);
         lds_barrier();
+    };
+    for (int ci = 0; ci < nchunk; ci += 2) {
+        chunk(ci, sa, sb);
+        if (ci + 1 < nchunk) chunk(ci + 1, sb, sa);
     }
+    *pend_o = last_o;
+    *pend_sk = last_sk;
     store_state(ckb + (long)nchunk * DH2, s);   // the state after step T-1
 }
 
@@ -309,7 +349,7 @@ struct BStage {
     float4 rq[2];    // two float4 of the segment's q or k rows
     float4 rw[3];    // the wave's dO, v, sk columns (192 float4 over 64 lanes)
     float4 rck[4];   // end-state tile: column colb + n, rows rowb + 4 hf .. (index 2n + hf)
-    float rab;       // lane j < CK: alpha of step j; CK <= j < 2CK: beta (1 and 0 past T)
+    float rab;       // lane j < CK: alpha of step j; CK <= j < 2CK: beta (as loaded)
     float rqk;       // the same lanes: |q|, |k| (fused backward)
 };
 
@@ -340,8 +380,10 @@ ASCA_DEV void bstage_load(BStage& st, int g, const float* __restrict__ q, const 
         const int gl = lane & (2 * CK - 1);
         const int t = t0 + (gl & (CK - 1));
         const long tc = min(t, T - 1);
-        const float x = (gl < CK ? alpha : beta)[gbase + tc * H];
-        st.rab = t < T ? x : (gl < CK ? 1.0f : 0.0f);
+        // raw values: bstage_store applies the padding past T, so these loads
+        // never turn into loads under a lane condition
+        (void)t;
+        st.rab = (gl < CK ? alpha : beta)[gbase + tc * H];
         st.rqk = FUSED ? (gl < CK ? qnorm : knorm)[gbase + tc * H] : 0.0f;
     }
     const float* const ce = ckb + (long)(g + 1) * DH2;   // the state after the segment
@@ -377,26 +419,33 @@ ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ n
     // Lanes j < CK hold alpha_j, lanes CK + j hold beta_j.
     // Lane j < CK writes alpha_j, G_{j+1}, 1/G_{j+1}, 1/alpha_j, |q_j| into row j;
     // lane CK + j writes beta_j, beta_j / G_{j+1}, |k_j| into row j.
+    // The callers (the scaled and the plain segment) both store here; without
+    // this opaque copy the compiler hoists the identical gate arithmetic of the
+    // two into the segment's start, right behind the loads it waits for.
+    float rab = st.rab, rqk = st.rqk;
+    asm volatile("" : "+v"(rab), "+v"(rqk));
     const bool w0 = w == 0;
     const bool ga = lane < CK;
     const bool gb = lane >= CK && lane < 2 * CK;
-    const float pr = prefix_prod<CK>(ga ? st.rab : 1.0f);   // lane j < CK: G_{j+1}
+    // steps past T: alpha = 1, beta = 0 leave the state unchanged
+    if (g * CK + (lane & (CK - 1)) >= T) rab = ga ? 1.0f : 0.0f;
+    const float pr = prefix_prod<CK>(ga ? rab : 1.0f);   // lane j < CK: G_{j+1}
     const float prb = __shfl(pr, lane & (CK - 1));           // lane CK + j: G_{j+1}
     float* const row = (w0 && (ga || gb)) ? nb + B_G + (lane & (CK - 1)) * 8 : sink;
     float* const rowa = (w0 && ga) ? row : sink;
-    row[ga ? 0 : 1] = st.rab;
-    row[ga ? 2 : 7] = ga ? pr : st.rab * __builtin_amdgcn_rcpf(prb);
-    row[ga ? 3 : 6] = ga ? __builtin_amdgcn_rcpf(pr) : st.rqk;
-    rowa[4] = __builtin_amdgcn_rcpf(st.rab);
-    rowa[5] = st.rqk;
+    row[ga ? 0 : 1] = rab;
+    row[ga ? 2 : 7] = ga ? pr : rab * __builtin_amdgcn_rcpf(prb);
+    row[ga ? 3 : 6] = ga ? __builtin_amdgcn_rcpf(pr) : rqk;
+    rowa[4] = __builtin_amdgcn_rcpf(rab);
+    rowa[5] = rqk;
     // The scaled walk runs backwards: stepping s_j back to s_{j-1} magnifies
     // rounding by 1/alpha_j, so over the segment by up to 1/prod(min(alpha, 1)).
     // It is taken when that product is at least 2^-8 and every alpha lies in
     // [2^-7, 2^7] (G within 2^+-112); other segments recompute their states
     // forwards.
-    const float pm = prefix_prod<CK>(ga ? fminf(st.rab, 1.0f) : 1.0f);
+    const float pm = prefix_prod<CK>(ga ? fminf(rab, 1.0f) : 1.0f);
     const float amp = readlane_f(pm, CK - 1);
-    const bool bad = ga && !(st.rab >= 0x1p-7f && st.rab <= 0x1p7f);
+    const bool bad = ga && !(rab >= 0x1p-7f && rab <= 0x1p7f);
     const bool in_range = __ballot(bad) == 0 && amp >= 0x1p-8f;
     *(w0 && lane == 0 ? nb + B_G + 8 * CK : sink + 3) = in_range ? 1.0f : 0.0f;
 }
@@ -642,8 +691,10 @@ ASCA_DEV void bsegment_plain(float (&ds)[BM][2], const BStage& stg, int g, int T
         // lanes < 32 hold dalpha pair sums, lanes >= 32 dbeta ones
         const float tot = add_xor16(group_sum<16>(pab));
         if ((lane & 31) == 0) buf[B_RAB + (jj * W + w) * 2 + (lane >> 5)] = tot;
-        if (jj == CK / 2) bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, cks, w, lane);
     }
+    // after the loop, not inside it under a condition: every path then provably
+    // waits for the staged loads here, and no later reuse of their registers does
+    bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, cks, w, lane);
 }
 
 template <bool FUSED, bool AL>
