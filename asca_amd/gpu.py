@@ -191,6 +191,24 @@ class MoeBwd:
         self.d_w1, self.d_b1, self.d_w2, self.d_b2, self.dxn = d_w1, d_b1, d_w2, d_b2, dxn
 
 
+class LogitsDev:
+    """Head logits kept on the device between the head forward and the
+    cross-entropy backward (rust/src/cuda/mod.rs:1398-1408): the (T x vocab)
+    logits and the (T x d) h_final that the d_head GEMM reads again."""
+
+    def __init__(self, logits: DevBuf, h_final: DevBuf, t_len: int, vocab: int, d: int):
+        self.logits, self.h_final = logits, h_final
+        self.t_len, self.vocab, self.d = t_len, vocab, d
+
+    def to_host(self) -> np.ndarray:
+        """The logits as a (T x vocab) host matrix (rust/src/cuda/mod.rs:1463-1471)."""
+        return self.logits.to_host((self.t_len, self.vocab))
+
+    def free(self) -> None:
+        self.logits.free()
+        self.h_final.free()
+
+
 def _mat(x, name, shape=None) -> np.ndarray:
     a = np.ascontiguousarray(x, dtype=_f32)
     if shape is not None and a.shape != tuple(shape):
@@ -379,6 +397,59 @@ class Gpu:
             return float(loss), bd.to_host((t_len, v))
         finally:
             for b in (bl, bt, bd, bs):
+                b.free()
+
+    # -- output head, logits resident ----------------------------------------
+    def head_forward_dev(self, h_final, head) -> LogitsDev:
+        """Gpu::head_forward_dev (rust/src/cuda/mod.rs:826-845): logits =
+        h_final @ head on the matrix cores, left on the device."""
+        h = _mat(h_final, "h_final")
+        t_len, d = h.shape
+        w = _mat(head, "head")
+        if w.shape[0] != d:
+            raise ValueError(f"head_forward_dev: head has {w.shape[0]} rows, h_final {d} columns")
+        v = w.shape[1]
+        dh, dw, dl = DevBuf.from_host(h), DevBuf.from_host(w), DevBuf(t_len * v * 4)
+        try:
+            _lib.call("asca_gemm", 0, 0, t_len, v, d, 1.0, _vp(dh), d, _vp(dw), v, 0.0, _vp(dl), v, None, None)
+            _lib.call("asca_sync")
+        except BaseException:
+            dh.free()
+            dl.free()
+            raise
+        finally:
+            dw.free()
+        return LogitsDev(dl, dh, t_len, v, d)
+
+    def head_bwd_dev(self, dev: LogitsDev, targets, head_t):
+        """Gpu::head_bwd_dev (rust/src/cuda/mod.rs:847-908): cross-entropy
+        backward on the resident logits, then d_head = h_final^T @ dlogits and
+        dh = dlogits @ head_t, dlogits never leaving the device.  Returns
+        (mean loss, d_head (d x vocab), dh (T x d)); the loss is the f32 sum
+        of the per-row losses times 1/T."""
+        t_len, v, d = dev.t_len, dev.vocab, dev.d
+        tg = np.ascontiguousarray(targets, dtype=np.uint32)
+        if tg.shape != (t_len,):
+            raise ValueError("head_bwd_dev: targets len must equal the logits rows")
+        ht = _mat(head_t, "head_t")
+        if ht.shape[0] != v:
+            raise ValueError("head_bwd_dev: head_t must be (vocab, d)")
+        if ht.shape[1] != d:
+            raise ValueError(f"head_bwd_dev: head_t has {ht.shape[1]} columns, h_final {d}")
+        bt, bht = DevBuf.from_array(tg), DevBuf.from_host(ht)
+        bdl, bls, bdw, bdh = DevBuf(t_len * v * 4), DevBuf(t_len * 4), DevBuf(d * v * 4), DevBuf(t_len * d * 4)
+        try:
+            _lib.call("asca_cross_entropy", _vp(dev.logits), _vp(bt), t_len, v, _vp(bdl), _vp(bls), None)
+            _lib.call("asca_gemm", 1, 0, d, v, t_len, 1.0, _vp(dev.h_final), d, _vp(bdl), v, 0.0, _vp(bdw), v,
+                      None, None)
+            _lib.call("asca_gemm", 0, 0, t_len, d, v, 1.0, _vp(bdl), v, _vp(bht), d, 0.0, _vp(bdh), d, None, None)
+            _lib.call("asca_sync")
+            losses = bls.to_host((t_len,))
+            inv_t = _f32(1.0) / _f32(t_len)
+            loss = (np.cumsum(losses, dtype=_f32)[-1] if t_len else _f32(0)) * inv_t
+            return float(loss), bdw.to_host((d, v)), bdh.to_host((t_len, d))
+        finally:
+            for b in (bt, bht, bdl, bls, bdw, bdh):
                 b.free()
 
     def gather_rows(self, src, idx):

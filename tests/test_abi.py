@@ -27,6 +27,60 @@ def test_library_exports_every_declared_symbol():
     assert set(_lib.SIGNATURES) == set(names)
 
 
+_C2RUST = {"int": "c_int", "long": "i64", "size_t": "usize", "float": "f32", "uint32_t": "u32", "uint64_t": "u64",
+           "int64_t": "i64", "int32_t": "i32", "uint16_t": "u16", "char": "c_char", "void": "c_void",
+           "asca_model": "AscaModel"}
+
+
+def _rust_type(c_type: str) -> str:
+    """The Rust FFI spelling of a C parameter / return type (sys.rs style)."""
+    t = c_type.strip()
+    const = t.startswith("const ")
+    if const:
+        t = t[len("const "):]
+    stars = t.count("*")
+    r = _C2RUST[t.replace("*", "").strip()]
+    if stars:
+        r = ("*const " if const else "*mut ") + r
+        r = "*mut " * (stars - 1) + r
+    return r
+
+
+def _header_prototypes():
+    text = (ROOT / "include" / "asca_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"ASCA_API\s+([\w\s\*]+?)\b(asca_\w+)\s*\(([^)]*)\)\s*;", text):
+        ret, params = " ".join(m.group(1).split()), m.group(3).strip()
+        types = []
+        for p in ([] if params in ("", "void") else params.split(",")):
+            p = " ".join(p.split())
+            types.append(_rust_type(p[: -len(re.search(r"(\w+)$", p).group(1))].replace(" *", "*")))
+        out[m.group(2)] = (types, "" if ret == "void" else _rust_type(ret))
+    return out
+
+
+def _integration_externs():
+    text = (ROOT / "INTEGRATION.md").read_text()
+    out = {}
+    for m in re.finditer(r"pub fn (asca_\w+)\s*\(([^)]*)\)\s*(?:->\s*([^;]+))?;", text):
+        types = [" ".join(p.split(":", 1)[1].split()) for p in m.group(2).split(",") if p.strip()]
+        out[m.group(1)] = (types, (m.group(3) or "").strip())
+    return out
+
+
+def test_integration_extern_blocks_match_the_header():
+    """The Rust extern blocks a maintainer pastes into the reference crate
+    (rust/src/hip/sys.rs, replacing rust/src/cuda/sys.rs) declare every entry
+    point of the header, each with the header's parameter and return types."""
+    hdr, rs = _header_prototypes(), _integration_externs()
+    assert set(hdr) == set(_header_symbols())
+    assert sorted(set(hdr) - set(rs)) == [], "entry points missing from INTEGRATION.md"
+    assert sorted(set(rs) - set(hdr)) == [], "INTEGRATION.md declares entry points the header lacks"
+    for name, proto in hdr.items():
+        assert rs[name] == proto, name
+
+
 def test_workspace_bytes_layout():
     from asca_amd import _lib
 

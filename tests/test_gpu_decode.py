@@ -55,6 +55,29 @@ def test_decode_config4_shape(orc, g):
     assert orc.rel_err(S_dev.to_host((n, H, dh, dh)), S_ref) <= 2e-5
 
 
+def test_decode_config4_all_steps(orc, g):
+    """configs[4] over its whole run: 512 sequences, H=16, dh=128, 256 steps,
+    seed 3, all decoded on the GPU; every 16th sequence is followed by the
+    oracle (the sequences are independent), its outputs at every step and its
+    states at the end."""
+    n, H, dh, steps = 512, 16, 128, 256
+    sub = np.arange(0, n, 16)
+    rng = np.random.default_rng(3)
+    S_ref = np.zeros((sub.size, H, dh, dh), dtype=np.float32)
+    S_dev = g.new_decode_states(n, H, dh)
+    worst = 0.0
+    for step in range(steps):
+        qkv, gate = _inputs(rng, n, H, dh)
+        o = g.delta_decode_step(S_dev, qkv, gate, H, dh)
+        o_ref = orc.delta_decode_step(S_ref, np.ascontiguousarray(qkv[sub]), np.ascontiguousarray(gate[sub]), H, dh)
+        worst = max(worst, orc.rel_err(o[sub], o_ref))
+        if step % 64 == 63:
+            print(f"[decode parity] configs[4] step {step + 1}/{steps}: worst o rel {worst:.2e}", flush=True)
+    assert worst <= 2e-5
+    S = S_dev.to_host((n, H, dh, dh))
+    assert orc.rel_err(S[sub], S_ref) <= 2e-5
+
+
 def test_decode_equals_forward_on_gpu(orc, g):
     # rust/tests/decode_parity.rs on the GPU path: token-by-token decode steps
     # reproduce the forward scan's outputs (rel <= 1e-4)

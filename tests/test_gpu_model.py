@@ -31,6 +31,7 @@ def _models(cfg, seed):
     ((256, 16, 2, 1, 2, 16), 1, 10),        # the reference's gradcheck_model shape
     ((256, 64, 4, 2, 8, 128), 2, 32),
     ((256, 512, 8, 1, 16, 1024), 2, 64),    # configs[3] widths, 128 tokens
+    ((256, 512, 8, 8, 16, 1024), 1, 1024),  # configs[3] at full depth and length, one of its 16 sequences
     ((200, 48, 3, 2, 5, 40), 3, 17),        # ragged: odd widths, dh 16, T not a multiple of 8
     ((256, 128, 4, 1, 4, 64), 3, 100),      # gate projection on the 16-column kernels with K = 128, 300 rows
     ((256, 256, 16, 1, 4, 64), 2, 20),      # 2H = 32 gate columns: the general GEMM

@@ -243,6 +243,36 @@ def test_hash_route_bit_exact(orc, g, n, E):
         np.testing.assert_array_equal(np.diff(off), [14, 20, 19, 17, 14, 18, 18, 20, 15, 15, 12, 19, 15, 13, 10, 17])
 
 
+@pytest.mark.parametrize("E", [2, 8, 16])
+def test_hash_route_replays_golden_ids(g, E):
+    """Token ids 0..4095 (beyond the byte vocabulary) against the golden
+    expert ids of hash_expert (rust/src/model.rs:70-77) in tests/golden."""
+    import json
+
+    from conftest import GOLDEN
+
+    gold = np.array(json.loads((GOLDEN / "hash.json").read_text())[str(E)], dtype=np.int32)
+    expert, perm, off = g.hash_route(np.arange(4096, dtype=np.uint32), E)
+    np.testing.assert_array_equal(expert, gold)
+    np.testing.assert_array_equal(np.diff(off), np.bincount(gold, minlength=E))
+    # counting-sort order: experts ascending, token order kept within an expert
+    np.testing.assert_array_equal(perm, np.argsort(gold, kind="stable"))
+
+
+@pytest.mark.parametrize("E", [16, 7, 256])
+def test_hash_route_full_range_ids(orc, g, E):
+    """Random ids over the whole u32 range, the top bits included."""
+    rng = np.random.default_rng(E)
+    ids = rng.integers(0, 2 ** 32, 100000, dtype=np.uint64).astype(np.uint32)
+    ids[:4] = [0, 1, 2 ** 31, 2 ** 32 - 1]
+    expert, perm, off = g.hash_route(ids, E)
+    ref = orc.hash_route(ids, E)
+    np.testing.assert_array_equal(expert, ref)
+    rperm, roff = orc.buckets(ref, E)
+    np.testing.assert_array_equal(off, roff)
+    np.testing.assert_array_equal(perm, rperm)
+
+
 @pytest.mark.parametrize("cols", [512, 37])
 def test_gather_scatter_bit_exact(g, cols):
     rng = np.random.default_rng(cols)
@@ -266,6 +296,52 @@ def test_cross_entropy(orc, g, T, V):
     rloss, rdl = orc.cross_entropy(logits, targets)
     assert abs(loss - rloss) <= FWD_TOL * max(1.0, abs(rloss))
     assert orc.rel_err(dl, rdl) <= GRAD_TOL
+
+
+@pytest.mark.parametrize("T,d,V", [(16384, 512, 256),   # configs[3]'s head
+                                   (512, 192, 12288),   # the reference's head gate (rust/src/main.rs:1058-1097)
+                                   (37, 20, 1000)])
+def test_head_resident(orc, g, T, d, V):
+    """head_forward_dev + head_bwd_dev (rust/src/cuda/mod.rs:826-908): the
+    logits stay on the device; loss, d_head and dh match the CPU path, and
+    the device path gives what the host path (logits downloaded, CE, two
+    GEMMs) gives on the same GPU, bit for bit where it runs the same kernels."""
+    rng = np.random.default_rng(T + d + V)
+    h = rng.uniform(-0.5, 0.5, (T, d)).astype(np.float32)
+    head = rng.uniform(-0.05, 0.05, (d, V)).astype(np.float32)
+    targets = rng.integers(0, V, T).astype(np.uint32)
+    print(f"[head] T={T} d={d} V={V}", flush=True)
+    dev = g.head_forward_dev(h, head)
+    try:
+        logits = dev.to_host()
+        loss, d_head, dh = g.head_bwd_dev(dev, targets, np.ascontiguousarray(head.T))
+    finally:
+        dev.free()
+    ref_logits = (h.astype(np.float64) @ head.astype(np.float64)).astype(np.float32)
+    assert orc.rel_err(logits, ref_logits) <= FWD_TOL
+    rloss, rdl = orc.cross_entropy(ref_logits, targets)
+    assert abs(loss - rloss) <= FWD_TOL * max(1.0, abs(rloss))
+    assert orc.rel_err(d_head, h.astype(np.float64).T @ rdl.astype(np.float64)) <= GRAD_TOL
+    assert orc.rel_err(dh, rdl.astype(np.float64) @ head.astype(np.float64).T) <= GRAD_TOL
+    # host path on the same logits: same CE kernel, same d_head GEMM
+    hloss, hdl = g.cross_entropy_bwd(logits, targets)
+    assert loss == hloss
+    np.testing.assert_array_equal(d_head, g.matmul_ta(h, hdl))
+    assert orc.rel_err(dh, g.matmul_t(hdl, head)) <= GRAD_TOL
+
+
+def test_head_bwd_dev_rejects_bad_shapes(g):
+    h = np.zeros((8, 4), np.float32)
+    dev = g.head_forward_dev(h, np.zeros((4, 6), np.float32))
+    try:
+        with pytest.raises(ValueError):
+            g.head_bwd_dev(dev, np.zeros(7, np.uint32), np.zeros((6, 4), np.float32))
+        with pytest.raises(ValueError):
+            g.head_bwd_dev(dev, np.zeros(8, np.uint32), np.zeros((4, 6), np.float32))
+    finally:
+        dev.free()
+    with pytest.raises(ValueError):
+        g.head_forward_dev(h, np.zeros((5, 6), np.float32))
 
 
 def test_adamw_bit_exact_over_steps(orc, g):
