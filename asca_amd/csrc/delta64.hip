@@ -15,18 +15,18 @@
 //    The k and q rows sit in LDS with row quarter p at float 20p, so the four
 //    distinct 16-byte addresses of a 16-lane read fall on four distinct bank
 //    groups.
-//  * Backward: lane (rg = lane & 7, cg = lane >> 3) holds rows 8rg..8rg+7 of
-//    columns 16w + 2cg, +1.  du = dS^T k is an 8-lane DPP sum; the column sums
-//    of dq and dk are transposed swap reductions (permlane32, permlane16, one DPP
-//    level) that leave every lane one whole row, written to LDS once per step.
-//    There is no register stash of recomputed states.  In a segment whose gates
-//    all lie in [2^-8, 2^8] the state is carried scaled, s_j = S_j / G_{j+1} with
-//    G_{j+1} = alpha_0 ... alpha_j of the segment, and that scaled state changes
-//    additively (s_j = s_{j-1} + k_j u~_j^T), so the walk starts from the state
-//    after the segment (the next checkpoint) and steps back with
-//    s_{j-1} = s_j - k_j u~_j^T: one FMA per element and step, no division by a
-//    gate.  A segment outside that range (zero, tiny or huge gates) recomputes
-//    every state it needs from the segment's first checkpoint instead.
+//  * Backward: lane (rg = lane & 7, cg = lane >> 3) holds the adjoint's rows
+//    8rg..8rg+7 of columns 16w + 2cg, +1, and a 16-step segment runs only the
+//    adjoint recurrence step by step: du = dS^T k is an 8-lane DPP sum and dS
+//    takes two rank-1 updates, 48 FMAs per lane and step.  Everything else is
+//    a product of 16-row matrices per segment, on the matrix cores (16x16x4 f32
+//    MFMA): dq and dk from the segment's first checkpoint, the adjoint at its
+//    top and the 16 x 16 step mixes u~ . dO~ and u~ . dsk~, dalpha from one
+//    exact <dS, S> at the segment's bottom carried up by per-step dot products
+//    (see bsegment_sc).  The products of inputs alone run interleaved with the
+//    steps.  A segment with a gate outside [2^-6, 2^6] (zero, tiny or huge
+//    values) runs the plain recurrence instead, recomputing every state it
+//    needs from its first checkpoint.
 #include "common.h"
 #include "delta.h"
 #include "runtime.h"
@@ -319,36 +319,59 @@ __global__ __launch_bounds__(NT) void delta_fwd64_k(const float* __restrict__ q,
 
 // ================================================================= backward
 
-constexpr int BM = 8;                       // rows per lane (two columns each)
-constexpr int BROW = 72;                    // padded q / k row: rows 32..63 shifted by 4 floats
-ASCA_DEV int bpad(int a) { return a + 4 * (a >> 5); }
-constexpr int RROW = 68;                    // reduction row buffer, same padding
-// Segment buffer (floats): per-step dq / dk row sums of each wave, the dalpha /
-// dbeta totals, the dv rows, the staged q and k rows, each wave's dO, v, sk
-// columns, the gate table (row j = alpha, beta, G_{j+1}, 1/G_{j+1}, 1/alpha,
-// |q|, |k|, beta/G_{j+1}) with the segment's range flag, and a sink.
-constexpr int B_RQ = 0;                          // [CK][W][RROW]
-constexpr int B_RK = B_RQ + CK * W * RROW;       // [CK][W][RROW]
-constexpr int B_RAB = B_RK + CK * W * RROW;      // [CK][W][2]
-constexpr int B_RV = B_RAB + CK * W * 2;         // [CK][DH]
-constexpr int B_Q = B_RV + CK * DH;              // [CK][BROW]
-constexpr int B_K = B_Q + CK * BROW;             // [CK][BROW]
-constexpr int B_W = B_K + CK * BROW;             // [W][CK][3][16]
-constexpr int B_G = B_W + W * CK * 48;           // [CK][8], flag at + 8 CK
-constexpr int B_SINK = B_G + 8 * CK + 4;
-constexpr int B_BUF = B_SINK + 8;
-static_assert(B_BUF % 4 == 0 && B_Q % 4 == 0 && B_W % 4 == 0 && B_G % 4 == 0, "float4 buffers");
-// After the two segment buffers: the next segment's end-state tile, 16 floats
-// per thread as [4][NT] float4.
-constexpr size_t B_LDS = (2 * (size_t)B_BUF + 16 * NT) * 4;
+constexpr int BM = 8;       // adjoint rows per lane (two columns each)
+constexpr int P = 68;       // LDS pitch of every 64-float row
+ASCA_DEV int rpad(int r) { return r + 4 * (r >> 5); }
+
+// k-order of a 64-float row for the 16x16x4 f32 MFMA: position 16 g + kb
+// holds column kcol(g, kb) = 16 (kb >> 2) + 4 g + (kb & 3).  Lane group g of an
+// MFMA then reads the 16 values it feeds as four 16-byte vectors, the strided
+// reads of a 64-row matrix by the four lane groups fall on disjoint banks, and
+// the columns 2c, 2c + 1 of the adjoint loop stay adjacent (one 8-byte access).
+ASCA_DEV int kpos(int i) { return 16 * ((i >> 2) & 3) + 4 * (i >> 4) + (i & 3); }
+ASCA_DEV int kcol(int g, int kb) { return 16 * (kb >> 2) + 4 * g + (kb & 3); }
+
+ASCA_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// Segment staging buffer (floats), written while the previous segment runs:
+constexpr int S_Q = 0;                   // [CK][P] q rows
+constexpr int S_K = S_Q + CK * P;        // [CK][P] k rows
+constexpr int S_DO = S_K + CK * P;       // [CK][P] dO, k-order (scaled segment: G_{j+1} dO_j)
+constexpr int S_U = S_DO + CK * P;       // [CK][P] u = beta (v - alpha sk), k-order (scaled: u_j / G_{j+1})
+constexpr int S_SK = S_U + CK * P;       // [CK][P] sk, k-order
+constexpr int S_WV = S_SK + CK * P;      // [CK][P] v - alpha sk, k-order
+constexpr int S_M = S_WV + CK * P;       // [DH][P] the state before the segment as S^T (row i = column i of S)
+constexpr int S_G = S_M + DH * P;        // [CK][8] gate table; the scaled-segment flag at S_G + 8 CK
+constexpr int S_SINK = S_G + 8 * CK + 4;
+constexpr int S_BUF = S_SINK + 12;
+// Work area after the two staging buffers.  A scaled segment uses:
+constexpr int W_XT = 0;                      // [DH][P] adjoint at the segment's top (scaled), row i = column i
+constexpr int W_DSK = W_XT + DH * P;         // [CK][P] G_j dsk_j, k-order
+constexpr int W_PP = W_DSK + CK * P;         // [W][CK][17] partial products u~ . dO~ over each wave's columns
+constexpr int W_RP = W_PP + W * CK * 17;     // [W][CK][17] partial products u~ . dsk~
+constexpr int W_DQ = W_RP + W * CK * 17;     // [CK][P] dq rows
+// a plain segment, over the same space: per-wave dq and dk row partials
+constexpr int W_RQ = 0;                      // [CK][W][P]
+constexpr int W_RK = CK * W * P;             // [CK][W][P]
+constexpr int W_DK = W_DQ + CK * P;          // [CK][P] dk rows
+constexpr int W_DU = W_DK + CK * P;          // [CK][P] du, k-order
+constexpr int W_AB = W_DU + CK * P;          // [CK][W][2] per-wave step sums (see the segment bodies)
+constexpr int W_QDQ = W_AB + CK * W * 2;     // [W][CK] per-wave partial q . dq
+constexpr int W_BR = W_QDQ + W * CK;         // [W] per-wave partial <dS, S> at the segment's bottom
+constexpr int W_END = W_BR + 8;
+static_assert(W_RK + CK * W * P == W_DK, "plain partials fill the scaled segment's space");
+static_assert(S_BUF % 4 == 0 && S_G % 4 == 0 && W_DQ % 4 == 0 && W_DU % 4 == 0, "16-byte rows");
+constexpr size_t B_LDS = (2 * (size_t)S_BUF + W_END) * 4;
 static_assert(B_LDS <= 160 * 1024, "backward LDS");
 
+// Gate rows (S_G + 8 j): alpha, beta, G_{j+1}, 1/G_{j+1}, 1/alpha, |q|, |k|.
+// Global -> registers for segment g; every lane loads (clamped addresses).
 // (vectors first: a scalar member ahead of the float4 array kept the compiler
 // from promoting the whole struct to registers)
 struct BStage {
     float4 rq[2];    // two float4 of the segment's q or k rows
-    float4 rw[3];    // the wave's dO, v, sk columns (192 float4 over 64 lanes)
-    float4 rck[4];   // end-state tile: column colb + n, rows rowb + 4 hf .. (index 2n + hf)
+    float4 rw[3];    // row j = tid / 16, floats 4 (tid % 16) .. + 3 of dO, v, sk
+    float4 rm[4];    // the state before the segment: S^T rows 16 e + tid / 16
     float rab;       // lane j < CK: alpha of step j; CK <= j < 2CK: beta (as loaded)
     float rqk;       // the same lanes: |q|, |k| (fused backward)
 };
@@ -359,7 +382,7 @@ ASCA_DEV void bstage_load(BStage& st, int g, const float* __restrict__ q, const 
                           const float* __restrict__ skv, const float* __restrict__ alpha,
                           const float* __restrict__ beta, const float* __restrict__ qnorm,
                           const float* __restrict__ knorm, const float* __restrict__ ckb, long ubase, long gbase,
-                          long d, int T, int H, int w, int lane, int rowb, int colb) {
+                          long d, int T, int H, int lane) {
     const int t0 = g * CK;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -368,97 +391,99 @@ ASCA_DEV void bstage_load(BStage& st, int g, const float* __restrict__ q, const 
         const long t = min(t0 + j, T - 1);
         st.rq[i] = ld4<AL>((tsr ? k : q) + ubase + t * d + 4 * c4);
     }
-    // tensor i: 0 dO, 1 v, 2 sk (the workspace's, always aligned)
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int j = lane >> 2, q4 = lane & 3;
-        const long t = min(t0 + j, T - 1);
-        const long o = ubase + t * d + 16 * w + 4 * q4;
-        st.rw[i] = i == 0 ? ld4<AL>(d_o + o) : (i == 1 ? ld4<AL>(v + o) : ld4<true>(skv + o));
+    {
+        const int j = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+        const long o = ubase + (long)min(t0 + j, T - 1) * d + 4 * c4;
+        st.rw[0] = ld4<AL>(d_o + o);
+        st.rw[1] = ld4<AL>(v + o);
+        st.rw[2] = ld4<true>(skv + o);   // the workspace's, always aligned
     }
     {
         const int gl = lane & (2 * CK - 1);
-        const int t = t0 + (gl & (CK - 1));
-        const long tc = min(t, T - 1);
+        const long tc = min(t0 + (gl & (CK - 1)), T - 1);
         // raw values: bstage_store applies the padding past T, so these loads
         // never turn into loads under a lane condition
-        (void)t;
         st.rab = (gl < CK ? alpha : beta)[gbase + tc * H];
         st.rqk = FUSED ? (gl < CK ? qnorm : knorm)[gbase + tc * H] : 0.0f;
     }
-    const float* const ce = ckb + (long)(g + 1) * DH2;   // the state after the segment
+    const float* const cs = ckb + (long)g * DH2;
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-            st.rck[2 * n + hf] = *reinterpret_cast<const float4*>(ce + (long)(colb + n) * DH + rowb + 4 * hf);
+    for (int e = 0; e < 4; ++e)
+        st.rm[e] = *reinterpret_cast<const float4*>(cs + (long)(16 * e + (threadIdx.x >> 4)) * DH +
+                                                    4 * (threadIdx.x & 15));
 }
 
-// Registers -> the buffer nb of segment g and this thread's end-state slot.
-// Every lane stores, lanes without an element into the sink, so no staged load
-// is ever moved down next to a conditional store.  Padded steps get dO = 0.
-ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ nb, float4* __restrict__ cks,
-                           int w, int lane) {
-    float* const sink = nb + B_SINK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cks[i * NT] = st.rck[i];
+// Registers -> the staging buffer nb of segment g.  Every wave derives the
+// gates, G_{j+1} and the segment's flag from its own copy of the gate loads.
+// Steps past T get alpha = 1, beta = 0 and dO = 0, which leave the adjoint
+// and every sum unchanged.
+ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ nb, int w, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int f = threadIdx.x + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
-        *reinterpret_cast<float4*>(nb + (tsr ? B_K : B_Q) + j * BROW + bpad(4 * c4)) = st.rq[i];
+        *reinterpret_cast<float4*>(nb + (tsr ? S_K : S_Q) + j * P + 4 * c4) = st.rq[i];
     }
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int j = lane >> 2, q4 = lane & 3;
-        float4 x = st.rw[i];
-        if (i == 0 && g * CK + j >= T) x = make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4*>(nb + B_W + ((w * CK + j) * 3 + i) * 16 + 4 * q4) = x;
-    }
-    // Gate table, written by wave 0 (the other waves compute into the sink).
-    // Lanes j < CK hold alpha_j, lanes CK + j hold beta_j.
-    // Lane j < CK writes alpha_j, G_{j+1}, 1/G_{j+1}, 1/alpha_j, |q_j| into row j;
-    // lane CK + j writes beta_j, beta_j / G_{j+1}, |k_j| into row j.
-    // The callers (the scaled and the plain segment) both store here; without
-    // this opaque copy the compiler hoists the identical gate arithmetic of the
-    // two into the segment's start, right behind the loads it waits for.
+    for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<float4*>(nb + S_M + (16 * e + (threadIdx.x >> 4)) * P + 4 * (threadIdx.x & 15)) =
+            st.rm[e];
+    // Both segment bodies store here; without this opaque copy the compiler
+    // hoists the identical gate arithmetic of the two into the segment's
+    // start, right behind the loads it waits for.
     float rab = st.rab, rqk = st.rqk;
     asm volatile("" : "+v"(rab), "+v"(rqk));
-    const bool w0 = w == 0;
     const bool ga = lane < CK;
     const bool gb = lane >= CK && lane < 2 * CK;
-    // steps past T: alpha = 1, beta = 0 leave the state unchanged
     if (g * CK + (lane & (CK - 1)) >= T) rab = ga ? 1.0f : 0.0f;
     const float pr = prefix_prod<CK>(ga ? rab : 1.0f);   // lane j < CK: G_{j+1}
-    const float prb = __shfl(pr, lane & (CK - 1));           // lane CK + j: G_{j+1}
-    float* const row = (w0 && (ga || gb)) ? nb + B_G + (lane & (CK - 1)) * 8 : sink;
+    // A segment is scaled when every alpha lies in [2^-6, 2^6]: G and 1/G stay
+    // within 2^+-96, and nothing divides by a gate but dalpha's final 1/alpha.
+    const bool bad = ga && !(rab >= 0x1p-6f && rab <= 0x1p6f);
+    const bool sc = __ballot(bad) == 0;
+    {
+        const int j = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+        const float aj = __shfl(rab, j), bj = __shfl(rab, CK + j), gj = __shfl(pr, j);
+        const float go = sc ? gj : 1.0f;
+        const float gu = sc ? __builtin_amdgcn_rcpf(gj) : 1.0f;
+        float4 x = st.rw[0];
+        const float s0 = g * CK + j < T ? go : 0.0f;
+        x = make_float4(x.x * s0, x.y * s0, x.z * s0, x.w * s0);
+        const float4 vv = st.rw[1], sk = st.rw[2];
+        const float4 wv = make_float4(fmaf(-aj, sk.x, vv.x), fmaf(-aj, sk.y, vv.y), fmaf(-aj, sk.z, vv.z),
+                                      fmaf(-aj, sk.w, vv.w));
+        const float bu = bj * gu;
+        const int o = j * P + kpos(4 * c4);
+        *reinterpret_cast<float4*>(nb + S_DO + o) = x;
+        *reinterpret_cast<float4*>(nb + S_U + o) = make_float4(bu * wv.x, bu * wv.y, bu * wv.z, bu * wv.w);
+        *reinterpret_cast<float4*>(nb + S_SK + o) = sk;
+        *reinterpret_cast<float4*>(nb + S_WV + o) = wv;
+    }
+    // gate table: wave 0, lane j < CK writes alpha_j, G_{j+1}, 1/G_{j+1},
+    // 1/alpha_j, |q_j| into row j; lane CK + j writes beta_j, |k_j|
+    float* const sink = nb + S_SINK;
+    const bool w0 = w == 0;
+    float* const row = (w0 && (ga || gb)) ? nb + S_G + (lane & (CK - 1)) * 8 : sink;
     float* const rowa = (w0 && ga) ? row : sink;
     row[ga ? 0 : 1] = rab;
-    row[ga ? 2 : 7] = ga ? pr : rab * __builtin_amdgcn_rcpf(prb);
-    row[ga ? 3 : 6] = ga ? __builtin_amdgcn_rcpf(pr) : rqk;
+    row[ga ? 5 : 6] = rqk;
+    rowa[2] = pr;
+    rowa[3] = __builtin_amdgcn_rcpf(pr);
     rowa[4] = __builtin_amdgcn_rcpf(rab);
-    rowa[5] = rqk;
-    // The scaled walk runs backwards: stepping s_j back to s_{j-1} magnifies
-    // rounding by 1/alpha_j, so over the segment by up to 1/prod(min(alpha, 1)).
-    // It is taken when that product is at least 2^-8 and every alpha lies in
-    // [2^-7, 2^7] (G within 2^+-112); other segments recompute their states
-    // forwards.
-    const float pm = prefix_prod<CK>(ga ? fminf(rab, 1.0f) : 1.0f);
-    const float amp = readlane_f(pm, CK - 1);
-    const bool bad = ga && !(rab >= 0x1p-7f && rab <= 0x1p7f);
-    const bool in_range = __ballot(bad) == 0 && amp >= 0x1p-8f;
-    *(w0 && lane == 0 ? nb + B_G + 8 * CK : sink + 3) = in_range ? 1.0f : 0.0f;
+    *(w0 && lane == 0 ? nb + S_G + 8 * CK : sink + 3) = sc ? 1.0f : 0.0f;
 }
 
+// Operands of one step of the adjoint loop for this lane: rows rowb .. rowb + 7
+// of q and k, and the lane's column pair (in k-order at kc) of dO, sk, v - alpha sk.
 struct BOps {
     float q[BM], k[BM];
-    float2 dO, v, sk;
-    float a, b, g1, r1, ia, cu;   // alpha, beta, G_{j+1}, 1/G_{j+1}, 1/alpha, beta/G_{j+1}
+    float2 dO, sk, wv;
+    float4 gt;   // alpha, beta, G_{j+1}, 1/G_{j+1}
 };
 
-ASCA_DEV void bops_read(BOps& o, const float* __restrict__ buf, int j, int w, int rowb, int cg) {
-    const float* const qr = buf + B_Q + j * BROW + bpad(rowb);
-    const float* const kr = buf + B_K + j * BROW + bpad(rowb);
+ASCA_DEV void bops_read(BOps& o, const float* __restrict__ buf, int j, int rowb, int kc) {
+    const float* const qr = buf + S_Q + j * P + rowb;
+    const float* const kr = buf + S_K + j * P + rowb;
 #pragma unroll
     for (int e = 0; e < BM; e += 4) {
         const float4 x = *reinterpret_cast<const float4*>(qr + e);
@@ -466,18 +491,10 @@ ASCA_DEV void bops_read(BOps& o, const float* __restrict__ buf, int j, int w, in
         o.q[e] = x.x; o.q[e + 1] = x.y; o.q[e + 2] = x.z; o.q[e + 3] = x.w;
         o.k[e] = y.x; o.k[e + 1] = y.y; o.k[e + 2] = y.z; o.k[e + 3] = y.w;
     }
-    const float* const sw = buf + B_W + (w * CK + j) * 48 + 2 * cg;
-    o.dO = *reinterpret_cast<const float2*>(sw);
-    o.v = *reinterpret_cast<const float2*>(sw + 16);
-    o.sk = *reinterpret_cast<const float2*>(sw + 32);
-    const float4 g0 = *reinterpret_cast<const float4*>(buf + B_G + 8 * j);
-    const float4 g1 = *reinterpret_cast<const float4*>(buf + B_G + 8 * j + 4);
-    o.a = g0.x;
-    o.b = g0.y;
-    o.g1 = g0.z;
-    o.r1 = g0.w;
-    o.ia = g1.x;
-    o.cu = g1.w;
+    o.dO = *reinterpret_cast<const float2*>(buf + S_DO + j * P + kc);
+    o.sk = *reinterpret_cast<const float2*>(buf + S_SK + j * P + kc);
+    o.wv = *reinterpret_cast<const float2*>(buf + S_WV + j * P + kc);
+    o.gt = *reinterpret_cast<const float4*>(buf + S_G + 8 * j);
 }
 
 // Column sums over the eight column groups of a wave (lane bits 3..5) of the
@@ -492,180 +509,256 @@ ASCA_DEV float colsum8(const float (&p)[BM], int lane) {
     return keep + dpp<DPP_ROW_ROR8>(send);
 }
 
-ASCA_DEV int rpad(int r) { return r + 4 * (r >> 5); }
-
-// One reverse step for this lane's 8 x 2 tile (rust/src/delta.rs:485-572 per
-// element).  sa: the state after the step; sm: the state before it.
-//   SC = true: sa = S_j / G_{j+1}, sm = S_{j-1} / G_j, ds = G_{j+1} dS; the step
-//     derives sm from sa in place (s) and every output term takes its scale from
-//     the gate row.
-//   SC = false: s holds S_j on entry, sm is given, ds = dS.
-//   first: the step is the first of its sequence, whose previous state is
-//     exactly zero (the scaled walk would leave rounding residue there).
-template <bool SC>
-ASCA_DEV void bstep(const BOps& in, float (&s)[BM][2], const float (&smp)[BM][2], float (&ds)[BM][2],
-                    float* __restrict__ rq, float* __restrict__ rk, float* __restrict__ rv, float& pab_out,
-                    int lane, int rg, int colb, bool first = false) {
-    float dO0 = in.dO.x, dO1 = in.dO.y;
-    if constexpr (SC) {
-        dO0 *= in.g1;
-        dO1 *= in.g1;
+// du of a step: the lane's column pair, written by the lanes of row group 0
+// (du) and, with DSK, 1 (G_j dsk) to their rows; a ds_write under a lane
+// condition is an LDS access, which no global wait depends on.
+template <bool DSK>
+ASCA_DEV void put_du(float* __restrict__ wk, int j, int kc, int rg, float du0, float du1, float sh0, float sh1) {
+    if (rg < (DSK ? 2 : 1)) {
+        const float2 x = rg == 0 ? make_float2(du0, du1) : make_float2(sh0, sh1);
+        *reinterpret_cast<float2*>(wk + (rg == 0 ? W_DU : W_DSK) + j * P + kc) = x;
     }
-    // dS += q dO^T  (delta.rs:508-511)
+}
+
+// One step of the scaled adjoint loop (rust/src/delta.rs:508-563 for the
+// adjoint only).  ds = G_{j+1} dS_j with dS_j excluding q_j dO_j^T on entry:
+//   ds += q_j (G_{j+1} dO_j)^T;  t = ds^T k_j = G_{j+1} du_j;
+//   G_j dsk_j = -beta_j t;        ds += k_j (G_j dsk_j)^T  (= G_j dS_{j-1} part).
+// Returns the lane's transposed (ea, eb) pair of the step: ea = -beta du.sk,
+// eb = du.(v - alpha sk) over the lane's columns (row group 0 only).
+ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ wk, int j, int kc, int rg) {
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
-        ds[m][0] = fmaf(in.q[m], dO0, ds[m][0]);
-        ds[m][1] = fmaf(in.q[m], dO1, ds[m][1]);
+        ds[m][0] = fmaf(in.q[m], in.dO.x, ds[m][0]);
+        ds[m][1] = fmaf(in.q[m], in.dO.y, ds[m][1]);
     }
-    // du = dS^T k  (delta.rs:536-542): 8-lane butterfly over the row groups
     float c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
         c0 = fmaf(ds[m][0], in.k[m], c0);
         c1 = fmaf(ds[m][1], in.k[m], c1);
     }
-    const float dt0 = group_sum<8>(c0), dt1 = group_sum<8>(c1);
-    const float du0 = SC ? dt0 * in.r1 : dt0, du1 = SC ? dt1 * in.r1 : dt1;
-    const float wv0 = fmaf(-in.a, in.sk.x, in.v.x), wv1 = fmaf(-in.a, in.sk.y, in.v.y);
-    // uh: the u that multiplies dS (u~ = u / G_{j+1} when scaled); sh: the dsk
-    // that multiplies S_{j-1} and updates dS (G_j dsk when scaled)
-    const float cu = SC ? in.cu : in.b;
-    const float uh0 = cu * wv0, uh1 = cu * wv1;
-    const float cs = SC ? -in.b : -in.b * in.a;
-    const float sh0 = cs * dt0, sh1 = cs * dt1;
-    // dv = beta du  (delta.rs:550), one LDS row per step
-    if (rg == 0) *reinterpret_cast<float2*>(rv + colb) = make_float2(in.b * du0, in.b * du1);
-
-    // dq = S_j dO  (delta.rs:504-507)
-    float pq[BM], pk[BM];
-#pragma unroll
-    for (int m = 0; m < BM; ++m) pq[m] = fmaf(s[m][1], dO1, s[m][0] * dO0);
-    if constexpr (SC) {
-        // back one step: s = S_{j-1} / G_j
-#pragma unroll
-        for (int m = 0; m < BM; ++m) {
-            s[m][0] = fmaf(-in.k[m], uh0, s[m][0]);
-            s[m][1] = fmaf(-in.k[m], uh1, s[m][1]);
-        }
-        if (first) {
-#pragma unroll
-            for (int m = 0; m < BM; ++m) s[m][0] = s[m][1] = 0.0f;
-        }
-    }
-    // sm: S_{j-1} (scaled: the caller passes s itself, now stepped back)
-    const float (&sm)[BM][2] = smp;
-    //   dk = dS u + S_{j-1} dsk    (delta.rs:532-534, 556-558)
-    //   dalpha = <dS, S_{j-1}> - beta du.sk ; dbeta = du.(v - alpha sk)   (:530, 548-553)
-    float pa0 = 0.0f, pa1 = 0.0f;
+    const float t0 = group_sum<8>(c0), t1 = group_sum<8>(c1);
+    const float du0 = t0 * in.gt.w, du1 = t1 * in.gt.w;
+    const float sh0 = -in.gt.y * t0, sh1 = -in.gt.y * t1;
+    put_du<true>(wk, j, kc, rg, du0, du1, sh0, sh1);
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
-        float x = uh0 * ds[m][0];
-        x = fmaf(uh1, ds[m][1], x);
-        x = fmaf(sh0, sm[m][0], x);
-        pk[m] = fmaf(sh1, sm[m][1], x);
-        pa0 = fmaf(ds[m][0], sm[m][0], pa0);
-        pa1 = fmaf(ds[m][1], sm[m][1], pa1);
+        ds[m][0] = fmaf(in.k[m], sh0, ds[m][0]);
+        ds[m][1] = fmaf(in.k[m], sh1, ds[m][1]);
     }
-    const float ea = -in.b * fmaf(du1, in.sk.y, du0 * in.sk.x);
-    const float eb = fmaf(du1, wv1, du0 * wv0);
-    const float pab = SC ? (pa0 + pa1) * in.ia : pa0 + pa1;
-    const float pa = pab + (rg == 0 ? ea : 0.0f);
-    const float pb = rg == 0 ? eb : 0.0f;
-    // dS <- alpha dS + k dsk^T  (delta.rs:543-545, 559-563)
-#pragma unroll
-    for (int m = 0; m < BM; ++m) {
-        if constexpr (SC) {
-            ds[m][0] = fmaf(in.k[m], sh0, ds[m][0]);
-            ds[m][1] = fmaf(in.k[m], sh1, ds[m][1]);
-        } else {
-            ds[m][0] = in.a * ds[m][0] + in.k[m] * sh0;
-            ds[m][1] = in.a * ds[m][1] + in.k[m] * sh1;
-        }
-    }
-    const int r = rpad(8 * (lane & 7) + (lane >> 3));
-    rq[r] = colsum8(pq, lane);
-    rk[r] = colsum8(pk, lane);
-    pab_out = tsum32(pa, pb);
+    const float ea = rg == 0 ? -in.gt.y * fmaf(du1, in.sk.y, du0 * in.sk.x) : 0.0f;
+    const float eb = rg == 0 ? fmaf(du1, in.wv.y, du0 * in.wv.x) : 0.0f;
+    return tsum32(ea, eb);
 }
 
-// S_{j} from S_{j-1} (rust/src/delta.rs:299-306), for the recompute of a plain
-// segment.
-ASCA_DEV void fwd_update(float (&x)[BM][2], const float* __restrict__ buf, int j, int w, int rowb, int cg) {
-    const float* const kr = buf + B_K + j * BROW + bpad(rowb);
-    const float* const sw = buf + B_W + (w * CK + j) * 48 + 2 * cg;
-    const float2 vv = *reinterpret_cast<const float2*>(sw + 16);
-    const float2 sk = *reinterpret_cast<const float2*>(sw + 32);
-    const float a = buf[B_G + 8 * j], bt = buf[B_G + 8 * j + 1];
-    const float u0 = bt * (vv.x - a * sk.x), u1 = bt * (vv.y - a * sk.y);
+// One scaled segment (every alpha in [2^-6, 2^6]).  With G_j the product of the
+// segment's alpha before step j, S the state before the segment, u~_j = u_j /
+// G_{j+1}, dO~_j = G_{j+1} dO_j, dsk~_j = G_j dsk_j and X~ the scaled adjoint
+// entering at the top, every output of the segment is a sum of 16-row matrix
+// products (rows j):
+//   dq = dO~ S^T + (M_le o P^T) K
+//   dk = dsk~ S^T + U~ X~^T + (M_ge o P) Q + (lower(R^T) + upper(R)) K
+// with P = U~ dO~^T and R = U~ dsk~^T (strict lower / upper parts), and
+//   dalpha_j = br_j / alpha_j - beta_j du_j.sk_j,
+//   br_j = <dS_out, S> - dsk_0.sk_0 + sum_{l<j} (u_l.du_l - q_l.dq_l - dsk_{l+1}.sk_{l+1}),
+// the scaled <dS_j, S_{j-1}> carried from the exact product at the bottom.  Only
+// the adjoint recurrence runs step by step (on the VALU); the products run on
+// the matrix cores, those of inputs alone interleaved with the steps.  Wave w
+// computes the dq / dk columns 16 w .. 16 w + 15 of every step; the products
+// over the columns (P, R) are summed from per-wave partials.
+ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, const float* __restrict__ buf,
+                          float* __restrict__ nb, float* __restrict__ wk, int w, int lane, int rg, int cg,
+                          int rowb, int kc) {
+    const int jr = lane & 15, gq = lane >> 4;
+    // products of inputs alone: dO~ S^T, U~ X~^T and the partial P
+    float a_do[16], a_u[16], b_s[16], b_x[16], p_u[4], p_d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float4 x = *reinterpret_cast<const float4*>(buf + S_DO + jr * P + 16 * gq + 4 * e);
+        const float4 y = *reinterpret_cast<const float4*>(buf + S_U + jr * P + 16 * gq + 4 * e);
+        a_do[4 * e] = x.x; a_do[4 * e + 1] = x.y; a_do[4 * e + 2] = x.z; a_do[4 * e + 3] = x.w;
+        a_u[4 * e] = y.x; a_u[4 * e + 1] = y.y; a_u[4 * e + 2] = y.z; a_u[4 * e + 3] = y.w;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 16; ++kb) {
+        b_s[kb] = buf[S_M + kcol(gq, kb) * P + 16 * w + jr];
+        b_x[kb] = wk[W_XT + kcol(gq, kb) * P + 16 * w + jr];
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        p_u[kb] = buf[S_U + jr * P + 16 * kb + 4 * w + gq];
+        p_d[kb] = buf[S_DO + jr * P + 16 * kb + 4 * w + gq];
+    }
+    f32x4 adq = {0.f, 0.f, 0.f, 0.f}, adk = adq, ap = adq;
+    float pab[CK];
+    BOps op[2];
+    bops_read(op[(CK - 1) & 1], buf, CK - 1, rowb, kc);
+#pragma unroll
+    for (int jj = CK - 1; jj >= 0; --jj) {
+        if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, rowb, kc);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kb = CK - 1 - jj;
+        adq = mfma4(a_do[kb], b_s[kb], adq);
+        adk = mfma4(a_u[kb], b_x[kb], adk);
+        if (kb < 4) ap = mfma4(p_u[kb], p_d[kb], ap);
+        pab[jj] = bstep_sc(op[jj & 1], ds, wk, jj, kc, rg);
+        if (jj == CK / 2) {
+            // the staged operands of the next segment (loads issued at this
+            // segment's start) go to its buffer; the fence keeps the scheduler
+            // from hoisting the stores, and their wait, to the segment's start
+            __builtin_amdgcn_sched_barrier(0);
+            bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, w, lane);
+        }
+    }
+    // ds = dS_{-1} without q_{-1} dO_{-1}^T (G_0 = 1): its product with S
+    {
+        float x = 0.0f;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int e = 0; e < BM; e += 4) {
+                const float4 s = *reinterpret_cast<const float4*>(buf + S_M + (16 * w + 2 * cg + n) * P + rowb + e);
+                x = fmaf(ds[e][n], s.x, x);
+                x = fmaf(ds[e + 1][n], s.y, x);
+                x = fmaf(ds[e + 2][n], s.z, x);
+                x = fmaf(ds[e + 3][n], s.w, x);
+            }
+        x = wave_sum(x);
+        if (lane == 0) wk[W_BR + w] = x;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wk[W_PP + (w * CK + 4 * gq + r) * 17 + jr] = ap[r];
+    cross_step_sum<CK, W>(pab, wk + W_AB, w, lane);
+    lds_barrier();   // dsk~, du, the partial P and the step sums of every wave
+
+    // products with dsk~: dsk~ S^T and the partial R
+    {
+        float r_u[4], r_d[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            r_u[kb] = buf[S_U + jr * P + 16 * kb + 4 * w + gq];
+            r_d[kb] = wk[W_DSK + jr * P + 16 * kb + 4 * w + gq];
+        }
+        f32x4 ar = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) ar = mfma4(r_u[kb], r_d[kb], ar);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wk[W_RP + (w * CK + 4 * gq + r) * 17 + jr] = ar[r];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float4 x = *reinterpret_cast<const float4*>(wk + W_DSK + jr * P + 16 * gq + 4 * e);
+            adk = mfma4(x.x, buf[S_M + kcol(gq, 4 * e) * P + 16 * w + jr], adk);
+            adk = mfma4(x.y, buf[S_M + kcol(gq, 4 * e + 1) * P + 16 * w + jr], adk);
+            adk = mfma4(x.z, buf[S_M + kcol(gq, 4 * e + 2) * P + 16 * w + jr], adk);
+            adk = mfma4(x.w, buf[S_M + kcol(gq, 4 * e + 3) * P + 16 * w + jr], adk);
+        }
+    }
+    lds_barrier();   // every wave's partial R
+
+    // the 16 x 16 step mixes: k = 4 kb + gq, row j = jr
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const int kk = 4 * kb + gq;
+        float pkj = 0.0f, pjk = 0.0f, rkj = 0.0f, rjk = 0.0f;
+#pragma unroll
+        for (int u4 = 0; u4 < W; ++u4) {
+            pkj += wk[W_PP + (u4 * CK + kk) * 17 + jr];
+            pjk += wk[W_PP + (u4 * CK + jr) * 17 + kk];
+            rkj += wk[W_RP + (u4 * CK + kk) * 17 + jr];
+            rjk += wk[W_RP + (u4 * CK + jr) * 17 + kk];
+        }
+        const float bk = buf[S_K + kk * P + 16 * w + jr];
+        const float bq = buf[S_Q + kk * P + 16 * w + jr];
+        adq = mfma4(kk <= jr ? pkj : 0.0f, bk, adq);
+        adk = mfma4(kk >= jr ? pjk : 0.0f, bq, adk);
+        adk = mfma4(kk < jr ? rkj : (kk > jr ? rjk : 0.0f), bk, adk);
+    }
+    // dq, dk rows and the partial q . dq of the wave's columns
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int j = 4 * gq + r;
+        wk[W_DQ + j * P + 16 * w + jr] = adq[r];
+        wk[W_DK + j * P + 16 * w + jr] = adk[r];
+        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + 16 * w + jr]);
+        if (jr == 0) wk[W_QDQ + w * CK + j] = x;
+    }
+}
+
+// Plain forms for a segment with some gate outside [2^-6, 2^6] (zeros, tiny or
+// huge values): every state the steps need is recomputed forwards from the
+// segment's first checkpoint, so no gate is ever divided by.
+ASCA_DEV void fwd_update(float (&x)[BM][2], const float* __restrict__ buf, int j, int rowb, int kc) {
+    const float* const kr = buf + S_K + j * P + rowb;
+    const float2 u = *reinterpret_cast<const float2*>(buf + S_U + j * P + kc);
+    const float a = buf[S_G + 8 * j];
 #pragma unroll
     for (int e = 0; e < BM; e += 4) {
         const float4 kk = *reinterpret_cast<const float4*>(kr + e);
         const float km[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            x[e + i][0] = a * x[e + i][0] + km[i] * u0;
-            x[e + i][1] = a * x[e + i][1] + km[i] * u1;
+            x[e + i][0] = a * x[e + i][0] + km[i] * u.x;
+            x[e + i][1] = a * x[e + i][1] + km[i] * u.y;
         }
     }
 }
 
-// One scaled segment in reverse (every gate of the segment in [2^-8, 2^8]).
-// se: this thread's tile of the state after the segment; ds enters and leaves
-// unscaled.  The next segment's staged operands are stored into nb halfway.
-ASCA_DEV void bsegment_sc(const float (&se)[BM][2], float (&ds)[BM][2], const BStage& stg, int g, int T,
-                          float* __restrict__ buf, float* __restrict__ nb, float4* __restrict__ cks, int w,
-                          int lane, int rg, int cg, int rowb, int colb) {
-    float s[BM][2];
-    const float rend = buf[B_G + 8 * (CK - 1) + 3];   // 1 / G_CK
-    const float gend = buf[B_G + 8 * (CK - 1) + 2];   // G_CK
+// One plain reverse step for this lane's 8 x 2 tile (rust/src/delta.rs:485-572
+// per element); s = S_j, sm = S_{j-1}, ds = dS_j without q_j dO_j^T on entry.
+// Writes the wave's dq / dk row partials and du; returns the lane's transposed
+// (dalpha, dbeta) pair partial.
+ASCA_DEV float bstep_plain(const BOps& in, const float (&s)[BM][2], const float (&sm)[BM][2], float (&ds)[BM][2],
+                           const float2 u, float* __restrict__ wk, int j, int w, int lane, int rg, int kc) {
+    const float a = in.gt.x, b = in.gt.y;
+    float pq[BM], pk[BM];
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
-        s[m][0] = se[m][0] * rend;
-        s[m][1] = se[m][1] * rend;
-        ds[m][0] *= gend;
-        ds[m][1] *= gend;
+        pq[m] = fmaf(s[m][1], in.dO.y, s[m][0] * in.dO.x);
+        ds[m][0] = fmaf(in.q[m], in.dO.x, ds[m][0]);
+        ds[m][1] = fmaf(in.q[m], in.dO.y, ds[m][1]);
     }
-    float pab[CK];
-    BOps op[2];
-    bops_read(op[(CK - 1) & 1], buf, CK - 1, w, rowb, cg);
+    float c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
-    for (int jj = CK - 1; jj >= 0; --jj) {
-        if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, w, rowb, cg);
-        // the operand reads of the next step stay a whole step ahead of their use
-        __builtin_amdgcn_sched_barrier(0);
-        bstep<true>(op[jj & 1], s, s, ds, buf + B_RQ + jj * W * RROW + w * RROW,
-                    buf + B_RK + jj * W * RROW + w * RROW, buf + B_RV + jj * DH, pab[jj], lane, rg, colb,
-                    jj == 0 && g == 0);
-        if (jj == CK / 2) {
-            // the staged operands of the next segment (loads issued at this
-            // segment's start) go to its buffer; the fence keeps the scheduler
-            // from hoisting the stores, and their wait, to the segment's start
-            __builtin_amdgcn_sched_barrier(0);
-            bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, cks, w, lane);
-        }
+    for (int m = 0; m < BM; ++m) {
+        c0 = fmaf(ds[m][0], in.k[m], c0);
+        c1 = fmaf(ds[m][1], in.k[m], c1);
     }
-    cross_step_sum<CK, W>(pab, buf + B_RAB, w, lane);
+    const float du0 = group_sum<8>(c0), du1 = group_sum<8>(c1);
+    const float dk0 = -a * b * du0, dk1 = -a * b * du1;
+    put_du<false>(wk, j, kc, rg, du0, du1, 0.0f, 0.0f);
+    float pa0 = 0.0f, pa1 = 0.0f;
+#pragma unroll
+    for (int m = 0; m < BM; ++m) {
+        float x = u.x * ds[m][0];
+        x = fmaf(u.y, ds[m][1], x);
+        x = fmaf(dk0, sm[m][0], x);
+        pk[m] = fmaf(dk1, sm[m][1], x);
+        pa0 = fmaf(ds[m][0], sm[m][0], pa0);
+        pa1 = fmaf(ds[m][1], sm[m][1], pa1);
+        ds[m][0] = a * ds[m][0] + in.k[m] * dk0;
+        ds[m][1] = a * ds[m][1] + in.k[m] * dk1;
+    }
+    const float ea = -b * fmaf(du1, in.sk.y, du0 * in.sk.x);
+    const float eb = fmaf(du1, in.wv.y, du0 * in.wv.x);
+    const int r = rpad(8 * (lane & 7) + (lane >> 3));
+    wk[W_RQ + (j * W + w) * P + r] = colsum8(pq, lane);
+    wk[W_RK + (j * W + w) * P + r] = colsum8(pk, lane);
+    return tsum32(pa0 + pa1 + (rg == 0 ? ea : 0.0f), rg == 0 ? eb : 0.0f);
 }
 
-// One plain segment in reverse (some gate of the segment outside [2^-8, 2^8]:
-// zeros, tiny or huge values).  Each step recomputes S_{j-1} and S_j from the
-// segment's first checkpoint, so no division by a gate occurs; a rolled loop,
-// since these segments are rare and their registers must not raise the
-// kernel's budget.
-ASCA_DEV void bsegment_plain(float (&ds)[BM][2], const BStage& stg, int g, int T, float* __restrict__ buf,
-                             float* __restrict__ nb, float4* __restrict__ cks, const float* __restrict__ ckb,
-                             int w, int lane, int rg, int cg, int rowb, int colb) {
+// A plain segment in reverse: a rolled loop, since these segments are rare and
+// their registers must not raise the kernel's budget.
+ASCA_DEV void bsegment_plain(float (&ds)[BM][2], const BStage& stg, int g, int T, const float* __restrict__ buf,
+                             float* __restrict__ nb, float* __restrict__ wk, int w, int lane, int rg, int cg,
+                             int rowb, int kc) {
     float st0[BM][2];
-    const float* const cs = ckb + (long)g * DH2;
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const float4 x = *reinterpret_cast<const float4*>(cs + (long)(colb + n) * DH + rowb + 4 * hf);
-            st0[4 * hf][n] = x.x;
-            st0[4 * hf + 1][n] = x.y;
-            st0[4 * hf + 2][n] = x.z;
-            st0[4 * hf + 3][n] = x.w;
+        for (int e = 0; e < BM; e += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(buf + S_M + (16 * w + 2 * cg + n) * P + rowb + e);
+            st0[e][n] = x.x; st0[e + 1][n] = x.y; st0[e + 2][n] = x.z; st0[e + 3][n] = x.w;
         }
 #pragma nounroll
     for (int jj = CK - 1; jj >= 0; --jj) {
@@ -676,25 +769,24 @@ ASCA_DEV void bsegment_plain(float (&ds)[BM][2], const BStage& stg, int g, int T
             sm[m][1] = st0[m][1];
         }
 #pragma nounroll
-        for (int i = 0; i < jj; ++i) fwd_update(sm, buf, i, w, rowb, cg);
+        for (int i = 0; i < jj; ++i) fwd_update(sm, buf, i, rowb, kc);
 #pragma unroll
         for (int m = 0; m < BM; ++m) {
             s[m][0] = sm[m][0];
             s[m][1] = sm[m][1];
         }
-        fwd_update(s, buf, jj, w, rowb, cg);
+        fwd_update(s, buf, jj, rowb, kc);
         BOps op;
-        bops_read(op, buf, jj, w, rowb, cg);
-        float pab;
-        bstep<false>(op, s, sm, ds, buf + B_RQ + jj * W * RROW + w * RROW, buf + B_RK + jj * W * RROW + w * RROW,
-                     buf + B_RV + jj * DH, pab, lane, rg, colb);
+        bops_read(op, buf, jj, rowb, kc);
+        const float2 u = *reinterpret_cast<const float2*>(buf + S_U + jj * P + kc);
+        const float pab = bstep_plain(op, s, sm, ds, u, wk, jj, w, lane, rg, kc);
         // lanes < 32 hold dalpha pair sums, lanes >= 32 dbeta ones
         const float tot = add_xor16(group_sum<16>(pab));
-        if ((lane & 31) == 0) buf[B_RAB + (jj * W + w) * 2 + (lane >> 5)] = tot;
+        if ((lane & 31) == 0) wk[W_AB + (jj * W + w) * 2 + (lane >> 5)] = tot;
     }
     // after the loop, not inside it under a condition: every path then provably
     // waits for the staged loads here, and no later reuse of their registers does
-    bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, cks, w, lane);
+    bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, w, lane);
 }
 
 template <bool FUSED, bool AL>
@@ -706,14 +798,14 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
     long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, int B, int T, int H, int nslots) {
     extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
-    float4* const cks = lds4 + 2 * B_BUF / 4 + threadIdx.x;
+    float* const wk = lds + 2 * S_BUF;
 
     const int unit = blockIdx.x;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int rg = lane & 7, cg = lane >> 3;
-    const int colb = 16 * w + 2 * cg;
     const int rowb = BM * rg;
+    const int kc = kpos(16 * w + 2 * cg);
     const long d = (long)H * DH;
     const long ubase = (long)b * T * d + (long)h * DH;
     const long gbase = (long)b * T * H + h;
@@ -726,33 +818,64 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
     for (int m = 0; m < BM; ++m) ds[m][0] = ds[m][1] = 0.0f;
 
     BStage stg;
-    bstage_load<FUSED, AL>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase, gbase, d, T, H, w,
-                       lane, rowb, colb);
-    bstage_store(stg, nseg - 1, T, lds + ((nseg - 1) & 1) * B_BUF, cks, w, lane);
+    bstage_load<FUSED, AL>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase, gbase, d, T, H,
+                           lane);
+    bstage_store(stg, nseg - 1, T, lds + ((nseg - 1) & 1) * S_BUF, w, lane);
+    lds_barrier();
 
     for (int g = nseg - 1; g >= 0; --g) {
         const int t0 = g * CK;
-        float* const buf = lds + (g & 1) * B_BUF;
-        float* const nb = lds + ((g + 1) & 1) * B_BUF;   // the next segment's (g - 1)
-        float se[BM][2];
+        float* const buf = lds + (g & 1) * S_BUF;
+        float* const nb = lds + ((g + 1) & 1) * S_BUF;   // the next segment's (g - 1)
+        const bool sc = __builtin_amdgcn_readfirstlane(__float_as_int(buf[S_G + 8 * CK])) == __float_as_int(1.0f);
+        if (sc) {
+            // the adjoint entering the segment, scaled by its G_CK, as X~^T
+            const float gend = buf[S_G + 8 * (CK - 1) + 2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 x = cks[i * NT];   // index 2n + hf: column n, rows 4hf..4hf+3
-            const int n = i >> 1, hf = i & 1;
-            se[4 * hf][n] = x.x;
-            se[4 * hf + 1][n] = x.y;
-            se[4 * hf + 2][n] = x.z;
-            se[4 * hf + 3][n] = x.w;
+            for (int n = 0; n < 2; ++n) {
+#pragma unroll
+                for (int m = 0; m < BM; ++m) ds[m][n] *= gend;
+#pragma unroll
+                for (int e = 0; e < BM; e += 4)
+                    *reinterpret_cast<float4*>(wk + W_XT + (16 * w + 2 * cg + n) * P + rowb + e) =
+                        make_float4(ds[e][n], ds[e + 1][n], ds[e + 2][n], ds[e + 3][n]);
+            }
         }
-        bstage_load<FUSED, AL>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase, gbase,
-                           d, T, H, w, lane, rowb, colb);
-        lds_barrier();   // this segment's staging visible to all waves
+        bstage_load<FUSED, AL>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase,
+                               gbase, d, T, H, lane);
+        lds_barrier();   // X~^T of every wave
 
-        if (__builtin_amdgcn_readfirstlane(__float_as_int(buf[B_G + 8 * CK])) == __float_as_int(1.0f))
-            bsegment_sc(se, ds, stg, g, T, buf, nb, cks, w, lane, rg, cg, rowb, colb);
+        if (sc)
+            bsegment_sc(ds, stg, g, T, buf, nb, wk, w, lane, rg, cg, rowb, kc);
         else
-            bsegment_plain(ds, stg, g, T, buf, nb, cks, ckb, w, lane, rg, cg, rowb, colb);
-        lds_barrier();   // this segment's row sums complete
+            bsegment_plain(ds, stg, g, T, buf, nb, wk, w, lane, rg, cg, rowb, kc);
+        lds_barrier();   // dq, dk rows, the step sums
+
+        // dalpha's bracket of a scaled segment: lanes j < CK of every wave
+        // carry br_j (exclusive prefix over the per-step dot products)
+        float br = 0.0f;
+        if (sc) {
+            const int l = lane & (CK - 1);
+            const int l1 = min(l + 1, CK - 1);
+            float ea = 0.0f, eb = 0.0f, ea1 = 0.0f, qdq = 0.0f, bsum = 0.0f;
+#pragma unroll
+            for (int u4 = 0; u4 < W; ++u4) {
+                ea += wk[W_AB + (l * W + u4) * 2];
+                eb += wk[W_AB + (l * W + u4) * 2 + 1];
+                ea1 += wk[W_AB + (l1 * W + u4) * 2];
+                qdq += wk[W_QDQ + u4 * CK + l];
+                bsum += wk[W_BR + u4];
+            }
+            const float al = buf[S_G + 8 * l], bl = buf[S_G + 8 * l + 1], al1 = buf[S_G + 8 * l1];
+            const float term = l + 1 < CK ? bl * eb - qdq - al1 * ea1 : 0.0f;
+            float x = term;   // inclusive prefix sum over the 16 lanes of each row
+            x += dpp_or<0x111>(0.0f, x);
+            x += dpp_or<0x112>(0.0f, x);
+            x += dpp_or<0x114>(0.0f, x);
+            x += dpp_or<0x118>(0.0f, x);
+            const float br0 = bsum - readlane_f(al, 0) * readlane_f(ea, 0);
+            br = br0 + (x - term);
+        }
 
         // cross-wave sums, fused norm / sigmoid backward, stores: wave w takes
         // steps w + W i, lane = row.  Every LDS read of the wave's steps is
@@ -760,32 +883,40 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
         // their stores), so the reads' latency is paid once per segment.
         constexpr int NS = CK / W;
         const int a = lane;
-        float dq[NS], dk[NS], dA[NS], dB[NS], dvv[NS], qa[NS], ka[NS], nq[NS], nk[NS], al[NS], be[NS];
+        float dq[NS], dk[NS], dA[NS], dB[NS], du[NS], qa[NS], ka[NS], nq[NS], nk[NS], al[NS], be[NS], ia[NS];
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int jj = w + W * i;
-            const float* const rq = buf + B_RQ + jj * W * RROW + rpad(a);
-            const float* const rk = buf + B_RK + jj * W * RROW + rpad(a);
-            const float* const rab = buf + B_RAB + jj * W * 2;
-            dq[i] = (rq[0] + rq[RROW]) + (rq[2 * RROW] + rq[3 * RROW]);
-            dk[i] = (rk[0] + rk[RROW]) + (rk[2 * RROW] + rk[3 * RROW]);
+            const float* const rab = wk + W_AB + jj * W * 2;
+            if (sc) {
+                dq[i] = wk[W_DQ + jj * P + a];
+                dk[i] = wk[W_DK + jj * P + a];
+            } else {
+                const float* const rq = wk + W_RQ + jj * W * P + rpad(a);
+                const float* const rk = wk + W_RK + jj * W * P + rpad(a);
+                dq[i] = (rq[0] + rq[P]) + (rq[2 * P] + rq[3 * P]);
+                dk[i] = (rk[0] + rk[P]) + (rk[2 * P] + rk[3 * P]);
+            }
             dA[i] = (rab[0] + rab[2]) + (rab[4] + rab[6]);
             dB[i] = (rab[1] + rab[3]) + (rab[5] + rab[7]);
-            dvv[i] = buf[B_RV + jj * DH + a];
-            qa[i] = buf[B_Q + jj * BROW + bpad(a)];
-            ka[i] = buf[B_K + jj * BROW + bpad(a)];
-            nq[i] = buf[B_G + 8 * jj + 5];
-            nk[i] = buf[B_G + 8 * jj + 6];
-            al[i] = buf[B_G + 8 * jj];
-            be[i] = buf[B_G + 8 * jj + 1];
+            du[i] = wk[W_DU + jj * P + kpos(a)];
+            qa[i] = buf[S_Q + jj * P + a];
+            ka[i] = buf[S_K + jj * P + a];
+            al[i] = buf[S_G + 8 * jj];
+            be[i] = buf[S_G + 8 * jj + 1];
+            ia[i] = buf[S_G + 8 * jj + 4];
+            nq[i] = buf[S_G + 8 * jj + 5];
+            nk[i] = buf[S_G + 8 * jj + 6];
         }
         static_assert(W == 4, "the cross-wave sums above add four waves");
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int jj = w + W * i;
+            // scaled segment: dA holds -beta du.sk, completed by the bracket
+            if (sc) dA[i] = fmaf(readlane_f(br, jj), ia[i], dA[i]);
             if (t0 + jj >= T) continue;   // wave-uniform
             const long r = (long)b * T + t0 + jj;
-            gv[r * ldx + hoff + a] = dvv[i];
+            gv[r * ldx + hoff + a] = be[i] * du[i];
             if constexpr (FUSED) {
                 const float dotq = wave_sum(qa[i] * dq[i]);
                 const float dotk = wave_sum(ka[i] * dk[i]);
@@ -805,6 +936,8 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
                 }
             }
         }
+        // a plain segment's row partials share space with the next segment's X~^T
+        if (!sc) lds_barrier();
     }
 }
 
