@@ -23,10 +23,14 @@
 //    MFMA): dq and dk from the segment's first checkpoint, the adjoint at its
 //    top and the 16 x 16 step mixes u~ . dO~ and u~ . dsk~, dalpha from one
 //    exact <dS, S> at the segment's bottom carried up by per-step dot products
-//    (see bsegment_sc).  The products of inputs alone run interleaved with the
-//    steps.  A segment with a gate outside [2^-6, 2^6] (zero, tiny or huge
-//    values) runs the plain recurrence instead, recomputing every state it
-//    needs from its first checkpoint.
+//    (see bsegment_sc).  The block has eight waves: when every gate of the unit
+//    lies in [2^-6, 2^6], four run the adjoint loop of one segment while the
+//    other four, one per SIMD beside them, run the products and the epilogue
+//    of the segment before it (a two-stage pipeline, see the pipelined
+//    backward).  A unit with a gate outside that range (zero, tiny or huge
+//    values) runs every segment on four waves instead, a segment with such a
+//    gate in the plain recurrence, recomputing every state it needs from its
+//    first checkpoint.
 #include "common.h"
 #include "delta.h"
 #include "runtime.h"
@@ -357,7 +361,8 @@ constexpr int W_DK = W_DQ + CK * P;          // [CK][P] dk rows
 constexpr int W_DU = W_DK + CK * P;          // [CK][P] du, k-order
 constexpr int W_AB = W_DU + CK * P;          // [CK][W][2] per-wave step sums (see the segment bodies)
 constexpr int W_QDQ = W_AB + CK * W * 2;     // [W][CK] per-wave partial q . dq
-constexpr int W_BR = W_QDQ + W * CK;         // [W] per-wave partial <dS, S> at the segment's bottom
+constexpr int W_KDK = W_QDQ + W * CK;        // [W][CK] per-wave partial k . dk
+constexpr int W_BR = W_KDK + W * CK;         // [W] per-wave partial <dS, S> at the segment's bottom
 constexpr int W_END = W_BR + 8;
 static_assert(W_RK + CK * W * P == W_DK, "plain partials fill the scaled segment's space");
 static_assert(S_BUF % 4 == 0 && S_G % 4 == 0 && W_DQ % 4 == 0 && W_DU % 4 == 0, "16-byte rows");
@@ -382,17 +387,17 @@ ASCA_DEV void bstage_load(BStage& st, int g, const float* __restrict__ q, const 
                           const float* __restrict__ skv, const float* __restrict__ alpha,
                           const float* __restrict__ beta, const float* __restrict__ qnorm,
                           const float* __restrict__ knorm, const float* __restrict__ ckb, long ubase, long gbase,
-                          long d, int T, int H, int lane) {
+                          long d, int T, int H, int tx, int lane) {
     const int t0 = g * CK;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int f = threadIdx.x + NT * i;
+        const int f = tx + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
         const long t = min(t0 + j, T - 1);
         st.rq[i] = ld4<AL>((tsr ? k : q) + ubase + t * d + 4 * c4);
     }
     {
-        const int j = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+        const int j = tx >> 4, c4 = tx & 15;
         const long o = ubase + (long)min(t0 + j, T - 1) * d + 4 * c4;
         st.rw[0] = ld4<AL>(d_o + o);
         st.rw[1] = ld4<AL>(v + o);
@@ -409,25 +414,24 @@ ASCA_DEV void bstage_load(BStage& st, int g, const float* __restrict__ q, const 
     const float* const cs = ckb + (long)g * DH2;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        st.rm[e] = *reinterpret_cast<const float4*>(cs + (long)(16 * e + (threadIdx.x >> 4)) * DH +
-                                                    4 * (threadIdx.x & 15));
+        st.rm[e] = *reinterpret_cast<const float4*>(cs + (long)(16 * e + (tx >> 4)) * DH + 4 * (tx & 15));
 }
 
 // Registers -> the staging buffer nb of segment g.  Every wave derives the
 // gates, G_{j+1} and the segment's flag from its own copy of the gate loads.
 // Steps past T get alpha = 1, beta = 0 and dO = 0, which leave the adjoint
 // and every sum unchanged.
-ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ nb, int w, int lane) {
+// tx: the thread's index among the NT staging threads, w: their wave.
+ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ nb, int tx, int w, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int f = threadIdx.x + NT * i;
+        const int f = tx + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
         *reinterpret_cast<float4*>(nb + (tsr ? S_K : S_Q) + j * P + 4 * c4) = st.rq[i];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        *reinterpret_cast<float4*>(nb + S_M + (16 * e + (threadIdx.x >> 4)) * P + 4 * (threadIdx.x & 15)) =
-            st.rm[e];
+        *reinterpret_cast<float4*>(nb + S_M + (16 * e + (tx >> 4)) * P + 4 * (tx & 15)) = st.rm[e];
     // Both segment bodies store here; without this opaque copy the compiler
     // hoists the identical gate arithmetic of the two into the segment's
     // start, right behind the loads it waits for.
@@ -442,7 +446,7 @@ ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ n
     const bool bad = ga && !(rab >= 0x1p-6f && rab <= 0x1p6f);
     const bool sc = __ballot(bad) == 0;
     {
-        const int j = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+        const int j = tx >> 4, c4 = tx & 15;
         const float aj = __shfl(rab, j), bj = __shfl(rab, CK + j), gj = __shfl(pr, j);
         const float go = sc ? gj : 1.0f;
         const float gu = sc ? __builtin_amdgcn_rcpf(gj) : 1.0f;
@@ -509,15 +513,15 @@ ASCA_DEV float colsum8(const float (&p)[BM], int lane) {
     return keep + dpp<DPP_ROW_ROR8>(send);
 }
 
-// du of a step: the lane's column pair, written by the lanes of row group 0
-// (du) and, with DSK, 1 (G_j dsk) to their rows; a ds_write under a lane
-// condition is an LDS access, which no global wait depends on.
+// du of a step for the lane's column pair: every lane of a column group holds
+// the same du and G_j dsk, so every lane writes, the even row groups du and
+// (with DSK) the odd ones G_j dsk; duplicates store identical values, and no
+// lane mask is set up around the store.
 template <bool DSK>
-ASCA_DEV void put_du(float* __restrict__ wk, int j, int kc, int rg, float du0, float du1, float sh0, float sh1) {
-    if (rg < (DSK ? 2 : 1)) {
-        const float2 x = rg == 0 ? make_float2(du0, du1) : make_float2(sh0, sh1);
-        *reinterpret_cast<float2*>(wk + (rg == 0 ? W_DU : W_DSK) + j * P + kc) = x;
-    }
+ASCA_DEV void put_du(float* __restrict__ dub, float* __restrict__ dskb, int j, int kc, int rg, float du0, float du1,
+                     float sh0, float sh1) {
+    const bool odd = DSK && (rg & 1);
+    *reinterpret_cast<float2*>((odd ? dskb : dub) + j * P + kc) = odd ? make_float2(sh0, sh1) : make_float2(du0, du1);
 }
 
 // One step of the scaled adjoint loop (rust/src/delta.rs:508-563 for the
@@ -526,7 +530,8 @@ ASCA_DEV void put_du(float* __restrict__ wk, int j, int kc, int rg, float du0, f
 //   G_j dsk_j = -beta_j t;        ds += k_j (G_j dsk_j)^T  (= G_j dS_{j-1} part).
 // Returns the lane's transposed (ea, eb) pair of the step: ea = -beta du.sk,
 // eb = du.(v - alpha sk) over the lane's columns (row group 0 only).
-ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ wk, int j, int kc, int rg) {
+ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ dub, float* __restrict__ dskb, int j,
+                        int kc, int rg) {
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
         ds[m][0] = fmaf(in.q[m], in.dO.x, ds[m][0]);
@@ -541,7 +546,7 @@ ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ 
     const float t0 = group_sum<8>(c0), t1 = group_sum<8>(c1);
     const float du0 = t0 * in.gt.w, du1 = t1 * in.gt.w;
     const float sh0 = -in.gt.y * t0, sh1 = -in.gt.y * t1;
-    put_du<true>(wk, j, kc, rg, du0, du1, sh0, sh1);
+    put_du<true>(dub, dskb, j, kc, rg, du0, du1, sh0, sh1);
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
         ds[m][0] = fmaf(in.k[m], sh0, ds[m][0]);
@@ -564,53 +569,45 @@ ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ 
 //   br_j = <dS_out, S> - dsk_0.sk_0 + sum_{l<j} (u_l.du_l - q_l.dq_l - dsk_{l+1}.sk_{l+1}),
 // the scaled <dS_j, S_{j-1}> carried from the exact product at the bottom.  Only
 // the adjoint recurrence runs step by step (on the VALU); the products run on
-// the matrix cores, those of inputs alone interleaved with the steps.  Wave w
-// computes the dq / dk columns 16 w .. 16 w + 15 of every step; the products
-// over the columns (P, R) are summed from per-wave partials.
+// the matrix cores after it.  Wave w computes the dq / dk columns 16 w .. 16 w
+// + 15 of every step; the products over the columns (P, R) are summed from
+// per-wave partials.
 ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, const float* __restrict__ buf,
                           float* __restrict__ nb, float* __restrict__ wk, int w, int lane, int rg, int cg,
                           int rowb, int kc) {
     const int jr = lane & 15, gq = lane >> 4;
-    // products of inputs alone: dO~ S^T, U~ X~^T and the partial P
-    float a_do[16], a_u[16], b_s[16], b_x[16], p_u[4], p_d[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float4 x = *reinterpret_cast<const float4*>(buf + S_DO + jr * P + 16 * gq + 4 * e);
-        const float4 y = *reinterpret_cast<const float4*>(buf + S_U + jr * P + 16 * gq + 4 * e);
-        a_do[4 * e] = x.x; a_do[4 * e + 1] = x.y; a_do[4 * e + 2] = x.z; a_do[4 * e + 3] = x.w;
-        a_u[4 * e] = y.x; a_u[4 * e + 1] = y.y; a_u[4 * e + 2] = y.z; a_u[4 * e + 3] = y.w;
-    }
-#pragma unroll
-    for (int kb = 0; kb < 16; ++kb) {
-        b_s[kb] = buf[S_M + kcol(gq, kb) * P + 16 * w + jr];
-        b_x[kb] = wk[W_XT + kcol(gq, kb) * P + 16 * w + jr];
-    }
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        p_u[kb] = buf[S_U + jr * P + 16 * kb + 4 * w + gq];
-        p_d[kb] = buf[S_DO + jr * P + 16 * kb + 4 * w + gq];
-    }
-    f32x4 adq = {0.f, 0.f, 0.f, 0.f}, adk = adq, ap = adq;
     float pab[CK];
     BOps op[2];
     bops_read(op[(CK - 1) & 1], buf, CK - 1, rowb, kc);
 #pragma unroll
     for (int jj = CK - 1; jj >= 0; --jj) {
+        // the operand reads of the next step are issued a whole step ahead
         if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, rowb, kc);
-        __builtin_amdgcn_sched_barrier(0);
-        const int kb = CK - 1 - jj;
-        adq = mfma4(a_do[kb], b_s[kb], adq);
-        adk = mfma4(a_u[kb], b_x[kb], adk);
-        if (kb < 4) ap = mfma4(p_u[kb], p_d[kb], ap);
-        pab[jj] = bstep_sc(op[jj & 1], ds, wk, jj, kc, rg);
+        pab[jj] = bstep_sc(op[jj & 1], ds, wk + W_DU, wk + W_DSK, jj, kc, rg);
         if (jj == CK / 2) {
             // the staged operands of the next segment (loads issued at this
             // segment's start) go to its buffer; the fence keeps the scheduler
             // from hoisting the stores, and their wait, to the segment's start
             __builtin_amdgcn_sched_barrier(0);
-            bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, w, lane);
+            bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, threadIdx.x, w, lane);
         }
     }
+    // products of inputs alone: dO~ S^T, U~ X~^T and the partial P
+    f32x4 adq = {0.f, 0.f, 0.f, 0.f}, adk = adq, ap = adq;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float4 x = *reinterpret_cast<const float4*>(buf + S_DO + jr * P + 16 * gq + 4 * e);
+        const float4 y = *reinterpret_cast<const float4*>(buf + S_U + jr * P + 16 * gq + 4 * e);
+        const float xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            adq = mfma4(xs[i], buf[S_M + kcol(gq, 4 * e + i) * P + 16 * w + jr], adq);
+            adk = mfma4(ys[i], wk[W_XT + kcol(gq, 4 * e + i) * P + 16 * w + jr], adk);
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+        ap = mfma4(buf[S_U + jr * P + 16 * kb + 4 * w + gq], buf[S_DO + jr * P + 16 * kb + 4 * w + gq], ap);
     // ds = dS_{-1} without q_{-1} dO_{-1}^T (G_0 = 1): its product with S
     {
         float x = 0.0f;
@@ -674,14 +671,18 @@ ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, c
         adk = mfma4(kk >= jr ? pjk : 0.0f, bq, adk);
         adk = mfma4(kk < jr ? rkj : (kk > jr ? rjk : 0.0f), bk, adk);
     }
-    // dq, dk rows and the partial q . dq of the wave's columns
+    // dq, dk rows and the partial q . dq, k . dk of the wave's columns
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int j = 4 * gq + r;
         wk[W_DQ + j * P + 16 * w + jr] = adq[r];
         wk[W_DK + j * P + 16 * w + jr] = adk[r];
         const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + 16 * w + jr]);
-        if (jr == 0) wk[W_QDQ + w * CK + j] = x;
+        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + 16 * w + jr]);
+        if (jr == 0) {
+            wk[W_QDQ + w * CK + j] = x;
+            wk[W_KDK + w * CK + j] = y;
+        }
     }
 }
 
@@ -726,7 +727,7 @@ ASCA_DEV float bstep_plain(const BOps& in, const float (&s)[BM][2], const float 
     }
     const float du0 = group_sum<8>(c0), du1 = group_sum<8>(c1);
     const float dk0 = -a * b * du0, dk1 = -a * b * du1;
-    put_du<false>(wk, j, kc, rg, du0, du1, 0.0f, 0.0f);
+    put_du<false>(wk + W_DU, wk + W_DSK, j, kc, rg, du0, du1, 0.0f, 0.0f);
     float pa0 = 0.0f, pa1 = 0.0f;
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
@@ -786,32 +787,34 @@ ASCA_DEV void bsegment_plain(float (&ds)[BM][2], const BStage& stg, int g, int T
     }
     // after the loop, not inside it under a condition: every path then provably
     // waits for the staged loads here, and no later reuse of their registers does
-    bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, w, lane);
+    bstage_store(stg, g > 0 ? g - 1 : 0, T, nb, threadIdx.x, w, lane);
 }
 
-template <bool FUSED, bool AL>
-__global__ __launch_bounds__(NT) void delta_bwd64_k(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ alpha, const float* __restrict__ beta, const float* __restrict__ d_o,
-    const float* __restrict__ skv, const float* __restrict__ ckpt, const float* __restrict__ qnorm,
-    const float* __restrict__ knorm, float* __restrict__ gq, float* __restrict__ gk, float* __restrict__ gv,
-    long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, int B, int T, int H, int nslots) {
-    extern __shared__ float4 lds4[];
-    float* const lds = reinterpret_cast<float*>(lds4);
-    float* const wk = lds + 2 * S_BUF;
+// Arguments shared by the backward's paths.
+struct BArgs {
+    const float* q; const float* k; const float* v; const float* alpha; const float* beta; const float* d_o;
+    const float* skv; const float* qnorm; const float* knorm;
+    float* gq; float* gk; float* gv; float* ga; float* gb;
+    const float* ckb;
+    long ldx, ldg, d, ubase, gbase, hoff;
+    int b, h, T, H, nseg;
+};
 
-    const int unit = blockIdx.x;
-    const int h = unit / B, b = unit - h * B;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// The serial path, on waves 0..3: each segment's products, sums and
+// epilogue follow its adjoint loop on the same waves.  Taken by every unit
+// that has a plain segment; waves 4..7 meanwhile only mirror its barriers
+// (bwd_mirror).
+template <bool FUSED, bool AL>
+ASCA_DEV void bwd_serial(const BArgs& A, float* __restrict__ lds, int w, int lane) {
+    const float *q = A.q, *k = A.k, *v = A.v, *alpha = A.alpha, *beta = A.beta, *d_o = A.d_o, *skv = A.skv;
+    const float *qnorm = A.qnorm, *knorm = A.knorm, *ckb = A.ckb;
+    float *gq = A.gq, *gk = A.gk, *gv = A.gv, *ga = A.ga, *gb = A.gb;
+    const long ldx = A.ldx, ldg = A.ldg, d = A.d, ubase = A.ubase, gbase = A.gbase, hoff = A.hoff;
+    const int b = A.b, h = A.h, T = A.T, H = A.H, nseg = A.nseg;
+    float* const wk = lds + 2 * S_BUF;
     const int rg = lane & 7, cg = lane >> 3;
     const int rowb = BM * rg;
     const int kc = kpos(16 * w + 2 * cg);
-    const long d = (long)H * DH;
-    const long ubase = (long)b * T * d + (long)h * DH;
-    const long gbase = (long)b * T * H + h;
-    const long hoff = (long)h * DH;
-    const float* const ckb = ckpt + (long)unit * nslots * DH2;
-    const int nseg = (T + CK - 1) / CK;
 
     float ds[BM][2];
 #pragma unroll
@@ -819,8 +822,8 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
 
     BStage stg;
     bstage_load<FUSED, AL>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase, gbase, d, T, H,
-                           lane);
-    bstage_store(stg, nseg - 1, T, lds + ((nseg - 1) & 1) * S_BUF, w, lane);
+                           threadIdx.x, lane);
+    bstage_store(stg, nseg - 1, T, lds + ((nseg - 1) & 1) * S_BUF, threadIdx.x, w, lane);
     lds_barrier();
 
     for (int g = nseg - 1; g >= 0; --g) {
@@ -842,7 +845,7 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
             }
         }
         bstage_load<FUSED, AL>(stg, g > 0 ? g - 1 : 0, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, ckb, ubase,
-                               gbase, d, T, H, lane);
+                               gbase, d, T, H, threadIdx.x, lane);
         lds_barrier();   // X~^T of every wave
 
         if (sc)
@@ -851,43 +854,52 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
             bsegment_plain(ds, stg, g, T, buf, nb, wk, w, lane, rg, cg, rowb, kc);
         lds_barrier();   // dq, dk rows, the step sums
 
-        // dalpha's bracket of a scaled segment: lanes j < CK of every wave
-        // carry br_j (exclusive prefix over the per-step dot products)
-        float br = 0.0f;
+        // Per-step scalars, lane l of every 16-lane row carrying step l: the
+        // totals of the per-wave step sums (scaled segment: ea = -beta du.sk,
+        // eb = du.(v - alpha sk), q.dq, k.dk; plain: dalpha, dbeta) and, for a
+        // scaled segment, dalpha's bracket br_l (an exclusive prefix over the
+        // per-step dot products).  Each wave then reads its steps' values by
+        // readlane instead of from LDS.
+        const int l = lane & (CK - 1);
+        float ea = 0.0f, eb = 0.0f, qdq = 0.0f, kdk = 0.0f;
+#pragma unroll
+        for (int u4 = 0; u4 < W; ++u4) {
+            ea += wk[W_AB + (l * W + u4) * 2];
+            eb += wk[W_AB + (l * W + u4) * 2 + 1];
+        }
+        const float4 gl0 = *reinterpret_cast<const float4*>(buf + S_G + 8 * l);       // alpha, beta, G, 1/G
+        const float4 gl1 = *reinterpret_cast<const float4*>(buf + S_G + 8 * l + 4);   // 1/alpha, |q|, |k|, -
+        float dal = ea;
         if (sc) {
-            const int l = lane & (CK - 1);
-            const int l1 = min(l + 1, CK - 1);
-            float ea = 0.0f, eb = 0.0f, ea1 = 0.0f, qdq = 0.0f, bsum = 0.0f;
+            float bsum = 0.0f;
 #pragma unroll
             for (int u4 = 0; u4 < W; ++u4) {
-                ea += wk[W_AB + (l * W + u4) * 2];
-                eb += wk[W_AB + (l * W + u4) * 2 + 1];
-                ea1 += wk[W_AB + (l1 * W + u4) * 2];
                 qdq += wk[W_QDQ + u4 * CK + l];
+                kdk += wk[W_KDK + u4 * CK + l];
                 bsum += wk[W_BR + u4];
             }
-            const float al = buf[S_G + 8 * l], bl = buf[S_G + 8 * l + 1], al1 = buf[S_G + 8 * l1];
-            const float term = l + 1 < CK ? bl * eb - qdq - al1 * ea1 : 0.0f;
+            const float ea1 = dpp_or<0x101>(0.0f, ea);       // row_shl 1: step l + 1
+            const float al1 = dpp_or<0x101>(1.0f, gl0.x);
+            const float term = l + 1 < CK ? gl0.y * eb - qdq - al1 * ea1 : 0.0f;
             float x = term;   // inclusive prefix sum over the 16 lanes of each row
             x += dpp_or<0x111>(0.0f, x);
             x += dpp_or<0x112>(0.0f, x);
             x += dpp_or<0x114>(0.0f, x);
             x += dpp_or<0x118>(0.0f, x);
-            const float br0 = bsum - readlane_f(al, 0) * readlane_f(ea, 0);
-            br = br0 + (x - term);
+            const float br = bsum - readlane_f(gl0.x, 0) * readlane_f(ea, 0) + (x - term);
+            dal = fmaf(br, gl1.x, ea);   // dalpha_l = br_l / alpha_l - beta_l du_l.sk_l
         }
 
-        // cross-wave sums, fused norm / sigmoid backward, stores: wave w takes
-        // steps w + W i, lane = row.  Every LDS read of the wave's steps is
-        // issued before the arithmetic and the stores (steps past T only skip
-        // their stores), so the reads' latency is paid once per segment.
+        // fused norm / sigmoid backward and stores: wave w takes steps w + W i,
+        // lane = row.  Every LDS read of the wave's steps is issued before the
+        // arithmetic and the stores (steps past T only skip their stores).
         constexpr int NS = CK / W;
         const int a = lane;
-        float dq[NS], dk[NS], dA[NS], dB[NS], du[NS], qa[NS], ka[NS], nq[NS], nk[NS], al[NS], be[NS], ia[NS];
+        const int ws = __builtin_amdgcn_readfirstlane(w);
+        float dq[NS], dk[NS], du[NS], qa[NS], ka[NS];
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            const int jj = w + W * i;
-            const float* const rab = wk + W_AB + jj * W * 2;
+            const int jj = ws + W * i;
             if (sc) {
                 dq[i] = wk[W_DQ + jj * P + a];
                 dk[i] = wk[W_DK + jj * P + a];
@@ -897,47 +909,358 @@ __global__ __launch_bounds__(NT) void delta_bwd64_k(
                 dq[i] = (rq[0] + rq[P]) + (rq[2 * P] + rq[3 * P]);
                 dk[i] = (rk[0] + rk[P]) + (rk[2 * P] + rk[3 * P]);
             }
-            dA[i] = (rab[0] + rab[2]) + (rab[4] + rab[6]);
-            dB[i] = (rab[1] + rab[3]) + (rab[5] + rab[7]);
             du[i] = wk[W_DU + jj * P + kpos(a)];
             qa[i] = buf[S_Q + jj * P + a];
             ka[i] = buf[S_K + jj * P + a];
-            al[i] = buf[S_G + 8 * jj];
-            be[i] = buf[S_G + 8 * jj + 1];
-            ia[i] = buf[S_G + 8 * jj + 4];
-            nq[i] = buf[S_G + 8 * jj + 5];
-            nk[i] = buf[S_G + 8 * jj + 6];
         }
-        static_assert(W == 4, "the cross-wave sums above add four waves");
+        static_assert(W == 4, "the step sums above add four waves");
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            const int jj = w + W * i;
-            // scaled segment: dA holds -beta du.sk, completed by the bracket
-            if (sc) dA[i] = fmaf(readlane_f(br, jj), ia[i], dA[i]);
+            const int jj = ws + W * i;
             if (t0 + jj >= T) continue;   // wave-uniform
+            const float dA = readlane_f(dal, jj), dB = readlane_f(eb, jj);
+            const float al = readlane_f(gl0.x, jj), be = readlane_f(gl0.y, jj);
             const long r = (long)b * T + t0 + jj;
-            gv[r * ldx + hoff + a] = be[i] * du[i];
+            gv[r * ldx + hoff + a] = be * du[i];
             if constexpr (FUSED) {
-                const float dotq = wave_sum(qa[i] * dq[i]);
-                const float dotk = wave_sum(ka[i] * dk[i]);
+                const float dotq = sc ? readlane_f(qdq, jj) : wave_sum(qa[i] * dq[i]);
+                const float dotk = sc ? readlane_f(kdk, jj) : wave_sum(ka[i] * dk[i]);
                 // 1/|q|, 1/|k| by the hardware reciprocal (within 1 ulp)
-                gq[r * ldx + hoff + a] = (dq[i] - qa[i] * dotq) * __builtin_amdgcn_rcpf(nq[i]);
-                gk[r * ldx + hoff + a] = (dk[i] - ka[i] * dotk) * __builtin_amdgcn_rcpf(nk[i]);
+                const float rq = __builtin_amdgcn_rcpf(readlane_f(gl1.y, jj));
+                const float rk = __builtin_amdgcn_rcpf(readlane_f(gl1.z, jj));
+                gq[r * ldx + hoff + a] = (dq[i] - qa[i] * dotq) * rq;
+                gk[r * ldx + hoff + a] = (dk[i] - ka[i] * dotk) * rk;
                 if (lane == 0) {
-                    ga[r * ldg + h] = dA[i] * al[i] * (1.0f - al[i]);
-                    gb[r * ldg + h] = dB[i] * be[i] * (1.0f - be[i]);
+                    ga[r * ldg + h] = dA * al * (1.0f - al);
+                    gb[r * ldg + h] = dB * be * (1.0f - be);
                 }
             } else {
                 gq[r * ldx + hoff + a] = dq[i];
                 gk[r * ldx + hoff + a] = dk[i];
                 if (lane == 0) {
-                    ga[r * ldg + h] = dA[i];
-                    gb[r * ldg + h] = dB[i];
+                    ga[r * ldg + h] = dA;
+                    gb[r * ldg + h] = dB;
                 }
             }
         }
         // a plain segment's row partials share space with the next segment's X~^T
         if (!sc) lds_barrier();
+    }
+}
+
+
+// Barriers of bwd_serial, for the waves that take no part in it.
+ASCA_DEV void bwd_mirror(const float* __restrict__ lds, int nseg) {
+    lds_barrier();
+    for (int g = nseg - 1; g >= 0; --g) {
+        lds_barrier();   // segment start
+        const float* const buf = lds + (g & 1) * S_BUF;
+        const bool sc = __builtin_amdgcn_readfirstlane(__float_as_int(buf[S_G + 8 * CK])) == __float_as_int(1.0f);
+        if (sc) {
+            lds_barrier();   // the scaled segment's two
+            lds_barrier();
+        }
+        lds_barrier();   // rows and sums
+        if (!sc) lds_barrier();
+    }
+}
+
+// ------------------------------------------------- pipelined backward
+// A unit whose segments are all scaled runs on eight waves as a two-stage
+// pipeline: in period p, the adjoint waves (0..3) run the adjoint loop of
+// segment g = nseg - 1 - p while the matrix waves (4..7) run the products and
+// the epilogue of segment g + 1, whose loop ended in period p - 1, and stage
+// segment g - 1.  One adjoint wave and one matrix wave share each SIMD, so
+// the matrix waves' MFMA and LDS latencies fill the adjoint loop's stalls.
+// Two block barriers per period: P0 at its start, P1 halfway through the
+// loop, which the matrix waves reach once they no longer read the staging
+// buffer of g + 1, so that they may restage it with g - 1.  Data the stages
+// hand over (the top adjoint X~, du, dsk~, step sums) alternate between two
+// slots by segment parity.
+constexpr int Q_STG = 0;                          // [2][S_BUF] staging
+constexpr int Q_XT = 2 * S_BUF;                   // [2][DH][P] X~^T
+constexpr int Q_DU = Q_XT + 2 * DH * P;           // [2][CK][P] du, k-order
+constexpr int Q_DSK = Q_DU + 2 * CK * P;          // [2][CK][P] G_j dsk_j, k-order
+constexpr int Q_DQ = Q_DSK + 2 * CK * P;          // [CK][P] dq rows
+constexpr int Q_DK = Q_DQ + CK * P;               // [CK][P] dk rows
+constexpr int Q_PR = Q_DK + CK * P;               // [W][2][CK][17] each matrix wave's P and R
+constexpr int Q_AB = Q_PR + W * 2 * CK * 17;      // [2][CK][W][2] step sums
+constexpr int Q_QDQ = Q_AB + 2 * CK * W * 2;      // [W][CK] per-wave partial q . dq
+constexpr int Q_KDK = Q_QDQ + W * CK;             // [W][CK] per-wave partial k . dk
+constexpr int Q_BR = Q_KDK + W * CK;              // [2][8] per-wave partial <dS, S>
+constexpr int Q_END = Q_BR + 16;
+static_assert(Q_DU % 4 == 0 && Q_DQ % 4 == 0 && Q_AB % 4 == 0, "16-byte rows");
+constexpr size_t B_LDS_ALL = (size_t)(Q_END > 2 * S_BUF + W_END ? Q_END : 2 * S_BUF + W_END) * 4;
+static_assert(B_LDS_ALL <= 160 * 1024, "backward LDS");
+
+// Adjoint waves: the loop of one scaled segment (as in bsegment_sc, without
+// the products), with P1 between steps CK/2 and CK/2 - 1; then the anchor
+// <dS_out, S> and the step sums.
+ASCA_DEV void aloop(float (&ds)[BM][2], const float* __restrict__ buf, float* __restrict__ dub,
+                    float* __restrict__ dskb, float* __restrict__ abb, float* __restrict__ brb, int w, int lane,
+                    int rg, int cg, int rowb, int kc) {
+    float pab[CK];
+    BOps op[2];
+    bops_read(op[(CK - 1) & 1], buf, CK - 1, rowb, kc);
+#pragma unroll
+    for (int jj = CK - 1; jj >= 0; --jj) {
+        if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, rowb, kc);
+        pab[jj] = bstep_sc(op[jj & 1], ds, dub, dskb, jj, kc, rg);
+        if (jj == CK / 2) lds_barrier();   // P1
+    }
+    float x = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int e = 0; e < BM; e += 4) {
+            const float4 s = *reinterpret_cast<const float4*>(buf + S_M + (16 * w + 2 * cg + n) * P + rowb + e);
+            x = fmaf(ds[e][n], s.x, x);
+            x = fmaf(ds[e + 1][n], s.y, x);
+            x = fmaf(ds[e + 2][n], s.z, x);
+            x = fmaf(ds[e + 3][n], s.w, x);
+        }
+    x = wave_sum(x);
+    if (lane == 0) brb[w] = x;
+    cross_step_sum<CK, W>(pab, abb, w, lane);
+}
+
+// What a matrix wave keeps of a segment's staging buffer for its epilogue.
+struct MEpi {
+    float qa[CK / W], ka[CK / W];   // q, k of the wave's steps, lane = row
+    float4 gl0, gl1;                // lane l < CK: step l's gate row
+};
+
+// Matrix wave mw: the products of one segment (bsegment_sc's formulas) for the
+// dq / dk columns 16 mw .. 16 mw + 15 of every step, with P and R in full
+// (each wave its own, through a private LDS area), the rows and the partial
+// q . dq, k . dk; then what the epilogue needs from the staging buffer.
+ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt, const float* __restrict__ dsk,
+                    float* __restrict__ lds, int mw, int lane, MEpi& e) {
+    const int jr = lane & 15, gq = lane >> 4;
+    float a_do[16], a_u[16], a_dk[16], b_s[16], b_x[16];
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+        const float4 x = *reinterpret_cast<const float4*>(buf + S_DO + jr * P + 16 * gq + 4 * e4);
+        const float4 y = *reinterpret_cast<const float4*>(buf + S_U + jr * P + 16 * gq + 4 * e4);
+        const float4 z = *reinterpret_cast<const float4*>(dsk + jr * P + 16 * gq + 4 * e4);
+        a_do[4 * e4] = x.x; a_do[4 * e4 + 1] = x.y; a_do[4 * e4 + 2] = x.z; a_do[4 * e4 + 3] = x.w;
+        a_u[4 * e4] = y.x; a_u[4 * e4 + 1] = y.y; a_u[4 * e4 + 2] = y.z; a_u[4 * e4 + 3] = y.w;
+        a_dk[4 * e4] = z.x; a_dk[4 * e4 + 1] = z.y; a_dk[4 * e4 + 2] = z.z; a_dk[4 * e4 + 3] = z.w;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 16; ++kb) {
+        b_s[kb] = buf[S_M + kcol(gq, kb) * P + 16 * mw + jr];
+        b_x[kb] = xt[kcol(gq, kb) * P + 16 * mw + jr];
+    }
+    f32x4 adq = {0.f, 0.f, 0.f, 0.f}, adk = adq, ap = adq, ar = adq;
+#pragma unroll
+    for (int kb = 0; kb < 16; ++kb) {
+        adq = mfma4(a_do[kb], b_s[kb], adq);
+        adk = mfma4(a_u[kb], b_x[kb], adk);
+        adk = mfma4(a_dk[kb], b_s[kb], adk);
+        ap = mfma4(a_u[kb], a_do[kb], ap);
+        ar = mfma4(a_u[kb], a_dk[kb], ar);
+    }
+    float* const prv = lds + Q_PR + mw * 2 * CK * 17;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        prv[(4 * gq + r) * 17 + jr] = ap[r];
+        prv[CK * 17 + (4 * gq + r) * 17 + jr] = ar[r];
+    }
+    // the wave reads back what its own lanes wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const int kk = 4 * kb + gq;
+        const float pkj = prv[kk * 17 + jr], pjk = prv[jr * 17 + kk];
+        const float rkj = prv[CK * 17 + kk * 17 + jr], rjk = prv[CK * 17 + jr * 17 + kk];
+        const float bk = buf[S_K + kk * P + 16 * mw + jr];
+        const float bq = buf[S_Q + kk * P + 16 * mw + jr];
+        adq = mfma4(kk <= jr ? pkj : 0.0f, bk, adq);
+        adk = mfma4(kk >= jr ? pjk : 0.0f, bq, adk);
+        adk = mfma4(kk < jr ? rkj : (kk > jr ? rjk : 0.0f), bk, adk);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int j = 4 * gq + r;
+        lds[Q_DQ + j * P + 16 * mw + jr] = adq[r];
+        lds[Q_DK + j * P + 16 * mw + jr] = adk[r];
+        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + 16 * mw + jr]);
+        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + 16 * mw + jr]);
+        if (jr == 0) {
+            lds[Q_QDQ + mw * CK + j] = x;
+            lds[Q_KDK + mw * CK + j] = y;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < CK / W; ++i) {
+        e.qa[i] = buf[S_Q + (mw + W * i) * P + lane];
+        e.ka[i] = buf[S_K + (mw + W * i) * P + lane];
+    }
+    e.gl0 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)));
+    e.gl1 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)) + 4);
+}
+
+// Matrix wave mw: dalpha's bracket and the epilogue of segment gp (as in
+// bwd_serial's), steps mw + W i.
+template <bool FUSED>
+ASCA_DEV void mepi(const BArgs& A, const MEpi& e, const float* __restrict__ lds, const float* __restrict__ abb,
+                   const float* __restrict__ brb, const float* __restrict__ dub, int gp, int mw, int lane) {
+    const int l = lane & (CK - 1);
+    float ea = 0.0f, eb = 0.0f, qdq = 0.0f, kdk = 0.0f, bsum = 0.0f;
+#pragma unroll
+    for (int u4 = 0; u4 < W; ++u4) {
+        ea += abb[(l * W + u4) * 2];
+        eb += abb[(l * W + u4) * 2 + 1];
+        qdq += lds[Q_QDQ + u4 * CK + l];
+        kdk += lds[Q_KDK + u4 * CK + l];
+        bsum += brb[u4];
+    }
+    const float ea1 = dpp_or<0x101>(0.0f, ea);       // row_shl 1: step l + 1
+    const float al1 = dpp_or<0x101>(1.0f, e.gl0.x);
+    const float term = l + 1 < CK ? e.gl0.y * eb - qdq - al1 * ea1 : 0.0f;
+    float x = term;   // inclusive prefix sum over the 16 lanes of each row
+    x += dpp_or<0x111>(0.0f, x);
+    x += dpp_or<0x112>(0.0f, x);
+    x += dpp_or<0x114>(0.0f, x);
+    x += dpp_or<0x118>(0.0f, x);
+    const float br = bsum - readlane_f(e.gl0.x, 0) * readlane_f(ea, 0) + (x - term);
+    const float dal = fmaf(br, e.gl1.x, ea);
+    const int t0 = gp * CK;
+    const int ws = __builtin_amdgcn_readfirstlane(mw);
+    float dq[CK / W], dk[CK / W], du[CK / W];
+#pragma unroll
+    for (int i = 0; i < CK / W; ++i) {
+        const int jj = ws + W * i;
+        dq[i] = lds[Q_DQ + jj * P + lane];
+        dk[i] = lds[Q_DK + jj * P + lane];
+        du[i] = dub[jj * P + kpos(lane)];
+    }
+#pragma unroll
+    for (int i = 0; i < CK / W; ++i) {
+        const int jj = ws + W * i;
+        if (t0 + jj >= A.T) continue;   // wave-uniform
+        const float dA = readlane_f(dal, jj), dB = readlane_f(eb, jj);
+        const float al = readlane_f(e.gl0.x, jj), be = readlane_f(e.gl0.y, jj);
+        const long r = (long)A.b * A.T + t0 + jj;
+        const long o = r * A.ldx + A.hoff + lane;
+        A.gv[o] = be * du[i];
+        if constexpr (FUSED) {
+            const float rq = __builtin_amdgcn_rcpf(readlane_f(e.gl1.y, jj));
+            const float rk = __builtin_amdgcn_rcpf(readlane_f(e.gl1.z, jj));
+            A.gq[o] = (dq[i] - e.qa[i] * readlane_f(qdq, jj)) * rq;
+            A.gk[o] = (dk[i] - e.ka[i] * readlane_f(kdk, jj)) * rk;
+            if (lane == 0) {
+                A.ga[r * A.ldg + A.h] = dA * al * (1.0f - al);
+                A.gb[r * A.ldg + A.h] = dB * be * (1.0f - be);
+            }
+        } else {
+            A.gq[o] = dq[i];
+            A.gk[o] = dk[i];
+            if (lane == 0) {
+                A.ga[r * A.ldg + A.h] = dA;
+                A.gb[r * A.ldg + A.h] = dB;
+            }
+        }
+    }
+}
+
+template <bool FUSED, bool AL>
+__global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ alpha, const float* __restrict__ beta, const float* __restrict__ d_o,
+    const float* __restrict__ skv, const float* __restrict__ ckpt, const float* __restrict__ qnorm,
+    const float* __restrict__ knorm, float* __restrict__ gq, float* __restrict__ gk, float* __restrict__ gv,
+    long ldx, float* __restrict__ ga, float* __restrict__ gb, long ldg, int B, int T, int H, int nslots) {
+    extern __shared__ float4 lds4[];
+    float* const lds = reinterpret_cast<float*>(lds4);
+
+    const int unit = blockIdx.x;
+    BArgs A;
+    A.q = q; A.k = k; A.v = v; A.alpha = alpha; A.beta = beta; A.d_o = d_o; A.skv = skv;
+    A.qnorm = qnorm; A.knorm = knorm; A.gq = gq; A.gk = gk; A.gv = gv; A.ga = ga; A.gb = gb;
+    A.h = unit / B;
+    A.b = unit - A.h * B;
+    A.T = T; A.H = H;
+    A.ldx = ldx; A.ldg = ldg;
+    A.d = (long)H * DH;
+    A.ubase = (long)A.b * T * A.d + (long)A.h * DH;
+    A.gbase = (long)A.b * T * H + A.h;
+    A.hoff = (long)A.h * DH;
+    A.ckb = ckpt + (long)unit * nslots * DH2;
+    A.nseg = (T + CK - 1) / CK;
+    const int nseg = A.nseg;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+
+    // every gate of the unit in the scaled range?  (the steps past T are padded in range)
+    int bad = 0;
+    for (int t = threadIdx.x; t < T; t += 2 * NT) {
+        const float a = alpha[A.gbase + (long)t * H];
+        bad |= !(a >= 0x1p-6f && a <= 0x1p6f);
+    }
+    if (__syncthreads_or(bad)) {
+        if (w < W) bwd_serial<FUSED, AL>(A, lds, w, lane);
+        else bwd_mirror(lds, nseg);
+        return;
+    }
+
+    const int rg = lane & 7, cg = lane >> 3;
+    const int rowb = BM * rg;
+    if (w < W) {
+        // adjoint waves
+        const int kc = kpos(16 * w + 2 * cg);
+        float ds[BM][2];
+#pragma unroll
+        for (int m = 0; m < BM; ++m) ds[m][0] = ds[m][1] = 0.0f;
+        lds_barrier();   // the first segment staged
+        for (int p = 0; p <= nseg; ++p) {
+            const int g = nseg - 1 - p;
+            lds_barrier();   // P0
+            if (g >= 0) {
+                const float* const buf = lds + Q_STG + (g & 1) * S_BUF;
+                const float gend = buf[S_G + 8 * (CK - 1) + 2];
+                float* const xt = lds + Q_XT + (g & 1) * DH * P;
+#pragma unroll
+                for (int n = 0; n < 2; ++n) {
+#pragma unroll
+                    for (int m = 0; m < BM; ++m) ds[m][n] *= gend;
+#pragma unroll
+                    for (int e = 0; e < BM; e += 4)
+                        *reinterpret_cast<float4*>(xt + (16 * w + 2 * cg + n) * P + rowb + e) =
+                            make_float4(ds[e][n], ds[e + 1][n], ds[e + 2][n], ds[e + 3][n]);
+                }
+                aloop(ds, buf, lds + Q_DU + (g & 1) * CK * P, lds + Q_DSK + (g & 1) * CK * P,
+                      lds + Q_AB + (g & 1) * CK * W * 2, lds + Q_BR + (g & 1) * 8, w, lane, rg, cg, rowb, kc);
+            } else {
+                lds_barrier();   // P1
+            }
+        }
+    } else {
+        // matrix waves
+        const int mw = w - W, tx = threadIdx.x - NT;
+        BStage stg;
+        bstage_load<FUSED, AL>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase, A.gbase,
+                               A.d, T, H, tx, lane);
+        bstage_store(stg, nseg - 1, T, lds + Q_STG + ((nseg - 1) & 1) * S_BUF, tx, mw, lane);
+        lds_barrier();   // the first segment staged
+        for (int p = 0; p <= nseg; ++p) {
+            const int g = nseg - 1 - p, gp = g + 1;
+            if (g >= 1)
+                bstage_load<FUSED, AL>(stg, g - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase,
+                                       A.gbase, A.d, T, H, tx, lane);
+            lds_barrier();   // P0
+            MEpi e;
+            if (gp < nseg)
+                mprod(lds + Q_STG + (gp & 1) * S_BUF, lds + Q_XT + (gp & 1) * DH * P, lds + Q_DSK + (gp & 1) * CK * P,
+                      lds, mw, lane, e);
+            lds_barrier();   // P1
+            if (gp < nseg)
+                mepi<FUSED>(A, e, lds, lds + Q_AB + (gp & 1) * CK * W * 2, lds + Q_BR + (gp & 1) * 8,
+                            lds + Q_DU + (gp & 1) * CK * P, gp, mw, lane);
+            if (g >= 1) bstage_store(stg, g - 1, T, lds + Q_STG + ((g - 1) & 1) * S_BUF, tx, mw, lane);
+        }
     }
 }
 
@@ -971,14 +1294,15 @@ static int launch_bwd64_t(const float* q, const float* k, const float* v, const 
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&d64::delta_bwd64_k<FUSED, AL>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)d64::B_LDS);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)d64::B_LDS_ALL);
         if (e != hipSuccess)
-            return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu): %s", d64::B_LDS, hipGetErrorString(e));
+            return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu): %s", d64::B_LDS_ALL, hipGetErrorString(e));
         attr = true;
     }
     int rc = pre_launch("delta_bwd64");
     if (rc) return rc;
-    hipLaunchKernelGGL((d64::delta_bwd64_k<FUSED, AL>), dim3(B * H), dim3(d64::NT), d64::B_LDS, st, q, k, v, alpha,
+    hipLaunchKernelGGL((d64::delta_bwd64_k<FUSED, AL>), dim3(B * H), dim3(2 * d64::NT), d64::B_LDS_ALL, st, q, k, v,
+                       alpha,
                        beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, ws.nslots);
     return post_launch("delta_bwd64");
 }
