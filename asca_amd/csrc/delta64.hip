@@ -1,20 +1,22 @@
-// Gated delta rule, recurrent form, f32, dh = 64, on four waves per
-// (sequence, head) unit: one wave per SIMD, 16 state elements per lane.
+// Gated delta rule, recurrent form, f32, dh = 64, one block per (sequence,
+// head) unit.
 //
 // Same math, outputs and workspace as delta.hip (DeltaBlock::scan_cpu,
 // rust/src/delta.rs:244-334, and bptt_cpu, :421-613).  When every unit has a
 // CU of its own (B*H > 128 on the 256 CUs of an MI355X), a unit's 4096 state
-// elements fill the CU's four SIMDs with one wave each, and a lane holding 16
-// elements instead of 8 halves the per-element share of all the work that is
-// not a state FMA: reductions, gate scalars, operand reads.
+// elements fill the CU's four SIMDs with one wave each (16 elements per lane,
+// which halves the per-element share of the reductions, gate scalars and
+// operand reads against 8), and a second wave on each SIMD does the block's
+// matrix products, outputs and staging beside it, so that each fills the
+// other's stalls.
 //
-//  * Forward: lane = 4c + p holds rows 16p..16p+15 of value column 16w + c, so
-//    S^T k and S^T q are two-level quad DPP sums.  Each wave builds the gate
-//    table of the next chunk (beta, 1/G, G) into LDS while the current chunk
-//    runs, and a step reads its row as one broadcast vector (no v_readlane).
-//    The k and q rows sit in LDS with row quarter p at float 20p, so the four
-//    distinct 16-byte addresses of a 16-lane read fall on four distinct bank
-//    groups.
+//  * Forward: lane = 4c + p of a state wave holds rows 16p..16p+15 of value
+//    column 16w + c, so S^T k is a two-level quad DPP sum; the k rows sit in
+//    LDS with row quarter p at float 20p, so the four distinct 16-byte
+//    addresses of a 16-lane read fall on four distinct bank groups.  The
+//    outputs o = S_j^T q_j of a 16-step chunk come from the matrix waves a
+//    chunk later, as 16-row products of the chunk's first state, its u rows
+//    and the products k . q (16x16x4 f32 MFMA).
 //  * Backward: lane (rg = lane & 7, cg = lane >> 3) holds the adjoint's rows
 //    8rg..8rg+7 of columns 16w + 2cg, +1, and a 16-step segment runs only the
 //    adjoint recurrence step by step: du = dS^T k is an 8-lane DPP sum and dS
@@ -56,84 +58,103 @@ ASCA_DEV float4 ld4(const float* __restrict__ p) {
     else return make_float4(p[0], p[1], p[2], p[3]);
 }
 
+// D += A B on a 16x16x4 f32 MFMA: lane l gives A[l % 16][l / 16] and
+// B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16] in register r.
+ASCA_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
 // ================================================================== forward
 
 constexpr int FR = 16;                       // rows per lane
 constexpr int FROW = 80;                     // padded k / q row: row quarter p at float 20p
 ASCA_DEV int fpad(int a) { return a + 4 * (a >> 4); }
-// Chunk buffer (floats): k rows [CK][FROW], q rows [CK][FROW], v rows [CK][DH],
-// one gate table per wave [W][CK][8], and a sink for the writes of lanes
-// without a table row.
+constexpr int FP = 68;                       // pitch of the state and u rows
+// Chunk staging buffer (floats): k rows [CK][FROW], q rows [CK][FROW], v rows
+// [CK][DH], one gate table per state wave [W][CK][8], the chunk's flag and a
+// sink for the writes of lanes without a table row.
 constexpr int F_K = 0;
 constexpr int F_Q = CK * FROW;
 constexpr int F_V = 2 * CK * FROW;
 constexpr int F_G = F_V + DH * CK;
-constexpr int F_SINK = F_G + W * CK * 8;
+constexpr int F_FLAG = F_G + W * CK * 8;
+constexpr int F_SINK = F_FLAG + 4;
 constexpr int F_BUF = F_SINK + 8;
 static_assert(F_BUF % 4 == 0, "float4 buffers");
+// The forward's LDS (floats): two staging buffers, then per chunk parity the
+// state before the chunk as S^T rows, the chunk's u rows (u / G_{j+1} in a
+// scaled chunk) and the matrix waves' partial products q . k.
+constexpr int F_ST = 2 * F_BUF;                  // [2][DH][FP]
+constexpr int F_U = F_ST + 2 * DH * FP;          // [2][CK][FP]
+constexpr int F_GP = F_U + 2 * CK * FP;          // [2][W][64] float4
+constexpr int F_END = F_GP + 2 * W * 64 * 4;
+constexpr size_t F_LDS = (size_t)F_END * 4;
+static_assert(F_LDS <= 160 * 1024 && F_ST % 4 == 0 && F_GP % 4 == 0, "forward LDS");
 
 struct FStage {
     float4 kq[2]; // two float4 of the chunk's k or q rows
     float4 v;     // one float4 of the chunk's v rows
-    float a, b;   // lane j (mod CK): alpha, beta of step t0 + j (1 and 0 past T)
+    float a, b;   // lane j (mod CK): alpha, beta of step t0 + j (as loaded)
 };
 
-// Global -> registers for chunk c; every lane loads (clamped addresses), so no
-// load sits under a lane condition.
+// Global -> registers for chunk c by the staging thread tx (0..NT-1); every
+// lane loads (clamped addresses), so no load sits under a lane condition.
 template <bool AL>
 ASCA_DEV void fstage_load(FStage& st, int c, const float* __restrict__ q, const float* __restrict__ k,
                           const float* __restrict__ v, const float* __restrict__ alpha,
-                          const float* __restrict__ beta, long ubase, long gbase, long d, int T, int H,
+                          const float* __restrict__ beta, long ubase, long gbase, long d, int T, int H, int tx,
                           int lane) {
     const int t0 = c * CK;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int f = threadIdx.x + NT * i;
+        const int f = tx + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
         const long t = min(t0 + j, T - 1);
         st.kq[i] = ld4<AL>((tsr ? q : k) + ubase + t * d + 4 * c4);
     }
     {
-        const int f = threadIdx.x;
-        const int j = f >> 4, c4 = f & 15;
+        const int j = tx >> 4, c4 = tx & 15;
         const long t = min(t0 + j, T - 1);
         st.v = ld4<AL>(v + ubase + t * d + 4 * c4);
     }
     {
-        const int t = t0 + (lane & (CK - 1));
-        const long tc = min(t, T - 1);
-        const float a = alpha[gbase + tc * H];
-        const float b = beta[gbase + tc * H];
-        // steps past T: alpha = 1, beta = 0 leave the state unchanged
-        st.a = t < T ? a : 1.0f;
-        st.b = t < T ? b : 0.0f;
+        // raw values: fstage_store applies the padding past T, so that no
+        // arithmetic on the loads waits for them here
+        const long tc = min(t0 + (lane & (CK - 1)), T - 1);
+        st.a = alpha[gbase + tc * H];
+        st.b = beta[gbase + tc * H];
     }
 }
 
-// Registers -> the chunk buffer; builds this wave's gate table, row j =
-// {beta_j, 1/G_{j+1}, alpha_j, 0, G_{j+1}, G_j, 0, 0}.  Returns whether every
-// alpha of the chunk lies in [2^-6, 2^6] (wave-uniform), the range in which the
-// scaled state of a 16-step chunk stays within 2^+-96 of the true one.
-ASCA_DEV bool fstage_store(const FStage& st, float* __restrict__ buf, int w, int lane) {
+// Registers -> the chunk buffer by staging thread tx of wave w; wave w builds
+// gate table w, row j = {beta_j, 1/G_{j+1}, alpha_j, 0, G_{j+1}, G_j, 0, 0}, and
+// wave 0 the flag: whether every alpha of the chunk lies in [2^-6, 2^6], the
+// range in which the scaled state of a 16-step chunk stays within 2^+-96 of
+// the true one.
+ASCA_DEV void fstage_store(const FStage& st, int c, int T, float* __restrict__ buf, int tx, int w, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int f = threadIdx.x + NT * i;
+        const int f = tx + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
         *reinterpret_cast<float4*>(buf + (tsr ? F_Q : F_K) + j * FROW + fpad(4 * c4)) = st.kq[i];
     }
     {
-        const int f = threadIdx.x;
-        const int j = f >> 4, c4 = f & 15;
+        const int j = tx >> 4, c4 = tx & 15;
         *reinterpret_cast<float4*>(buf + F_V + j * DH + 4 * c4) = st.v;
     }
+    float sa = st.a, sb = st.b;
+    asm volatile("" : "+v"(sa), "+v"(sb));   // keeps the gate arithmetic here, after the loads' wait
+    // steps past T: alpha = 1, beta = 0 leave the state unchanged
+    if (c * CK + (lane & (CK - 1)) >= T) {
+        sa = 1.0f;
+        sb = 0.0f;
+    }
     const bool gl = lane < CK;
-    const float pr = prefix_prod<CK>(gl ? st.a : 1.0f);   // G_{j+1} in lane j
-    const float pv = dpp_or<0x111>(1.0f, pr);              // G_j (row_shr 1; lane 0 keeps 1)
+    const float pr = prefix_prod<CK>(gl ? sa : 1.0f);   // G_{j+1} in lane j
+    const float pv = dpp_or<0x111>(1.0f, pr);            // G_j (row_shr 1; lane 0 keeps 1)
     float* const row = gl ? buf + F_G + (w * CK + lane) * 8 : buf + F_SINK;
-    *reinterpret_cast<float4*>(row) = make_float4(st.b, __builtin_amdgcn_rcpf(pr), st.a, 0.0f);
+    *reinterpret_cast<float4*>(row) = make_float4(sb, __builtin_amdgcn_rcpf(pr), sa, 0.0f);
     *reinterpret_cast<float2*>(row + 4) = make_float2(pr, pv);
-    const bool bad = gl && !(st.a >= 0x1p-6f && st.a <= 0x1p6f);
-    return __ballot(bad) == 0;
+    const bool bad = gl && !(sa >= 0x1p-6f && sa <= 0x1p6f);
+    *(w == 0 && lane == 0 ? buf + F_FLAG : buf + F_SINK + 3) = __ballot(bad) == 0 ? 1.0f : 0.0f;
 }
 
 ASCA_DEV void rd16(float (&x)[FR], const float* __restrict__ p) {
@@ -144,181 +165,238 @@ ASCA_DEV void rd16(float (&x)[FR], const float* __restrict__ p) {
     }
 }
 
-// The CK steps of a chunk for this lane's 16 rows (rust/src/delta.rs:289-314
-// per step), with the chunk's global stores spread over its steps: at the
-// checkpoint-wide rate of every wave a chunk's stores issued at once queue the
-// next chunk's loads behind them.  Steps 0..3 each store a quarter of the
-// checkpoint ck (the state before the chunk, as S^T) to ckdst; lane p of a
-// column's quad keeps the o and S^T k of step p + 4h and stores them after
-// step 4h + 3 (rows past nvalid go to the trash), except the last group's,
-// which it returns in last_o / last_sk (already rescaled) for the caller to
-// store once the next chunk's loads are queued: loads and stores complete in
-// order, and a load queued behind a fresh store waits for it.
-//   SC = false: s is the state; S <- alpha S + k u^T.
-//   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta (v / G_{j+1} - x) and
-//     s <- s + k (u / G_{j+1})^T (one FMA per element); o and S^T k are
-//     rescaled by G_{j+1} and G_j at their store.
-template <bool SC>
-ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float* __restrict__ gt,
-                     const float (&vv)[CK], int p, const float (&ck)[FR], float* __restrict__ ckdst,
-                     float* __restrict__ od, float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr,
-                     float& last_o, float& last_sk) {
-    const float* const kr = buf + F_K + fpad(16 * p);
-    const float* const qr = buf + F_Q + fpad(16 * p);
-    float kk[2][FR], qq[2][FR];
-    float4 gg[2];
-    float2 gs = make_float2(1.0f, 1.0f);   // G_{jj+1}, G_jj of this lane's step jj = p + 4h
-    float ho = 0.0f, hs = 0.0f;
-    rd16(kk[0], kr);
-    rd16(qq[0], qr);
-    gg[0] = *reinterpret_cast<const float4*>(gt);
-#pragma unroll
-    for (int j = 0; j < CK; ++j) {
-        const int cs = j & 1;
-        if (j + 1 < CK) {
-            rd16(kk[cs ^ 1], kr + (j + 1) * FROW);
-            rd16(qq[cs ^ 1], qr + (j + 1) * FROW);
-            gg[cs ^ 1] = *reinterpret_cast<const float4*>(gt + (j + 1) * 8);
-        }
-        if (SC && (j & 3) == 0) gs = *reinterpret_cast<const float2*>(gt + (p + j) * 8 + 4);
-        if (j < FR / 4)
-            *reinterpret_cast<float4*>(ckdst + 4 * j) = make_float4(ck[4 * j], ck[4 * j + 1], ck[4 * j + 2], ck[4 * j + 3]);
-        // one wave per SIMD: nothing else hides LDS latency, so the reads of
-        // step j + 1 stay at the top of step j, a whole step ahead of their use
-        __builtin_amdgcn_sched_barrier(0);
-        const float4 g = gg[cs];
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-        for (int m = 0; m < FR; m += 2) {
-            a0 = fmaf(s[m], kk[cs][m], a0);
-            a1 = fmaf(s[m + 1], kk[cs][m + 1], a1);
-        }
-        const float x = group_sum<4>(a0 + a1);
-        float o0 = 0.0f, o1 = 0.0f;
-        if constexpr (SC) {
-            const float ut = g.x * fmaf(vv[j], g.y, -x);
-#pragma unroll
-            for (int m = 0; m < FR; m += 2) {
-                s[m] = fmaf(kk[cs][m], ut, s[m]);
-                s[m + 1] = fmaf(kk[cs][m + 1], ut, s[m + 1]);
-                o0 = fmaf(s[m], qq[cs][m], o0);
-                o1 = fmaf(s[m + 1], qq[cs][m + 1], o1);
-            }
-        } else {
-            const float a = g.z;
-            const float u = g.x * (vv[j] - a * x);
-#pragma unroll
-            for (int m = 0; m < FR; m += 2) {
-                s[m] = a * s[m] + kk[cs][m] * u;
-                s[m + 1] = a * s[m + 1] + kk[cs][m + 1] * u;
-                o0 = fmaf(s[m], qq[cs][m], o0);
-                o1 = fmaf(s[m + 1], qq[cs][m + 1], o1);
-            }
-        }
-        const float oo = group_sum<4>(o0 + o1);
-        const bool mine = p == (j & 3);
-        ho = mine ? oo : ho;
-        hs = mine ? x : hs;
-        if ((j & 3) == 3 && j + 1 < CK) {
-            const int jj = p + (j & ~3);
-            const bool ok = jj < nvalid;
-            *(ok ? od + jj * d : tr) = SC ? ho * gs.x : ho;
-            *(ok ? skd + jj * d : tr + 1) = SC ? hs * gs.y : hs;
-        }
-        if (j + 1 == CK) {
-            last_o = SC ? ho * gs.x : ho;
-            last_sk = SC ? hs * gs.y : hs;
-        }
-    }
-}
-
 ASCA_DEV void store_state(float* __restrict__ dst, const float (&s)[FR]) {
 #pragma unroll
     for (int e = 0; e < FR; e += 4)
         *reinterpret_cast<float4*>(dst + e) = make_float4(s[e], s[e + 1], s[e + 2], s[e + 3]);
 }
 
+// State waves: the CK steps of a chunk for this lane's 16 rows of column col
+// (rust/src/delta.rs:289-314 per step, without the output o), with P1 between
+// steps CK/2 - 1 and CK/2.  Step j writes its u row (u / G_{j+1} when scaled)
+// for the matrix waves; steps 0..3 each store a quarter of the checkpoint ck
+// (the state before the chunk, as S^T); lane p of a column's quad keeps the
+// S^T k of step p + 4h and stores it after step 4h + 3 (rows past nvalid go
+// to the trash).
+//   SC = false: s is the state; S <- alpha S + k u^T.
+//   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta (v / G_{j+1} - x) and
+//     s <- s + k (u / G_{j+1})^T (one FMA per element); S^T k is rescaled by
+//     G_j at its store.
+template <bool SC>
+ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float* __restrict__ gt,
+                     const float (&vv)[CK], int p, int col, const float (&ck)[FR], float* __restrict__ ckdst,
+                     float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr, float* __restrict__ ub) {
+    const float* const kr = buf + F_K + fpad(16 * p);
+    float kk[2][FR];
+    float4 gg[2];
+    float gs = 1.0f;   // G_jj of this lane's step jj = p + 4h
+    float hs = 0.0f;
+    rd16(kk[0], kr);
+    gg[0] = *reinterpret_cast<const float4*>(gt);
+#pragma unroll
+    for (int j = 0; j < CK; ++j) {
+        const int cs = j & 1;
+        if (j + 1 < CK) {
+            rd16(kk[cs ^ 1], kr + (j + 1) * FROW);
+            gg[cs ^ 1] = *reinterpret_cast<const float4*>(gt + (j + 1) * 8);
+        }
+        if (SC && (j & 3) == 0) gs = gt[(p + j) * 8 + 5];
+        if (j < FR / 4)
+            *reinterpret_cast<float4*>(ckdst + 4 * j) = make_float4(ck[4 * j], ck[4 * j + 1], ck[4 * j + 2], ck[4 * j + 3]);
+        // the reads of step j + 1 stay at the top of step j, a whole step ahead
+        // of their use (without the fence the two k buffers are merged and each
+        // step waits for its own reads)
+        __builtin_amdgcn_sched_barrier(0);
+        const float4 g = gg[cs];
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < FR; m += 4) {
+            a0 = fmaf(s[m], kk[cs][m], a0);
+            a1 = fmaf(s[m + 1], kk[cs][m + 1], a1);
+            a2 = fmaf(s[m + 2], kk[cs][m + 2], a2);
+            a3 = fmaf(s[m + 3], kk[cs][m + 3], a3);
+        }
+        const float x = group_sum<4>((a0 + a1) + (a2 + a3));
+        float uw;
+        if constexpr (SC) {
+            uw = g.x * fmaf(vv[j], g.y, -x);
+#pragma unroll
+            for (int m = 0; m < FR; ++m) s[m] = fmaf(kk[cs][m], uw, s[m]);
+        } else {
+            const float a = g.z;
+            uw = g.x * (vv[j] - a * x);
+#pragma unroll
+            for (int m = 0; m < FR; ++m) s[m] = a * s[m] + kk[cs][m] * uw;
+        }
+        ub[j * FP + col] = uw;   // the quad's four lanes store the same value
+        hs = p == (j & 3) ? x : hs;
+        if ((j & 3) == 3) {
+            const int jj = p + (j & ~3);
+            *(jj < nvalid ? skd + jj * d : tr) = SC ? hs * gs : hs;
+        }
+        if (j == CK / 2 - 1) lds_barrier();   // P1
+    }
+}
+
+// Matrix wave mw: the outputs o of one chunk for the columns 16 mw .. 16 mw +
+// 15 of every step, rows j:
+//   scaled chunk: o = G_{j+1} (S^T q_j + sum_{l <= j} u~_l (k_l . q_j))
+//   plain chunk:  o = G_{j+1} S^T q_j + sum_{l <= j} Gamma_{jl} u_l (k_l . q_j)
+// with S the state before the chunk, G_{j+1} the product of the chunk's alpha
+// up to step j and Gamma_{jl} that from step l + 1 to j (both formed by
+// multiplication only).  S^T q runs on the matrix cores (16x16x4 f32 MFMA) from
+// the q rows and the state's rows; the 16 x 16 products k_l . q_j arrive as
+// per-wave partials (fgram, a chunk earlier) in exactly the lane layout the
+// step mix takes as its operand.
+ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st, const float* __restrict__ ub,
+                    const float4* __restrict__ gpart, int mw, int lane, float* __restrict__ od, long d, int nvalid,
+                    float* __restrict__ tr) {
+    const int jr = lane & 15, gq = lane >> 4;
+    const bool sc = buf[F_FLAG] == 1.0f;
+    const float* const gt = buf + F_G;   // gate table 0
+    // k_l . q_jr for l = 4 r + gq, masked to l <= jr (plain: times Gamma)
+    float4 gm = gpart[lane];
+#pragma unroll
+    for (int v4 = 1; v4 < W; ++v4) {
+        const float4 y = gpart[v4 * 64 + lane];
+        gm.x += y.x; gm.y += y.y; gm.z += y.z; gm.w += y.w;
+    }
+    float am[4] = {gm.x, gm.y, gm.z, gm.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int l = 4 * r + gq;
+        if (!sc) {
+            float x = 1.0f;
+#pragma unroll
+            for (int m = 1; m < CK; ++m) x *= (m > l && m <= jr) ? gt[m * 8 + 2] : 1.0f;
+            am[r] *= x;
+        }
+        am[r] = l <= jr ? am[r] : 0.0f;
+    }
+    f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1;
+    // S^T q: k index a = 16 m + 4 gq + e (e = 0..3), both operands as 16-byte vectors
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float4 x = *reinterpret_cast<const float4*>(buf + F_Q + jr * FROW + fpad(16 * m + 4 * gq));
+        const float4 y = *reinterpret_cast<const float4*>(st + (16 * mw + jr) * FP + 16 * m + 4 * gq);
+        a1 = mfma4(x.x, y.x, a1);
+        a1 = mfma4(x.y, y.y, a1);
+        a1 = mfma4(x.z, y.z, a1);
+        a1 = mfma4(x.w, y.w, a1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a2 = mfma4(am[r], ub[(4 * r + gq) * FP + 16 * mw + jr], a2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int j = 4 * gq + r;
+        const float g1 = gt[j * 8 + 4];
+        const float ov = sc ? g1 * (a1[r] + a2[r]) : fmaf(g1, a1[r], a2[r]);
+        *(j < nvalid ? od + j * d + 16 * mw + jr : tr + r) = ov;
+    }
+}
+
+// Matrix wave mw: its partial of the products k_l . q_j of a chunk over the
+// rows a = 16 mw .. 16 mw + 15, as D = K_pi Q^T with pi(m) = 4 (m & 3) + m / 4,
+// so that lane (gq, jr) register r holds k_{4r+gq} . q_jr.
+ASCA_DEV void fgram(const float* __restrict__ buf, float4* __restrict__ gpart, int mw, int lane) {
+    const int jr = lane & 15, gq = lane >> 4;
+    const int pj = 4 * (jr & 3) + (jr >> 2);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const int a = fpad(16 * mw + 4 * kb + gq);
+        acc = mfma4(buf[F_K + pj * FROW + a], buf[F_Q + jr * FROW + a], acc);
+    }
+    gpart[mw * 64 + lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
 // One block per unit = h*B + b (the reference's s_pre order,
-// rust/src/delta.rs:54-56).
+// rust/src/delta.rs:54-56), as a two-stage pipeline over chunks: in period c
+// the state waves (0..3) run chunk c while the matrix waves (4..7) form the
+// outputs of chunk c - 1, the partial products k . q of chunk c and stage chunk
+// c + 1.  Two block barriers per period: P0 at its start and P1 halfway
+// through the chunk, after which the matrix waves restage the buffer of chunk
+// c - 1.  One state wave and one matrix wave share each SIMD.
 template <bool AL>
-__global__ __launch_bounds__(NT) void delta_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
-                                                    const float* __restrict__ v, const float* __restrict__ alpha,
-                                                    const float* __restrict__ beta, float* __restrict__ o,
-                                                    float* __restrict__ sk_out, float* __restrict__ ckpt, int B,
-                                                    int T, int H, int nslots) {
-    __shared__ float4 lds4[2 * F_BUF / 4];
+__global__ __launch_bounds__(2 * NT) void delta_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, const float* __restrict__ alpha,
+                                                        const float* __restrict__ beta, float* __restrict__ o,
+                                                        float* __restrict__ sk_out, float* __restrict__ ckpt, int B,
+                                                        int T, int H, int nslots) {
+    extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
     const int unit = blockIdx.x;
     const int h = unit / B, b = unit - h * B;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int c = lane >> 2, p = lane & 3;
-    const int col = 16 * w + c;
     const long d = (long)H * DH;
     const long ubase = (long)b * T * d + (long)h * DH;
     const long gbase = (long)b * T * H + h;
-    float* const ckb = ckpt + (long)unit * nslots * DH2 + col * DH + 16 * p;
-    float* const tr = trash(threadIdx.x * 8);
     const int nchunk = (T + CK - 1) / CK;
+    float* const tr = trash((threadIdx.x & (NT - 1)) * 8);
 
-    float s[FR];
+    if (w < W) {
+        // state waves
+        const int c = lane >> 2, p = lane & 3;
+        const int col = 16 * w + c;
+        float* const ckb = ckpt + (long)unit * nslots * DH2 + col * DH + 16 * p;
+        float s[FR];
 #pragma unroll
-    for (int m = 0; m < FR; ++m) s[m] = 0.0f;
-
-    // Staged loads run two chunks ahead (the loads of chunk ci + 2 are queued
-    // at the start of chunk ci, into the register set that chunk ci + 1's data
-    // has just left for LDS), so each has two chunks of compute to arrive.
-    FStage sa, sb;
-    fstage_load<AL>(sa, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
-    bool sc_next = fstage_store(sa, lds, w, lane);
-    fstage_load<AL>(sa, min(1, nchunk - 1), q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
-    lds_barrier();
-
-    // the last output group of the previous chunk, stored after this chunk's loads
-    float* pend_o = tr;
-    float* pend_sk = tr + 1;
-    float last_o = 0.0f, last_sk = 0.0f;
-    // chunk ci: `cur` holds chunk ci + 1 (stored to LDS at the end), `nxt` is
-    // loaded with chunk ci + 2
-    auto chunk = [&](int ci, FStage& cur, FStage& nxt) {
-        const int t0 = ci * CK;
-        const float* const buf = lds + (ci & 1) * F_BUF;
-        const float* const gt = buf + F_G + w * CK * 8;
-        const bool sc = sc_next;
-        fstage_load<AL>(nxt, min(ci + 2, nchunk - 1), q, k, v, alpha, beta, ubase, gbase, d, T, H, lane);
-        *pend_o = last_o;
-        *pend_sk = last_sk;
-        float vv[CK];
+        for (int m = 0; m < FR; ++m) s[m] = 0.0f;
+        lds_barrier();   // chunk 0 staged
+        for (int ci = 0; ci <= nchunk; ++ci) {
+            lds_barrier();   // P0
+            if (ci == nchunk) {
+                lds_barrier();   // P1
+                break;
+            }
+            const int t0 = ci * CK;
+            const float* const buf = lds + (ci & 1) * F_BUF;
+            const float* const gt = buf + F_G + w * CK * 8;
+            const bool sc = __builtin_amdgcn_readfirstlane(__float_as_int(buf[F_FLAG])) == __float_as_int(1.0f);
+            float vv[CK];
 #pragma unroll
-        for (int j = 0; j < CK; ++j) vv[j] = buf[F_V + j * DH + col];
-        float ck[FR];   // the checkpoint: S before step t0
+            for (int j = 0; j < CK; ++j) vv[j] = buf[F_V + j * DH + col];
+            float ck[FR];   // the checkpoint: S before step t0
 #pragma unroll
-        for (int m = 0; m < FR; ++m) ck[m] = s[m];
-        float* const od = o + ubase + (long)t0 * d + col;
-        float* const skd = sk_out + ubase + (long)t0 * d + col;
-        if (sc) {
-            fsteps<true>(s, buf, gt, vv, p, ck, ckb + (long)ci * DH2, od, skd, d, T - t0, tr, last_o, last_sk);
-            const float ge = gt[(CK - 1) * 8 + 4];
+            for (int m = 0; m < FR; ++m) ck[m] = s[m];
+            store_state(lds + F_ST + (ci & 1) * DH * FP + col * FP + 16 * p, s);
+            float* const skd = sk_out + ubase + (long)t0 * d + col;
+            float* const ub = lds + F_U + (ci & 1) * CK * FP;
+            if (sc) {
+                fsteps<true>(s, buf, gt, vv, p, col, ck, ckb + (long)ci * DH2, skd, d, T - t0, tr, ub);
+                const float ge = gt[(CK - 1) * 8 + 4];
 #pragma unroll
-            for (int m = 0; m < FR; ++m) s[m] *= ge;
-        } else {
-            fsteps<false>(s, buf, gt, vv, p, ck, ckb + (long)ci * DH2, od, skd, d, T - t0, tr, last_o, last_sk);
+                for (int m = 0; m < FR; ++m) s[m] *= ge;
+            } else {
+                fsteps<false>(s, buf, gt, vv, p, col, ck, ckb + (long)ci * DH2, skd, d, T - t0, tr, ub);
+            }
         }
-        {
-            const int jj = p + CK - 4;
-            const bool ok = jj < T - t0;
-            pend_o = ok ? od + jj * d : tr;
-            pend_sk = ok ? skd + jj * d : tr + 1;
+        store_state(ckb + (long)nchunk * DH2, s);   // the state after step T-1
+    } else {
+        // matrix waves
+        const int mw = w - W, tx = threadIdx.x - NT;
+        FStage stg;
+        fstage_load<AL>(stg, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
+        fstage_store(stg, 0, T, lds, tx, mw, lane);
+        // the loads of chunk ci + 1 are issued right after P1 of period ci - 1,
+        // a whole period ahead of their store
+        if (nchunk > 1) fstage_load<AL>(stg, 1, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
+        lds_barrier();   // chunk 0 staged
+        for (int ci = 0; ci <= nchunk; ++ci) {
+            lds_barrier();   // P0
+            if (ci < nchunk)
+                fgram(lds + (ci & 1) * F_BUF, reinterpret_cast<float4*>(lds + F_GP) + (ci & 1) * W * 64, mw, lane);
+            if (ci > 0) {
+                const int cp = ci - 1;
+                fprod(lds + (cp & 1) * F_BUF, lds + F_ST + (cp & 1) * DH * FP, lds + F_U + (cp & 1) * CK * FP,
+                      reinterpret_cast<const float4*>(lds + F_GP) + (cp & 1) * W * 64, mw, lane,
+                      o + ubase + (long)cp * CK * d, d, T - cp * CK, tr);
+            }
+            lds_barrier();   // P1
+            if (ci + 1 < nchunk) fstage_store(stg, ci + 1, T, lds + ((ci + 1) & 1) * F_BUF, tx, mw, lane);
+            if (ci + 2 < nchunk) fstage_load<AL>(stg, ci + 2, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
         }
-        sc_next = fstage_store(cur, lds + ((ci + 1) & 1) * F_BUF, w, lane);
-        lds_barrier();
-    };
-    for (int ci = 0; ci < nchunk; ci += 2) {
-        chunk(ci, sa, sb);
-        if (ci + 1 < nchunk) chunk(ci + 1, sb, sa);
     }
-    *pend_o = last_o;
-    *pend_sk = last_sk;
-    store_state(ckb + (long)nchunk * DH2, s);   // the state after step T-1
 }
 
 // ================================================================= backward
@@ -335,7 +413,6 @@ ASCA_DEV int rpad(int r) { return r + 4 * (r >> 5); }
 ASCA_DEV int kpos(int i) { return 16 * ((i >> 2) & 3) + 4 * (i >> 4) + (i & 3); }
 ASCA_DEV int kcol(int g, int kb) { return 16 * (kb >> 2) + 4 * g + (kb & 3); }
 
-ASCA_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
 // Segment staging buffer (floats), written while the previous segment runs:
 constexpr int S_Q = 0;                   // [CK][P] q rows
@@ -1244,22 +1321,28 @@ __global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
         bstage_load<FUSED, AL>(stg, nseg - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase, A.gbase,
                                A.d, T, H, tx, lane);
         bstage_store(stg, nseg - 1, T, lds + Q_STG + ((nseg - 1) & 1) * S_BUF, tx, mw, lane);
+        // the loads of segment g - 1 are issued right after P1 of the period
+        // before (of segment g + 1), a whole period ahead of their store, and
+        // ahead of that period's epilogue stores
+        if (nseg > 1)
+            bstage_load<FUSED, AL>(stg, nseg - 2, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase,
+                                   A.gbase, A.d, T, H, tx, lane);
         lds_barrier();   // the first segment staged
         for (int p = 0; p <= nseg; ++p) {
             const int g = nseg - 1 - p, gp = g + 1;
-            if (g >= 1)
-                bstage_load<FUSED, AL>(stg, g - 1, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase,
-                                       A.gbase, A.d, T, H, tx, lane);
             lds_barrier();   // P0
             MEpi e;
             if (gp < nseg)
                 mprod(lds + Q_STG + (gp & 1) * S_BUF, lds + Q_XT + (gp & 1) * DH * P, lds + Q_DSK + (gp & 1) * CK * P,
                       lds, mw, lane, e);
             lds_barrier();   // P1
+            if (g >= 1) bstage_store(stg, g - 1, T, lds + Q_STG + ((g - 1) & 1) * S_BUF, tx, mw, lane);
+            if (g >= 2)
+                bstage_load<FUSED, AL>(stg, g - 2, q, k, v, d_o, skv, alpha, beta, qnorm, knorm, A.ckb, A.ubase,
+                                       A.gbase, A.d, T, H, tx, lane);
             if (gp < nseg)
                 mepi<FUSED>(A, e, lds, lds + Q_AB + (gp & 1) * CK * W * 2, lds + Q_BR + (gp & 1) * 8,
                             lds + Q_DU + (gp & 1) * CK * P, gp, mw, lane);
-            if (g >= 1) bstage_store(stg, g - 1, T, lds + Q_STG + ((g - 1) & 1) * S_BUF, tx, mw, lane);
         }
     }
 }
@@ -1269,10 +1352,18 @@ __global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
 template <bool AL>
 static int launch_fwd64_t(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
                           float* o, const DeltaWs& ws, int B, int T, int H, hipStream_t st) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&d64::delta_fwd64_k<AL>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)d64::F_LDS);
+        if (e != hipSuccess)
+            return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu): %s", d64::F_LDS, hipGetErrorString(e));
+        attr = true;
+    }
     int rc = pre_launch("delta_fwd64");
     if (rc) return rc;
-    hipLaunchKernelGGL(d64::delta_fwd64_k<AL>, dim3(B * H), dim3(d64::NT), 0, st, q, k, v, alpha, beta, o, ws.sk,
-                       ws.ckpt, B, T, H, ws.nslots);
+    hipLaunchKernelGGL(d64::delta_fwd64_k<AL>, dim3(B * H), dim3(2 * d64::NT), d64::F_LDS, st, q, k, v, alpha, beta, o,
+                       ws.sk, ws.ckpt, B, T, H, ws.nslots);
     return post_launch("delta_fwd64");
 }
 
@@ -1302,8 +1393,7 @@ static int launch_bwd64_t(const float* q, const float* k, const float* v, const 
     int rc = pre_launch("delta_bwd64");
     if (rc) return rc;
     hipLaunchKernelGGL((d64::delta_bwd64_k<FUSED, AL>), dim3(B * H), dim3(2 * d64::NT), d64::B_LDS_ALL, st, q, k, v,
-                       alpha,
-                       beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, ws.nslots);
+                       alpha, beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, ws.nslots);
     return post_launch("delta_bwd64");
 }
 
