@@ -64,21 +64,24 @@ ASCA_DEV f32x4 mfma4(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f
 
 // ================================================================== forward
 
-constexpr int FR = 16;                       // rows per lane
-constexpr int FROW = 80;                     // padded k / q row: row quarter p at float 20p
-ASCA_DEV int fpad(int a) { return a + 4 * (a >> 4); }
-constexpr int FP = 68;                       // pitch of the state and u rows
-// Chunk staging buffer (floats): k rows [CK][FROW], q rows [CK][FROW], v rows
-// [CK][DH], one gate table per state wave [W][CK][8], the chunk's flag and a
-// sink for the writes of lanes without a table row.
+constexpr int SW = 8;                        // state waves of the forward
+constexpr int FNT = 64 * (SW + W);           // forward block: SW state waves, then W matrix waves
+// Pitch of every 64-float row in the forward's LDS (k, q, the state's S^T rows,
+// u): 68 = 4 mod 32, so the 16-byte reads of eight consecutive rows at one
+// offset, or of one row at eight consecutive offsets, fall on distinct banks.
+constexpr int FP = 68;
+// Chunk staging buffer (floats): k rows [CK][FP], q rows [CK][FP], the rows
+// beta_j v_j (divided by G_{j+1} in a scaled chunk) [CK][DH] for the state
+// waves, one gate table per matrix wave [W][CK][8], the chunk's flag and a sink
+// for the writes of lanes without a table row.
 constexpr int F_K = 0;
-constexpr int F_Q = CK * FROW;
-constexpr int F_V = 2 * CK * FROW;
+constexpr int F_Q = CK * FP;
+constexpr int F_V = 2 * CK * FP;
 constexpr int F_G = F_V + DH * CK;
 constexpr int F_FLAG = F_G + W * CK * 8;
 constexpr int F_SINK = F_FLAG + 4;
 constexpr int F_BUF = F_SINK + 8;
-static_assert(F_BUF % 4 == 0, "float4 buffers");
+static_assert(F_BUF % 4 == 0 && F_V % 4 == 0, "float4 buffers");
 // The forward's LDS (floats): two staging buffers, then per chunk parity the
 // state before the chunk as S^T rows, the chunk's u rows (u / G_{j+1} in a
 // scaled chunk) and the matrix waves' partial products q . k.
@@ -95,20 +98,21 @@ struct FStage {
     float a, b;   // lane j (mod CK): alpha, beta of step t0 + j (as loaded)
 };
 
-// Global -> registers for chunk c by the staging thread tx (0..NT-1); every
-// lane loads (clamped addresses), so no load sits under a lane condition.
+// Global -> registers for chunk c by the staging thread tx (0..NT-1) of matrix
+// wave w = tx / 64, which stages the k and q columns 16 w .. 16 w + 15 of every
+// step (the ones its own products fgram read); every lane loads (clamped
+// addresses), so no load sits under a lane condition.
 template <bool AL>
 ASCA_DEV void fstage_load(FStage& st, int c, const float* __restrict__ q, const float* __restrict__ k,
                           const float* __restrict__ v, const float* __restrict__ alpha,
                           const float* __restrict__ beta, long ubase, long gbase, long d, int T, int H, int tx,
                           int lane) {
     const int t0 = c * CK;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int f = tx + NT * i;
-        const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
+    {
+        const int j = lane >> 2, c4 = 4 * (tx >> 6) + (lane & 3);
         const long t = min(t0 + j, T - 1);
-        st.kq[i] = ld4<AL>((tsr ? q : k) + ubase + t * d + 4 * c4);
+        st.kq[0] = ld4<AL>(k + ubase + t * d + 4 * c4);
+        st.kq[1] = ld4<AL>(q + ubase + t * d + 4 * c4);
     }
     {
         const int j = tx >> 4, c4 = tx & 15;
@@ -124,21 +128,17 @@ ASCA_DEV void fstage_load(FStage& st, int c, const float* __restrict__ q, const 
     }
 }
 
-// Registers -> the chunk buffer by staging thread tx of wave w; wave w builds
-// gate table w, row j = {beta_j, 1/G_{j+1}, alpha_j, 0, G_{j+1}, G_j, 0, 0}, and
-// wave 0 the flag: whether every alpha of the chunk lies in [2^-6, 2^6], the
-// range in which the scaled state of a 16-step chunk stays within 2^+-96 of
-// the true one.
+// Registers -> the chunk buffer by staging thread tx of matrix wave w; wave w
+// builds gate table w, row j = {beta_j, 1/G_{j+1}, alpha_j, alpha_j beta_j,
+// G_{j+1}, G_j, 0, 0}, and wave 0 the flag: whether every alpha of the chunk
+// lies in [2^-6, 2^6], the range in which the scaled state of a 16-step chunk
+// stays within 2^+-96 of the true one.  The state waves' v rows carry beta_j
+// (and 1/G_{j+1} when the chunk is scaled) already.
 ASCA_DEV void fstage_store(const FStage& st, int c, int T, float* __restrict__ buf, int tx, int w, int lane) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int f = tx + NT * i;
-        const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
-        *reinterpret_cast<float4*>(buf + (tsr ? F_Q : F_K) + j * FROW + fpad(4 * c4)) = st.kq[i];
-    }
     {
-        const int j = tx >> 4, c4 = tx & 15;
-        *reinterpret_cast<float4*>(buf + F_V + j * DH + 4 * c4) = st.v;
+        const int j = lane >> 2, c4 = 4 * w + (lane & 3);
+        *reinterpret_cast<float4*>(buf + F_K + j * FP + 4 * c4) = st.kq[0];
+        *reinterpret_cast<float4*>(buf + F_Q + j * FP + 4 * c4) = st.kq[1];
     }
     float sa = st.a, sb = st.b;
     asm volatile("" : "+v"(sa), "+v"(sb));   // keeps the gate arithmetic here, after the loads' wait
@@ -150,89 +150,108 @@ ASCA_DEV void fstage_store(const FStage& st, int c, int T, float* __restrict__ b
     const bool gl = lane < CK;
     const float pr = prefix_prod<CK>(gl ? sa : 1.0f);   // G_{j+1} in lane j
     const float pv = dpp_or<0x111>(1.0f, pr);            // G_j (row_shr 1; lane 0 keeps 1)
+    const float rp = __builtin_amdgcn_rcpf(pr);
     float* const row = gl ? buf + F_G + (w * CK + lane) * 8 : buf + F_SINK;
-    *reinterpret_cast<float4*>(row) = make_float4(sb, __builtin_amdgcn_rcpf(pr), sa, 0.0f);
+    *reinterpret_cast<float4*>(row) = make_float4(sb, rp, sa, sa * sb);
     *reinterpret_cast<float2*>(row + 4) = make_float2(pr, pv);
     const bool bad = gl && !(sa >= 0x1p-6f && sa <= 0x1p6f);
-    *(w == 0 && lane == 0 ? buf + F_FLAG : buf + F_SINK + 3) = __ballot(bad) == 0 ? 1.0f : 0.0f;
-}
-
-ASCA_DEV void rd16(float (&x)[FR], const float* __restrict__ p) {
-#pragma unroll
-    for (int e = 0; e < FR; e += 4) {
-        const float4 y = *reinterpret_cast<const float4*>(p + fpad(e));
-        x[e] = y.x; x[e + 1] = y.y; x[e + 2] = y.z; x[e + 3] = y.w;
+    const bool scal = __ballot(bad) == 0;
+    *(w == 0 && lane == 0 ? buf + F_FLAG : buf + F_SINK + 3) = scal ? 1.0f : 0.0f;
+    {
+        // row j of v times beta_j (over G_{j+1} when scaled), the factor taken
+        // from lane j of this wave
+        const int j = tx >> 4, c4 = tx & 15;
+        const float fj = __shfl(scal ? sb * rp : sb, j);
+        *reinterpret_cast<float4*>(buf + F_V + j * DH + 4 * c4) =
+            make_float4(st.v.x * fj, st.v.y * fj, st.v.z * fj, st.v.w * fj);
     }
 }
 
-ASCA_DEV void store_state(float* __restrict__ dst, const float (&s)[FR]) {
-#pragma unroll
-    for (int e = 0; e < FR; e += 4)
-        *reinterpret_cast<float4*>(dst + e) = make_float4(s[e], s[e + 1], s[e + 2], s[e + 3]);
+// Sum over the 16 lanes of each lane row of a state wave that hold one column:
+// x0 is the lane's partial of its own column, x1 that of the other column of
+// its pair, whose own lanes sit 8 lanes away (row_ror 8).  The result is
+// bitwise identical in the 8 lanes that own the column.
+ASCA_DEV float col_sum(float x0, float x1) {
+    float x = x0 + dpp<DPP_ROW_ROR8>(x1);
+    x += dpp<DPP_QUAD_XOR1>(x);
+    x += dpp<DPP_QUAD_XOR2>(x);
+    x += dpp<DPP_HALF_MIRROR>(x);   // valid: quad-uniform
+    return x;
 }
 
-// State waves: the CK steps of a chunk for this lane's 16 rows of column col
-// (rust/src/delta.rs:289-314 per step, without the output o), with P1 between
-// steps CK/2 - 1 and CK/2.  Step j writes its u row (u / G_{j+1} when scaled)
-// for the matrix waves; steps 0..3 each store a quarter of the checkpoint ck
-// (the state before the chunk, as S^T); lane p of a column's quad keeps the
-// S^T k of step p + 4h and stores it after step 4h + 3 (rows past nvalid go
-// to the trash).
-//   SC = false: s is the state; S <- alpha S + k u^T.
-//   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta (v / G_{j+1} - x) and
+ASCA_DEV void st4(float* __restrict__ dst, float a, float b, float c, float e) {
+    *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, e);
+}
+
+// State wave w (0..SW-1), lane = 16 cp + 8 n + r: rows 4 rg .. 4 rg + 3 (rg =
+// lane & 15) of the column pair 8 w + 2 cp, + 1.  The lane's own column is 8 w +
+// 2 cp + n (s[m][0]), the other one s[m][1]; the 16 lanes of a lane row hold
+// all 64 rows of both columns.  The CK steps of a chunk (rust/src/delta.rs:
+// 289-314 per step, without the output o), with P1 between steps CK/2 - 1 and
+// CK/2.  Step j writes the own column's u (u / G_{j+1} when scaled) to its u
+// row for the matrix waves; steps 0 and 1 store the lane's part of the
+// checkpoint ck (the state before the chunk, as S^T) of the own and the other
+// column; lane r of a column keeps the S^T k of step r + 8h and stores it after
+// step 8h + 7 (rows past nvalid go to the trash).  The gates arrive
+// lane-distributed (lane j of each lane row: step j) and are read out with
+// v_readlane.
+//   SC = false: s is the state; u = beta v - alpha beta x, S <- alpha S + k u^T.
+//   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta v / G_{j+1} - beta x and
 //     s <- s + k (u / G_{j+1})^T (one FMA per element); S^T k is rescaled by
 //     G_j at its store.
 template <bool SC>
-ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float* __restrict__ gt,
-                     const float (&vv)[CK], int p, int col, const float (&ck)[FR], float* __restrict__ ckdst,
-                     float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr, float* __restrict__ ub) {
-    const float* const kr = buf + F_K + fpad(16 * p);
-    float kk[2][FR];
-    float4 gg[2];
-    float gs = 1.0f;   // G_jj of this lane's step jj = p + 4h
+ASCA_DEV void fsteps(float (&s)[4][2], const float* __restrict__ ks, const float (&vb)[CK], float gb, float ga,
+                     float gab, const float (&ck)[4][2], float* __restrict__ ck0, float* __restrict__ ck1,
+                     float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr, float* __restrict__ ub,
+                     int r, const float (&gsk)[2]) {
+    float4 kk[2];
     float hs = 0.0f;
-    rd16(kk[0], kr);
-    gg[0] = *reinterpret_cast<const float4*>(gt);
+    kk[0] = *reinterpret_cast<const float4*>(ks);
 #pragma unroll
     for (int j = 0; j < CK; ++j) {
         const int cs = j & 1;
-        if (j + 1 < CK) {
-            rd16(kk[cs ^ 1], kr + (j + 1) * FROW);
-            gg[cs ^ 1] = *reinterpret_cast<const float4*>(gt + (j + 1) * 8);
-        }
-        if (SC && (j & 3) == 0) gs = gt[(p + j) * 8 + 5];
-        if (j < FR / 4)
-            *reinterpret_cast<float4*>(ckdst + 4 * j) = make_float4(ck[4 * j], ck[4 * j + 1], ck[4 * j + 2], ck[4 * j + 3]);
-        // the reads of step j + 1 stay at the top of step j, a whole step ahead
-        // of their use (without the fence the two k buffers are merged and each
-        // step waits for its own reads)
+        if (j + 1 < CK) kk[cs ^ 1] = *reinterpret_cast<const float4*>(ks + (j + 1) * FP);
+        if (j == 0) st4(ck0, ck[0][0], ck[1][0], ck[2][0], ck[3][0]);
+        if (j == 1) st4(ck1, ck[0][1], ck[1][1], ck[2][1], ck[3][1]);
+        // the read of step j + 1 stays at the top of step j, a whole step ahead
+        // of its use
         __builtin_amdgcn_sched_barrier(0);
-        const float4 g = gg[cs];
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-        for (int m = 0; m < FR; m += 4) {
-            a0 = fmaf(s[m], kk[cs][m], a0);
-            a1 = fmaf(s[m + 1], kk[cs][m + 1], a1);
-            a2 = fmaf(s[m + 2], kk[cs][m + 2], a2);
-            a3 = fmaf(s[m + 3], kk[cs][m + 3], a3);
-        }
-        const float x = group_sum<4>((a0 + a1) + (a2 + a3));
-        float uw;
+        const float4 k = kk[cs];
+        float a0 = s[0][0] * k.x, a1 = s[0][1] * k.x;
+        a0 = fmaf(s[1][0], k.y, a0);
+        a1 = fmaf(s[1][1], k.y, a1);
+        a0 = fmaf(s[2][0], k.z, a0);
+        a1 = fmaf(s[2][1], k.z, a1);
+        a0 = fmaf(s[3][0], k.w, a0);
+        a1 = fmaf(s[3][1], k.w, a1);
+        const float x = col_sum(a0, a1);
+        float u0;
         if constexpr (SC) {
-            uw = g.x * fmaf(vv[j], g.y, -x);
-#pragma unroll
-            for (int m = 0; m < FR; ++m) s[m] = fmaf(kk[cs][m], uw, s[m]);
+            u0 = fmaf(-readlane_f(gb, j), x, vb[j]);
         } else {
-            const float a = g.z;
-            uw = g.x * (vv[j] - a * x);
-#pragma unroll
-            for (int m = 0; m < FR; ++m) s[m] = a * s[m] + kk[cs][m] * uw;
+            u0 = fmaf(-readlane_f(gab, j), x, vb[j]);
         }
-        ub[j * FP + col] = uw;   // the quad's four lanes store the same value
-        hs = p == (j & 3) ? x : hs;
-        if ((j & 3) == 3) {
-            const int jj = p + (j & ~3);
-            *(jj < nvalid ? skd + jj * d : tr) = SC ? hs * gs : hs;
+        const float u1 = dpp<DPP_ROW_ROR8>(u0);
+        const float kv[4] = {k.x, k.y, k.z, k.w};
+        if constexpr (SC) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                s[m][0] = fmaf(kv[m], u0, s[m][0]);
+                s[m][1] = fmaf(kv[m], u1, s[m][1]);
+            }
+        } else {
+            const float a = readlane_f(ga, j);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                s[m][0] = fmaf(a, s[m][0], kv[m] * u0);
+                s[m][1] = fmaf(a, s[m][1], kv[m] * u1);
+            }
+        }
+        ub[j * FP] = u0;   // the 8 lanes of a column store the same value
+        hs = r == (j & 7) ? x : hs;
+        if ((j & 7) == 7) {
+            const int jj = r + (j & 8);
+            *(jj < nvalid ? skd + jj * d : tr) = SC ? hs * gsk[j >> 3] : hs;
         }
         if (j == CK / 2 - 1) lds_barrier();   // P1
     }
@@ -245,16 +264,16 @@ ASCA_DEV void fsteps(float (&s)[FR], const float* __restrict__ buf, const float*
 // with S the state before the chunk, G_{j+1} the product of the chunk's alpha
 // up to step j and Gamma_{jl} that from step l + 1 to j (both formed by
 // multiplication only).  S^T q runs on the matrix cores (16x16x4 f32 MFMA) from
-// the q rows and the state's rows; the 16 x 16 products k_l . q_j arrive as
-// per-wave partials (fgram, a chunk earlier) in exactly the lane layout the
-// step mix takes as its operand.
+// the q rows and the state's rows, as two accumulation chains; the 16 x 16
+// products k_l . q_j arrive as per-wave partials (fgram, a chunk earlier) in
+// exactly the lane layout the step mix takes as its operand (l = 4 gq + r).
 ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st, const float* __restrict__ ub,
                     const float4* __restrict__ gpart, int mw, int lane, float* __restrict__ od, long d, int nvalid,
                     float* __restrict__ tr) {
     const int jr = lane & 15, gq = lane >> 4;
     const bool sc = buf[F_FLAG] == 1.0f;
     const float* const gt = buf + F_G;   // gate table 0
-    // k_l . q_jr for l = 4 r + gq, masked to l <= jr (plain: times Gamma)
+    // k_l . q_jr for l = 4 gq + r, masked to l <= jr (plain: times Gamma)
     float4 gm = gpart[lane];
 #pragma unroll
     for (int v4 = 1; v4 < W; ++v4) {
@@ -264,7 +283,7 @@ ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st,
     float am[4] = {gm.x, gm.y, gm.z, gm.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int l = 4 * r + gq;
+        const int l = 4 * gq + r;
         if (!sc) {
             float x = 1.0f;
 #pragma unroll
@@ -273,56 +292,64 @@ ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st,
         }
         am[r] = l <= jr ? am[r] : 0.0f;
     }
-    f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1;
+    f32x4 a1[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, a2 = a1[0];
     // S^T q: k index a = 16 m + 4 gq + e (e = 0..3), both operands as 16-byte vectors
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const float4 x = *reinterpret_cast<const float4*>(buf + F_Q + jr * FROW + fpad(16 * m + 4 * gq));
+        const float4 x = *reinterpret_cast<const float4*>(buf + F_Q + jr * FP + 16 * m + 4 * gq);
         const float4 y = *reinterpret_cast<const float4*>(st + (16 * mw + jr) * FP + 16 * m + 4 * gq);
-        a1 = mfma4(x.x, y.x, a1);
-        a1 = mfma4(x.y, y.y, a1);
-        a1 = mfma4(x.z, y.z, a1);
-        a1 = mfma4(x.w, y.w, a1);
+        f32x4& acc = a1[m & 1];
+        acc = mfma4(x.x, y.x, acc);
+        acc = mfma4(x.y, y.y, acc);
+        acc = mfma4(x.z, y.z, acc);
+        acc = mfma4(x.w, y.w, acc);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) a2 = mfma4(am[r], ub[(4 * r + gq) * FP + 16 * mw + jr], a2);
+    for (int r = 0; r < 4; ++r) a2 = mfma4(am[r], ub[(4 * gq + r) * FP + 16 * mw + jr], a2);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int j = 4 * gq + r;
         const float g1 = gt[j * 8 + 4];
-        const float ov = sc ? g1 * (a1[r] + a2[r]) : fmaf(g1, a1[r], a2[r]);
+        const float sq = a1[0][r] + a1[1][r];
+        const float ov = sc ? g1 * (sq + a2[r]) : fmaf(g1, sq, a2[r]);
         *(j < nvalid ? od + j * d + 16 * mw + jr : tr + r) = ov;
     }
 }
 
 // Matrix wave mw: its partial of the products k_l . q_j of a chunk over the
-// rows a = 16 mw .. 16 mw + 15, as D = K_pi Q^T with pi(m) = 4 (m & 3) + m / 4,
-// so that lane (gq, jr) register r holds k_{4r+gq} . q_jr.
+// rows a = 16 mw .. 16 mw + 15, as D = K Q^T (MFMA e takes a = 16 mw + 4 gq + e
+// from lane group gq, so each lane reads its operands as one 16-byte vector),
+// so that lane (gq, jr) register r holds k_{4gq+r} . q_jr.  It reads only what
+// the wave's own lanes staged (fstage_store), right after staging them.
 ASCA_DEV void fgram(const float* __restrict__ buf, float4* __restrict__ gpart, int mw, int lane) {
     const int jr = lane & 15, gq = lane >> 4;
-    const int pj = 4 * (jr & 3) + (jr >> 2);
+    // the wave reads back what its own lanes wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float4 x = *reinterpret_cast<const float4*>(buf + F_K + jr * FP + 16 * mw + 4 * gq);
+    const float4 y = *reinterpret_cast<const float4*>(buf + F_Q + jr * FP + 16 * mw + 4 * gq);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        const int a = fpad(16 * mw + 4 * kb + gq);
-        acc = mfma4(buf[F_K + pj * FROW + a], buf[F_Q + jr * FROW + a], acc);
-    }
+    acc = mfma4(x.x, y.x, acc);
+    acc = mfma4(x.y, y.y, acc);
+    acc = mfma4(x.z, y.z, acc);
+    acc = mfma4(x.w, y.w, acc);
     gpart[mw * 64 + lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
 // One block per unit = h*B + b (the reference's s_pre order,
 // rust/src/delta.rs:54-56), as a two-stage pipeline over chunks: in period c
-// the state waves (0..3) run chunk c while the matrix waves (4..7) form the
-// outputs of chunk c - 1, the partial products k . q of chunk c and stage chunk
-// c + 1.  Two block barriers per period: P0 at its start and P1 halfway
-// through the chunk, after which the matrix waves restage the buffer of chunk
-// c - 1.  One state wave and one matrix wave share each SIMD.
+// the state waves (0..SW-1, two per SIMD) run chunk c while the matrix waves
+// (SW..SW+W-1, one per SIMD) form the outputs of chunk c - 1, then stage chunk
+// c + 1 and its partial products k . q.  Two block barriers per period: P0 at
+// its start and P1 halfway through the chunk, after which the matrix waves
+// restage the buffer of chunk c - 1.
 template <bool AL>
-__global__ __launch_bounds__(2 * NT) void delta_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
-                                                        const float* __restrict__ v, const float* __restrict__ alpha,
-                                                        const float* __restrict__ beta, float* __restrict__ o,
-                                                        float* __restrict__ sk_out, float* __restrict__ ckpt, int B,
-                                                        int T, int H, int nslots) {
+__global__ __launch_bounds__(FNT) void delta_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v, const float* __restrict__ alpha,
+                                                     const float* __restrict__ beta, float* __restrict__ o,
+                                                     float* __restrict__ sk_out, float* __restrict__ ckpt, int B,
+                                                     int T, int H, int nslots) {
     extern __shared__ float4 lds4[];
     float* const lds = reinterpret_cast<float*>(lds4);
     const int unit = blockIdx.x;
@@ -334,14 +361,14 @@ __global__ __launch_bounds__(2 * NT) void delta_fwd64_k(const float* __restrict_
     const int nchunk = (T + CK - 1) / CK;
     float* const tr = trash((threadIdx.x & (NT - 1)) * 8);
 
-    if (w < W) {
+    if (w < SW) {
         // state waves
-        const int c = lane >> 2, p = lane & 3;
-        const int col = 16 * w + c;
-        float* const ckb = ckpt + (long)unit * nslots * DH2 + col * DH + 16 * p;
-        float s[FR];
+        const int rg = lane & 15, r = lane & 7, n = (lane >> 3) & 1, cp = lane >> 4;
+        const int col = 8 * w + 2 * cp + n, oth = col ^ 1;
+        float* const ckb = ckpt + (long)unit * nslots * DH2 + 4 * rg;
+        float s[4][2];
 #pragma unroll
-        for (int m = 0; m < FR; ++m) s[m] = 0.0f;
+        for (int m = 0; m < 4; ++m) s[m][0] = s[m][1] = 0.0f;
         lds_barrier();   // chunk 0 staged
         for (int ci = 0; ci <= nchunk; ++ci) {
             lds_barrier();   // P0
@@ -351,54 +378,67 @@ __global__ __launch_bounds__(2 * NT) void delta_fwd64_k(const float* __restrict_
             }
             const int t0 = ci * CK;
             const float* const buf = lds + (ci & 1) * F_BUF;
-            const float* const gt = buf + F_G + w * CK * 8;
+            const float* const gt = buf + F_G + (w & (W - 1)) * CK * 8;
             const bool sc = __builtin_amdgcn_readfirstlane(__float_as_int(buf[F_FLAG])) == __float_as_int(1.0f);
-            float vv[CK];
+            float vb[CK];
 #pragma unroll
-            for (int j = 0; j < CK; ++j) vv[j] = buf[F_V + j * DH + col];
-            float ck[FR];   // the checkpoint: S before step t0
+            for (int j = 0; j < CK; ++j) vb[j] = buf[F_V + j * DH + col];
+            const float4 g4 = *reinterpret_cast<const float4*>(gt + rg * 8);   // step rg's gate row
+            const float gsk[2] = {gt[r * 8 + 5], gt[(r + 8) * 8 + 5]};
+            float ck[4][2];   // the checkpoint: S before step t0
 #pragma unroll
-            for (int m = 0; m < FR; ++m) ck[m] = s[m];
-            store_state(lds + F_ST + (ci & 1) * DH * FP + col * FP + 16 * p, s);
+            for (int m = 0; m < 4; ++m) ck[m][0] = s[m][0], ck[m][1] = s[m][1];
+            float* const stb = lds + F_ST + (ci & 1) * DH * FP + 4 * rg;
+            st4(stb + col * FP, s[0][0], s[1][0], s[2][0], s[3][0]);
+            st4(stb + oth * FP, s[0][1], s[1][1], s[2][1], s[3][1]);
             float* const skd = sk_out + ubase + (long)t0 * d + col;
-            float* const ub = lds + F_U + (ci & 1) * CK * FP;
+            float* const ub = lds + F_U + (ci & 1) * CK * FP + col;
+            float* const ckc = ckb + (long)ci * DH2;
             if (sc) {
-                fsteps<true>(s, buf, gt, vv, p, col, ck, ckb + (long)ci * DH2, skd, d, T - t0, tr, ub);
+                fsteps<true>(s, buf + F_K + 4 * rg, vb, g4.x, g4.z, g4.w, ck, ckc + col * DH, ckc + oth * DH, skd,
+                             d, T - t0, tr, ub, r, gsk);
                 const float ge = gt[(CK - 1) * 8 + 4];
 #pragma unroll
-                for (int m = 0; m < FR; ++m) s[m] *= ge;
+                for (int m = 0; m < 4; ++m) s[m][0] *= ge, s[m][1] *= ge;
             } else {
-                fsteps<false>(s, buf, gt, vv, p, col, ck, ckb + (long)ci * DH2, skd, d, T - t0, tr, ub);
+                fsteps<false>(s, buf + F_K + 4 * rg, vb, g4.x, g4.z, g4.w, ck, ckc + col * DH, ckc + oth * DH, skd,
+                              d, T - t0, tr, ub, r, gsk);
             }
         }
-        store_state(ckb + (long)nchunk * DH2, s);   // the state after step T-1
+        // the state after step T-1
+        float* const ckl = ckb + (long)nchunk * DH2;
+        st4(ckl + col * DH, s[0][0], s[1][0], s[2][0], s[3][0]);
+        st4(ckl + oth * DH, s[0][1], s[1][1], s[2][1], s[3][1]);
     } else {
         // matrix waves
-        const int mw = w - W, tx = threadIdx.x - NT;
+        const int mw = w - SW, tx = threadIdx.x - 64 * SW;
         FStage stg;
+        float4* const gp = reinterpret_cast<float4*>(lds + F_GP);
         fstage_load<AL>(stg, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
         fstage_store(stg, 0, T, lds, tx, mw, lane);
+        fgram(lds, gp, mw, lane);
         // the loads of chunk ci + 1 are issued right after P1 of period ci - 1,
         // a whole period ahead of their store
         if (nchunk > 1) fstage_load<AL>(stg, 1, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
         lds_barrier();   // chunk 0 staged
         for (int ci = 0; ci <= nchunk; ++ci) {
             lds_barrier();   // P0
-            if (ci < nchunk)
-                fgram(lds + (ci & 1) * F_BUF, reinterpret_cast<float4*>(lds + F_GP) + (ci & 1) * W * 64, mw, lane);
             if (ci > 0) {
                 const int cp = ci - 1;
                 fprod(lds + (cp & 1) * F_BUF, lds + F_ST + (cp & 1) * DH * FP, lds + F_U + (cp & 1) * CK * FP,
-                      reinterpret_cast<const float4*>(lds + F_GP) + (cp & 1) * W * 64, mw, lane,
+                      gp + (cp & 1) * W * 64, mw, lane,
                       o + ubase + (long)cp * CK * d, d, T - cp * CK, tr);
             }
             lds_barrier();   // P1
-            if (ci + 1 < nchunk) fstage_store(stg, ci + 1, T, lds + ((ci + 1) & 1) * F_BUF, tx, mw, lane);
-            if (ci + 2 < nchunk) fstage_load<AL>(stg, ci + 2, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
+            if (ci + 1 < nchunk) {
+                fstage_store(stg, ci + 1, T, lds + ((ci + 1) & 1) * F_BUF, tx, mw, lane);
+                if (ci + 2 < nchunk)
+                    fstage_load<AL>(stg, ci + 2, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
+                fgram(lds + ((ci + 1) & 1) * F_BUF, gp + ((ci + 1) & 1) * W * 64, mw, lane);
+            }
         }
     }
 }
-
 // ================================================================= backward
 
 constexpr int BM = 8;       // adjoint rows per lane (two columns each)
@@ -1362,7 +1402,7 @@ static int launch_fwd64_t(const float* q, const float* k, const float* v, const 
     }
     int rc = pre_launch("delta_fwd64");
     if (rc) return rc;
-    hipLaunchKernelGGL(d64::delta_fwd64_k<AL>, dim3(B * H), dim3(2 * d64::NT), d64::F_LDS, st, q, k, v, alpha, beta, o,
+    hipLaunchKernelGGL(d64::delta_fwd64_k<AL>, dim3(B * H), dim3(d64::FNT), d64::F_LDS, st, q, k, v, alpha, beta, o,
                        ws.sk, ws.ckpt, B, T, H, ws.nslots);
     return post_launch("delta_fwd64");
 }
