@@ -81,6 +81,9 @@ SIGNATURES: dict[str, tuple] = {
     "asca_chunk_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "asca_chunk_fwd": (_i, [_p] * 7 + [_i] * 5 + [_p]),
     "asca_chunk_bwd": (_i, [_p] * 10 + [_i] * 5 + [_p]),
+    "asca_chunk_ws_bytes_f32": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
+    "asca_chunk_fwd_f32": (_i, [_p] * 7 + [_i] * 5 + [_p]),
+    "asca_chunk_bwd_f32": (_i, [_p] * 7 + [_i] * 5 + [_p]),
     "asca_model_create": (_i, [_i] * 6 + [C.POINTER(_p)]),
     "asca_model_destroy": (_i, [_p]),
     "asca_model_num_tensors": (_i, [_p, C.POINTER(_i)]),

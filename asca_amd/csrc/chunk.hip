@@ -65,7 +65,9 @@ struct ChunkWs {
     size_t total;  // floats
 };
 
-static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
+// fusedlayout: the C = 64, dh = 128 bf16 kernels' workspace (see below); the
+// f32 entry points always take the decomposed layout.
+static ChunkWs chunk_ws(const ChunkDims& d, float* base, bool fusedlayout = true) {
     ChunkWs w;
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -76,7 +78,7 @@ static ChunkWs chunk_ws(const ChunkDims& d, float* base) {
     const size_t N = d.N, CD = d.CD, CC = d.CC, DD = d.DD, C = d.C;
     // the fused C = 64, dh = 128 kernels need only the forward factors, the
     // states and U; the decomposed path's other regions are left out
-    const bool fused = d.C == 64 && d.dh == 128;
+    const bool fused = fusedlayout && d.C == 64 && d.dh == 128;
     auto opt = [&](size_t n) -> float* { return fused ? nullptr : take(n); };
     // f32 copies of q, k, v: the fused kernels read the bf16 inputs instead
     w.Qu = opt(N * CD);
@@ -144,6 +146,28 @@ __global__ __launch_bounds__(256) void ck_in_k(const uint16_t* __restrict__ src,
         const uint2 x = *reinterpret_cast<const uint2*>(src + ((size_t)(b * T + t) * H + h) * dh + j);
         v = make_float4(__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u), __uint_as_float(x.y << 16),
                         __uint_as_float(x.y & 0xffff0000u));
+    }
+    reinterpret_cast<float4*>(dst)[i] = v;
+}
+
+// token-major f32 (B*T, H*dh) -> unit-major f32 [u][Tp][dh], zero padding;
+// four elements per thread, one 16-byte access when the source is 16-byte
+// aligned (AL)
+template <bool AL>
+__global__ __launch_bounds__(256) void ck_in_f32_k(const float* __restrict__ src, float* __restrict__ dst, int T,
+                                                   int H, int dh, int Tp, int total4) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= total4) return;
+    const int q4 = dh >> 2;
+    const int j = 4 * (i % q4);
+    const int r = i / q4;
+    const int t = r % Tp, u = r / Tp;
+    const int b = u / H, h = u - b * H;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < T) {
+        const float* const x = src + ((size_t)(b * T + t) * H + h) * dh + j;
+        if constexpr (AL) v = *reinterpret_cast<const float4*>(x);
+        else v = make_float4(x[0], x[1], x[2], x[3]);
     }
     reinterpret_cast<float4*>(dst)[i] = v;
 }
@@ -1876,10 +1900,11 @@ static int scan2(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, hipStr
 }
 
 // The state scan and the outputs O = Qp S + M Uv.
-static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, float* o, hipStream_t st) {
+static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, float* o, hipStream_t st,
+                          bool fused) {
     const int C = d.C, dh = d.dh;
     int rc;
-    if (C == FP_C && dh == FP_D) {
+    if (fused) {
         if ((rc = scan2(d, w, k, st))) return rc;
         CK_LAUNCH_LDS("chunk_out_fused", ck_out_fused_k, dim3((unsigned)d.N), dim3(FO_NT),
                   (size_t)FO_LDS_F * sizeof(float), d.T, d.H, d.NC, w, o);
@@ -1900,6 +1925,11 @@ static int chunk_fwd_tail(const ChunkDims& d, const ChunkWs& w, const uint16_t* 
 }  // namespace asca
 
 using namespace asca;
+
+static int chunk_fwd_decomposed(const ChunkDims& d, const ChunkWs& w, const float* alpha, const float* beta,
+                                float* o, hipStream_t st);
+static int chunk_bwd_decomposed(const ChunkDims& d, const ChunkWs& w, float* dq, float* dk, float* dv,
+                                float* dalpha, float* dbeta, hipStream_t st);
 
 extern "C" {
 
@@ -1935,12 +1965,23 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
         hipLaunchKernelGGL(ck_fwd_prep_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, alpha, beta, T, H,
                            d.NC, w);
         if ((rc = post_launch("chunk_fwd_prep"))) return rc;
-        return chunk_fwd_tail(d, w, k, o, st);
+        return chunk_fwd_tail(d, w, k, o, st, true);
     }
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), q, w.Qu, T, H, dh, d.Tp, tot_in4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), k, w.Ku, T, H, dh, d.Tp, tot_in4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), v, w.Vu, T, H, dh, d.Tp, tot_in4);
+    return chunk_fwd_decomposed(d, w, alpha, beta, o, st);
+}
+
+}  // extern "C"
+
+// The decomposed forward from the unit-major f32 copies of q, k, v in the
+// workspace (Qu, Ku, Vu): every per-chunk product a batched GEMM.
+static int chunk_fwd_decomposed(const ChunkDims& d, const ChunkWs& w, const float* alpha, const float* beta,
+                                float* o, hipStream_t st) {
+    const int T = d.T, H = d.H, dh = d.dh, C = d.C;
+    int rc;
     CK_LAUNCH("chunk_gates_in", ck_gates_in_k, dim3(nblk(d.U * d.Tp)), dim3(256), alpha, beta, w.al, w.be, T, H, d.Tp,
               d.U * d.Tp);
     // per-chunk state-independent parts
@@ -1965,8 +2006,10 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
                     "chunk_H")))
         return rc;
     CK_LAUNCH("chunk_diag", ck_diag_k, dim3(nblk(d.N * dh)), dim3(256), w.Gp, w.gC, dh, d.N * dh);
-    return chunk_fwd_tail(d, w, k, o, st);
+    return chunk_fwd_tail(d, w, nullptr, o, st, false);
 }
+
+extern "C" {
 
 int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* d_o, void* ws, float* dq,
                    float* dk, float* dv, float* dalpha, float* dbeta, int B, int T, int H, int dh, int C,
@@ -2010,6 +2053,18 @@ int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     }
     const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
     CK_LAUNCH("chunk_in", ck_in_k, dim3(nblk(tot_in4)), dim3(256), d_o, w.dOu, T, H, dh, d.Tp, tot_in4);
+    return chunk_bwd_decomposed(d, w, dq, dk, dv, dalpha, dbeta, st);
+}
+
+}  // extern "C"
+
+// The decomposed backward from the forward's workspace and the unit-major f32
+// copy of dO (dOu).
+static int chunk_bwd_decomposed(const ChunkDims& d, const ChunkWs& w, float* dq, float* dk, float* dv,
+                                float* dalpha, float* dbeta, hipStream_t st) {
+    const int B = d.B, T = d.T, H = d.H, dh = d.dh, C = d.C;
+    const int tot_in4 = (int)(d.U * d.Tp * dh / 4);
+    int rc;
     CK_LAUNCH("chunk_rowscale", ck_rowscale_k, dim3(nblk(tot_in4)), dim3(256), w.dOu, w.gam, w.dOg, dh, tot_in4);
     // E_c = Qp^T dO_c; reverse scan dS'_{c-1} = G'_c^T dS'_c + E_c, dS'_{NC-1} = 0
     if ((rc = bgemm(1, 0, dh, dh, C, 1.f, w.Qp, dh, d.CD, w.dOu, dh, d.CD, 0.f, w.E, dh, d.DD, nullptr, 0, d.N, st,
@@ -2059,6 +2114,57 @@ int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     CK_LAUNCH("chunk_gates_out", ck_gates_out_k, dim3(nblk(tot_g)), dim3(256), w.dal, w.dbe, T, H, d.Tp, dalpha, dbeta,
               tot_g);
     return ASCA_OK;
+}
+
+extern "C" {
+
+int asca_chunk_ws_bytes_f32(int B, int T, int H, int dh, int C, size_t* bytes) {
+    if (!bytes) return fail(ASCA_ERR_INVALID, "null output pointer");
+    int rc = chunk_check(B, T, H, dh, C);
+    if (rc) return rc;
+    *bytes = chunk_ws(chunk_dims(B, T, H, dh, C), nullptr, false).total * sizeof(float);
+    return ASCA_OK;
+}
+
+static int chunk_in_f32(const float* src, float* dst, const ChunkDims& d, hipStream_t st) {
+    const int tot_in4 = (int)(d.U * d.Tp * d.dh / 4);
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0)
+        CK_LAUNCH("chunk_in_f32", ck_in_f32_k<true>, dim3(nblk(tot_in4)), dim3(256), src, dst, d.T, d.H, d.dh, d.Tp,
+                  tot_in4);
+    else
+        CK_LAUNCH("chunk_in_f32", ck_in_f32_k<false>, dim3(nblk(tot_in4)), dim3(256), src, dst, d.T, d.H, d.dh, d.Tp,
+                  tot_in4);
+    return ASCA_OK;
+}
+
+int asca_chunk_fwd_f32(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                       float* o, void* ws, int B, int T, int H, int dh, int C, void* stream) {
+    int rc = chunk_check(B, T, H, dh, C);
+    if (rc) return rc;
+    if ((long)B * T * H == 0) return ASCA_OK;
+    if (!q || !k || !v || !alpha || !beta || !o || !ws)
+        return fail(ASCA_ERR_INVALID, "asca_chunk_fwd_f32: null pointer");
+    const ChunkDims d = chunk_dims(B, T, H, dh, C);
+    const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws), false);
+    const hipStream_t st = as_stream(stream);
+    if ((rc = chunk_in_f32(q, w.Qu, d, st)) || (rc = chunk_in_f32(k, w.Ku, d, st)) ||
+        (rc = chunk_in_f32(v, w.Vu, d, st)))
+        return rc;
+    return chunk_fwd_decomposed(d, w, alpha, beta, o, st);
+}
+
+int asca_chunk_bwd_f32(const float* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha, float* dbeta,
+                       int B, int T, int H, int dh, int C, void* stream) {
+    int rc = chunk_check(B, T, H, dh, C);
+    if (rc) return rc;
+    if ((long)B * T * H == 0) return ASCA_OK;
+    if (!d_o || !ws || !dq || !dk || !dv || !dalpha || !dbeta)
+        return fail(ASCA_ERR_INVALID, "asca_chunk_bwd_f32: null pointer");
+    const ChunkDims d = chunk_dims(B, T, H, dh, C);
+    const ChunkWs w = chunk_ws(d, reinterpret_cast<float*>(ws), false);
+    const hipStream_t st = as_stream(stream);
+    if ((rc = chunk_in_f32(d_o, w.dOu, d, st))) return rc;
+    return chunk_bwd_decomposed(d, w, dq, dk, dv, dalpha, dbeta, st);
 }
 
 }  // extern "C"

@@ -680,6 +680,47 @@ class Gpu:
             for b in (bdo, *outs):
                 b.free()
 
+    def delta_chunked_f32(self, q, k, v, alpha, beta, batch: int, seq: int, n_heads: int, dh: int,
+                          chunk: int = 32):
+        """Forward of the chunked form on f32 q, k, v (asca_chunk_fwd_f32, the
+        batched-GEMM path at any chunk size); returns (o f32, ChunkDev).  The
+        workspace keeps f32 copies of q, k, v, so the backward takes only dO."""
+        d, t_len = n_heads * dh, batch * seq
+        for name, m in zip("qkv", (q, k, v)):
+            if m.shape != (t_len, d):
+                raise ValueError(f"delta_chunked_f32: {name} has shape {m.shape}, expected {(t_len, d)}")
+        wsb = C.c_size_t()
+        _lib.call("asca_chunk_ws_bytes_f32", batch, seq, n_heads, dh, chunk, C.byref(wsb))
+        ins = [DevBuf.from_host(x) for x in (q, k, v, alpha, beta)]
+        ws, out = DevBuf(wsb.value), DevBuf(t_len * d * 4)
+        try:
+            _lib.call("asca_chunk_fwd_f32", *[_vp(x) for x in ins], _vp(out), _vp(ws), batch, seq, n_heads, dh,
+                      chunk, None)
+            _lib.call("asca_sync")
+            o = out.to_host((t_len, d))
+        except Exception:
+            ws.free()
+            raise
+        finally:
+            for x in (*ins, out):
+                x.free()
+        return o, ChunkDev(ws, (), batch, seq, n_heads, dh, chunk)
+
+    def delta_chunked_f32_bwd(self, dev: ChunkDev, d_o):
+        """Raw gradients (dq, dk, dv, dalpha, dbeta) of delta_chunked_f32 given
+        f32 dO."""
+        B, T, H, dh, Cc = dev.batch, dev.seq, dev.n_heads, dev.dh, dev.chunk
+        t_len, d = B * T, H * dh
+        bdo = DevBuf.from_host(d_o)
+        outs = [DevBuf(t_len * d * 4) for _ in range(3)] + [DevBuf(t_len * H * 4) for _ in range(2)]
+        try:
+            _lib.call("asca_chunk_bwd_f32", _vp(bdo), _vp(dev.ws), *[_vp(o) for o in outs], B, T, H, dh, Cc, None)
+            _lib.call("asca_sync")
+            return tuple([o.to_host((t_len, d)) for o in outs[:3]] + [o.to_host((t_len, H)) for o in outs[3:]])
+        finally:
+            for b in (bdo, *outs):
+                b.free()
+
     # -- decode -------------------------------------------------------------
     def new_decode_states(self, n_seq: int, n_heads: int, dh: int) -> DevBuf:
         """Zeroed device states (n_seq, H, dh, dh) for delta_decode_step; the

@@ -369,6 +369,128 @@ def train_flops_per_token(V, d, H, L, E, dff):
     return L * (3 * gemm_fwd + 24 * dh * dh * H) + 3 * 2 * d * V
 
 
+def chunk_flops(B, T, H, dh, Cc):
+    """MFMA flops the batched chunked path executes (its GEMM list in
+    chunk.hip, forward then backward): per chunk 30 C^2 d + 20 C d^2 + 4 d^3
+    (the two state scans are d x d products per chunk)."""
+    nc = -(-T // Cc)
+    per_chunk = 30 * Cc * Cc * dh + 20 * Cc * dh * dh + 4 * dh ** 3
+    return B * H * nc * per_chunk
+
+
+def bench_chunk64(args):
+    """The MFMA route at the headline shape: configs[1] (B32 T512 H8 dh64, f32,
+    seed 1) through the f32 chunked path (asca_chunk_fwd_f32 +
+    asca_chunk_bwd_f32, batched MFMA GEMMs over chunks) at C = 16, 32, 64,
+    timed next to the recurrent kernels on the same device inputs
+    (asca_delta_fwd + asca_delta_bwd_raw: the same raw gradients)."""
+    from asca_amd import _lib, gpu
+    from asca_amd.gpu import DevBuf
+
+    B, T, H, dh, seed = 32, 512, 8, 64, 1
+    g = gpu.gpu()
+    if g is None:
+        raise SystemExit(f"no GPU backend: {gpu.describe()}")
+    x = synth_inputs(B, T, H, dh, seed)
+    dev = {n: DevBuf.from_host(x[n]) for n in ("q", "k", "v", "alpha", "beta", "d_o")}
+    rows, d = B * T, H * dh
+    o = DevBuf(rows * d * 4)
+    grads = [DevBuf(rows * d * 4) for _ in range(3)] + [DevBuf(rows * H * 4) for _ in range(2)]
+    tm = Timer()
+    sp = C.c_void_p(tm.stream)
+    P = {n: C.c_void_p(b.ptr) for n, b in dev.items()}
+    G = [C.c_void_p(b.ptr) for b in grads]
+    K = args.steps or 20
+    W = min(args.warmup, 3)
+
+    def timed(fwd, bwd):
+        for _ in range(W):
+            fwd()
+            bwd()
+        tm.sync()
+        ev = [tm.event() for _ in range(3)]
+        f_ms = b_ms = 0.0
+        for _ in range(K):
+            tm.record(ev[0])
+            fwd()
+            tm.record(ev[1])
+            bwd()
+            tm.record(ev[2])
+            tm.sync()
+            f_ms += tm.elapsed(ev[0], ev[1])
+            b_ms += tm.elapsed(ev[1], ev[2])
+        tm.destroy(*ev)
+        return f_ms / K, b_ms / K
+
+    print(f"bench chunk64: {gpu.describe()}; B{B} T{T} H{H} dh{dh} f32; warmup {W}, steps {K}", flush=True)
+    per_c = {}
+    for Cc in (16, 32, 64):
+        wsb = C.c_size_t()
+        _lib.call("asca_chunk_ws_bytes_f32", B, T, H, dh, Cc, C.byref(wsb))
+        ws = DevBuf(wsb.value)
+        wp = C.c_void_p(ws.ptr)
+
+        def fwd():
+            _lib.call("asca_chunk_fwd_f32", P["q"], P["k"], P["v"], P["alpha"], P["beta"], C.c_void_p(o.ptr), wp,
+                      B, T, H, dh, Cc, sp)
+
+        def bwd():
+            _lib.call("asca_chunk_bwd_f32", P["d_o"], wp, *G, B, T, H, dh, Cc, sp)
+
+        f_ms, b_ms = timed(fwd, bwd)
+        ws.free()
+        fl = chunk_flops(B, T, H, dh, Cc)
+        per_c[Cc] = {"fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4), "step_ms": round(f_ms + b_ms, 4),
+                     "ws_mib": round(wsb.value / 2**20, 1), "mfma_gflop": round(fl / 1e9, 2),
+                     "mfma_tflops": round(fl / ((f_ms + b_ms) * 1e-3) / 1e12, 2)}
+        print(f"bench chunk64: C={Cc}: fwd {f_ms:.4f} ms, bwd {b_ms:.4f} ms, "
+              f"{per_c[Cc]['mfma_tflops']} TFLOP/s MFMA", flush=True)
+    # the recurrent kernels on the same inputs (raw gradients, like the chunked path)
+    wsb = C.c_size_t()
+    _lib.call("asca_delta_ws_bytes", B, T, H, dh, C.byref(wsb))
+    ws = DevBuf(wsb.value)
+    wp = C.c_void_p(ws.ptr)
+
+    def rfwd():
+        _lib.call("asca_delta_fwd", P["q"], P["k"], P["v"], P["alpha"], P["beta"], C.c_void_p(o.ptr), wp,
+                  B, T, H, dh, sp)
+
+    def rbwd():
+        _lib.call("asca_delta_bwd_raw", P["q"], P["k"], P["v"], P["alpha"], P["beta"], P["d_o"], wp, *G,
+                  B, T, H, dh, sp)
+
+    rf, rb = timed(rfwd, rbwd)
+    ws.free()
+    print(f"bench chunk64: recurrent: fwd {rf:.4f} ms, bwd {rb:.4f} ms", flush=True)
+    best = min(per_c, key=lambda c: per_c[c]["step_ms"])
+    step_ms = per_c[best]["step_ms"]
+    fl = chunk_flops(B, T, H, dh, best)
+    result = {
+        "metric": "chunked (MFMA) delta fwd+BPTT tokens/s at the headline shape (B32 T512 H8 dh64 f32)",
+        "value": round(B * T / (step_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic (reference Rng stream, configs[1] distributions, seed {seed})",
+        "config": {"workload": "chunked delta-rule fwd+BPTT on f32 (asca_chunk_fwd_f32 + asca_chunk_bwd_f32)",
+                   "B": B, "T": T, "H": H, "dh": dh, "chunk": best},
+        "roofline": {"bound": "mfma", "achieved": per_c[best]["mfma_tflops"], "peak": PEAK_F32 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(fl / (step_ms * 1e-3) / PEAK_F32, 4), "traffic": None,
+                     "kernel": "step", "algorithmic_flops": fl,
+                     "note": "flops the batched chunked path executes (30 C^2 d + 20 C d^2 + 4 d^3 per chunk)"},
+        "per_chunk_size": per_c,
+        "recurrent_same_inputs_ms": {"delta_fwd": round(rf, 4), "delta_bwd_raw": round(rb, 4),
+                                     "step": round(rf + rb, 4)},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def bench_train(args):
     """one full training step (forward, BPTT backward, AdamW over
     all 143.1M parameters) of the 8-layer model, B=16 x T=1024 byte tokens,
@@ -519,9 +641,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train", "chunk", "gemm"],
+    ap.add_argument("--workload", default="delta", choices=["delta", "decode", "train", "chunk", "chunk64", "gemm"],
                     help="delta: the headline fwd+BPTT (configs[1]); decode: configs[4]; train: configs[3]; "
-                         "chunk: configs[2]; gemm: the f32 GEMM on the configs[3] product shapes")
+                         "chunk: configs[2]; chunk64: the chunked (MFMA) form at the configs[1] shape, f32; "
+                         "gemm: the f32 GEMM on the configs[3] product shapes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib", action="store_true",
                     help="also run the known-size copy kernel (for counter calibration)")
@@ -537,6 +660,9 @@ def main():
         return
     if args.workload == "train":
         bench_train(args)
+        return
+    if args.workload == "chunk64":
+        bench_chunk64(args)
         return
     if args.workload == "chunk":
         bench_chunk(args)

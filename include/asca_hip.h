@@ -387,6 +387,21 @@ ASCA_API int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t
 ASCA_API int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* d_o, void* ws,
                             float* dq, float* dk, float* dv, float* dalpha, float* dbeta, int B, int T, int H,
                             int dh, int C, void* stream);
+/* The same chunked form on f32 q, k, v, d_o (any alignment), for the f32
+ * recurrent configs (configs[1]: B32 T512 H8 dh64): the same math and outputs
+ * as asca_chunk_fwd / asca_chunk_bwd, every per-chunk product a batched f32
+ * MFMA GEMM over chunks at any C (1..64) and dh.  ws : asca_chunk_ws_bytes_f32
+ * bytes (it holds unit-major f32 copies of q, k, v, so the backward takes only
+ * d_o).  No reference counterpart: the reference's SPEC_V2 names the form
+ * (docs/SPEC_V2.md:50-69) and its f32 path is the recurrence; these let the
+ * MFMA route be measured against the recurrent kernels on the same f32
+ * inputs. */
+ASCA_API int asca_chunk_ws_bytes_f32(int B, int T, int H, int dh, int C, size_t* bytes);
+ASCA_API int asca_chunk_fwd_f32(const float* q, const float* k, const float* v, const float* alpha,
+                                const float* beta, float* o, void* ws, int B, int T, int H, int dh, int C,
+                                void* stream);
+ASCA_API int asca_chunk_bwd_f32(const float* d_o, void* ws, float* dq, float* dk, float* dv, float* dalpha,
+                                float* dbeta, int B, int T, int H, int dh, int C, void* stream);
 
 /* ----------------------------------------------------- training step -- */
 
