@@ -791,8 +791,9 @@ def main():
             "traffic": traffic,
             "traffic_note": traffic_note,
             "valu_ceiling": PEAK_F32_VALU / 1e12,
-            "note": "the recurrence issues no MFMA: f32 FMAs on the VALU, whose non-packed rate is "
-                    "half the 157.3 TFLOP/s peak",
+            "note": "the state recurrence (S^T k and the rank-1 updates, the adjoint in the backward) runs "
+                    "as f32 FMAs on the VALU, whose non-packed rate is half the 157.3 TFLOP/s peak; the "
+                    "per-chunk products (outputs o, dq, dk) run on f32 MFMA in matrix waves beside it",
             "kernel": dominant,
             "algorithmic_bytes": dom_b,
             "algorithmic_flops": dom_f,
