@@ -98,9 +98,11 @@ def test_workspace_bytes_layout():
     part_x = 2 * 2 * 4 * 128 * 4 * 32 * 4
     part_g = 2 * 4 * 128 * 2 * 4 * 4
     assert out.value == base + part_x + part_g
+    # dh = 64 runs a block per unit at any unit count (configs[3]'s 128 units too)
     _lib.call("asca_delta_ws_bytes", 16, 1024, 8, 64, C.byref(out))
-    base = 16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 8 + 1) * 64 * 64 * 4
-    assert out.value == base + 2 * 2 * 16 * 1024 * 8 * 64 * 4 + 2 * 16 * 1024 * 2 * 8 * 4
+    assert out.value == 16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 16 + 1) * 64 * 64 * 4
+    _lib.call("asca_delta_ws_bytes", 1, 40, 2, 64, C.byref(out))
+    assert out.value == 256 * ((1 * 40 * 2 * 64 * 4 + 255) // 256) + 2 * (40 // 16 + 2) * 64 * 64 * 4
     with pytest.raises(_lib.AscaError) as ei:
         _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))
     assert ei.value.code == 3
