@@ -443,6 +443,9 @@ __global__ __launch_bounds__(FNT) void delta_fwd64_k(const float* __restrict__ q
 
 constexpr int BM = 8;       // adjoint rows per lane (two columns each)
 constexpr int P = 68;       // LDS pitch of every 64-float row
+// Position of element r in a padded row (4 floats after the first 32): the
+// 16-byte reads of rows 8 rg .. 8 rg + 7 by the eight row groups of the adjoint
+// loop then fall on distinct banks.
 ASCA_DEV int rpad(int r) { return r + 4 * (r >> 5); }
 
 // k-order of a 64-float row for the 16x16x4 f32 MFMA: position 16 g + kb
@@ -455,8 +458,8 @@ ASCA_DEV int kcol(int g, int kb) { return 16 * (kb >> 2) + 4 * g + (kb & 3); }
 
 
 // Segment staging buffer (floats), written while the previous segment runs:
-constexpr int S_Q = 0;                   // [CK][P] q rows
-constexpr int S_K = S_Q + CK * P;        // [CK][P] k rows
+constexpr int S_Q = 0;                   // [CK][P] q rows, element a at rpad(a)
+constexpr int S_K = S_Q + CK * P;        // [CK][P] k rows, element a at rpad(a)
 constexpr int S_DO = S_K + CK * P;       // [CK][P] dO, k-order (scaled segment: G_{j+1} dO_j)
 constexpr int S_U = S_DO + CK * P;       // [CK][P] u = beta (v - alpha sk), k-order (scaled: u_j / G_{j+1})
 constexpr int S_SK = S_U + CK * P;       // [CK][P] sk, k-order
@@ -544,7 +547,7 @@ ASCA_DEV void bstage_store(const BStage& st, int g, int T, float* __restrict__ n
     for (int i = 0; i < 2; ++i) {
         const int f = tx + NT * i;
         const int tsr = f >> 8, j = (f >> 4) & (CK - 1), c4 = f & 15;
-        *reinterpret_cast<float4*>(nb + (tsr ? S_K : S_Q) + j * P + 4 * c4) = st.rq[i];
+        *reinterpret_cast<float4*>(nb + (tsr ? S_K : S_Q) + j * P + rpad(4 * c4)) = st.rq[i];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -603,8 +606,8 @@ struct BOps {
 };
 
 ASCA_DEV void bops_read(BOps& o, const float* __restrict__ buf, int j, int rowb, int kc) {
-    const float* const qr = buf + S_Q + j * P + rowb;
-    const float* const kr = buf + S_K + j * P + rowb;
+    const float* const qr = buf + S_Q + j * P + rpad(rowb);
+    const float* const kr = buf + S_K + j * P + rpad(rowb);
 #pragma unroll
     for (int e = 0; e < BM; e += 4) {
         const float4 x = *reinterpret_cast<const float4*>(qr + e);
@@ -782,8 +785,8 @@ ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, c
             rkj += wk[W_RP + (u4 * CK + kk) * 17 + jr];
             rjk += wk[W_RP + (u4 * CK + jr) * 17 + kk];
         }
-        const float bk = buf[S_K + kk * P + 16 * w + jr];
-        const float bq = buf[S_Q + kk * P + 16 * w + jr];
+        const float bk = buf[S_K + kk * P + rpad(16 * w + jr)];
+        const float bq = buf[S_Q + kk * P + rpad(16 * w + jr)];
         adq = mfma4(kk <= jr ? pkj : 0.0f, bk, adq);
         adk = mfma4(kk >= jr ? pjk : 0.0f, bq, adk);
         adk = mfma4(kk < jr ? rkj : (kk > jr ? rjk : 0.0f), bk, adk);
@@ -794,8 +797,8 @@ ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, c
         const int j = 4 * gq + r;
         wk[W_DQ + j * P + 16 * w + jr] = adq[r];
         wk[W_DK + j * P + 16 * w + jr] = adk[r];
-        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + 16 * w + jr]);
-        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + 16 * w + jr]);
+        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + rpad(16 * w + jr)]);
+        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + rpad(16 * w + jr)]);
         if (jr == 0) {
             wk[W_QDQ + w * CK + j] = x;
             wk[W_KDK + w * CK + j] = y;
@@ -807,7 +810,7 @@ ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, c
 // huge values): every state the steps need is recomputed forwards from the
 // segment's first checkpoint, so no gate is ever divided by.
 ASCA_DEV void fwd_update(float (&x)[BM][2], const float* __restrict__ buf, int j, int rowb, int kc) {
-    const float* const kr = buf + S_K + j * P + rowb;
+    const float* const kr = buf + S_K + j * P + rpad(rowb);
     const float2 u = *reinterpret_cast<const float2*>(buf + S_U + j * P + kc);
     const float a = buf[S_G + 8 * j];
 #pragma unroll
@@ -1027,8 +1030,8 @@ ASCA_DEV void bwd_serial(const BArgs& A, float* __restrict__ lds, int w, int lan
                 dk[i] = (rk[0] + rk[P]) + (rk[2 * P] + rk[3 * P]);
             }
             du[i] = wk[W_DU + jj * P + kpos(a)];
-            qa[i] = buf[S_Q + jj * P + a];
-            ka[i] = buf[S_K + jj * P + a];
+            qa[i] = buf[S_Q + jj * P + rpad(a)];
+            ka[i] = buf[S_K + jj * P + rpad(a)];
         }
         static_assert(W == 4, "the step sums above add four waves");
 #pragma unroll
@@ -1193,8 +1196,8 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
         const int kk = 4 * kb + gq;
         const float pkj = prv[kk * 17 + jr], pjk = prv[jr * 17 + kk];
         const float rkj = prv[CK * 17 + kk * 17 + jr], rjk = prv[CK * 17 + jr * 17 + kk];
-        const float bk = buf[S_K + kk * P + 16 * mw + jr];
-        const float bq = buf[S_Q + kk * P + 16 * mw + jr];
+        const float bk = buf[S_K + kk * P + rpad(16 * mw + jr)];
+        const float bq = buf[S_Q + kk * P + rpad(16 * mw + jr)];
         adq = mfma4(kk <= jr ? pkj : 0.0f, bk, adq);
         adk = mfma4(kk >= jr ? pjk : 0.0f, bq, adk);
         adk = mfma4(kk < jr ? rkj : (kk > jr ? rjk : 0.0f), bk, adk);
@@ -1204,8 +1207,8 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
         const int j = 4 * gq + r;
         lds[Q_DQ + j * P + 16 * mw + jr] = adq[r];
         lds[Q_DK + j * P + 16 * mw + jr] = adk[r];
-        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + 16 * mw + jr]);
-        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + 16 * mw + jr]);
+        const float x = group_sum<16>(adq[r] * buf[S_Q + j * P + rpad(16 * mw + jr)]);
+        const float y = group_sum<16>(adk[r] * buf[S_K + j * P + rpad(16 * mw + jr)]);
         if (jr == 0) {
             lds[Q_QDQ + mw * CK + j] = x;
             lds[Q_KDK + mw * CK + j] = y;
@@ -1213,8 +1216,8 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
     }
 #pragma unroll
     for (int i = 0; i < CK / W; ++i) {
-        e.qa[i] = buf[S_Q + (mw + W * i) * P + lane];
-        e.ka[i] = buf[S_K + (mw + W * i) * P + lane];
+        e.qa[i] = buf[S_Q + (mw + W * i) * P + rpad(lane)];
+        e.ka[i] = buf[S_K + (mw + W * i) * P + rpad(lane)];
     }
     e.gl0 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)));
     e.gl1 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)) + 4);
@@ -1223,7 +1226,7 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
 // Matrix wave mw: dalpha's bracket and the epilogue of segment gp (as in
 // bwd_serial's), steps mw + W i.
 template <bool FUSED>
-ASCA_DEV void mepi(const BArgs& A, const MEpi& e, const float* __restrict__ lds, const float* __restrict__ abb,
+ASCA_DEV void mepi(const BArgs& A, const MEpi& e, float* __restrict__ lds, const float* __restrict__ abb,
                    const float* __restrict__ brb, const float* __restrict__ dub, int gp, int mw, int lane) {
     const int l = lane & (CK - 1);
     float ea = 0.0f, eb = 0.0f, qdq = 0.0f, kdk = 0.0f, bsum = 0.0f;
@@ -1247,6 +1250,25 @@ ASCA_DEV void mepi(const BArgs& A, const MEpi& e, const float* __restrict__ lds,
     const float dal = fmaf(br, e.gl1.x, ea);
     const int t0 = gp * CK;
     const int ws = __builtin_amdgcn_readfirstlane(mw);
+    // the per-step factors of the row stores (lane l: step l) go through the
+    // wave's own product scratch (free until the next period's products) and
+    // come back as broadcast 16-byte reads: no v_readlane per stored row
+    float* const fac = lds + Q_PR + mw * 2 * CK * 17;   // [CK][8]
+    if (lane < CK) {
+        if constexpr (FUSED)
+            *reinterpret_cast<float4*>(fac + 8 * lane) =
+                make_float4(e.gl0.y, qdq, __builtin_amdgcn_rcpf(e.gl1.y), kdk);
+        else
+            *reinterpret_cast<float4*>(fac + 8 * lane) = make_float4(e.gl0.y, 0.0f, 1.0f, 0.0f);
+        fac[8 * lane + 4] = FUSED ? __builtin_amdgcn_rcpf(e.gl1.z) : 1.0f;
+    }
+    // dalpha and dbeta of every step of the segment from wave 0, lane l = step l
+    if (ws == 0 && lane < CK && t0 + lane < A.T) {
+        const long r = (long)A.b * A.T + t0 + lane;
+        const float al = e.gl0.x, be = e.gl0.y;
+        A.ga[r * A.ldg + A.h] = FUSED ? dal * al * (1.0f - al) : dal;
+        A.gb[r * A.ldg + A.h] = FUSED ? eb * be * (1.0f - be) : eb;
+    }
     float dq[CK / W], dk[CK / W], du[CK / W];
 #pragma unroll
     for (int i = 0; i < CK / W; ++i) {
@@ -1255,31 +1277,30 @@ ASCA_DEV void mepi(const BArgs& A, const MEpi& e, const float* __restrict__ lds,
         dk[i] = lds[Q_DK + jj * P + lane];
         du[i] = dub[jj * P + kpos(lane)];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float4 c[CK / W];
+    float rk[CK / W];
+#pragma unroll
+    for (int i = 0; i < CK / W; ++i) {
+        const int jj = ws + W * i;
+        c[i] = *reinterpret_cast<const float4*>(fac + 8 * jj);
+        rk[i] = fac[8 * jj + 4];
+    }
 #pragma unroll
     for (int i = 0; i < CK / W; ++i) {
         const int jj = ws + W * i;
         if (t0 + jj >= A.T) continue;   // wave-uniform
-        const float dA = readlane_f(dal, jj), dB = readlane_f(eb, jj);
-        const float al = readlane_f(e.gl0.x, jj), be = readlane_f(e.gl0.y, jj);
         const long r = (long)A.b * A.T + t0 + jj;
         const long o = r * A.ldx + A.hoff + lane;
-        A.gv[o] = be * du[i];
+        A.gv[o] = c[i].x * du[i];
         if constexpr (FUSED) {
-            const float rq = __builtin_amdgcn_rcpf(readlane_f(e.gl1.y, jj));
-            const float rk = __builtin_amdgcn_rcpf(readlane_f(e.gl1.z, jj));
-            A.gq[o] = (dq[i] - e.qa[i] * readlane_f(qdq, jj)) * rq;
-            A.gk[o] = (dk[i] - e.ka[i] * readlane_f(kdk, jj)) * rk;
-            if (lane == 0) {
-                A.ga[r * A.ldg + A.h] = dA * al * (1.0f - al);
-                A.gb[r * A.ldg + A.h] = dB * be * (1.0f - be);
-            }
+            A.gq[o] = (dq[i] - e.qa[i] * c[i].y) * c[i].z;
+            A.gk[o] = (dk[i] - e.ka[i] * c[i].w) * rk[i];
         } else {
             A.gq[o] = dq[i];
             A.gk[o] = dk[i];
-            if (lane == 0) {
-                A.ga[r * A.ldg + A.h] = dA;
-                A.gb[r * A.ldg + A.h] = dB;
-            }
         }
     }
 }
