@@ -183,11 +183,13 @@ def test_empty_and_invalid_shapes(g):
     assert ei.value.code == 3
 
 
-# dh = 64 with more than 128 (sequence, head) units runs on the four-wave
-# kernels (16 state elements per lane, 16-step chunks; the backward steps its
-# scaled state back from the checkpoint after each segment).  Ragged tails, a single step, fewer
-# steps than a segment, and the extreme gate patterns of test_extreme_gates.
-@pytest.mark.parametrize("B,T,H", [(129, 1, 1), (17, 5, 8), (20, 16, 8), (17, 29, 8), (33, 67, 4), (3, 40, 48)])
+# dh = 64 runs on the one-block-per-unit kernels of delta64.hip at any unit
+# count (16-step chunks; state and matrix waves side by side).  One unit, few
+# units, more units than CUs (blocks queued behind a full round), ragged tails,
+# a single step, fewer steps than a segment, and the extreme gate patterns of
+# test_extreme_gates.
+@pytest.mark.parametrize("B,T,H", [(129, 1, 1), (17, 5, 8), (20, 16, 8), (17, 29, 8), (33, 67, 4), (3, 40, 48),
+                                   (1, 37, 1), (2, 50, 4), (40, 20, 8)])
 def test_four_wave_dh64_shapes(orc, g, B, T, H):
     dh = 64
     _check_all(orc, g, orc.DeltaInputs(300 + B * T + H, B, T, H, dh), B, T, H, dh, "dh64 four-wave")
@@ -207,8 +209,8 @@ def test_four_wave_dh64_extreme_gates(orc, g):
 
 
 def test_four_wave_dh64_batch_isolation(orc, g):
-    # 136 units together, then each sequence alone (8 units: the eight-lane
-    # column-split kernels); forward and fused backward agree to the bar
+    # 136 units together, then each sequence alone (8 units); forward and fused
+    # backward agree to the bar
     B, T, H, dh = 17, 24, 8, 64
     x = orc.DeltaInputs(31, B, T, H, dh)
     o, dev = g.delta_scan(x.q, x.k, x.v, x.alpha, x.beta, B, T, H, dh)
