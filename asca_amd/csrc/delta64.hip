@@ -82,13 +82,16 @@ constexpr int F_FLAG = F_G + W * CK * 8;
 constexpr int F_SINK = F_FLAG + 4;
 constexpr int F_BUF = F_SINK + 8;
 static_assert(F_BUF % 4 == 0 && F_V % 4 == 0, "float4 buffers");
-// The forward's LDS (floats): two staging buffers, then per chunk parity the
-// state before the chunk as S^T rows, the chunk's u rows (u / G_{j+1} in a
-// scaled chunk) and the matrix waves' partial products q . k.
-constexpr int F_ST = 2 * F_BUF;                  // [2][DH][FP]
+// The forward's LDS (floats): three staging buffers (chunk c in buffer c mod
+// 3), then per chunk parity the state before the chunk as S^T rows, the
+// chunk's u rows (u / G_{j+1} in a scaled chunk) and its rows S^T k (over G_j
+// in a scaled chunk), and per chunk mod 3 the matrix waves' partial products
+// k . q.
+constexpr int F_ST = 3 * F_BUF;                  // [2][DH][FP]
 constexpr int F_U = F_ST + 2 * DH * FP;          // [2][CK][FP]
-constexpr int F_GP = F_U + 2 * CK * FP;          // [2][W][64] float4
-constexpr int F_END = F_GP + 2 * W * 64 * 4;
+constexpr int F_X = F_U + 2 * CK * FP;           // [2][CK][FP]
+constexpr int F_GP = F_X + 2 * CK * FP;          // [3][W][64] float4
+constexpr int F_END = F_GP + 3 * W * 64 * 4;
 constexpr size_t F_LDS = (size_t)F_END * 4;
 static_assert(F_LDS <= 160 * 1024 && F_ST % 4 == 0 && F_GP % 4 == 0, "forward LDS");
 
@@ -167,93 +170,60 @@ ASCA_DEV void fstage_store(const FStage& st, int c, int T, float* __restrict__ b
     }
 }
 
-// Sum over the 16 lanes of each lane row of a state wave that hold one column:
-// x0 is the lane's partial of its own column, x1 that of the other column of
-// its pair, whose own lanes sit 8 lanes away (row_ror 8).  The result is
-// bitwise identical in the 8 lanes that own the column.
-ASCA_DEV float col_sum(float x0, float x1) {
-    float x = x0 + dpp<DPP_ROW_ROR8>(x1);
-    x += dpp<DPP_QUAD_XOR1>(x);
-    x += dpp<DPP_QUAD_XOR2>(x);
-    x += dpp<DPP_HALF_MIRROR>(x);   // valid: quad-uniform
-    return x;
-}
-
 ASCA_DEV void st4(float* __restrict__ dst, float a, float b, float c, float e) {
     *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, e);
 }
 
-// State wave w (0..SW-1), lane = 16 cp + 8 n + r: rows 4 rg .. 4 rg + 3 (rg =
-// lane & 15) of the column pair 8 w + 2 cp, + 1.  The lane's own column is 8 w +
-// 2 cp + n (s[m][0]), the other one s[m][1]; the 16 lanes of a lane row hold
-// all 64 rows of both columns.  The CK steps of a chunk (rust/src/delta.rs:
-// 289-314 per step, without the output o), with P1 between steps CK/2 - 1 and
-// CK/2.  Step j writes the own column's u (u / G_{j+1} when scaled) to its u
-// row for the matrix waves; steps 0 and 1 store the lane's part of the
-// checkpoint ck (the state before the chunk, as S^T) of the own and the other
-// column; lane r of a column keeps the S^T k of step r + 8h and stores it after
-// step 8h + 7 (rows past nvalid go to the trash).  The gates arrive
-// lane-distributed (lane j of each lane row: step j) and are read out with
-// v_readlane.
+// State wave w (0..SW-1), lane = 8 c + g: column 8 w + c, rows 4 g .. 4 g + 3
+// (s[0..3]) and 32 + 4 g .. 32 + 4 g + 3 (s[4..7]), so the 8 lanes of a column
+// hold its 64 rows, S^T k is three DPP levels inside them, and the two 16-byte
+// k reads of a step cover 32 consecutive floats across the 8 lanes (distinct
+// banks).  The CK steps of a chunk (rust/src/delta.rs:289-314 per step,
+// without the output o).  Step j
+// writes its column's u (u / G_{j+1} when scaled) and x = S^T k (over G_j when
+// scaled) to row j of the chunk's u and x rows; the matrix waves take them from
+// there (the outputs, the stored S^T k).  The gates arrive lane-distributed
+// (lane j: step j) and are read out with v_readlane.  No barrier inside the
+// chunk: the matrix waves never write what the state waves read in it.
 //   SC = false: s is the state; u = beta v - alpha beta x, S <- alpha S + k u^T.
 //   SC = true:  s = S / G_j; x = s^T k, u / G_{j+1} = beta v / G_{j+1} - beta x and
-//     s <- s + k (u / G_{j+1})^T (one FMA per element); S^T k is rescaled by
-//     G_j at its store.
+//     s <- s + k (u / G_{j+1})^T (one FMA per element).
 template <bool SC>
-ASCA_DEV void fsteps(float (&s)[4][2], const float* __restrict__ ks, const float (&vb)[CK], float gb, float ga,
-                     float gab, const float (&ck)[4][2], float* __restrict__ ck0, float* __restrict__ ck1,
-                     float* __restrict__ skd, long d, int nvalid, float* __restrict__ tr, float* __restrict__ ub,
-                     int r, const float (&gsk)[2]) {
-    float4 kk[2];
-    float hs = 0.0f;
-    kk[0] = *reinterpret_cast<const float4*>(ks);
+ASCA_DEV void fsteps(float (&s)[8], const float* __restrict__ ks, const float (&vb)[CK], float gb, float ga,
+                     float gab, float* __restrict__ ub, float* __restrict__ xb) {
+    float4 kk[2][2];
+    kk[0][0] = *reinterpret_cast<const float4*>(ks);
+    kk[0][1] = *reinterpret_cast<const float4*>(ks + 32);
 #pragma unroll
     for (int j = 0; j < CK; ++j) {
         const int cs = j & 1;
-        if (j + 1 < CK) kk[cs ^ 1] = *reinterpret_cast<const float4*>(ks + (j + 1) * FP);
-        if (j == 0) st4(ck0, ck[0][0], ck[1][0], ck[2][0], ck[3][0]);
-        if (j == 1) st4(ck1, ck[0][1], ck[1][1], ck[2][1], ck[3][1]);
-        // the read of step j + 1 stays at the top of step j, a whole step ahead
-        // of its use
+        if (j + 1 < CK) {
+            kk[cs ^ 1][0] = *reinterpret_cast<const float4*>(ks + (j + 1) * FP);
+            kk[cs ^ 1][1] = *reinterpret_cast<const float4*>(ks + (j + 1) * FP + 32);
+        }
+        // the reads of step j + 1 stay at the top of step j, a whole step ahead
+        // of their use
         __builtin_amdgcn_sched_barrier(0);
-        const float4 k = kk[cs];
-        float a0 = s[0][0] * k.x, a1 = s[0][1] * k.x;
-        a0 = fmaf(s[1][0], k.y, a0);
-        a1 = fmaf(s[1][1], k.y, a1);
-        a0 = fmaf(s[2][0], k.z, a0);
-        a1 = fmaf(s[2][1], k.z, a1);
-        a0 = fmaf(s[3][0], k.w, a0);
-        a1 = fmaf(s[3][1], k.w, a1);
-        const float x = col_sum(a0, a1);
+        const float kv[8] = {kk[cs][0].x, kk[cs][0].y, kk[cs][0].z, kk[cs][0].w,
+                             kk[cs][1].x, kk[cs][1].y, kk[cs][1].z, kk[cs][1].w};
+        float a = s[0] * kv[0];
+#pragma unroll
+        for (int m = 1; m < 8; ++m) a = fmaf(s[m], kv[m], a);
+        const float x = group_sum<8>(a);
         float u0;
         if constexpr (SC) {
             u0 = fmaf(-readlane_f(gb, j), x, vb[j]);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) s[m] = fmaf(kv[m], u0, s[m]);
         } else {
             u0 = fmaf(-readlane_f(gab, j), x, vb[j]);
-        }
-        const float u1 = dpp<DPP_ROW_ROR8>(u0);
-        const float kv[4] = {k.x, k.y, k.z, k.w};
-        if constexpr (SC) {
+            const float al = readlane_f(ga, j);
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                s[m][0] = fmaf(kv[m], u0, s[m][0]);
-                s[m][1] = fmaf(kv[m], u1, s[m][1]);
-            }
-        } else {
-            const float a = readlane_f(ga, j);
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                s[m][0] = fmaf(a, s[m][0], kv[m] * u0);
-                s[m][1] = fmaf(a, s[m][1], kv[m] * u1);
-            }
+            for (int m = 0; m < 8; ++m) s[m] = fmaf(al, s[m], kv[m] * u0);
         }
-        ub[j * FP] = u0;   // the 8 lanes of a column store the same value
-        hs = r == (j & 7) ? x : hs;
-        if ((j & 7) == 7) {
-            const int jj = r + (j & 8);
-            *(jj < nvalid ? skd + jj * d : tr) = SC ? hs * gsk[j >> 3] : hs;
-        }
-        if (j == CK / 2 - 1) lds_barrier();   // P1
+        // the 8 lanes of a column store the same values
+        ub[j * FP] = u0;
+        xb[j * FP] = x;
     }
 }
 
@@ -267,8 +237,12 @@ ASCA_DEV void fsteps(float (&s)[4][2], const float* __restrict__ ks, const float
 // the q rows and the state's rows, as two accumulation chains; the 16 x 16
 // products k_l . q_j arrive as per-wave partials (fgram, a chunk earlier) in
 // exactly the lane layout the step mix takes as its operand (l = 4 gq + r).
+// The wave also stores the chunk's checkpoint rows 16 mw .. 16 mw + 15 (S^T,
+// read here for S^T q) and the S^T k of its columns (times G_j in a scaled
+// chunk) from the state waves' x rows.
 ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st, const float* __restrict__ ub,
-                    const float4* __restrict__ gpart, int mw, int lane, float* __restrict__ od, long d, int nvalid,
+                    const float* __restrict__ xb, const float4* __restrict__ gpart, int mw, int lane,
+                    float* __restrict__ od, float* __restrict__ skd, float* __restrict__ ckd, long d, int nvalid,
                     float* __restrict__ tr) {
     const int jr = lane & 15, gq = lane >> 4;
     const bool sc = buf[F_FLAG] == 1.0f;
@@ -303,9 +277,16 @@ ASCA_DEV void fprod(const float* __restrict__ buf, const float* __restrict__ st,
         acc = mfma4(x.y, y.y, acc);
         acc = mfma4(x.z, y.z, acc);
         acc = mfma4(x.w, y.w, acc);
+        *reinterpret_cast<float4*>(ckd + (16 * mw + jr) * DH + 16 * m + 4 * gq) = y;
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) a2 = mfma4(am[r], ub[(4 * gq + r) * FP + 16 * mw + jr], a2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int j = 4 * gq + r;
+        const float xv = xb[j * FP + 16 * mw + jr];
+        *(j < nvalid ? skd + j * d + 16 * mw + jr : tr + 4 + r) = sc ? xv * gt[j * 8 + 5] : xv;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int j = 4 * gq + r;
@@ -341,9 +322,9 @@ ASCA_DEV void fgram(const float* __restrict__ buf, float4* __restrict__ gpart, i
 // rust/src/delta.rs:54-56), as a two-stage pipeline over chunks: in period c
 // the state waves (0..SW-1, two per SIMD) run chunk c while the matrix waves
 // (SW..SW+W-1, one per SIMD) form the outputs of chunk c - 1, then stage chunk
-// c + 1 and its partial products k . q.  Two block barriers per period: P0 at
-// its start and P1 halfway through the chunk, after which the matrix waves
-// restage the buffer of chunk c - 1.
+// c + 1 and its partial products k . q.  One block barrier per period, at its
+// start: with three staging buffers the buffer being restaged (that of chunk
+// c - 2) is one that no wave reads any more in the period.
 template <bool AL>
 __global__ __launch_bounds__(FNT) void delta_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v, const float* __restrict__ alpha,
@@ -363,52 +344,41 @@ __global__ __launch_bounds__(FNT) void delta_fwd64_k(const float* __restrict__ q
 
     if (w < SW) {
         // state waves
-        const int rg = lane & 15, r = lane & 7, n = (lane >> 3) & 1, cp = lane >> 4;
-        const int col = 8 * w + 2 * cp + n, oth = col ^ 1;
-        float* const ckb = ckpt + (long)unit * nslots * DH2 + 4 * rg;
-        float s[4][2];
+        const int g = lane & 7, col = 8 * w + (lane >> 3);
+        float s[8];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) s[m][0] = s[m][1] = 0.0f;
+        for (int m = 0; m < 8; ++m) s[m] = 0.0f;
         lds_barrier();   // chunk 0 staged
-        for (int ci = 0; ci <= nchunk; ++ci) {
+        for (int ci = 0, b3 = 0; ci < nchunk; ++ci, b3 = b3 == 2 ? 0 : b3 + 1) {
             lds_barrier();   // P0
-            if (ci == nchunk) {
-                lds_barrier();   // P1
-                break;
-            }
-            const int t0 = ci * CK;
-            const float* const buf = lds + (ci & 1) * F_BUF;
+            const float* const buf = lds + b3 * F_BUF;
             const float* const gt = buf + F_G + (w & (W - 1)) * CK * 8;
             const bool sc = __builtin_amdgcn_readfirstlane(__float_as_int(buf[F_FLAG])) == __float_as_int(1.0f);
             float vb[CK];
 #pragma unroll
             for (int j = 0; j < CK; ++j) vb[j] = buf[F_V + j * DH + col];
-            const float4 g4 = *reinterpret_cast<const float4*>(gt + rg * 8);   // step rg's gate row
-            const float gsk[2] = {gt[r * 8 + 5], gt[(r + 8) * 8 + 5]};
-            float ck[4][2];   // the checkpoint: S before step t0
-#pragma unroll
-            for (int m = 0; m < 4; ++m) ck[m][0] = s[m][0], ck[m][1] = s[m][1];
-            float* const stb = lds + F_ST + (ci & 1) * DH * FP + 4 * rg;
-            st4(stb + col * FP, s[0][0], s[1][0], s[2][0], s[3][0]);
-            st4(stb + oth * FP, s[0][1], s[1][1], s[2][1], s[3][1]);
-            float* const skd = sk_out + ubase + (long)t0 * d + col;
+            // lane j (< CK): step j's gate row
+            const float4 g4 = *reinterpret_cast<const float4*>(gt + (lane & (CK - 1)) * 8);
+            // the state before the chunk (the checkpoint) as S^T rows
+            float* const stb = lds + F_ST + (ci & 1) * DH * FP + col * FP + 4 * g;
+            st4(stb, s[0], s[1], s[2], s[3]);
+            st4(stb + 32, s[4], s[5], s[6], s[7]);
             float* const ub = lds + F_U + (ci & 1) * CK * FP + col;
-            float* const ckc = ckb + (long)ci * DH2;
+            float* const xb = lds + F_X + (ci & 1) * CK * FP + col;
             if (sc) {
-                fsteps<true>(s, buf + F_K + 4 * rg, vb, g4.x, g4.z, g4.w, ck, ckc + col * DH, ckc + oth * DH, skd,
-                             d, T - t0, tr, ub, r, gsk);
+                fsteps<true>(s, buf + F_K + 4 * g, vb, g4.x, g4.z, g4.w, ub, xb);
                 const float ge = gt[(CK - 1) * 8 + 4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) s[m][0] *= ge, s[m][1] *= ge;
+                for (int m = 0; m < 8; ++m) s[m] *= ge;
             } else {
-                fsteps<false>(s, buf + F_K + 4 * rg, vb, g4.x, g4.z, g4.w, ck, ckc + col * DH, ckc + oth * DH, skd,
-                              d, T - t0, tr, ub, r, gsk);
+                fsteps<false>(s, buf + F_K + 4 * g, vb, g4.x, g4.z, g4.w, ub, xb);
             }
         }
+        lds_barrier();   // P0 of the period in which the matrix waves finish the last chunk
         // the state after step T-1
-        float* const ckl = ckb + (long)nchunk * DH2;
-        st4(ckl + col * DH, s[0][0], s[1][0], s[2][0], s[3][0]);
-        st4(ckl + oth * DH, s[0][1], s[1][1], s[2][1], s[3][1]);
+        float* const ckl = ckpt + ((long)unit * nslots + nchunk) * DH2 + col * DH + 4 * g;
+        st4(ckl, s[0], s[1], s[2], s[3]);
+        st4(ckl + 32, s[4], s[5], s[6], s[7]);
     } else {
         // matrix waves
         const int mw = w - SW, tx = threadIdx.x - 64 * SW;
@@ -417,24 +387,25 @@ __global__ __launch_bounds__(FNT) void delta_fwd64_k(const float* __restrict__ q
         fstage_load<AL>(stg, 0, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
         fstage_store(stg, 0, T, lds, tx, mw, lane);
         fgram(lds, gp, mw, lane);
-        // the loads of chunk ci + 1 are issued right after P1 of period ci - 1,
-        // a whole period ahead of their store
+        // the loads of chunk ci + 2 are issued in period ci, right after the
+        // store of chunk ci + 1, a whole period ahead of their own store
         if (nchunk > 1) fstage_load<AL>(stg, 1, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
         lds_barrier();   // chunk 0 staged
-        for (int ci = 0; ci <= nchunk; ++ci) {
+        for (int ci = 0, b3 = 0; ci <= nchunk; ++ci, b3 = b3 == 2 ? 0 : b3 + 1) {
             lds_barrier();   // P0
             if (ci > 0) {
-                const int cp = ci - 1;
-                fprod(lds + (cp & 1) * F_BUF, lds + F_ST + (cp & 1) * DH * FP, lds + F_U + (cp & 1) * CK * FP,
-                      gp + (cp & 1) * W * 64, mw, lane,
-                      o + ubase + (long)cp * CK * d, d, T - cp * CK, tr);
+                const int cp = ci - 1, bp = b3 == 0 ? 2 : b3 - 1;
+                fprod(lds + bp * F_BUF, lds + F_ST + (cp & 1) * DH * FP, lds + F_U + (cp & 1) * CK * FP,
+                      lds + F_X + (cp & 1) * CK * FP, gp + bp * W * 64, mw, lane,
+                      o + ubase + (long)cp * CK * d, sk_out + ubase + (long)cp * CK * d,
+                      ckpt + ((long)unit * nslots + cp) * DH2, d, T - cp * CK, tr);
             }
-            lds_barrier();   // P1
             if (ci + 1 < nchunk) {
-                fstage_store(stg, ci + 1, T, lds + ((ci + 1) & 1) * F_BUF, tx, mw, lane);
+                const int bn = b3 == 2 ? 0 : b3 + 1;
+                fstage_store(stg, ci + 1, T, lds + bn * F_BUF, tx, mw, lane);
                 if (ci + 2 < nchunk)
                     fstage_load<AL>(stg, ci + 2, q, k, v, alpha, beta, ubase, gbase, d, T, H, tx, lane);
-                fgram(lds + ((ci + 1) & 1) * F_BUF, gp + ((ci + 1) & 1) * W * 64, mw, lane);
+                fgram(lds + bn * F_BUF, gp + bn * W * 64, mw, lane);
             }
         }
     }
@@ -648,8 +619,12 @@ ASCA_DEV void put_du(float* __restrict__ dub, float* __restrict__ dskb, int j, i
 // adjoint only).  ds = G_{j+1} dS_j with dS_j excluding q_j dO_j^T on entry:
 //   ds += q_j (G_{j+1} dO_j)^T;  t = ds^T k_j = G_{j+1} du_j;
 //   G_j dsk_j = -beta_j t;        ds += k_j (G_j dsk_j)^T  (= G_j dS_{j-1} part).
-// Returns the lane's transposed (ea, eb) pair of the step: ea = -beta du.sk,
-// eb = du.(v - alpha sk) over the lane's columns (row group 0 only).
+// AB: returns the lane's transposed (ea, eb) pair of the step: ea = -beta
+// du.sk, eb = du.(v - alpha sk) over the lane's columns (row group 0 only),
+// and every lane stores du (even row groups) or G_j dsk (odd ones).  Without
+// AB (the pipelined backward, whose matrix waves form these step sums from the
+// du rows), nothing is returned and every lane stores both rows.
+template <bool AB>
 ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ dub, float* __restrict__ dskb, int j,
                         int kc, int rg) {
 #pragma unroll
@@ -666,15 +641,24 @@ ASCA_DEV float bstep_sc(const BOps& in, float (&ds)[BM][2], float* __restrict__ 
     const float t0 = group_sum<8>(c0), t1 = group_sum<8>(c1);
     const float du0 = t0 * in.gt.w, du1 = t1 * in.gt.w;
     const float sh0 = -in.gt.y * t0, sh1 = -in.gt.y * t1;
-    put_du<true>(dub, dskb, j, kc, rg, du0, du1, sh0, sh1);
+    if constexpr (AB) {
+        put_du<true>(dub, dskb, j, kc, rg, du0, du1, sh0, sh1);
+    } else {
+        *reinterpret_cast<float2*>(dub + j * P + kc) = make_float2(du0, du1);
+        *reinterpret_cast<float2*>(dskb + j * P + kc) = make_float2(sh0, sh1);
+    }
 #pragma unroll
     for (int m = 0; m < BM; ++m) {
         ds[m][0] = fmaf(in.k[m], sh0, ds[m][0]);
         ds[m][1] = fmaf(in.k[m], sh1, ds[m][1]);
     }
-    const float ea = rg == 0 ? -in.gt.y * fmaf(du1, in.sk.y, du0 * in.sk.x) : 0.0f;
-    const float eb = rg == 0 ? fmaf(du1, in.wv.y, du0 * in.wv.x) : 0.0f;
-    return tsum32(ea, eb);
+    if constexpr (AB) {
+        const float ea = rg == 0 ? -in.gt.y * fmaf(du1, in.sk.y, du0 * in.sk.x) : 0.0f;
+        const float eb = rg == 0 ? fmaf(du1, in.wv.y, du0 * in.wv.x) : 0.0f;
+        return tsum32(ea, eb);
+    } else {
+        return 0.0f;
+    }
 }
 
 // One scaled segment (every alpha in [2^-6, 2^6]).  With G_j the product of the
@@ -703,7 +687,7 @@ ASCA_DEV void bsegment_sc(float (&ds)[BM][2], const BStage& stg, int g, int T, c
     for (int jj = CK - 1; jj >= 0; --jj) {
         // the operand reads of the next step are issued a whole step ahead
         if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, rowb, kc);
-        pab[jj] = bstep_sc(op[jj & 1], ds, wk + W_DU, wk + W_DSK, jj, kc, rg);
+        pab[jj] = bstep_sc<true>(op[jj & 1], ds, wk + W_DU, wk + W_DSK, jj, kc, rg);
         if (jj == CK / 2) {
             // the staged operands of the next segment (loads issued at this
             // segment's start) go to its buffer; the fence keeps the scheduler
@@ -1114,18 +1098,17 @@ constexpr size_t B_LDS_ALL = (size_t)(Q_END > 2 * S_BUF + W_END ? Q_END : 2 * S_
 static_assert(B_LDS_ALL <= 160 * 1024, "backward LDS");
 
 // Adjoint waves: the loop of one scaled segment (as in bsegment_sc, without
-// the products), with P1 between steps CK/2 and CK/2 - 1; then the anchor
-// <dS_out, S> and the step sums.
+// the products and the step sums), with P1 between steps CK/2 and CK/2 - 1;
+// then the anchor <dS_out, S>.
 ASCA_DEV void aloop(float (&ds)[BM][2], const float* __restrict__ buf, float* __restrict__ dub,
-                    float* __restrict__ dskb, float* __restrict__ abb, float* __restrict__ brb, int w, int lane,
-                    int rg, int cg, int rowb, int kc) {
-    float pab[CK];
+                    float* __restrict__ dskb, float* __restrict__ brb, int w, int lane, int rg, int cg, int rowb,
+                    int kc) {
     BOps op[2];
     bops_read(op[(CK - 1) & 1], buf, CK - 1, rowb, kc);
 #pragma unroll
     for (int jj = CK - 1; jj >= 0; --jj) {
         if (jj > 0) bops_read(op[(jj - 1) & 1], buf, jj - 1, rowb, kc);
-        pab[jj] = bstep_sc(op[jj & 1], ds, dub, dskb, jj, kc, rg);
+        bstep_sc<false>(op[jj & 1], ds, dub, dskb, jj, kc, rg);
         if (jj == CK / 2) lds_barrier();   // P1
     }
     float x = 0.0f;
@@ -1141,7 +1124,6 @@ ASCA_DEV void aloop(float (&ds)[BM][2], const float* __restrict__ buf, float* __
         }
     x = wave_sum(x);
     if (lane == 0) brb[w] = x;
-    cross_step_sum<CK, W>(pab, abb, w, lane);
 }
 
 // What a matrix wave keeps of a segment's staging buffer for its epilogue.
@@ -1155,7 +1137,8 @@ struct MEpi {
 // (each wave its own, through a private LDS area), the rows and the partial
 // q . dq, k . dk; then what the epilogue needs from the staging buffer.
 ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt, const float* __restrict__ dsk,
-                    float* __restrict__ lds, int mw, int lane, MEpi& e) {
+                    const float* __restrict__ dub, float* __restrict__ abb, float* __restrict__ lds, int mw,
+                    int lane, MEpi& e) {
     const int jr = lane & 15, gq = lane >> 4;
     float a_do[16], a_u[16], a_dk[16], b_s[16], b_x[16];
 #pragma unroll
@@ -1221,6 +1204,25 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
     }
     e.gl0 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)));
     e.gl1 = *reinterpret_cast<const float4*>(buf + S_G + 8 * (lane & (CK - 1)) + 4);
+    {
+        // the step sums of dalpha / dbeta over the k-order positions 16 mw ..
+        // 16 mw + 15 (lane: step jr, positions 16 mw + 4 gq .. + 3):
+        // ea_j = -beta_j du_j . sk_j, eb_j = du_j . (v_j - alpha_j sk_j)
+        const int c0 = 16 * mw + 4 * gq;
+        const float4 u = *reinterpret_cast<const float4*>(dub + jr * P + c0);
+        const float4 a = *reinterpret_cast<const float4*>(buf + S_SK + jr * P + c0);
+        const float4 b = *reinterpret_cast<const float4*>(buf + S_WV + jr * P + c0);
+        float ea = u.x * a.x, eb = u.x * b.x;
+        ea = fmaf(u.y, a.y, ea);
+        eb = fmaf(u.y, b.y, eb);
+        ea = fmaf(u.z, a.z, ea);
+        eb = fmaf(u.z, b.z, eb);
+        ea = fmaf(u.w, a.w, ea);
+        eb = fmaf(u.w, b.w, eb);
+        ea = add_xor32(add_xor16(ea));
+        eb = add_xor32(add_xor16(eb));
+        if (gq == 0) *reinterpret_cast<float2*>(abb + (jr * W + mw) * 2) = make_float2(-buf[S_G + 8 * jr + 1] * ea, eb);
+    }
 }
 
 // Matrix wave mw: dalpha's bracket and the epilogue of segment gp (as in
@@ -1370,7 +1372,7 @@ __global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
                             make_float4(ds[e][n], ds[e + 1][n], ds[e + 2][n], ds[e + 3][n]);
                 }
                 aloop(ds, buf, lds + Q_DU + (g & 1) * CK * P, lds + Q_DSK + (g & 1) * CK * P,
-                      lds + Q_AB + (g & 1) * CK * W * 2, lds + Q_BR + (g & 1) * 8, w, lane, rg, cg, rowb, kc);
+                      lds + Q_BR + (g & 1) * 8, w, lane, rg, cg, rowb, kc);
             } else {
                 lds_barrier();   // P1
             }
@@ -1395,7 +1397,7 @@ __global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
             MEpi e;
             if (gp < nseg)
                 mprod(lds + Q_STG + (gp & 1) * S_BUF, lds + Q_XT + (gp & 1) * DH * P, lds + Q_DSK + (gp & 1) * CK * P,
-                      lds, mw, lane, e);
+                      lds + Q_DU + (gp & 1) * CK * P, lds + Q_AB + (gp & 1) * CK * W * 2, lds, mw, lane, e);
             lds_barrier();   // P1
             if (g >= 1) bstage_store(stg, g - 1, T, lds + Q_STG + ((g - 1) & 1) * S_BUF, tx, mw, lane);
             if (g >= 2)
