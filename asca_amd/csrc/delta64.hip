@@ -1092,7 +1092,8 @@ constexpr int Q_AB = Q_PR + W * 2 * CK * 17;      // [2][CK][W][2] step sums
 constexpr int Q_QDQ = Q_AB + 2 * CK * W * 2;      // [W][CK] per-wave partial q . dq
 constexpr int Q_KDK = Q_QDQ + W * CK;             // [W][CK] per-wave partial k . dk
 constexpr int Q_BR = Q_KDK + W * CK;              // [2][8] per-wave partial <dS, S>
-constexpr int Q_END = Q_BR + 16;
+constexpr int Q_D0 = Q_BR + 16;                   // [CK][DH] dO~ S^T from the adjoint waves
+constexpr int Q_END = Q_D0 + CK * DH;
 static_assert(Q_DU % 4 == 0 && Q_DQ % 4 == 0 && Q_AB % 4 == 0, "16-byte rows");
 constexpr size_t B_LDS_ALL = (size_t)(Q_END > 2 * S_BUF + W_END ? Q_END : 2 * S_BUF + W_END) * 4;
 static_assert(B_LDS_ALL <= 160 * 1024, "backward LDS");
@@ -1126,6 +1127,28 @@ ASCA_DEV void aloop(float (&ds)[BM][2], const float* __restrict__ buf, float* __
     if (lane == 0) brb[w] = x;
 }
 
+// Adjoint wave w, after the loop of a segment: the part dO~ S^T of its dq
+// columns 16 w .. 16 w + 15 (a product of staged inputs only), computed as
+// mprod would, into d0, where matrix wave w starts its dq sums from it a
+// period later; the adjoint waves have this time to spare before the next
+// period while the matrix waves run the epilogue.
+ASCA_DEV void adj_dq(const float* __restrict__ buf, float* __restrict__ d0, int w, int lane) {
+    const int jr = lane & 15, gq = lane >> 4;
+    float a_do[16], b_s[16];
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+        const float4 x = *reinterpret_cast<const float4*>(buf + S_DO + jr * P + 16 * gq + 4 * e4);
+        a_do[4 * e4] = x.x; a_do[4 * e4 + 1] = x.y; a_do[4 * e4 + 2] = x.z; a_do[4 * e4 + 3] = x.w;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 16; ++kb) b_s[kb] = buf[S_M + kcol(gq, kb) * P + 16 * w + jr];
+    f32x4 adq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 16; ++kb) adq = mfma4(a_do[kb], b_s[kb], adq);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d0[(4 * gq + r) * DH + 16 * w + jr] = adq[r];
+}
+
 // What a matrix wave keeps of a segment's staging buffer for its epilogue.
 struct MEpi {
     float qa[CK / W], ka[CK / W];   // q, k of the wave's steps, lane = row
@@ -1139,6 +1162,7 @@ struct MEpi {
 ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt, const float* __restrict__ dsk,
                     const float* __restrict__ dub, float* __restrict__ abb, float* __restrict__ lds, int mw,
                     int lane, MEpi& e) {
+    // dq starts from dO~ S^T (adj_dq, the adjoint waves' product)
     const int jr = lane & 15, gq = lane >> 4;
     float a_do[16], a_u[16], a_dk[16], b_s[16], b_x[16];
 #pragma unroll
@@ -1155,10 +1179,11 @@ ASCA_DEV void mprod(const float* __restrict__ buf, const float* __restrict__ xt,
         b_s[kb] = buf[S_M + kcol(gq, kb) * P + 16 * mw + jr];
         b_x[kb] = xt[kcol(gq, kb) * P + 16 * mw + jr];
     }
-    f32x4 adq = {0.f, 0.f, 0.f, 0.f}, adk = adq, ap = adq, ar = adq;
+    f32x4 adk = {0.f, 0.f, 0.f, 0.f}, ap = adk, ar = adk, adq;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) adq[r] = lds[Q_D0 + (4 * gq + r) * DH + 16 * mw + jr];
 #pragma unroll
     for (int kb = 0; kb < 16; ++kb) {
-        adq = mfma4(a_do[kb], b_s[kb], adq);
         adk = mfma4(a_u[kb], b_x[kb], adk);
         adk = mfma4(a_dk[kb], b_s[kb], adk);
         ap = mfma4(a_u[kb], a_do[kb], ap);
@@ -1373,6 +1398,7 @@ __global__ __launch_bounds__(2 * NT) void delta_bwd64_k(
                 }
                 aloop(ds, buf, lds + Q_DU + (g & 1) * CK * P, lds + Q_DSK + (g & 1) * CK * P,
                       lds + Q_BR + (g & 1) * 8, w, lane, rg, cg, rowb, kc);
+                adj_dq(buf, lds + Q_D0, w, lane);
             } else {
                 lds_barrier();   // P1
             }
