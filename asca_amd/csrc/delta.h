@@ -69,6 +69,8 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
 constexpr int D64_CK = 16;
 int launch_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                  const DeltaWs& ws, int B, int T, int H, hipStream_t st);
+int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
+                    const DeltaWs& ws, int B, int T, int H, hipStream_t st);
 int launch_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
                  const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
                  float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,

@@ -1289,6 +1289,12 @@ int asca_delta_bwd_fused(const float* q, const float* k, const float* v, const f
                             d_gate, d_gate + H, 2L * H, B, T, H, dh, as_stream(stream));
 }
 
+ASCA_API int asca_dev_ut_fwd(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                             float* o, void* ws, int B, int T, int H) {
+    DeltaWs w = ws_layout(B, T, H, 64, ws);
+    return launch_ut_fwd64(q, k, v, alpha, beta, o, w, B, T, H, nullptr);
+}
+
 int asca_delta_states(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
                       float* states, int B, int T, int H, int dh, void* stream) {
     int rc = check_shape(B, T, H, dh);
