@@ -17,6 +17,7 @@ struct DeltaWs {
     float* ckpt;
     float* part_x;  // column split: partial dq, dk  [2][CS][B*T][H*dh]
     float* part_g;  // column split: partial dalpha, dbeta  [CS][B*T][2H]
+    float* rec;     // dh = 64 blocked form: per unit and 16-step block, K K^T, Q K^T, T, M
     int ck;
     int nslots;
     int cs;
@@ -71,6 +72,10 @@ int launch_fwd64(const float* q, const float* k, const float* v, const float* al
                  const DeltaWs& ws, int B, int T, int H, hipStream_t st);
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st);
+int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
+                    const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
+                    float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
+                    hipStream_t st);
 int launch_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
                  const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
                  float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,

@@ -1114,12 +1114,15 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
     const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
     const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
+    const size_t rec_bytes =
+        four_wave(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * 1024 * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
     w.sk = reinterpret_cast<float*>(base);
     w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
     w.part_x = base && px_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
     w.part_g = base && pg_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes) : nullptr;
-    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes;
+    w.rec = base && rec_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes) : nullptr;
+    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes;
     return w;
 }
 
@@ -1293,6 +1296,18 @@ ASCA_API int asca_dev_ut_fwd(const float* q, const float* k, const float* v, con
                              float* o, void* ws, int B, int T, int H) {
     DeltaWs w = ws_layout(B, T, H, 64, ws);
     return launch_ut_fwd64(q, k, v, alpha, beta, o, w, B, T, H, nullptr);
+}
+
+ASCA_API int asca_dev_ut_bwd(int fused, const float* q, const float* k, const float* v, const float* alpha,
+                             const float* beta, const float* qn, const float* kn, const float* d_o, void* ws,
+                             float* o1, float* o2, float* o3, float* o4, float* o5, int B, int T, int H) {
+    DeltaWs w = ws_layout(B, T, H, 64, ws);
+    const long d = (long)H * 64;
+    if (fused)
+        return launch_ut_bwd64(true, q, k, v, alpha, beta, d_o, w, qn, kn, o1, o1 + d, o1 + 2 * d, 3 * d, o2, o2 + H,
+                               2L * H, B, T, H, nullptr);
+    return launch_ut_bwd64(false, q, k, v, alpha, beta, d_o, w, nullptr, nullptr, o1, o2, o3, d, o4, o5, H, B, T, H,
+                           nullptr);
 }
 
 int asca_delta_states(const float* q, const float* k, const float* v, const float* alpha, const float* beta,

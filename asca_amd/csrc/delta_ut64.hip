@@ -36,7 +36,7 @@ namespace asca {
 namespace ut64 {
 
 constexpr int DH = 64;
-constexpr int C = 16;          // steps per block (= checkpoint interval)
+constexpr int C = 16;          // steps per block = checkpoint interval
 constexpr int NW = 4;          // waves per unit
 constexpr int NT = 64 * NW;
 constexpr int DH2 = DH * DH;
@@ -72,8 +72,13 @@ struct PrepIn {
 // Forms block p's matrices from its loads into the slot `ps`.  Steps past the
 // sequence end get alpha = 1, beta = 0: they leave the state, T and the
 // products of the live steps unchanged.  `scr` is the wave's own scratch.
+// Record of a block for the backward (1024 floats): K K^T, Q K^T, T and M in
+// the accumulator layout, 16 bytes per lane (float4 index 64 m + lane holds
+// matrix m's elements [4 (lane/16) + j][lane % 16], j = 0..3).
+constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_SZ = 1024;
+
 ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ ps, float* __restrict__ scr,
-                           int lane) {
+                           float* __restrict__ rec, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const bool live = p * C + n < T;
     const float a = live ? pi.a : 1.0f;
@@ -128,6 +133,13 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
             *reinterpret_cast<float4*>(ps + P_T + n * 16 + 4 * q4) =
                 make_float4(x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]);
     }
+    float4* rq = reinterpret_cast<float4*>(rec);
+    rq[(R_A >> 2) + lane] = make_float4(A[0], A[1], A[2], A[3]);
+    rq[(R_BQ >> 2) + lane] = make_float4(Bq[0], Bq[1], Bq[2], Bq[3]);
+    const float* tp = ps + P_T + 64 * g + n;
+    rq[(R_T >> 2) + lane] = make_float4(tp[0], tp[16], tp[32], tp[48]);
+    const float* mp = ps + P_M + 64 * g + n;
+    rq[(R_M >> 2) + lane] = make_float4(mp[0], mp[16], mp[32], mp[48]);
 }
 
 // Staging of a group's k, q, v rows in LDS: buffer of 4 blocks x 16 rows, row
@@ -138,9 +150,9 @@ constexpr int G_ROWS = NW * C;               // rows of one group
 constexpr int S_MAT = G_ROWS * RP;           // one matrix of a group
 constexpr int S_BUF = 3 * S_MAT;             // k, q, v
 constexpr int F_STG = F_FLOATS;              // [2][S_BUF]
-constexpr int F_OT = F_STG + 2 * S_BUF;      // per wave: the o and u tiles [2][16][20] on their way out
+constexpr int F_OT = F_STG + 2 * S_BUF;      // per wave: the o and u tiles and a state tile [3][16][20] on their way out
 constexpr int OTP = 20;
-constexpr int F_ALL = F_OT + NW * 2 * C * OTP;
+constexpr int F_ALL = F_OT + NW * 3 * C * OTP;
 constexpr size_t F_LDS = (size_t)F_ALL * 4;
 static_assert(F_LDS <= 160 * 1024, "forward LDS");
 
@@ -174,13 +186,21 @@ ASCA_DEV void stage_store(const Stage& st, float* __restrict__ buf, int w, int l
     }
 }
 
-// Checkpoint slot layout (4096 floats): the accumulator tiles as the forward's
-// waves hold them, 16 bytes per lane: float4 index (w*4 + r)*64 + lane holds
-// S[16r + 4(lane/16) + j][16w + lane%16], j = 0..3.
-ASCA_DEV void ck_store(float* __restrict__ slot, const f32x4 (&S)[4], int w, int lane) {
+// Checkpoint slot layout (4096 floats), the state before a block as the
+// backward's key-slab waves read it, 16 bytes per lane: float4 index
+// (r*4 + c)*64 + lane holds S[16r + lane%16][16c + 4(lane/16) + j], j = 0..3
+// (key tile r, value tile c).  The forward's wave w holds value tile c = w with
+// keys and values swapped within each 16 x 16 tile, so every tile is transposed
+// through the wave's LDS scratch `st` on its way out.
+ASCA_DEV void ck_store(float* __restrict__ slot, const f32x4 (&S)[4], float* __restrict__ st, int w, int lane) {
+    const int n = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<float4*>(slot + ((w * 4 + r) * 64 + lane) * 4) = make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[(4 * g + i) * OTP + n] = S[r][i];
+        const float4 t4 = *reinterpret_cast<const float4*>(st + n * OTP + 4 * g);
+        *reinterpret_cast<float4*>(slot + ((r * 4 + w) * 64 + lane) * 4) = t4;
+    }
 }
 
 // One block of 16 steps for the wave's 64 x 16 slab of S: outputs o, the u rows
@@ -234,7 +254,7 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
     for (int i = 0; i < 4; ++i) O[i] = el(gm, i) * (qa[i] + qb2[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) O = mfma4(el(mr, i), U[i], O);
-    ck_store(ckb + (long)c * DH2, S, w, lane);
+    ck_store(ckb + (long)c * DH2, S, ot + 2 * C * OTP, w, lane);
     // o and u rows leave as 16-byte stores: the 16 x 16 tiles go through the
     // wave's LDS scratch (lane: row lane / 4, columns 4 (lane % 4) .. +3)
 #pragma unroll
@@ -275,7 +295,7 @@ ASCA_DEV void gate_load(float& a, float& b, int c, const float* __restrict__ alp
 
 // The helper wave's prep of block p from its staged rows (rows 16 hw .. of `buf`).
 ASCA_DEV void helper_prep(int p, const float* __restrict__ buf, float a, float b, float* __restrict__ ps,
-                          float* __restrict__ scr, int T, int hw, int lane) {
+                          float* __restrict__ scr, float* __restrict__ rec, int T, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
     PrepIn pi;
 #pragma unroll
@@ -285,7 +305,7 @@ ASCA_DEV void helper_prep(int p, const float* __restrict__ buf, float a, float b
     }
     pi.a = a;
     pi.b = b;
-    prep_compute(pi, p, T, ps, scr, lane);
+    prep_compute(pi, p, T, ps, scr, rec + (long)p * R_SZ, lane);
 }
 
 // Block of 2 NW waves.  Waves 0 .. NW-1 (one per SIMD) run the chain: wave w owns
@@ -300,8 +320,8 @@ template <bool AL>
 __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v, const float* __restrict__ alpha,
                                                      const float* __restrict__ beta, float* __restrict__ o,
-                                                     float* __restrict__ ws_u, float* __restrict__ ckpt, int B,
-                                                     int T, int H, int nslots) {
+                                                     float* __restrict__ ws_u, float* __restrict__ ckpt,
+                                                     float* __restrict__ rec, int B, int T, int H, int nslots) {
     extern __shared__ float lds[];
     const int unit = blockIdx.x;  // h*B + b
     const int h = unit / B, b = unit - h * B;
@@ -314,12 +334,13 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
         const int hw = w - NW;
         const long gbase = (long)b * T * H + h;
         float* scr = lds + F_SCR + hw * 256;
+        float* recb = rec + (long)unit * NC * R_SZ;
         Stage stg;
         float ga, gb;
         stage_load<AL>(stg, min(hw, NC - 1), q, k, v, ubase, d, T, lane);
         gate_load(ga, gb, min(hw, NC - 1), alpha, beta, gbase, T, H, lane);
         stage_store(stg, lds + F_STG, hw, lane);
-        if (hw < NC) helper_prep(hw, lds + F_STG, ga, gb, lds + hw * P_SZ, scr, T, hw, lane);
+        if (hw < NC) helper_prep(hw, lds + F_STG, ga, gb, lds + hw * P_SZ, scr, recb, T, hw, lane);
         stage_load<AL>(stg, min(NW + hw, NC - 1), q, k, v, ubase, d, T, lane);
         gate_load(ga, gb, min(NW + hw, NC - 1), alpha, beta, gbase, T, H, lane);
         lds_barrier();
@@ -330,13 +351,13 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
             const float a = ga, bb = gb;
             stage_load<AL>(stg, min(pn + NW, NC - 1), q, k, v, ubase, d, T, lane);
             gate_load(ga, gb, min(pn + NW, NC - 1), alpha, beta, gbase, T, H, lane);
-            if (pn < NC) helper_prep(pn, nbuf, a, bb, lds + (pn % NSLOT) * P_SZ, scr, T, hw, lane);
+            if (pn < NC) helper_prep(pn, nbuf, a, bb, lds + (pn % NSLOT) * P_SZ, scr, recb, T, hw, lane);
             lds_barrier();
         }
         return;
     }
 
-    float* ot = lds + F_OT + w * 2 * C * OTP;
+    float* ot = lds + F_OT + w * 3 * C * OTP;
     float* ckb = ckpt + (long)unit * nslots * DH2;
     f32x4 S[4];
 #pragma unroll
@@ -357,7 +378,562 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
         }
         lds_barrier();
     }
-    ck_store(ckb + (long)NC * DH2, S, w, lane);
+    ck_store(ckb + (long)NC * DH2, S, ot + 2 * C * OTP, w, lane);
+}
+
+// ================================================================= backward
+//
+// Reverse over the blocks, with X = dL/dS' the gradient of the state after the
+// block (zero after the last step, as bptt_cpu starts, delta.rs:475-587), the
+// block's gradients follow from the UT form (the oracle's chunked restatement):
+//
+//     dU = M^T dO + diag(Gamma[15][:]) K X,      Y = T^T dU,     dv = diag(beta) Y
+//     X_prev = gamma_15 X + (diag(gamma) Q)^T dO - K^T diag(beta gamma) Y
+//     dM = tril(dO U^T),   dL = -strict_tril(Y U^T),   dA = dL o beta_row o Gamma
+//     dq = diag(gamma) dO S^T + (Gamma o dM) K
+//     dk = -diag(beta gamma) Y S^T + diag(Gamma[15][:]) U X^T + (Gamma o dM)^T Q + (dA + dA^T) K
+//     dbeta, dgamma, dGamma from row sums, dalpha from running products (no division).
+//
+// Eight waves per unit.  The four chain waves own value columns 16w .. 16w + 15
+// of X (accumulator tiles, like the forward's state) and run only the X
+// recurrence (K X, M^T dO, T^T dU, the update: 56 MFMAs per block) plus dv and
+// their share of dO U^T and Y U^T.  They hand X (before its update) and Y over
+// in LDS.  The four helper waves own key columns 16hw .. 16hw + 15 of dq and dk:
+// one block behind the chain they form dO S^T, Y S^T, U X^T over all value
+// columns (S from the forward's checkpoint of the block), dq and dk and their row
+// sums; one more block behind, the L2-norm backward of dq, dk (from the row dots
+// of all four helpers), the gate gradients (helper 0) and the stores.  The
+// helpers also stage the k, q, dO, u rows of the block after next.  One barrier
+// per block.
+constexpr int SB_MAT = C * RP;
+constexpr int SB_K = 0, SB_Q = SB_MAT, SB_DO = 2 * SB_MAT, SB_U = 3 * SB_MAT;
+constexpr int SB_BUF = 4 * SB_MAT;
+constexpr int NSB = 3;                       // stage buffers: block c in buffer c % 3
+constexpr int HO_DS = 0;                     // X tiles, checkpoint layout [r][c][lane][4]
+constexpr int HO_Y = 4096;                   // Y tiles: [c][lane] float4 = Y[n][16c + 4g ..]
+constexpr int HO_DM = 5120;                  // per chain wave dO_w U_w^T (accumulator layout)
+constexpr int HO_DL = 6144;                  // per chain wave Y_w U_w^T
+constexpr int HO_YV = 7168;                  // per chain wave row sums of Y_w o V_w [w][16]
+constexpr int HO_SZ = 7232;
+constexpr int EP_ROW = 0;                    // [hw][5][16]: q.dq, k.dk, q.F, k.Zt, k.D over the helper's keys
+constexpr int EP_RQ = 0, EP_RK = 1, EP_QF = 2, EP_ZK = 3, EP_KD = 4;
+constexpr int EP_DSS = 320;                  // [hw]: <X, S> over the helper's keys
+constexpr int EP_YV = 324;                   // [16]: row sums of Y o V
+constexpr int EP_SZ = 344;
+constexpr int WSCR = 2 * C * OTP;            // per wave: a transpose tile and a vector area
+constexpr int B_STG = 0;
+constexpr int B_HO = B_STG + NSB * SB_BUF;
+constexpr int B_EP = B_HO + 2 * HO_SZ;
+constexpr int B_SCR = B_EP + 2 * EP_SZ;
+constexpr int B_G = B_SCR + 2 * NW * WSCR;   // helper 0: dGamma and Gamma rows [2][16][16]
+constexpr int B_END = B_G + 512;
+constexpr size_t B_LDS = (size_t)B_END * 4;
+static_assert(B_LDS <= 160 * 1024 && B_HO % 4 == 0 && B_EP % 4 == 0 && B_SCR % 4 == 0, "backward LDS");
+
+// Orders the wave's own LDS writes before its reads of other lanes' values.
+ASCA_DEV void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 16x16 tile in the accumulator layout (lane (g, n) holds X[4g + j][n]) ->
+// lane (g, n) receives X[n][4g .. 4g + 3].
+ASCA_DEV float4 tile_t(const f32x4& x, float* __restrict__ st, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st[(4 * g + j) * OTP + n] = x[j];
+    wave_sync();
+    const float4 r = *reinterpret_cast<const float4*>(st + n * OTP + 4 * g);
+    wave_sync();
+    return r;
+}
+
+// Values held by lane t of each 16-lane row (the same in every row) -> lane
+// (g, n) receives those of lanes 4g .. 4g + 3.
+ASCA_DEV float4 rows4(float x, float* __restrict__ sv, int lane) {
+    if (lane < 16) sv[lane] = x;
+    wave_sync();
+    const float4 r = *reinterpret_cast<const float4*>(sv + 4 * (lane >> 4));
+    wave_sync();
+    return r;
+}
+
+// Exclusive suffix product over each 16-lane row: lane m gets prod_{m<s<16} x_s.
+ASCA_DEV float suffix_excl_prod(float x) {
+    x *= dpp_or<0x101>(1.0f, x);
+    x *= dpp_or<0x102>(1.0f, x);
+    x *= dpp_or<0x104>(1.0f, x);
+    x *= dpp_or<0x108>(1.0f, x);
+    return dpp_or<0x101>(1.0f, x);
+}
+
+// G[j] = Gamma[4g + j][n] = prod_{n<s<=4g+j} alpha_s for 4g + j >= n, else 0
+// (alpha of step s in lane s of the row).
+ASCA_DEV void gamma_acc(float a, float (&G)[4], int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    float pr = 1.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < C; ++s) {
+        const float as = readlane_f(a, s);
+        pr = s > n ? pr * as : pr;
+        if ((s >> 2) == g) G[s & 3] = s >= n ? pr : 0.0f;
+    }
+}
+
+template <bool AL>
+ASCA_DEV void store4(float* __restrict__ p, float4 x) {
+    if constexpr (AL) *reinterpret_cast<float4*>(p) = x;
+    else { p[0] = x.x; p[1] = x.y; p[2] = x.z; p[3] = x.w; }
+}
+
+ASCA_DEV float4 f4scale(float s, float4 x) { return make_float4(s * x.x, s * x.y, s * x.z, s * x.w); }
+ASCA_DEV float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+struct BArgs {
+    const float *q, *k, *v, *alpha, *beta, *d_o, *u, *ckpt, *rec, *qn, *kn;
+    float *gq, *gk, *gv, *ga, *gb;
+    long ldx, ldg, d, ubase, gbase, rowbase;
+    int B, T, H, h, nslots, NC, unit;
+};
+
+struct BChainIn {
+    float a, b;       // gates of step 16c + n
+    float4 v;         // V[16c + n][16w + 4g ..]
+    float4 tr, mr;    // T and M of the block (accumulator layout)
+};
+
+template <bool AL>
+ASCA_DEV void bchain_load(BChainIn& ci, int c, const BArgs& A, int w, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const long t = min(c * C + n, A.T - 1);
+    ci.a = A.alpha[A.gbase + t * A.H];
+    ci.b = A.beta[A.gbase + t * A.H];
+    ci.v = ld4<AL>(A.v + A.ubase + t * A.d + 16 * w + 4 * g);
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    ci.tr = rq[(R_T >> 2) + lane];
+    ci.mr = rq[(R_M >> 2) + lane];
+}
+
+template <bool AL>
+ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __restrict__ sb, float* __restrict__ ho,
+                          float* __restrict__ scr, int c, const BArgs& A, int w, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const bool live = c * C + n < A.T;
+    const float a = live ? ci.a : 1.0f;
+    const float bt = live ? ci.b : 0.0f;
+    const float gam = prefix_prod<16>(a);
+    const float g15 = readlane_f(gam, 15);
+    float* sv = scr + C * OTP;
+    const float4 gm = rows4(gam, sv, lane);
+    const float4 bg = rows4(bt * gam, sv + 16, lane);
+    const float4 gc = rows4(suffix_excl_prod(a), sv + 32, lane);
+    float4 kc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) kc[r] = *reinterpret_cast<const float4*>(sb + SB_K + n * RP + 16 * r + 4 * g);
+    float dO[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dO[j] = sb[SB_DO + (4 * g + j) * RP + 16 * w + n];
+    f32x4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0;
+#pragma unroll
+    for (int r = 0; r < 4; r += 2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            k0 = mfma4(el(kc[r], j), X[r][j], k0);
+            k1 = mfma4(el(kc[r + 1], j), X[r + 1][j], k1);
+        }
+    f32x4 dU;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dU[j] = el(gc, j) * (k0[j] + k1[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dU = mfma4(el(ci.mr, j), dO[j], dU);
+    f32x4 Y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Y = mfma4(el(ci.tr, j), dU[j], Y);
+    // hand X (the gradient after this block) and Y over to the helpers
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float4*>(ho + HO_DS + ((r * 4 + w) * 64 + lane) * 4) = tile_t(X[r], scr, lane);
+    const float4 y4 = tile_t(Y, scr, lane);  // Y[n][16w + 4g ..]
+    *reinterpret_cast<float4*>(ho + HO_Y + (w * 64 + lane) * 4) = y4;
+    if (live) store4<AL>(A.gv + (A.rowbase + c * C + n) * A.ldx + A.h * DH + 16 * w + 4 * g, f4scale(bt, y4));
+    // the wave's shares of dO U^T and Y U^T, and of the row sums of Y o V
+    const float4 do4 = *reinterpret_cast<const float4*>(sb + SB_DO + n * RP + 16 * w + 4 * g);
+    const float4 u4 = *reinterpret_cast<const float4*>(sb + SB_U + n * RP + 16 * w + 4 * g);
+    f32x4 pm = {0.f, 0.f, 0.f, 0.f}, pl = pm;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        pm = mfma4(el(do4, j), el(u4, j), pm);
+        pl = mfma4(el(y4, j), el(u4, j), pl);
+    }
+    *reinterpret_cast<float4*>(ho + HO_DM + (w * 64 + lane) * 4) = make_float4(pm[0], pm[1], pm[2], pm[3]);
+    *reinterpret_cast<float4*>(ho + HO_DL + (w * 64 + lane) * 4) = make_float4(pl[0], pl[1], pl[2], pl[3]);
+    const float4 vv = live ? ci.v : make_float4(0.f, 0.f, 0.f, 0.f);
+    float yv = y4.x * vv.x + y4.y * vv.y + y4.z * vv.z + y4.w * vv.w;
+    yv = add_xor32(add_xor16(yv));
+    if (lane < 16) ho[HO_YV + w * 16 + lane] = yv;
+    // X <- gamma_15 X + (diag(gamma) Q)^T dO - K^T diag(beta gamma) Y
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        X[r] *= g15;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float qv = sb[SB_Q + (4 * g + j) * RP + 16 * r + n];
+            const float kv = sb[SB_K + (4 * g + j) * RP + 16 * r + n];
+            X[r] = mfma4(el(gm, j) * qv, dO[j], X[r]);
+            X[r] = mfma4(-el(bg, j) * kv, Y[j], X[r]);
+        }
+    }
+}
+
+struct BHelpIn {
+    float4 sk[4];        // S of the block: S[16hw + n][16c + 4g ..], value tile c
+    float a, b;          // gates of step 16c + n
+    float qn[4], kn[4];  // norms of rows 16c + 4g + j
+    float4 ar, bq;       // helper 0: K K^T and Q K^T of the block (accumulator layout)
+};
+
+template <bool FUSED>
+ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + ((long)A.unit * A.nslots + c) * DH2);
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = sp[(hw * 4 + cc) * 64 + lane];
+    const long t = min(c * C + n, A.T - 1);
+    hi.a = A.alpha[A.gbase + t * A.H];
+    hi.b = A.beta[A.gbase + t * A.H];
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const long tj = min(c * C + 4 * g + j, A.T - 1);
+            hi.qn[j] = A.qn[A.gbase + tj * A.H];
+            hi.kn[j] = A.kn[A.gbase + tj * A.H];
+        }
+    }
+    if (hw == 0) {
+        const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+        hi.ar = rq[(R_A >> 2) + lane];
+        hi.bq = rq[(R_BQ >> 2) + lane];
+    }
+}
+
+// What a helper carries from the products of a block to its epilogue.
+struct BCarry {
+    f32x4 dq, dk;        // raw dq, dk of rows 4g + j, keys 16hw + n
+    float qb[4], kb[4];  // q, k at the same places
+    float qn[4], kn[4];
+    // helper 0: the gate epilogue's operands
+    f32x4 dM, dL;
+    float G[4];
+    float4 ar, bq;
+    float a, b, gam;
+};
+
+ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
+
+ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restrict__ sb, const float* __restrict__ ho,
+                             float* __restrict__ ep, float* __restrict__ scr, int c, const BArgs& A, int hw,
+                             int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    const bool live = c * C + n < A.T;
+    const float a = live ? hi.a : 1.0f;
+    const float bt = live ? hi.b : 0.0f;
+    const float gam = prefix_prod<16>(a);
+    float* sv = scr + C * OTP;
+    const float4 gm = rows4(gam, sv, lane);
+    const float4 bg = rows4(bt * gam, sv + 16, lane);
+    const float4 gc = rows4(suffix_excl_prod(a), sv + 32, lane);
+    const float4 bb = rows4(bt, sv + 48, lane);
+    float G[4];
+    gamma_acc(a, G, lane);
+    // dO S^T, Y S^T, U X^T for the helper's keys, over all value columns
+    f32x4 F = {0.f, 0.f, 0.f, 0.f}, Zt = F, D = F;
+    float dss = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        const float4 dO4 = *reinterpret_cast<const float4*>(sb + SB_DO + n * RP + 16 * cc + 4 * g);
+        const float4 u4 = *reinterpret_cast<const float4*>(sb + SB_U + n * RP + 16 * cc + 4 * g);
+        const float4 y4 = *reinterpret_cast<const float4*>(ho + HO_Y + (cc * 64 + lane) * 4);
+        const float4 x4 = *reinterpret_cast<const float4*>(ho + HO_DS + ((hw * 4 + cc) * 64 + lane) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            F = mfma4(el(dO4, j), el(hi.sk[cc], j), F);
+            Zt = mfma4(el(y4, j), el(hi.sk[cc], j), Zt);
+            D = mfma4(el(u4, j), el(x4, j), D);
+            dss += el(x4, j) * el(hi.sk[cc], j);
+        }
+    }
+    // dM = tril(dO U^T), dL = -strict_tril(Y U^T) from the chain waves' shares
+    float4 pm = *reinterpret_cast<const float4*>(ho + HO_DM + lane * 4);
+    float4 pl = *reinterpret_cast<const float4*>(ho + HO_DL + lane * 4);
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        pm = f4add(pm, *reinterpret_cast<const float4*>(ho + HO_DM + (w * 64 + lane) * 4));
+        pl = f4add(pl, *reinterpret_cast<const float4*>(ho + HO_DL + (w * 64 + lane) * 4));
+    }
+    f32x4 dM, dL, GdM, dA;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 4 * g + j;
+        dM[j] = n <= t ? el(pm, j) : 0.0f;
+        dL[j] = n < t ? -el(pl, j) : 0.0f;
+        GdM[j] = G[j] * dM[j];
+        dA[j] = dL[j] * el(bb, j) * G[j];
+    }
+    const float4 gdmt = tile_t(GdM, scr, lane);  // (Gamma o dM)[n][4g ..]
+    const float4 dat = tile_t(dA, scr, lane);    // dA[n][4g ..]
+    float kb[4], qb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        kb[j] = sb[SB_K + (4 * g + j) * RP + 16 * hw + n];
+        qb[j] = sb[SB_Q + (4 * g + j) * RP + 16 * hw + n];
+    }
+    f32x4 dq, dk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        dq[j] = el(gm, j) * F[j];
+        dk[j] = el(gc, j) * D[j] - el(bg, j) * Zt[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        dq = mfma4(el(gdmt, j), kb[j], dq);
+        dk = mfma4(GdM[j], qb[j], dk);
+        dk = mfma4(dA[j] + el(dat, j), kb[j], dk);
+    }
+    // row sums over the helper's keys (rows 4g + j)
+    float rs[5][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        rs[EP_RQ][j] = rowsum16(qb[j] * dq[j]);
+        rs[EP_RK][j] = rowsum16(kb[j] * dk[j]);
+        rs[EP_QF][j] = rowsum16(qb[j] * F[j]);
+        rs[EP_ZK][j] = rowsum16(kb[j] * Zt[j]);
+        rs[EP_KD][j] = rowsum16(kb[j] * D[j]);
+    }
+    if (n == 0) {
+#pragma unroll
+        for (int e = 0; e < 5; ++e)
+            *reinterpret_cast<float4*>(ep + EP_ROW + (hw * 5 + e) * 16 + 4 * g) =
+                make_float4(rs[e][0], rs[e][1], rs[e][2], rs[e][3]);
+    }
+    dss = wave_sum(dss);
+    if (lane == 0) ep[EP_DSS + hw] = dss;
+    if (hw == 0 && lane < 16) {
+        float yv = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) yv += ho[HO_YV + w * 16 + lane];
+        ep[EP_YV + lane] = yv;
+    }
+    cy.dq = dq;
+    cy.dk = dk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        cy.qb[j] = qb[j];
+        cy.kb[j] = kb[j];
+        cy.qn[j] = hi.qn[j];
+        cy.kn[j] = hi.kn[j];
+        cy.G[j] = G[j];
+    }
+    cy.dM = dM;
+    cy.dL = dL;
+    cy.ar = hi.ar;
+    cy.bq = hi.bq;
+    cy.a = a;
+    cy.b = bt;
+    cy.gam = gam;
+}
+
+template <bool FUSED, bool AL>
+ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, float* __restrict__ scr,
+                             float* __restrict__ gsc, int c, const BArgs& A, int hw, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    f32x4 dq = cy.dq, dk = cy.dk;
+    if constexpr (FUSED) {
+        float4 dotq = *reinterpret_cast<const float4*>(ep + EP_ROW + EP_RQ * 16 + 4 * g);
+        float4 dotk = *reinterpret_cast<const float4*>(ep + EP_ROW + EP_RK * 16 + 4 * g);
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            dotq = f4add(dotq, *reinterpret_cast<const float4*>(ep + EP_ROW + (w * 5 + EP_RQ) * 16 + 4 * g));
+            dotk = f4add(dotk, *reinterpret_cast<const float4*>(ep + EP_ROW + (w * 5 + EP_RK) * 16 + 4 * g));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            dq[j] = (dq[j] - cy.qb[j] * el(dotq, j)) * __builtin_amdgcn_rcpf(cy.qn[j]);
+            dk[j] = (dk[j] - cy.kb[j] * el(dotk, j)) * __builtin_amdgcn_rcpf(cy.kn[j]);
+        }
+    }
+    const float4 q4 = tile_t(dq, scr, lane);
+    const float4 k4 = tile_t(dk, scr, lane);
+    if (c * C + n < A.T) {
+        const long o = (A.rowbase + c * C + n) * A.ldx + A.h * DH + 16 * hw + 4 * g;
+        store4<AL>(A.gq + o, q4);
+        store4<AL>(A.gk + o, k4);
+    }
+    if (hw != 0) return;
+    // gate gradients of the block: lane t of each row holds step t
+    float szk = 0.f, sqf = 0.f, skd = 0.f, dss = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        szk += ep[EP_ROW + (w * 5 + EP_ZK) * 16 + n];
+        sqf += ep[EP_ROW + (w * 5 + EP_QF) * 16 + n];
+        skd += ep[EP_ROW + (w * 5 + EP_KD) * 16 + n];
+        dss += ep[EP_DSS + w];
+    }
+    const float yv = ep[EP_YV + n];
+    const float dgam = -cy.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
+    float* sv = scr + C * OTP;
+    const float4 dg4 = rows4(dgam, sv, lane);
+    const float4 bb = rows4(cy.b, sv + 16, lane);
+    // dGamma (strict lower part), row sums of dL o Gamma o A, and the first term of dalpha
+    float dgs[4], t1 = 0.0f, rb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = 4 * g + j;
+        const float lga = cy.dL[j] * cy.G[j] * el(cy.ar, j);
+        rb[j] = rowsum16(lga);
+        dgs[j] = n < t ? cy.dM[j] * el(cy.bq, j) + cy.dL[j] * el(bb, j) * el(cy.ar, j) + (t == C - 1 ? skd : 0.0f)
+                       : 0.0f;
+        t1 += cy.G[j] * el(dg4, j);
+    }
+    t1 = add_xor32(add_xor16(t1));
+    // second term: R[t][m] = sum_{i<m} dGs[t][i] Gamma[m-1][i], then sum_t Gamma[t][m] R[t][m]
+    float* gs = gsc;
+    float* gg = gsc + 256;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        gs[(4 * g + j) * 16 + n] = dgs[j];
+        gg[(4 * g + j) * 16 + n] = cy.G[j];
+    }
+    wave_sync();
+    float t2 = 0.0f;
+    if (n > 0) {
+        float gr[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 x = *reinterpret_cast<const float4*>(gg + (n - 1) * 16 + 4 * q4);
+            gr[4 * q4] = x.x; gr[4 * q4 + 1] = x.y; gr[4 * q4 + 2] = x.z; gr[4 * q4 + 3] = x.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float R = 0.0f;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 x = *reinterpret_cast<const float4*>(gs + (4 * g + j) * 16 + 4 * q4);
+                R += (4 * q4 + 0 < n ? x.x * gr[4 * q4 + 0] : 0.0f) + (4 * q4 + 1 < n ? x.y * gr[4 * q4 + 1] : 0.0f) +
+                     (4 * q4 + 2 < n ? x.z * gr[4 * q4 + 2] : 0.0f) + (4 * q4 + 3 < n ? x.w * gr[4 * q4 + 3] : 0.0f);
+            }
+            t2 += cy.G[j] * R;
+        }
+    }
+    t2 = add_xor32(add_xor16(t2));
+    wave_sync();
+    const float gprev = dpp_or<0x111>(1.0f, cy.gam);   // gamma_{n-1}
+    const float dal = gprev * t1 + t2;
+    // dbeta of step n: Y.V - gamma Z'.K + sum_l dL Gamma A
+    if (n == 0) *reinterpret_cast<float4*>(sv + 48 + 4 * g) = make_float4(rb[0], rb[1], rb[2], rb[3]);
+    wave_sync();
+    float rbn = 0.0f;
+    if (lane < 16) rbn = sv[48 + lane];
+    wave_sync();
+    const float dbe = yv - cy.gam * szk + rbn;
+    if (lane < 16 && c * C + n < A.T) {
+        const long r = (A.rowbase + c * C + n) * A.ldg + A.h;
+        A.ga[r] = FUSED ? dal * cy.a * (1.0f - cy.a) : dal;
+        A.gb[r] = FUSED ? dbe * cy.b * (1.0f - cy.b) : dbe;
+    }
+}
+
+// A helper's staging of block c: rows 4hw .. 4hw + 3 of k, q, dO and u, one
+// 16-byte load per matrix and lane (row 4hw + lane/16, columns 4 (lane%16) ..);
+// rows past the sequence end are zero.
+struct BStage {
+    float4 x[4];
+};
+
+template <bool AL>
+ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
+    const long t = min(c * C + 4 * hw + (lane >> 4), A.T - 1);
+    const long off = A.ubase + t * A.d + 4 * (lane & 15);
+    st.x[0] = ld4<AL>(A.k + off);
+    st.x[1] = ld4<AL>(A.q + off);
+    st.x[2] = ld4<AL>(A.d_o + off);
+    st.x[3] = *reinterpret_cast<const float4*>(A.u + off);
+}
+
+ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int T, int hw, int lane) {
+    const int row = 4 * hw + (lane >> 4);
+    const bool live = c * C + row < T;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<float4*>(sb + m * SB_MAT + row * RP + 4 * (lane & 15)) =
+            live ? st.x[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <bool FUSED, bool AL>
+__global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
+    extern __shared__ float lds[];
+    {
+        A.unit = blockIdx.x;  // h*B + b
+        A.h = A.unit / A.B;
+        const int b = A.unit - A.h * A.B;
+        A.ubase = (long)b * A.T * A.d + (long)A.h * DH;
+        A.gbase = (long)b * A.T * A.H + A.h;
+        A.rowbase = (long)b * A.T;
+    }
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int NC = A.NC;
+    float* scr = lds + B_SCR + w * WSCR;
+    if (w >= NW) {
+        const int hw = w - NW;
+        BStage stg;
+        BHelpIn hin;
+        BCarry cy;
+        bstage_load<AL>(stg, NC - 1, A, hw, lane);
+        bstage_store(stg, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
+        bstage_load<AL>(stg, max(NC - 2, 0), A, hw, lane);
+        bhelp_load<FUSED>(hin, NC - 1, A, hw, lane);
+        lds_barrier();
+        for (int s = 0; s < NC + 2; ++s) {
+            const int ce = NC + 1 - s, cp = NC - s, cw = NC - 2 - s;
+            if (ce >= 0 && ce < NC)
+                bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, lds + B_G, ce, A, hw, lane);
+            if (cp >= 0 && cp < NC) {
+                bhelp_products(cy, hin, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
+                               lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
+                bhelp_load<FUSED>(hin, max(cp - 1, 0), A, hw, lane);
+            }
+            if (cw >= 0) {
+                bstage_store(stg, cw, lds + B_STG + (cw % NSB) * SB_BUF, A.T, hw, lane);
+                bstage_load<AL>(stg, max(cw - 1, 0), A, hw, lane);
+            }
+            lds_barrier();
+        }
+        return;
+    }
+    f32x4 X[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) X[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    BChainIn cb[2];
+    bchain_load<AL>(cb[0], NC - 1, A, w, lane);
+    lds_barrier();
+    for (int s = 0; s < NC + 2; ++s) {
+        const int c = NC - 1 - s;
+        if (c >= 0) {
+            // buffers alternate by block parity (static indices: no register copies)
+            if ((s & 1) == 0) {
+                bchain_load<AL>(cb[1], max(c - 1, 0), A, w, lane);
+                bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
+                                lane);
+            } else {
+                bchain_load<AL>(cb[0], max(c - 1, 0), A, w, lane);
+                bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
+                                lane);
+            }
+        }
+        lds_barrier();
+    }
 }
 
 }  // namespace ut64
@@ -379,7 +955,7 @@ static int launch_ut_fwd64_t(const float* q, const float* k, const float* v, con
     int rc = pre_launch("ut_fwd64");
     if (rc) return rc;
     hipLaunchKernelGGL(ut64::ut_fwd64_k<AL>, dim3(units), dim3(2 * ut64::NT), lds, st, q, k, v, alpha, beta, o, ws.sk,
-                       ws.ckpt, B, T, H, ws.nslots);
+                       ws.ckpt, ws.rec, B, T, H, ws.nslots);
     return post_launch("ut_fwd64");
 }
 
@@ -389,6 +965,40 @@ int launch_ut_fwd64(const float* q, const float* k, const float* v, const float*
     return ut_aligned16(q) && ut_aligned16(k) && ut_aligned16(v) && ut_aligned16(o)
                ? launch_ut_fwd64_t<true>(q, k, v, alpha, beta, o, ws, B, T, H, st)
                : launch_ut_fwd64_t<false>(q, k, v, alpha, beta, o, ws, B, T, H, st);
+}
+
+template <bool FUSED, bool AL>
+static int launch_ut_bwd64_t(const ut64::BArgs& a, int units, hipStream_t st) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ut64::ut_bwd64_k<FUSED, AL>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)ut64::B_LDS);
+        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr = true;
+    }
+    int rc = pre_launch("ut_bwd64");
+    if (rc) return rc;
+    hipLaunchKernelGGL((ut64::ut_bwd64_k<FUSED, AL>), dim3(units), dim3(2 * ut64::NT), ut64::B_LDS, st, a);
+    return post_launch("ut_bwd64");
+}
+
+int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
+                    const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
+                    float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
+                    hipStream_t st) {
+    if (ws.cs != 1 || !ws.rec) return fail(ASCA_ERR_INVALID, "ut_bwd64: workspace layout mismatch");
+    ut64::BArgs a;
+    a.q = q; a.k = k; a.v = v; a.alpha = alpha; a.beta = beta; a.d_o = d_o; a.u = ws.sk; a.ckpt = ws.ckpt;
+    a.rec = ws.rec; a.qn = qn; a.kn = kn; a.gq = gq; a.gk = gk; a.gv = gv; a.ga = ga; a.gb = gb;
+    a.ldx = ldx; a.ldg = ldg; a.d = (long)H * ut64::DH; a.T = T; a.H = H; a.nslots = ws.nslots;
+    a.NC = (T + ut64::C - 1) / ut64::C;
+    // per-unit fields are filled in the kernel from blockIdx
+    const bool al = ut_aligned16(q) && ut_aligned16(k) && ut_aligned16(v) && ut_aligned16(d_o) && ut_aligned16(gq) &&
+                    ut_aligned16(gk) && ut_aligned16(gv) && (ldx * 4) % 16 == 0;
+    const int units = B * H;
+    a.B = B; a.unit = 0; a.h = 0; a.ubase = 0; a.gbase = 0; a.rowbase = 0;
+    if (fused) return al ? launch_ut_bwd64_t<true, true>(a, units, st) : launch_ut_bwd64_t<true, false>(a, units, st);
+    return al ? launch_ut_bwd64_t<false, true>(a, units, st) : launch_ut_bwd64_t<false, false>(a, units, st);
 }
 
 }  // namespace asca
