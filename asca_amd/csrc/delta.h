@@ -1,16 +1,18 @@
-// Internals shared by the recurrent delta-rule translation units (delta.hip:
-// every dh up to 128 on eight-lane column groups; delta64.hip: dh = 64 on four
-// waves per unit).  Both write and read the same workspace layout.
+// Internals shared by the delta-rule translation units (delta.hip: the
+// recurrent kernels for every dh other than 64, on eight-lane column groups, and
+// the entry points; delta_ut64.hip: dh = 64 in the blocked form).
 #pragma once
 #include "common.h"
 
 namespace asca {
 
 // Workspace of one forward / backward pair (asca_delta_ws_bytes):
-//  * sk: the per-step S_{t-1}^T k_t vectors, layout of v;
+//  * sk: the recurrent kernels' per-step S_{t-1}^T k_t vectors (the blocked
+//    form's u rows), layout of v;
 //  * ckpt: per unit (h*B + b), nslots = ceil(T/ck) + 1 states of dh^2 floats
-//    stored as S^T (element (a, i) at i*dh + a): slot j is the state before step
-//    j*ck for j < ceil(T/ck), the last slot the state after step T-1;
+//    (the recurrent kernels store S^T, element (a, i) at i*dh + a; the blocked
+//    form its own tile order): slot j is the state before step j*ck for
+//    j < ceil(T/ck), the last slot the state after step T-1;
 //  * part_x / part_g: partial dq, dk and dalpha, dbeta of a column-split backward.
 struct DeltaWs {
     float* sk;
@@ -64,21 +66,18 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
     }
 }
 
-// dh = 64 kernels on four waves per (sequence, head) unit (delta64.hip), used
-// for every dh = 64 shape with one block per unit (ws.cs == 1); their workspace
-// has a checkpoint every D64_CK steps.  Any pointer alignment.
+// dh = 64: the blocked (UT) form on the matrix cores (delta_ut64.hip), used for
+// every dh = 64 shape with one block per unit (ws.cs == 1).  Its workspace: the
+// u rows in `sk`, the state before every D64_CK-step block (and the final state)
+// in `ckpt`, and per block a record of D64_REC floats in `rec`.  Any pointer
+// alignment.
 constexpr int D64_CK = 16;
-int launch_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
-                 const DeltaWs& ws, int B, int T, int H, hipStream_t st);
+constexpr int D64_REC = 1280;
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st);
 int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
                     const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
                     float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
                     hipStream_t st);
-int launch_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,
-                 const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
-                 float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
-                 hipStream_t st);
 
 }  // namespace asca

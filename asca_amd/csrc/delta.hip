@@ -1100,7 +1100,7 @@ static int col_split(int B, int H, int dh, int dhc) {
     return (long)B * H <= SPLIT_UNITS || dhc == 128 ? 2 : 1;
 }
 
-static bool four_wave(int dh, int cs) { return dh == 64 && cs == 1; }
+static bool blocked64(int dh, int cs) { return dh == 64 && cs == 1; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1108,14 +1108,14 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     DeltaWs w;
     const int dhc = dh_class(dh);
     w.cs = col_split(B, H, dh, dhc);
-    w.ck = four_wave(dh, w.cs) ? D64_CK : ck_for(dhc);
+    w.ck = blocked64(dh, w.cs) ? D64_CK : ck_for(dhc);
     w.nslots = (T + w.ck - 1) / w.ck + 1;   // the state before every chunk, then the final state
     const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
     const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
     const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
     const size_t rec_bytes =
-        four_wave(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * 1024 * sizeof(float)) : 0;
+        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * D64_REC * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
     w.sk = reinterpret_cast<float*>(base);
     w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
@@ -1153,7 +1153,7 @@ static int launch_fwd(const float* q, const float* k, const float* v, const floa
                       float* o, const DeltaWs& ws, int B, int T, int H, int dh, hipStream_t st) {
     const int dhc = dh_class(dh);
     const bool exact = dh == dhc && aligned16(q) && aligned16(k);
-    if (four_wave(dh, ws.cs)) return launch_fwd64(q, k, v, alpha, beta, o, ws, B, T, H, st);
+    if (blocked64(dh, ws.cs)) return launch_ut_fwd64(q, k, v, alpha, beta, o, ws, B, T, H, st);
 #define ASCA_FWD(DHC)                                                                                    \
     if (dhc == DHC)                                                                                      \
         return exact ? launch_fwd_t<DHC, true>(q, k, v, alpha, beta, o, ws, B, T, H, dh, st)             \
@@ -1224,8 +1224,8 @@ static int launch_bwd(const float* q, const float* k, const float* v, const floa
     const int dhc = dh_class(dh);
     const bool exact = dh == dhc && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(d_o) &&
                        aligned16(gv) && ((ldx * 4) % 16 == 0);
-    if (four_wave(dh, ws.cs))
-        return launch_bwd64(FUSED, q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, st);
+    if (blocked64(dh, ws.cs))
+        return launch_ut_bwd64(FUSED, q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, B, T, H, st);
 #define ASCA_BWD(DHC)                                                                                            \
     if (dhc == DHC)                                                                                              \
         return exact ? launch_bwd_t<DHC, true, FUSED>(q, k, v, alpha, beta, d_o, ws, qn, kn, gq, gk, gv, ldx, ga, \
@@ -1290,24 +1290,6 @@ int asca_delta_bwd_fused(const float* q, const float* k, const float* v, const f
     const long d = (long)H * dh;
     return launch_bwd<true>(q, k, v, alpha, beta, d_o, w, qnorm, knorm, d_qkv, d_qkv + d, d_qkv + 2 * d, 3 * d,
                             d_gate, d_gate + H, 2L * H, B, T, H, dh, as_stream(stream));
-}
-
-ASCA_API int asca_dev_ut_fwd(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
-                             float* o, void* ws, int B, int T, int H) {
-    DeltaWs w = ws_layout(B, T, H, 64, ws);
-    return launch_ut_fwd64(q, k, v, alpha, beta, o, w, B, T, H, nullptr);
-}
-
-ASCA_API int asca_dev_ut_bwd(int fused, const float* q, const float* k, const float* v, const float* alpha,
-                             const float* beta, const float* qn, const float* kn, const float* d_o, void* ws,
-                             float* o1, float* o2, float* o3, float* o4, float* o5, int B, int T, int H) {
-    DeltaWs w = ws_layout(B, T, H, 64, ws);
-    const long d = (long)H * 64;
-    if (fused)
-        return launch_ut_bwd64(true, q, k, v, alpha, beta, d_o, w, qn, kn, o1, o1 + d, o1 + 2 * d, 3 * d, o2, o2 + H,
-                               2L * H, B, T, H, nullptr);
-    return launch_ut_bwd64(false, q, k, v, alpha, beta, d_o, w, nullptr, nullptr, o1, o2, o3, d, o4, o5, H, B, T, H,
-                           nullptr);
 }
 
 int asca_delta_states(const float* q, const float* k, const float* v, const float* alpha, const float* beta,

@@ -72,10 +72,11 @@ struct PrepIn {
 // Forms block p's matrices from its loads into the slot `ps`.  Steps past the
 // sequence end get alpha = 1, beta = 0: they leave the state, T and the
 // products of the live steps unchanged.  `scr` is the wave's own scratch.
-// Record of a block for the backward (1024 floats): K K^T, Q K^T, T and M in
-// the accumulator layout, 16 bytes per lane (float4 index 64 m + lane holds
+// Record of a block for the backward (1280 floats): K K^T, Q K^T, T, M and
+// Gamma (zero above the diagonal) in the accumulator layout, 16 bytes per lane (float4 index 64 m + lane holds
 // matrix m's elements [4 (lane/16) + j][lane % 16], j = 0..3).
-constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_SZ = 1024;
+constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_G = 1024, R_SZ = 1280;
+static_assert(R_SZ == D64_REC, "record size");
 
 ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ ps, float* __restrict__ scr,
                            float* __restrict__ rec, int lane) {
@@ -140,6 +141,8 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
     rq[(R_T >> 2) + lane] = make_float4(tp[0], tp[16], tp[32], tp[48]);
     const float* mp = ps + P_M + 64 * g + n;
     rq[(R_M >> 2) + lane] = make_float4(mp[0], mp[16], mp[32], mp[48]);
+    rq[(R_G >> 2) + lane] = make_float4(n <= 4 * g ? G[0] : 0.f, n <= 4 * g + 1 ? G[1] : 0.f,
+                                        n <= 4 * g + 2 ? G[2] : 0.f, n <= 4 * g + 3 ? G[3] : 0.f);
 }
 
 // Staging of a group's k, q, v rows in LDS: buffer of 4 blocks x 16 rows, row
@@ -419,23 +422,23 @@ constexpr int EP_ROW = 0;                    // [hw][5][16]: q.dq, k.dk, q.F, k.
 constexpr int EP_RQ = 0, EP_RK = 1, EP_QF = 2, EP_ZK = 3, EP_KD = 4;
 constexpr int EP_DSS = 320;                  // [hw]: <X, S> over the helper's keys
 constexpr int EP_YV = 324;                   // [16]: row sums of Y o V
-constexpr int EP_SZ = 344;
-constexpr int WSCR = 2 * C * OTP;            // per wave: a transpose tile and a vector area
+constexpr int EP_DM = 344;                   // dM = tril(dO U^T), accumulator layout [lane][4]
+constexpr int EP_DL = 600;                   // dL = -strict_tril(Y U^T)
+constexpr int EP_SZ = 856;
+constexpr int WSCR = 2 * C * OTP + 128;      // per wave: two transpose tiles and a vector area
+constexpr int SVO = 2 * C * OTP;             // the vector area's offset
 constexpr int B_STG = 0;
 constexpr int B_HO = B_STG + NSB * SB_BUF;
 constexpr int B_EP = B_HO + 2 * HO_SZ;
 constexpr int B_SCR = B_EP + 2 * EP_SZ;
-constexpr int B_G = B_SCR + 2 * NW * WSCR;   // helper 0: dGamma and Gamma rows [2][16][16]
-constexpr int B_END = B_G + 512;
+constexpr int B_END = B_SCR + 2 * NW * WSCR;
 constexpr size_t B_LDS = (size_t)B_END * 4;
 static_assert(B_LDS <= 160 * 1024 && B_HO % 4 == 0 && B_EP % 4 == 0 && B_SCR % 4 == 0, "backward LDS");
 
-// Orders the wave's own LDS writes before its reads of other lanes' values.
-ASCA_DEV void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+// Orders the wave's own LDS writes before its reads of other lanes' values.  The
+// LDS executes one wave's instructions in issue order, so only the compiler has
+// to keep them in program order: a compiler barrier, no wait.
+ASCA_DEV void wave_sync() { asm volatile("" ::: "memory"); }
 
 // 16x16 tile in the accumulator layout (lane (g, n) holds X[4g + j][n]) ->
 // lane (g, n) receives X[n][4g .. 4g + 3].
@@ -457,6 +460,33 @@ ASCA_DEV float4 rows4(float x, float* __restrict__ sv, int lane) {
     const float4 r = *reinterpret_cast<const float4*>(sv + 4 * (lane >> 4));
     wave_sync();
     return r;
+}
+
+// rows4 for several values at once (one LDS round trip).
+template <int NQ>
+ASCA_DEV void rows4x(const float (&x)[NQ], float4 (&out)[NQ], float* __restrict__ sv, int lane) {
+    if (lane < 16) {
+#pragma unroll
+        for (int e = 0; e < NQ; ++e) sv[16 * e + lane] = x[e];
+    }
+    wave_sync();
+#pragma unroll
+    for (int e = 0; e < NQ; ++e) out[e] = *reinterpret_cast<const float4*>(sv + 16 * e + 4 * (lane >> 4));
+    wave_sync();
+}
+
+// Two 16x16 accumulator tiles transposed at once (see tile_t).
+ASCA_DEV void tile_t2(const f32x4& x, const f32x4& y, float4& xt, float4& yt, float* __restrict__ st, int lane) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        st[(4 * g + j) * OTP + n] = x[j];
+        st[C * OTP + (4 * g + j) * OTP + n] = y[j];
+    }
+    wave_sync();
+    xt = *reinterpret_cast<const float4*>(st + n * OTP + 4 * g);
+    yt = *reinterpret_cast<const float4*>(st + C * OTP + n * OTP + 4 * g);
+    wave_sync();
 }
 
 // Exclusive suffix product over each 16-lane row: lane m gets prod_{m<s<16} x_s.
@@ -526,10 +556,12 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
     const float bt = live ? ci.b : 0.0f;
     const float gam = prefix_prod<16>(a);
     const float g15 = readlane_f(gam, 15);
-    float* sv = scr + C * OTP;
-    const float4 gm = rows4(gam, sv, lane);
-    const float4 bg = rows4(bt * gam, sv + 16, lane);
-    const float4 gc = rows4(suffix_excl_prod(a), sv + 32, lane);
+    float4 vec[3];
+    {
+        const float x[3] = {gam, bt * gam, suffix_excl_prod(a)};
+        rows4x<3>(x, vec, scr + SVO, lane);
+    }
+    const float4 gm = vec[0], bg = vec[1], gc = vec[2];
     float4 kc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) kc[r] = *reinterpret_cast<const float4*>(sb + SB_K + n * RP + 16 * r + 4 * g);
@@ -592,7 +624,7 @@ struct BHelpIn {
     float4 sk[4];        // S of the block: S[16hw + n][16c + 4g ..], value tile c
     float a, b;          // gates of step 16c + n
     float qn[4], kn[4];  // norms of rows 16c + 4g + j
-    float4 ar, bq;       // helper 0: K K^T and Q K^T of the block (accumulator layout)
+    float4 gr;           // Gamma of the block (accumulator layout)
 };
 
 template <bool FUSED>
@@ -612,11 +644,8 @@ ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
             hi.kn[j] = A.kn[A.gbase + tj * A.H];
         }
     }
-    if (hw == 0) {
-        const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
-        hi.ar = rq[(R_A >> 2) + lane];
-        hi.bq = rq[(R_BQ >> 2) + lane];
-    }
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    hi.gr = rq[(R_G >> 2) + lane];
 }
 
 // What a helper carries from the products of a block to its epilogue.
@@ -624,11 +653,6 @@ struct BCarry {
     f32x4 dq, dk;        // raw dq, dk of rows 4g + j, keys 16hw + n
     float qb[4], kb[4];  // q, k at the same places
     float qn[4], kn[4];
-    // helper 0: the gate epilogue's operands
-    f32x4 dM, dL;
-    float G[4];
-    float4 ar, bq;
-    float a, b, gam;
 };
 
 ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
@@ -641,13 +665,13 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     const float a = live ? hi.a : 1.0f;
     const float bt = live ? hi.b : 0.0f;
     const float gam = prefix_prod<16>(a);
-    float* sv = scr + C * OTP;
-    const float4 gm = rows4(gam, sv, lane);
-    const float4 bg = rows4(bt * gam, sv + 16, lane);
-    const float4 gc = rows4(suffix_excl_prod(a), sv + 32, lane);
-    const float4 bb = rows4(bt, sv + 48, lane);
-    float G[4];
-    gamma_acc(a, G, lane);
+    float4 vec[4];
+    {
+        const float x[4] = {gam, bt * gam, suffix_excl_prod(a), bt};
+        rows4x<4>(x, vec, scr + SVO, lane);
+    }
+    const float4 gm = vec[0], bg = vec[1], gc = vec[2], bb = vec[3];
+    const float G[4] = {hi.gr.x, hi.gr.y, hi.gr.z, hi.gr.w};
     // dO S^T, Y S^T, U X^T for the helper's keys, over all value columns
     f32x4 F = {0.f, 0.f, 0.f, 0.f}, Zt = F, D = F;
     float dss = 0.0f;
@@ -682,8 +706,8 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         GdM[j] = G[j] * dM[j];
         dA[j] = dL[j] * el(bb, j) * G[j];
     }
-    const float4 gdmt = tile_t(GdM, scr, lane);  // (Gamma o dM)[n][4g ..]
-    const float4 dat = tile_t(dA, scr, lane);    // dA[n][4g ..]
+    float4 gdmt, dat;  // (Gamma o dM)[n][4g ..], dA[n][4g ..]
+    tile_t2(GdM, dA, gdmt, dat, scr, lane);
     float kb[4], qb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -720,11 +744,15 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
     dss = wave_sum(dss);
     if (lane == 0) ep[EP_DSS + hw] = dss;
-    if (hw == 0 && lane < 16) {
-        float yv = 0.0f;
+    if (hw == 0) {
+        if (lane < 16) {
+            float yv = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) yv += ho[HO_YV + w * 16 + lane];
-        ep[EP_YV + lane] = yv;
+            for (int w = 0; w < NW; ++w) yv += ho[HO_YV + w * 16 + lane];
+            ep[EP_YV + lane] = yv;
+        }
+        *reinterpret_cast<float4*>(ep + EP_DM + 4 * lane) = make_float4(dM[0], dM[1], dM[2], dM[3]);
+        *reinterpret_cast<float4*>(ep + EP_DL + 4 * lane) = make_float4(dL[0], dL[1], dL[2], dL[3]);
     }
     cy.dq = dq;
     cy.dk = dk;
@@ -734,20 +762,12 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         cy.kb[j] = kb[j];
         cy.qn[j] = hi.qn[j];
         cy.kn[j] = hi.kn[j];
-        cy.G[j] = G[j];
     }
-    cy.dM = dM;
-    cy.dL = dL;
-    cy.ar = hi.ar;
-    cy.bq = hi.bq;
-    cy.a = a;
-    cy.b = bt;
-    cy.gam = gam;
 }
 
 template <bool FUSED, bool AL>
-ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, float* __restrict__ scr,
-                             float* __restrict__ gsc, int c, const BArgs& A, int hw, int lane) {
+ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, float* __restrict__ scr, int c,
+                             const BArgs& A, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
     f32x4 dq = cy.dq, dk = cy.dk;
     if constexpr (FUSED) {
@@ -764,15 +784,44 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
             dk[j] = (dk[j] - cy.kb[j] * el(dotk, j)) * __builtin_amdgcn_rcpf(cy.kn[j]);
         }
     }
-    const float4 q4 = tile_t(dq, scr, lane);
-    const float4 k4 = tile_t(dk, scr, lane);
+    float4 q4, k4;
+    tile_t2(dq, dk, q4, k4, scr, lane);
     if (c * C + n < A.T) {
         const long o = (A.rowbase + c * C + n) * A.ldx + A.h * DH + 16 * hw + 4 * g;
         store4<AL>(A.gq + o, q4);
         store4<AL>(A.gk + o, k4);
     }
-    if (hw != 0) return;
-    // gate gradients of the block: lane t of each row holds step t
+}
+
+// Gate gradients of block c (dalpha, dbeta and their sigmoid backward), run by
+// one chain wave from the helpers' sums in `ep`; lane t of each row is step t.
+struct BGateIn {
+    float4 ar, bq, gr;  // K K^T, Q K^T, Gamma of the block (accumulator layout)
+    float a, b;         // gates of step 16c + n
+};
+
+ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    gi.ar = rq[(R_A >> 2) + lane];
+    gi.bq = rq[(R_BQ >> 2) + lane];
+    gi.gr = rq[(R_G >> 2) + lane];
+    const long t = min(c * C + (lane & 15), A.T - 1);
+    gi.a = A.alpha[A.gbase + t * A.H];
+    gi.b = A.beta[A.gbase + t * A.H];
+}
+
+template <bool FUSED>
+ASCA_DEV void bgate(const BGateIn& gin, const float* __restrict__ ep, float* __restrict__ scr, int c, const BArgs& A,
+                    int lane) {
+    const int n = lane & 15, g = lane >> 4;
+    BGateIn gi = gin;
+    if (c * C + n >= A.T) { gi.a = 1.0f; gi.b = 0.0f; }
+    const float gam = prefix_prod<16>(gi.a);
+    const float4 pm = *reinterpret_cast<const float4*>(ep + EP_DM + 4 * lane);
+    const float4 pl = *reinterpret_cast<const float4*>(ep + EP_DL + 4 * lane);
+    const float dM[4] = {pm.x, pm.y, pm.z, pm.w};
+    const float dL[4] = {pl.x, pl.y, pl.z, pl.w};
+    const float G[4] = {gi.gr.x, gi.gr.y, gi.gr.z, gi.gr.w};
     float szk = 0.f, sqf = 0.f, skd = 0.f, dss = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
@@ -782,66 +831,52 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
         dss += ep[EP_DSS + w];
     }
     const float yv = ep[EP_YV + n];
-    const float dgam = -cy.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
-    float* sv = scr + C * OTP;
-    const float4 dg4 = rows4(dgam, sv, lane);
-    const float4 bb = rows4(cy.b, sv + 16, lane);
+    const float dgam = -gi.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
+    float4 vec[2];
+    {
+        const float x[2] = {dgam, gi.b};
+        rows4x<2>(x, vec, scr + SVO, lane);
+    }
+    const float4 dg4 = vec[0], bb = vec[1];
     // dGamma (strict lower part), row sums of dL o Gamma o A, and the first term of dalpha
-    float dgs[4], t1 = 0.0f, rb[4];
+    f32x4 dgs, Gv;
+    float t1 = 0.0f, rb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int t = 4 * g + j;
-        const float lga = cy.dL[j] * cy.G[j] * el(cy.ar, j);
-        rb[j] = rowsum16(lga);
-        dgs[j] = n < t ? cy.dM[j] * el(cy.bq, j) + cy.dL[j] * el(bb, j) * el(cy.ar, j) + (t == C - 1 ? skd : 0.0f)
+        rb[j] = rowsum16(dL[j] * G[j] * el(gi.ar, j));
+        dgs[j] = n < t ? dM[j] * el(gi.bq, j) + dL[j] * el(bb, j) * el(gi.ar, j) + (t == C - 1 ? skd : 0.0f)
                        : 0.0f;
-        t1 += cy.G[j] * el(dg4, j);
+        Gv[j] = G[j];
+        t1 += G[j] * el(dg4, j);
     }
     t1 = add_xor32(add_xor16(t1));
-    // second term: R[t][m] = sum_{i<m} dGs[t][i] Gamma[m-1][i], then sum_t Gamma[t][m] R[t][m]
-    float* gs = gsc;
-    float* gg = gsc + 256;
+    // second term: R = dGs Gamma'^T with Gamma'[m][i] = Gamma[m-1][i] (the row above,
+    // zero for m = 0) on the matrix cores, then sum_t Gamma[t][m] R[t][m]
+    float4 dgst, gt;
+    tile_t2(dgs, Gv, dgst, gt, scr, lane);   // dGs[n][4g ..], Gamma[n][4g ..]
+    const float gp[4] = {dpp_or<0x111>(0.0f, gt.x), dpp_or<0x111>(0.0f, gt.y), dpp_or<0x111>(0.0f, gt.z),
+                         dpp_or<0x111>(0.0f, gt.w)};   // Gamma[n-1][4g ..]
+    f32x4 R = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        gs[(4 * g + j) * 16 + n] = dgs[j];
-        gg[(4 * g + j) * 16 + n] = cy.G[j];
-    }
-    wave_sync();
+    for (int j = 0; j < 4; ++j) R = mfma4(el(dgst, j), gp[j], R);
     float t2 = 0.0f;
-    if (n > 0) {
-        float gr[16];
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const float4 x = *reinterpret_cast<const float4*>(gg + (n - 1) * 16 + 4 * q4);
-            gr[4 * q4] = x.x; gr[4 * q4 + 1] = x.y; gr[4 * q4 + 2] = x.z; gr[4 * q4 + 3] = x.w;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float R = 0.0f;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 x = *reinterpret_cast<const float4*>(gs + (4 * g + j) * 16 + 4 * q4);
-                R += (4 * q4 + 0 < n ? x.x * gr[4 * q4 + 0] : 0.0f) + (4 * q4 + 1 < n ? x.y * gr[4 * q4 + 1] : 0.0f) +
-                     (4 * q4 + 2 < n ? x.z * gr[4 * q4 + 2] : 0.0f) + (4 * q4 + 3 < n ? x.w * gr[4 * q4 + 3] : 0.0f);
-            }
-            t2 += cy.G[j] * R;
-        }
-    }
+    for (int j = 0; j < 4; ++j) t2 += G[j] * R[j];
     t2 = add_xor32(add_xor16(t2));
-    wave_sync();
-    const float gprev = dpp_or<0x111>(1.0f, cy.gam);   // gamma_{n-1}
+    const float gprev = dpp_or<0x111>(1.0f, gam);   // gamma_{n-1}
     const float dal = gprev * t1 + t2;
     // dbeta of step n: Y.V - gamma Z'.K + sum_l dL Gamma A
-    if (n == 0) *reinterpret_cast<float4*>(sv + 48 + 4 * g) = make_float4(rb[0], rb[1], rb[2], rb[3]);
+    float* sv = scr + SVO;
+    if (n == 0) *reinterpret_cast<float4*>(sv + 4 * g) = make_float4(rb[0], rb[1], rb[2], rb[3]);
     wave_sync();
-    float rbn = 0.0f;
-    if (lane < 16) rbn = sv[48 + lane];
+    const float rbn = sv[n];
     wave_sync();
-    const float dbe = yv - cy.gam * szk + rbn;
+    const float dbe = yv - gam * szk + rbn;
     if (lane < 16 && c * C + n < A.T) {
         const long r = (A.rowbase + c * C + n) * A.ldg + A.h;
-        A.ga[r] = FUSED ? dal * cy.a * (1.0f - cy.a) : dal;
-        A.gb[r] = FUSED ? dbe * cy.b * (1.0f - cy.b) : dbe;
+        A.ga[r] = FUSED ? dal * gi.a * (1.0f - gi.a) : dal;
+        A.gb[r] = FUSED ? dbe * gi.b * (1.0f - gi.b) : dbe;
     }
 }
 
@@ -886,51 +921,70 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     const int NC = A.NC;
     float* scr = lds + B_SCR + w * WSCR;
     if (w >= NW) {
+        // helper: step s stages block NC - 2 - s, runs the epilogue of block
+        // NC + 1 - s and the products of block NC - s.  Every global load is made
+        // two steps ahead into buffer s & 1, unconditionally (clamped block
+        // indices), and consumed at the start of its step, so no wait falls on a
+        // recent memory operation.
         const int hw = w - NW;
-        BStage stg;
-        BHelpIn hin;
+        BStage stg[2];
+        BHelpIn hin[2];
         BCarry cy;
-        bstage_load<AL>(stg, NC - 1, A, hw, lane);
-        bstage_store(stg, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
-        bstage_load<AL>(stg, max(NC - 2, 0), A, hw, lane);
-        bhelp_load<FUSED>(hin, NC - 1, A, hw, lane);
+        bstage_load<AL>(stg[0], NC - 1, A, hw, lane);
+        bstage_store(stg[0], NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
+        bstage_load<AL>(stg[0], max(NC - 2, 0), A, hw, lane);
+        bstage_load<AL>(stg[1], max(NC - 3, 0), A, hw, lane);
+        bhelp_load<FUSED>(hin[1], NC - 1, A, hw, lane);
+        bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, hw, lane);
         lds_barrier();
-        for (int s = 0; s < NC + 2; ++s) {
+        auto step = [&](int s, BHelpIn& hb, BStage& sg) {
             const int ce = NC + 1 - s, cp = NC - s, cw = NC - 2 - s;
-            if (ce >= 0 && ce < NC)
-                bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, lds + B_G, ce, A, hw, lane);
-            if (cp >= 0 && cp < NC) {
-                bhelp_products(cy, hin, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
+            if (cw >= 0) bstage_store(sg, cw, lds + B_STG + (cw % NSB) * SB_BUF, A.T, hw, lane);
+            if (ce >= 0 && ce < NC) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, ce, A, hw, lane);
+            if (cp >= 0 && cp < NC)
+                bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
                                lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
-                bhelp_load<FUSED>(hin, max(cp - 1, 0), A, hw, lane);
-            }
-            if (cw >= 0) {
-                bstage_store(stg, cw, lds + B_STG + (cw % NSB) * SB_BUF, A.T, hw, lane);
-                bstage_load<AL>(stg, max(cw - 1, 0), A, hw, lane);
-            }
+            bstage_load<AL>(sg, min(max(cw - 2, 0), NC - 1), A, hw, lane);
+            bhelp_load<FUSED>(hb, min(max(cp - 2, 0), NC - 1), A, hw, lane);
             lds_barrier();
+        };
+        for (int s = 0; s < NC + 2; s += 2) {
+            step(s, hin[0], stg[0]);
+            if (s + 1 < NC + 2) step(s + 1, hin[1], stg[1]);
         }
         return;
     }
+    // chain: step s runs block NC - 1 - s and, on wave (c & 3) for c = NC + 1 - s,
+    // the gate gradients of block c from the helpers' sums
     f32x4 X[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) X[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     BChainIn cb[2];
+    BGateIn gin;
     bchain_load<AL>(cb[0], NC - 1, A, w, lane);
+    bchain_load<AL>(cb[1], max(NC - 2, 0), A, w, lane);
+    // each chain wave's first gate block (the last c < NC with c & 3 == w), then
+    // the one four blocks before it, loaded right after the last use
+    bgate_load(gin, max(NC - 1 - ((NC - 1 - w) & 3), 0), A, lane);
     lds_barrier();
     for (int s = 0; s < NC + 2; ++s) {
-        const int c = NC - 1 - s;
-        if (c >= 0) {
-            // buffers alternate by block parity (static indices: no register copies)
-            if ((s & 1) == 0) {
-                bchain_load<AL>(cb[1], max(c - 1, 0), A, w, lane);
+        const int c = NC - 1 - s, cg = NC + 1 - s;
+        // the chain's inputs are loaded two steps ahead into buffer s & 1
+        // (static indices: no register copies)
+        if ((s & 1) == 0) {
+            if (c >= 0)
                 bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                                 lane);
-            } else {
-                bchain_load<AL>(cb[0], max(c - 1, 0), A, w, lane);
+            bchain_load<AL>(cb[0], max(c - 2, 0), A, w, lane);
+        } else {
+            if (c >= 0)
                 bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                                 lane);
-            }
+            bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
+        }
+        if (cg >= 0 && cg < NC && (cg & 3) == w) {
+            bgate<FUSED>(gin, lds + B_EP + (cg & 1) * EP_SZ, scr, cg, A, lane);
+            bgate_load(gin, max(cg - 4, 0), A, lane);
         }
         lds_barrier();
     }
