@@ -606,7 +606,13 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
     float yv = y4.x * vv.x + y4.y * vv.y + y4.z * vv.z + y4.w * vv.w;
     yv = add_xor32(add_xor16(yv));
     if (lane < 16) ho[HO_YV + w * 16 + lane] = yv;
-    // X <- gamma_15 X + (diag(gamma) Q)^T dO - K^T diag(beta gamma) Y
+    // X <- gamma_15 X + Q^T (diag(gamma) dO) - K^T (diag(beta gamma) Y)
+    float dOg[4], Yb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        dOg[j] = el(gm, j) * dO[j];
+        Yb[j] = -el(bg, j) * Y[j];
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         X[r] *= g15;
@@ -614,8 +620,8 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
         for (int j = 0; j < 4; ++j) {
             const float qv = sb[SB_Q + (4 * g + j) * RP + 16 * r + n];
             const float kv = sb[SB_K + (4 * g + j) * RP + 16 * r + n];
-            X[r] = mfma4(el(gm, j) * qv, dO[j], X[r]);
-            X[r] = mfma4(-el(bg, j) * kv, Y[j], X[r]);
+            X[r] = mfma4(qv, dOg[j], X[r]);
+            X[r] = mfma4(kv, Yb[j], X[r]);
         }
     }
 }
@@ -726,21 +732,43 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         dk = mfma4(GdM[j], qb[j], dk);
         dk = mfma4(dA[j] + el(dat, j), kb[j], dk);
     }
-    // row sums over the helper's keys (rows 4g + j)
-    float rs[5][4];
+    // row sums over the helper's keys (rows 4g + j) of the 20 products, as one
+    // transposed reduction over the 16 lanes of a row: the lane pairs of lane bit
+    // 3 (row_ror 8) and then of bit 2 (half mirror) each keep half of the values,
+    // the last two levels are plain butterflies
+    float rv[20];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        rs[EP_RQ][j] = rowsum16(qb[j] * dq[j]);
-        rs[EP_RK][j] = rowsum16(kb[j] * dk[j]);
-        rs[EP_QF][j] = rowsum16(qb[j] * F[j]);
-        rs[EP_ZK][j] = rowsum16(kb[j] * Zt[j]);
-        rs[EP_KD][j] = rowsum16(kb[j] * D[j]);
+        rv[EP_RQ * 4 + j] = qb[j] * dq[j];
+        rv[EP_RK * 4 + j] = kb[j] * dk[j];
+        rv[EP_QF * 4 + j] = qb[j] * F[j];
+        rv[EP_ZK * 4 + j] = kb[j] * Zt[j];
+        rv[EP_KD * 4 + j] = kb[j] * D[j];
     }
-    if (n == 0) {
+    const bool b3 = (n & 8) != 0, b2 = (n & 4) != 0;
+    float h10[10];
 #pragma unroll
-        for (int e = 0; e < 5; ++e)
-            *reinterpret_cast<float4*>(ep + EP_ROW + (hw * 5 + e) * 16 + 4 * g) =
-                make_float4(rs[e][0], rs[e][1], rs[e][2], rs[e][3]);
+    for (int i = 0; i < 10; ++i) {
+        const float keep = b3 ? rv[10 + i] : rv[i];
+        const float send = b3 ? rv[i] : rv[10 + i];
+        h10[i] = keep + dpp<DPP_ROW_ROR8>(send);
+    }
+    float h5[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const float keep = b2 ? h10[5 + i] : h10[i];
+        const float send = b2 ? h10[i] : h10[5 + i];
+        h5[i] = keep + dpp<DPP_HALF_MIRROR>(send);
+    }
+#pragma unroll
+    for (int i = 0; i < 5; ++i) h5[i] = group_sum<4>(h5[i]);
+    if ((n & 3) == 0) {
+        const int base = (b3 ? 10 : 0) + (b2 ? 5 : 0);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int idx = base + i;   // quantity idx / 4, row 4g + idx % 4
+            ep[EP_ROW + (hw * 5 + (idx >> 2)) * 16 + 4 * g + (idx & 3)] = h5[i];
+        }
     }
     dss = wave_sum(dss);
     if (lane == 0) ep[EP_DSS + hw] = dss;
