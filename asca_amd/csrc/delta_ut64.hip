@@ -527,6 +527,7 @@ struct BArgs {
     float *gq, *gk, *gv, *ga, *gb;
     long ldx, ldg, d, ubase, gbase, rowbase;
     int B, T, H, h, nslots, NC, unit;
+    int di, ldxi, ldgi;   // d, ldx, ldg as 32-bit strides (the launcher checks they fit)
 };
 
 struct BChainIn {
@@ -538,11 +539,11 @@ struct BChainIn {
 template <bool AL>
 ASCA_DEV void bchain_load(BChainIn& ci, int c, const BArgs& A, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const long t = min(c * C + n, A.T - 1);
-    ci.a = A.alpha[A.gbase + t * A.H];
-    ci.b = A.beta[A.gbase + t * A.H];
-    ci.v = ld4<AL>(A.v + A.ubase + t * A.d + 16 * w + 4 * g);
-    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    const int t = min(c * C + n, A.T - 1);
+    ci.a = A.alpha[(unsigned)(t * A.H)];
+    ci.b = A.beta[(unsigned)(t * A.H)];
+    ci.v = ld4<AL>(A.v + (unsigned)(t * A.di + 16 * w + 4 * g));
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
     ci.tr = rq[(R_T >> 2) + lane];
     ci.mr = rq[(R_M >> 2) + lane];
 }
@@ -590,7 +591,7 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
         *reinterpret_cast<float4*>(ho + HO_DS + ((r * 4 + w) * 64 + lane) * 4) = tile_t(X[r], scr, lane);
     const float4 y4 = tile_t(Y, scr, lane);  // Y[n][16w + 4g ..]
     *reinterpret_cast<float4*>(ho + HO_Y + (w * 64 + lane) * 4) = y4;
-    if (live) store4<AL>(A.gv + (A.rowbase + c * C + n) * A.ldx + A.h * DH + 16 * w + 4 * g, f4scale(bt, y4));
+    if (live) store4<AL>(A.gv + (unsigned)((c * C + n) * A.ldxi + 16 * w + 4 * g), f4scale(bt, y4));
     // the wave's shares of dO U^T and Y U^T, and of the row sums of Y o V
     const float4 do4 = *reinterpret_cast<const float4*>(sb + SB_DO + n * RP + 16 * w + 4 * g);
     const float4 u4 = *reinterpret_cast<const float4*>(sb + SB_U + n * RP + 16 * w + 4 * g);
@@ -636,21 +637,21 @@ struct BHelpIn {
 template <bool FUSED>
 ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + ((long)A.unit * A.nslots + c) * DH2);
+    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + (unsigned)(c * DH2));
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = sp[(hw * 4 + cc) * 64 + lane];
-    const long t = min(c * C + n, A.T - 1);
-    hi.a = A.alpha[A.gbase + t * A.H];
-    hi.b = A.beta[A.gbase + t * A.H];
+    const int t = min(c * C + n, A.T - 1);
+    hi.a = A.alpha[(unsigned)(t * A.H)];
+    hi.b = A.beta[(unsigned)(t * A.H)];
     if constexpr (FUSED) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const long tj = min(c * C + 4 * g + j, A.T - 1);
-            hi.qn[j] = A.qn[A.gbase + tj * A.H];
-            hi.kn[j] = A.kn[A.gbase + tj * A.H];
+            const int tj = min(c * C + 4 * g + j, A.T - 1);
+            hi.qn[j] = A.qn[(unsigned)(tj * A.H)];
+            hi.kn[j] = A.kn[(unsigned)(tj * A.H)];
         }
     }
-    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
     hi.gr = rq[(R_G >> 2) + lane];
 }
 
@@ -815,7 +816,7 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
     float4 q4, k4;
     tile_t2(dq, dk, q4, k4, scr, lane);
     if (c * C + n < A.T) {
-        const long o = (A.rowbase + c * C + n) * A.ldx + A.h * DH + 16 * hw + 4 * g;
+        const unsigned o = (unsigned)((c * C + n) * A.ldxi + 16 * hw + 4 * g);
         store4<AL>(A.gq + o, q4);
         store4<AL>(A.gk + o, k4);
     }
@@ -829,13 +830,13 @@ struct BGateIn {
 };
 
 ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
-    const float4* rq = reinterpret_cast<const float4*>(A.rec + ((long)A.unit * A.NC + c) * R_SZ);
+    const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
     gi.ar = rq[(R_A >> 2) + lane];
     gi.bq = rq[(R_BQ >> 2) + lane];
     gi.gr = rq[(R_G >> 2) + lane];
-    const long t = min(c * C + (lane & 15), A.T - 1);
-    gi.a = A.alpha[A.gbase + t * A.H];
-    gi.b = A.beta[A.gbase + t * A.H];
+    const int t = min(c * C + (lane & 15), A.T - 1);
+    gi.a = A.alpha[(unsigned)(t * A.H)];
+    gi.b = A.beta[(unsigned)(t * A.H)];
 }
 
 template <bool FUSED>
@@ -902,7 +903,7 @@ ASCA_DEV void bgate(const BGateIn& gin, const float* __restrict__ ep, float* __r
     wave_sync();
     const float dbe = yv - gam * szk + rbn;
     if (lane < 16 && c * C + n < A.T) {
-        const long r = (A.rowbase + c * C + n) * A.ldg + A.h;
+        const unsigned r = (unsigned)((c * C + n) * A.ldgi);
         A.ga[r] = FUSED ? dal * gi.a * (1.0f - gi.a) : dal;
         A.gb[r] = FUSED ? dbe * gi.b * (1.0f - gi.b) : dbe;
     }
@@ -917,8 +918,8 @@ struct BStage {
 
 template <bool AL>
 ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
-    const long t = min(c * C + 4 * hw + (lane >> 4), A.T - 1);
-    const long off = A.ubase + t * A.d + 4 * (lane & 15);
+    const int t = min(c * C + 4 * hw + (lane >> 4), A.T - 1);
+    const unsigned off = (unsigned)(t * A.di + 4 * (lane & 15));
     st.x[0] = ld4<AL>(A.k + off);
     st.x[1] = ld4<AL>(A.q + off);
     st.x[2] = ld4<AL>(A.d_o + off);
@@ -941,9 +942,19 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         A.unit = blockIdx.x;  // h*B + b
         A.h = A.unit / A.B;
         const int b = A.unit - A.h * A.B;
-        A.ubase = (long)b * A.T * A.d + (long)A.h * DH;
-        A.gbase = (long)b * A.T * A.H + A.h;
-        A.rowbase = (long)b * A.T;
+        const long ubase = (long)b * A.T * A.d + (long)A.h * DH;
+        const long gbase = (long)b * A.T * A.H + A.h;
+        const long rowbase = (long)b * A.T;
+        // every pointer rebased on the unit: the per-block offsets are 32-bit
+        A.q += ubase; A.k += ubase; A.v += ubase; A.d_o += ubase; A.u += ubase;
+        A.alpha += gbase; A.beta += gbase;
+        if (A.qn) { A.qn += gbase; A.kn += gbase; }
+        A.ckpt += (long)A.unit * A.nslots * DH2;
+        A.rec += (long)A.unit * A.NC * R_SZ;
+        A.gq += rowbase * A.ldx + (long)A.h * DH; A.gk += rowbase * A.ldx + (long)A.h * DH;
+        A.gv += rowbase * A.ldx + (long)A.h * DH;
+        A.ga += rowbase * A.ldg + A.h; A.gb += rowbase * A.ldg + A.h;
+        A.ubase = 0; A.gbase = 0; A.rowbase = 0;
     }
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int NC = A.NC;
@@ -1079,6 +1090,10 @@ int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, 
                     ut_aligned16(gk) && ut_aligned16(gv) && (ldx * 4) % 16 == 0;
     const int units = B * H;
     a.B = B; a.unit = 0; a.h = 0; a.ubase = 0; a.gbase = 0; a.rowbase = 0;
+    if ((long)T * (ldx > a.d ? ldx : a.d) >= (1L << 31) || (long)T * ldg >= (1L << 31) ||
+        (long)((T + ut64::C - 1) / ut64::C + 1) * ut64::DH2 >= (1L << 31))
+        return fail(ASCA_ERR_UNSUPPORTED, "ut_bwd64: one sequence's rows exceed 32-bit offsets");
+    a.di = (int)a.d; a.ldxi = (int)ldx; a.ldgi = (int)ldg;
     if (fused) return al ? launch_ut_bwd64_t<true, true>(a, units, st) : launch_ut_bwd64_t<true, false>(a, units, st);
     return al ? launch_ut_bwd64_t<false, true>(a, units, st) : launch_ut_bwd64_t<false, false>(a, units, st);
 }
