@@ -19,7 +19,8 @@ struct DeltaWs {
     float* ckpt;
     float* part_x;  // column split: partial dq, dk  [2][CS][B*T][H*dh]
     float* part_g;  // column split: partial dalpha, dbeta  [CS][B*T][2H]
-    float* rec;     // dh = 64 blocked form: per unit and 16-step block, K K^T, Q K^T, T, M
+    float* rec;     // dh = 64 blocked form: per unit and 16-step block, K K^T, Q K^T, T, M, Gamma
+    float* bsc;     // dh = 64 blocked form: the backward's per-block gate sums (scratch)
     int ck;
     int nslots;
     int cs;
@@ -69,10 +70,13 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
 // dh = 64: the blocked (UT) form on the matrix cores (delta_ut64.hip), used for
 // every dh = 64 shape with one block per unit (ws.cs == 1).  Its workspace: the
 // u rows in `sk`, the state before every D64_CK-step block (and the final state)
-// in `ckpt`, and per block a record of D64_REC floats in `rec`.  Any pointer
-// alignment.
+// in `ckpt`, per block a record of D64_REC floats in `rec` (all written by the
+// forward), and per block D64_BSC floats of backward scratch in `bsc` (written
+// and read inside one backward: backwards on one workspace must not overlap).
+// Any pointer alignment.
 constexpr int D64_CK = 16;
 constexpr int D64_REC = 1280;
+constexpr int D64_BSC = 768;
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st);
 int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,

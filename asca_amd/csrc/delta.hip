@@ -1121,8 +1121,12 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
     w.part_x = base && px_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
     w.part_g = base && pg_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes) : nullptr;
+    const size_t bsc_bytes =
+        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * D64_BSC * sizeof(float)) : 0;
     w.rec = base && rec_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes) : nullptr;
-    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes;
+    w.bsc = base && bsc_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes)
+                              : nullptr;
+    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes + bsc_bytes;
     return w;
 }
 

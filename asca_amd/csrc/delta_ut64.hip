@@ -425,6 +425,14 @@ constexpr int EP_YV = 324;                   // [16]: row sums of Y o V
 constexpr int EP_DM = 344;                   // dM = tril(dO U^T), accumulator layout [lane][4]
 constexpr int EP_DL = 600;                   // dL = -strict_tril(Y U^T)
 constexpr int EP_SZ = 856;
+// per unit and block in the workspace's backward scratch (D64_BSC floats): what
+// the gate gradients need, written by the helpers, read after the block loop
+constexpr int GS_ROW = 0;                    // [hw][3][16]: q.F, k.Zt, k.D row sums per helper
+constexpr int GS_DSS = 192;                  // [hw]: <X, S> per helper
+constexpr int GS_YV = 196;                   // [16]: row sums of Y o V
+constexpr int GS_DM = 256;                   // dM, accumulator layout [lane][4]
+constexpr int GS_DL = 512;                   // dL
+static_assert(GS_DL + 256 == D64_BSC, "backward scratch");
 constexpr int WSCR = 2 * C * OTP + 128;      // per wave: two transpose tiles and a vector area
 constexpr int SVO = 2 * C * OTP;             // the vector area's offset
 constexpr int B_STG = 0;
@@ -525,6 +533,7 @@ ASCA_DEV float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + 
 struct BArgs {
     const float *q, *k, *v, *alpha, *beta, *d_o, *u, *ckpt, *rec, *qn, *kn;
     float *gq, *gk, *gv, *ga, *gb;
+    float* bsc;   // the workspace's backward scratch
     long ldx, ldg, d, ubase, gbase, rowbase;
     int B, T, H, h, nslots, NC, unit;
     int di, ldxi, ldgi;   // d, ldx, ldg as 32-bit strides (the launcher checks they fit)
@@ -763,25 +772,28 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
 #pragma unroll
     for (int i = 0; i < 5; ++i) h5[i] = group_sum<4>(h5[i]);
+    float* gs = A.bsc + (unsigned)(c * D64_BSC);
     if ((n & 3) == 0) {
         const int base = (b3 ? 10 : 0) + (b2 ? 5 : 0);
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
             const int idx = base + i;   // quantity idx / 4, row 4g + idx % 4
-            ep[EP_ROW + (hw * 5 + (idx >> 2)) * 16 + 4 * g + (idx & 3)] = h5[i];
+            const int e = idx >> 2, row = 4 * g + (idx & 3);
+            if (e < EP_QF) ep[EP_ROW + (hw * 5 + e) * 16 + row] = h5[i];
+            else gs[GS_ROW + (hw * 3 + e - EP_QF) * 16 + row] = h5[i];
         }
     }
     dss = wave_sum(dss);
-    if (lane == 0) ep[EP_DSS + hw] = dss;
+    if (lane == 0) gs[GS_DSS + hw] = dss;
     if (hw == 0) {
         if (lane < 16) {
             float yv = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) yv += ho[HO_YV + w * 16 + lane];
-            ep[EP_YV + lane] = yv;
+            gs[GS_YV + lane] = yv;
         }
-        *reinterpret_cast<float4*>(ep + EP_DM + 4 * lane) = make_float4(dM[0], dM[1], dM[2], dM[3]);
-        *reinterpret_cast<float4*>(ep + EP_DL + 4 * lane) = make_float4(dL[0], dL[1], dL[2], dL[3]);
+        *reinterpret_cast<float4*>(gs + GS_DM + 4 * lane) = make_float4(dM[0], dM[1], dM[2], dM[3]);
+        *reinterpret_cast<float4*>(gs + GS_DL + 4 * lane) = make_float4(dL[0], dL[1], dL[2], dL[3]);
     }
     cy.dq = dq;
     cy.dk = dk;
@@ -840,26 +852,26 @@ ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
 }
 
 template <bool FUSED>
-ASCA_DEV void bgate(const BGateIn& gin, const float* __restrict__ ep, float* __restrict__ scr, int c, const BArgs& A,
+ASCA_DEV void bgate(const BGateIn& gin, const float* __restrict__ gs, float* __restrict__ scr, int c, const BArgs& A,
                     int lane) {
     const int n = lane & 15, g = lane >> 4;
     BGateIn gi = gin;
     if (c * C + n >= A.T) { gi.a = 1.0f; gi.b = 0.0f; }
     const float gam = prefix_prod<16>(gi.a);
-    const float4 pm = *reinterpret_cast<const float4*>(ep + EP_DM + 4 * lane);
-    const float4 pl = *reinterpret_cast<const float4*>(ep + EP_DL + 4 * lane);
+    const float4 pm = *reinterpret_cast<const float4*>(gs + GS_DM + 4 * lane);
+    const float4 pl = *reinterpret_cast<const float4*>(gs + GS_DL + 4 * lane);
     const float dM[4] = {pm.x, pm.y, pm.z, pm.w};
     const float dL[4] = {pl.x, pl.y, pl.z, pl.w};
     const float G[4] = {gi.gr.x, gi.gr.y, gi.gr.z, gi.gr.w};
     float szk = 0.f, sqf = 0.f, skd = 0.f, dss = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        szk += ep[EP_ROW + (w * 5 + EP_ZK) * 16 + n];
-        sqf += ep[EP_ROW + (w * 5 + EP_QF) * 16 + n];
-        skd += ep[EP_ROW + (w * 5 + EP_KD) * 16 + n];
-        dss += ep[EP_DSS + w];
+        sqf += gs[GS_ROW + (w * 3 + 0) * 16 + n];
+        szk += gs[GS_ROW + (w * 3 + 1) * 16 + n];
+        skd += gs[GS_ROW + (w * 3 + 2) * 16 + n];
+        dss += gs[GS_DSS + w];
     }
-    const float yv = ep[EP_YV + n];
+    const float yv = gs[GS_YV + n];
     const float dgam = -gi.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
     float4 vec[2];
     {
@@ -935,6 +947,21 @@ ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int 
             live ? st.x[m] : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// After the block loop: the gate gradients of every block, block c on wave
+// c mod 8, from the helpers' sums in the backward scratch.
+template <bool FUSED>
+ASCA_DEV void bgate_tail(const BArgs& A, float* __restrict__ scr, int w, int lane) {
+    __syncthreads();   // the scratch writes of every wave are visible
+    BGateIn gin;
+    if (w < A.NC) bgate_load(gin, w, A, lane);
+    for (int c = w; c < A.NC; c += 2 * NW) {
+        const float* gs = A.bsc + (unsigned)(c * D64_BSC);
+        BGateIn cur = gin;
+        if (c + 2 * NW < A.NC) bgate_load(gin, c + 2 * NW, A, lane);
+        bgate<FUSED>(cur, gs, scr, c, A, lane);
+    }
+}
+
 template <bool FUSED, bool AL>
 __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     extern __shared__ float lds[];
@@ -951,6 +978,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         if (A.qn) { A.qn += gbase; A.kn += gbase; }
         A.ckpt += (long)A.unit * A.nslots * DH2;
         A.rec += (long)A.unit * A.NC * R_SZ;
+        A.bsc += (long)A.unit * A.NC * D64_BSC;
         A.gq += rowbase * A.ldx + (long)A.h * DH; A.gk += rowbase * A.ldx + (long)A.h * DH;
         A.gv += rowbase * A.ldx + (long)A.h * DH;
         A.ga += rowbase * A.ldg + A.h; A.gb += rowbase * A.ldg + A.h;
@@ -991,23 +1019,19 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
             step(s, hin[0], stg[0]);
             if (s + 1 < NC + 2) step(s + 1, hin[1], stg[1]);
         }
+        bgate_tail<FUSED>(A, scr, w, lane);
         return;
     }
-    // chain: step s runs block NC - 1 - s and, on wave (c & 3) for c = NC + 1 - s,
-    // the gate gradients of block c from the helpers' sums
+    // chain: step s runs block NC - 1 - s
     f32x4 X[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) X[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     BChainIn cb[2];
-    BGateIn gin;
     bchain_load<AL>(cb[0], NC - 1, A, w, lane);
     bchain_load<AL>(cb[1], max(NC - 2, 0), A, w, lane);
-    // each chain wave's first gate block (the last c < NC with c & 3 == w), then
-    // the one four blocks before it, loaded right after the last use
-    bgate_load(gin, max(NC - 1 - ((NC - 1 - w) & 3), 0), A, lane);
     lds_barrier();
     for (int s = 0; s < NC + 2; ++s) {
-        const int c = NC - 1 - s, cg = NC + 1 - s;
+        const int c = NC - 1 - s;
         // the chain's inputs are loaded two steps ahead into buffer s & 1
         // (static indices: no register copies)
         if ((s & 1) == 0) {
@@ -1021,12 +1045,9 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
                                 lane);
             bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
         }
-        if (cg >= 0 && cg < NC && (cg & 3) == w) {
-            bgate<FUSED>(gin, lds + B_EP + (cg & 1) * EP_SZ, scr, cg, A, lane);
-            bgate_load(gin, max(cg - 4, 0), A, lane);
-        }
         lds_barrier();
     }
+    bgate_tail<FUSED>(A, scr, w, lane);
 }
 
 }  // namespace ut64
@@ -1079,10 +1100,10 @@ int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, 
                     const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
                     float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
                     hipStream_t st) {
-    if (ws.cs != 1 || !ws.rec) return fail(ASCA_ERR_INVALID, "ut_bwd64: workspace layout mismatch");
+    if (ws.cs != 1 || !ws.rec || !ws.bsc) return fail(ASCA_ERR_INVALID, "ut_bwd64: workspace layout mismatch");
     ut64::BArgs a;
     a.q = q; a.k = k; a.v = v; a.alpha = alpha; a.beta = beta; a.d_o = d_o; a.u = ws.sk; a.ckpt = ws.ckpt;
-    a.rec = ws.rec; a.qn = qn; a.kn = kn; a.gq = gq; a.gk = gk; a.gv = gv; a.ga = ga; a.gb = gb;
+    a.rec = ws.rec; a.bsc = ws.bsc; a.qn = qn; a.kn = kn; a.gq = gq; a.gk = gk; a.gv = gv; a.ga = ga; a.gb = gb;
     a.ldx = ldx; a.ldg = ldg; a.d = (long)H * ut64::DH; a.T = T; a.H = H; a.nslots = ws.nslots;
     a.NC = (T + ut64::C - 1) / ut64::C;
     // per-unit fields are filled in the kernel from blockIdx
