@@ -1091,10 +1091,11 @@ static int ck_for(int dhc) {
 // blocks of 8 waves hold their ~215 without spilling.  A function of the shape
 // only, so the workspace size never depends on the device state.
 constexpr long SPLIT_UNITS = 128;
-// dh = 64 always runs a block per unit on the kernels of delta64.hip: even with
-// few units they are faster than two blocks per unit (measured from 1 to 256
-// units at T = 1024: forward ~150 against ~157 us, backward ~345 against ~470
-// us at 8-128 units).
+// dh = 64 always runs a block per unit on the blocked kernels of delta_ut64.hip:
+// the unit's state lives in the accumulator tiles of one block's four chain
+// waves.  Even the per-step dh = 64 kernels they replaced were faster on one
+// block per unit than on two at any unit count (T = 1024, 8-128 units: forward
+// ~150 against ~157 us, backward ~345 against ~470 us).
 static int col_split(int B, int H, int dh, int dhc) {
     if (dh == 64) return 1;
     return (long)B * H <= SPLIT_UNITS || dhc == 128 ? 2 : 1;

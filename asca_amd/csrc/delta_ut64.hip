@@ -405,9 +405,11 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
 // one block behind the chain they form dO S^T, Y S^T, U X^T over all value
 // columns (S from the forward's checkpoint of the block), dq and dk and their row
 // sums; one more block behind, the L2-norm backward of dq, dk (from the row dots
-// of all four helpers), the gate gradients (helper 0) and the stores.  The
-// helpers also stage the k, q, dO, u rows of the block after next.  One barrier
-// per block.
+// of all four helpers) and the stores.  The helpers also stage the k, q, dO, u
+// rows of the block after next.  One barrier per block.  The gate gradients
+// need sums over all four helpers and all value columns: the helpers leave
+// theirs in the workspace's backward scratch, and after the block loop all
+// eight waves form dalpha, dbeta of every block from them.
 constexpr int SB_MAT = C * RP;
 constexpr int SB_K = 0, SB_Q = SB_MAT, SB_DO = 2 * SB_MAT, SB_U = 3 * SB_MAT;
 constexpr int SB_BUF = 4 * SB_MAT;
@@ -418,13 +420,10 @@ constexpr int HO_DM = 5120;                  // per chain wave dO_w U_w^T (accum
 constexpr int HO_DL = 6144;                  // per chain wave Y_w U_w^T
 constexpr int HO_YV = 7168;                  // per chain wave row sums of Y_w o V_w [w][16]
 constexpr int HO_SZ = 7232;
-constexpr int EP_ROW = 0;                    // [hw][5][16]: q.dq, k.dk, q.F, k.Zt, k.D over the helper's keys
+// a helper's five row sums over its keys: q.dq, k.dk (to the epilogue, in LDS
+// [hw][2][16]) and q.F, k.Zt, k.D (to the gate gradients, in the backward scratch)
 constexpr int EP_RQ = 0, EP_RK = 1, EP_QF = 2, EP_ZK = 3, EP_KD = 4;
-constexpr int EP_DSS = 320;                  // [hw]: <X, S> over the helper's keys
-constexpr int EP_YV = 324;                   // [16]: row sums of Y o V
-constexpr int EP_DM = 344;                   // dM = tril(dO U^T), accumulator layout [lane][4]
-constexpr int EP_DL = 600;                   // dL = -strict_tril(Y U^T)
-constexpr int EP_SZ = 856;
+constexpr int EP_SZ = NW * 2 * 16;
 // per unit and block in the workspace's backward scratch (D64_BSC floats): what
 // the gate gradients need, written by the helpers, read after the block loop
 constexpr int GS_ROW = 0;                    // [hw][3][16]: q.F, k.Zt, k.D row sums per helper
@@ -504,21 +503,6 @@ ASCA_DEV float suffix_excl_prod(float x) {
     x *= dpp_or<0x104>(1.0f, x);
     x *= dpp_or<0x108>(1.0f, x);
     return dpp_or<0x101>(1.0f, x);
-}
-
-// G[j] = Gamma[4g + j][n] = prod_{n<s<=4g+j} alpha_s for 4g + j >= n, else 0
-// (alpha of step s in lane s of the row).
-ASCA_DEV void gamma_acc(float a, float (&G)[4], int lane) {
-    const int n = lane & 15, g = lane >> 4;
-    float pr = 1.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < C; ++s) {
-        const float as = readlane_f(a, s);
-        pr = s > n ? pr * as : pr;
-        if ((s >> 2) == g) G[s & 3] = s >= n ? pr : 0.0f;
-    }
 }
 
 template <bool AL>
@@ -779,7 +763,7 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         for (int i = 0; i < 5; ++i) {
             const int idx = base + i;   // quantity idx / 4, row 4g + idx % 4
             const int e = idx >> 2, row = 4 * g + (idx & 3);
-            if (e < EP_QF) ep[EP_ROW + (hw * 5 + e) * 16 + row] = h5[i];
+            if (e < EP_QF) ep[(hw * 2 + e) * 16 + row] = h5[i];
             else gs[GS_ROW + (hw * 3 + e - EP_QF) * 16 + row] = h5[i];
         }
     }
@@ -812,12 +796,12 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
     const int n = lane & 15, g = lane >> 4;
     f32x4 dq = cy.dq, dk = cy.dk;
     if constexpr (FUSED) {
-        float4 dotq = *reinterpret_cast<const float4*>(ep + EP_ROW + EP_RQ * 16 + 4 * g);
-        float4 dotk = *reinterpret_cast<const float4*>(ep + EP_ROW + EP_RK * 16 + 4 * g);
+        float4 dotq = *reinterpret_cast<const float4*>(ep + EP_RQ * 16 + 4 * g);
+        float4 dotk = *reinterpret_cast<const float4*>(ep + EP_RK * 16 + 4 * g);
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
-            dotq = f4add(dotq, *reinterpret_cast<const float4*>(ep + EP_ROW + (w * 5 + EP_RQ) * 16 + 4 * g));
-            dotk = f4add(dotk, *reinterpret_cast<const float4*>(ep + EP_ROW + (w * 5 + EP_RK) * 16 + 4 * g));
+            dotq = f4add(dotq, *reinterpret_cast<const float4*>(ep + (w * 2 + EP_RQ) * 16 + 4 * g));
+            dotk = f4add(dotk, *reinterpret_cast<const float4*>(ep + (w * 2 + EP_RK) * 16 + 4 * g));
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -835,7 +819,8 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
 }
 
 // Gate gradients of block c (dalpha, dbeta and their sigmoid backward), run by
-// one chain wave from the helpers' sums in `ep`; lane t of each row is step t.
+// one wave from the sums the helpers left in the backward scratch `gs`; lane t
+// of each row is step t.
 struct BGateIn {
     float4 ar, bq, gr;  // K K^T, Q K^T, Gamma of the block (accumulator layout)
     float a, b;         // gates of step 16c + n

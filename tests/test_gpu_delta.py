@@ -183,19 +183,20 @@ def test_empty_and_invalid_shapes(g):
     assert ei.value.code == 3
 
 
-# dh = 64 runs on the one-block-per-unit kernels of delta64.hip at any unit
-# count (16-step chunks; state and matrix waves side by side).  One unit, few
-# units, more units than CUs (blocks queued behind a full round), ragged tails,
-# a single step, fewer steps than a segment, and the extreme gate patterns of
-# test_extreme_gates.
+# dh = 64 runs on the one-block-per-unit kernels of delta_ut64.hip at any unit
+# count: 16-step blocks of the UT form on the matrix cores, the state in the
+# chain waves' accumulators.  One unit, few units, more units than CUs (blocks
+# queued behind a full round), ragged tails (a partial last block, one inside a
+# partial group of four), a single step, fewer steps than a block, and the
+# extreme gate patterns of test_extreme_gates.
 @pytest.mark.parametrize("B,T,H", [(129, 1, 1), (17, 5, 8), (20, 16, 8), (17, 29, 8), (33, 67, 4), (3, 40, 48),
                                    (1, 37, 1), (2, 50, 4), (40, 20, 8)])
-def test_four_wave_dh64_shapes(orc, g, B, T, H):
+def test_blocked_dh64_shapes(orc, g, B, T, H):
     dh = 64
-    _check_all(orc, g, orc.DeltaInputs(300 + B * T + H, B, T, H, dh), B, T, H, dh, "dh64 four-wave")
+    _check_all(orc, g, orc.DeltaInputs(300 + B * T + H, B, T, H, dh), B, T, H, dh, "dh64 blocked")
 
 
-def test_four_wave_dh64_extreme_gates(orc, g):
+def test_blocked_dh64_extreme_gates(orc, g):
     B, T, H, dh = 17, 75, 8, 64
     x = orc.DeltaInputs(77, B, T, H, dh)
     t = np.arange(B * T) % T
@@ -205,10 +206,10 @@ def test_four_wave_dh64_extreme_gates(orc, g):
     a[(t >= 44) & (t < 48)] = 1.5
     a[t % 37 == 5] = 0.0
     a[t % 11 == 3, -1] = 1e-6
-    _check_all(orc, g, x, B, T, H, dh, "dh64 four-wave extreme gates")
+    _check_all(orc, g, x, B, T, H, dh, "dh64 blocked extreme gates")
 
 
-def test_four_wave_dh64_batch_isolation(orc, g):
+def test_blocked_dh64_batch_isolation(orc, g):
     # 136 units together, then each sequence alone (8 units); forward and fused
     # backward agree to the bar
     B, T, H, dh = 17, 24, 8, 64
@@ -227,18 +228,17 @@ def test_four_wave_dh64_batch_isolation(orc, g):
 
 
 @pytest.mark.parametrize("a", [0.5, 0.6, 0.7, 0.72, 0.75, 0.8, 0.9, 0.99])
-def test_four_wave_dh64_constant_gates(orc, g, a):
-    # Every alpha equal: each 16-step segment has gate product a^16, which puts
-    # a <= 0.70 on the forward recompute and a >= 0.71 on the backward walk of
-    # the scaled state (rounding magnified by up to 1/a^16 <= 256).
+def test_blocked_dh64_constant_gates(orc, g, a):
+    # Every alpha equal: each 16-step block has gate product a^16 (down to
+    # 1.5e-5 at a = 0.5) in gamma, Gamma and the decay of the carried state.
     B, T, H, dh = 17, 80, 8, 64
     x = orc.DeltaInputs(500, B, T, H, dh)
     x.alpha[:] = np.float32(a)
     _check_all(orc, g, x, B, T, H, dh, f"dh64 alpha={a}")
 
 
-def test_four_wave_dh64_unaligned_pointers(orc, g):
-    # q, k, v and dO one float past a 16-byte boundary: the four-wave kernels
+def test_blocked_dh64_unaligned_pointers(orc, g):
+    # q, k, v and dO one float past a 16-byte boundary: the blocked kernels
     # load them with scalar accesses and give the aligned results' parity.
     import ctypes as C
     from asca_amd import _lib
