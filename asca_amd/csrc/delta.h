@@ -69,12 +69,14 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
 
 // dh = 64: the blocked (UT) form on the matrix cores (delta_ut64.hip), used for
 // every dh = 64 shape with one block per unit (ws.cs == 1).  Its workspace: the
-// u rows in `sk`, the state before every D64_CK-step block (and the final state)
-// in `ckpt`, per block a record of D64_REC floats in `rec` (all written by the
+// u rows in `sk`, the state before every other D64_BLK-step block (every
+// D64_CK steps) and the final state in `ckpt`, per block a record of D64_REC
+// floats in `rec` (all written by the
 // forward), and per block D64_BSC floats of backward scratch in `bsc` (written
 // and read inside one backward: backwards on one workspace must not overlap).
 // Any pointer alignment.
-constexpr int D64_CK = 16;
+constexpr int D64_BLK = 16;
+constexpr int D64_CK = 2 * D64_BLK;
 constexpr int D64_REC = 1280;
 constexpr int D64_BSC = 768;
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,

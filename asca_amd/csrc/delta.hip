@@ -1116,14 +1116,14 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
     const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
     const size_t rec_bytes =
-        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * D64_REC * sizeof(float)) : 0;
+        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_BLK - 1) / D64_BLK) * D64_REC * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
     w.sk = reinterpret_cast<float*>(base);
     w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
     w.part_x = base && px_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
     w.part_g = base && pg_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes) : nullptr;
     const size_t bsc_bytes =
-        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_CK - 1) / D64_CK) * D64_BSC * sizeof(float)) : 0;
+        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_BLK - 1) / D64_BLK) * D64_BSC * sizeof(float)) : 0;
     w.rec = base && rec_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes) : nullptr;
     w.bsc = base && bsc_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes)
                               : nullptr;

@@ -36,7 +36,7 @@ namespace asca {
 namespace ut64 {
 
 constexpr int DH = 64;
-constexpr int C = 16;          // steps per block = checkpoint interval
+constexpr int C = 16;          // steps per block; a checkpoint every 2 C steps
 constexpr int NW = 4;          // waves per unit
 constexpr int NT = 64 * NW;
 constexpr int DH2 = DH * DH;
@@ -77,6 +77,7 @@ struct PrepIn {
 // matrix m's elements [4 (lane/16) + j][lane % 16], j = 0..3).
 constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_G = 1024, R_SZ = 1280;
 static_assert(R_SZ == D64_REC, "record size");
+static_assert(C == D64_BLK && D64_CK == 2 * C, "a checkpoint before every other block");
 
 ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ ps, float* __restrict__ scr,
                            float* __restrict__ rec, int lane) {
@@ -207,13 +208,13 @@ ASCA_DEV void ck_store(float* __restrict__ slot, const f32x4 (&S)[4], float* __r
 }
 
 // One block of 16 steps for the wave's 64 x 16 slab of S: outputs o, the u rows
-// (for the backward), the checkpoint (state before the block) and the block
+// (for the backward), the checkpoint (state before the block, even blocks) and the block
 // update.  `kb` points at the block's first staged k row
 // (q and v rows follow at S_MAT and 2 S_MAT).
 template <bool FULL, bool AL>
 ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const float* __restrict__ ps,
                          float* __restrict__ ot, int c, float* __restrict__ o, float* __restrict__ ws_u,
-                         float* __restrict__ ckb, long ubase, long d, int T, int w, int lane) {
+                         float* __restrict__ ckb, bool ckw, long ubase, long d, int T, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const float* qb = kb + S_MAT;
     const float* vb = kb + 2 * S_MAT;
@@ -257,7 +258,7 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
     for (int i = 0; i < 4; ++i) O[i] = el(gm, i) * (qa[i] + qb2[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) O = mfma4(el(mr, i), U[i], O);
-    ck_store(ckb + (long)c * DH2, S, ot + 2 * C * OTP, w, lane);
+    if (ckw) ck_store(ckb + (long)(c >> 1) * DH2, S, ot + 2 * C * OTP, w, lane);
     // o and u rows leave as 16-byte stores: the 16 x 16 tiles go through the
     // wave's LDS scratch (lane: row lane / 4, columns 4 (lane % 4) .. +3)
 #pragma unroll
@@ -373,15 +374,16 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
 #pragma unroll
             for (int j = 0; j < NW; ++j)
                 chain_step<true, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, ws_u, ckb,
+                                     (j & 1) == 0,
                                      ubase, d, T, w, lane);
         } else {
             for (int j = 0; j < NW && c0 + j < NC; ++j)
                 chain_step<false, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, ws_u,
-                                      ckb, ubase, d, T, w, lane);
+                                      ckb, ((c0 + j) & 1) == 0, ubase, d, T, w, lane);
         }
         lds_barrier();
     }
-    ck_store(ckb + (long)NC * DH2, S, ot + 2 * C * OTP, w, lane);
+    ck_store(ckb + (long)((NC + 1) >> 1) * DH2, S, ot + 2 * C * OTP, w, lane);
 }
 
 // ================================================================= backward
@@ -403,7 +405,8 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
 // their share of dO U^T and Y U^T.  They hand X (before its update) and Y over
 // in LDS.  The four helper waves own key columns 16hw .. 16hw + 15 of dq and dk:
 // one block behind the chain they form dO S^T, Y S^T, U X^T over all value
-// columns (S from the forward's checkpoint of the block), dq and dk and their row
+// columns (S from the forward's checkpoint, advanced by one block for odd
+// blocks), dq and dk and their row
 // sums; one more block behind, the L2-norm backward of dq, dk (from the row dots
 // of all four helpers) and the stores.  The helpers also stage the k, q, dO, u
 // rows of the block after next.  One barrier per block.  The gate gradients
@@ -621,8 +624,9 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
 }
 
 struct BHelpIn {
-    float4 sk[4];        // S of the block: S[16hw + n][16c + 4g ..], value tile c
+    float4 sk[4];        // checkpoint before block c & ~1: S[16hw + n][16c + 4g ..], value tile c
     float a, b;          // gates of step 16c + n
+    float ap;            // alpha of step 16(c - 1) + n (odd c)
     float qn[4], kn[4];  // norms of rows 16c + 4g + j
     float4 gr;           // Gamma of the block (accumulator layout)
 };
@@ -630,11 +634,12 @@ struct BHelpIn {
 template <bool FUSED>
 ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + (unsigned)(c * DH2));
+    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + (unsigned)((c >> 1) * DH2));
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = sp[(hw * 4 + cc) * 64 + lane];
     const int t = min(c * C + n, A.T - 1);
     hi.a = A.alpha[(unsigned)(t * A.H)];
+    hi.ap = A.alpha[(unsigned)(max((c - 1) * C + n, 0) * A.H)];  // block c - 1 is whole for odd c
     hi.b = A.beta[(unsigned)(t * A.H)];
     if constexpr (FUSED) {
 #pragma unroll
@@ -657,9 +662,9 @@ struct BCarry {
 
 ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
 
-ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restrict__ sb, const float* __restrict__ ho,
-                             float* __restrict__ ep, float* __restrict__ scr, int c, const BArgs& A, int hw,
-                             int lane) {
+ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restrict__ sb,
+                             const float* __restrict__ sbp, const float* __restrict__ ho, float* __restrict__ ep,
+                             float* __restrict__ scr, int c, const BArgs& A, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const bool live = c * C + n < A.T;
     const float a = live ? hi.a : 1.0f;
@@ -672,6 +677,30 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
     const float4 gm = vec[0], bg = vec[1], gc = vec[2], bb = vec[3];
     const float G[4] = {hi.gr.x, hi.gr.y, hi.gr.z, hi.gr.w};
+    // The forward stores the state before every other block.  An odd block's
+    // state follows from the block before (staged in `sbp`, always whole):
+    // S = gamma'_15 S' + K'^T diag(Gamma'[15][:]) U', here for the helper's 16
+    // keys (rows) as the transposed tiles of the checkpoint layout.
+    float4 sk[4] = {hi.sk[0], hi.sk[1], hi.sk[2], hi.sk[3]};
+    if (c & 1) {
+        const float gcp = suffix_excl_prod(hi.ap);  // lane m: Gamma'[15][m]
+        const float g15 = readlane_f(gcp, 0) * readlane_f(hi.ap, 0);
+        float* sv = scr + SVO + 64;
+        if (lane < 16) sv[(n & 3) * 4 + (n >> 2)] = gcp;
+        wave_sync();
+        const float4 gq = *reinterpret_cast<const float4*>(sv + 4 * g);  // Gamma'[15][4i + g], i = 0..3
+        wave_sync();
+        float kg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kg[i] = el(gq, i) * sbp[SB_K + (4 * i + g) * RP + 16 * hw + n];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            f32x4 t4 = {g15 * sk[cc].x, g15 * sk[cc].y, g15 * sk[cc].z, g15 * sk[cc].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t4 = mfma4(sbp[SB_U + (4 * i + g) * RP + 16 * cc + n], kg[i], t4);
+            sk[cc] = make_float4(t4[0], t4[1], t4[2], t4[3]);
+        }
+    }
     // dO S^T, Y S^T, U X^T for the helper's keys, over all value columns
     f32x4 F = {0.f, 0.f, 0.f, 0.f}, Zt = F, D = F;
     float dss = 0.0f;
@@ -683,10 +712,10 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         const float4 x4 = *reinterpret_cast<const float4*>(ho + HO_DS + ((hw * 4 + cc) * 64 + lane) * 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            F = mfma4(el(dO4, j), el(hi.sk[cc], j), F);
-            Zt = mfma4(el(y4, j), el(hi.sk[cc], j), Zt);
+            F = mfma4(el(dO4, j), el(sk[cc], j), F);
+            Zt = mfma4(el(y4, j), el(sk[cc], j), Zt);
             D = mfma4(el(u4, j), el(x4, j), D);
-            dss += el(x4, j) * el(hi.sk[cc], j);
+            dss += el(x4, j) * el(sk[cc], j);
         }
     }
     // dM = tril(dO U^T), dL = -strict_tril(Y U^T) from the chain waves' shares
@@ -994,7 +1023,8 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
             if (cw >= 0) bstage_store(sg, cw, lds + B_STG + (cw % NSB) * SB_BUF, A.T, hw, lane);
             if (ce >= 0 && ce < NC) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, ce, A, hw, lane);
             if (cp >= 0 && cp < NC)
-                bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
+                bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF,
+                               lds + B_STG + ((cp + NSB - 1) % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
                                lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
             bstage_load<AL>(sg, min(max(cw - 2, 0), NC - 1), A, hw, lane);
             bhelp_load<FUSED>(hb, min(max(cp - 2, 0), NC - 1), A, hw, lane);
@@ -1060,7 +1090,7 @@ static int launch_ut_fwd64_t(const float* q, const float* k, const float* v, con
 
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st) {
-    if (ws.ck != ut64::C || ws.cs != 1) return fail(ASCA_ERR_INVALID, "ut_fwd64: workspace layout mismatch");
+    if (ws.ck != D64_CK || ws.cs != 1) return fail(ASCA_ERR_INVALID, "ut_fwd64: workspace layout mismatch");
     return ut_aligned16(q) && ut_aligned16(k) && ut_aligned16(v) && ut_aligned16(o)
                ? launch_ut_fwd64_t<true>(q, k, v, alpha, beta, o, ws, B, T, H, st)
                : launch_ut_fwd64_t<false>(q, k, v, alpha, beta, o, ws, B, T, H, st);
