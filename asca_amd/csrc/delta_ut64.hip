@@ -403,13 +403,13 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
 // of X (accumulator tiles, like the forward's state) and run only the X
 // recurrence (K X, M^T dO, T^T dU, the update: 56 MFMAs per block) plus dv and
 // their share of dO U^T and Y U^T.  They hand X (before its update) and Y over
-// in LDS.  The four helper waves own key columns 16hw .. 16hw + 15 of dq and dk:
+// in LDS, and stage the k, q, dO, u rows of the block after theirs.  The four
+// helper waves own key columns 16hw .. 16hw + 15 of dq and dk:
 // one block behind the chain they form dO S^T, Y S^T, U X^T over all value
 // columns (S from the forward's checkpoint, advanced by one block for odd
 // blocks), dq and dk and their row
 // sums; one more block behind, the L2-norm backward of dq, dk (from the row dots
-// of all four helpers) and the stores.  The helpers also stage the k, q, dO, u
-// rows of the block after next.  One barrier per block.  The gate gradients
+// of all four helpers) and the stores.  One barrier per block.  The gate gradients
 // need sums over all four helpers and all value columns: the helpers leave
 // theirs in the workspace's backward scratch, and after the block loop all
 // eight waves form dalpha, dbeta of every block from them.
@@ -1002,63 +1002,69 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     const int NC = A.NC;
     float* scr = lds + B_SCR + w * WSCR;
     if (w >= NW) {
-        // helper: step s stages block NC - 2 - s, runs the epilogue of block
-        // NC + 1 - s and the products of block NC - s.  Every global load is made
-        // two steps ahead into buffer s & 1, unconditionally (clamped block
+        // helper: step s runs the epilogue of block NC + 1 - s and the products
+        // of block NC - s (the chain waves stage the rows).  Every global load is
+        // made two steps ahead into buffer s & 1, unconditionally (clamped block
         // indices), and consumed at the start of its step, so no wait falls on a
         // recent memory operation.
         const int hw = w - NW;
-        BStage stg[2];
         BHelpIn hin[2];
         BCarry cy;
-        bstage_load<AL>(stg[0], NC - 1, A, hw, lane);
-        bstage_store(stg[0], NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
-        bstage_load<AL>(stg[0], max(NC - 2, 0), A, hw, lane);
-        bstage_load<AL>(stg[1], max(NC - 3, 0), A, hw, lane);
+        {
+            BStage st0;
+            bstage_load<AL>(st0, NC - 1, A, hw, lane);
+            bstage_store(st0, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
+        }
         bhelp_load<FUSED>(hin[1], NC - 1, A, hw, lane);
         bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, hw, lane);
         lds_barrier();
-        auto step = [&](int s, BHelpIn& hb, BStage& sg) {
-            const int ce = NC + 1 - s, cp = NC - s, cw = NC - 2 - s;
-            if (cw >= 0) bstage_store(sg, cw, lds + B_STG + (cw % NSB) * SB_BUF, A.T, hw, lane);
+        auto step = [&](int s, BHelpIn& hb) {
+            const int ce = NC + 1 - s, cp = NC - s;
             if (ce >= 0 && ce < NC) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, ce, A, hw, lane);
             if (cp >= 0 && cp < NC)
                 bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF,
                                lds + B_STG + ((cp + NSB - 1) % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
                                lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
-            bstage_load<AL>(sg, min(max(cw - 2, 0), NC - 1), A, hw, lane);
             bhelp_load<FUSED>(hb, min(max(cp - 2, 0), NC - 1), A, hw, lane);
             lds_barrier();
         };
         for (int s = 0; s < NC + 2; s += 2) {
-            step(s, hin[0], stg[0]);
-            if (s + 1 < NC + 2) step(s + 1, hin[1], stg[1]);
+            step(s, hin[0]);
+            if (s + 1 < NC + 2) step(s + 1, hin[1]);
         }
         bgate_tail<FUSED>(A, scr, w, lane);
         return;
     }
-    // chain: step s runs block NC - 1 - s
+    // chain: step s runs block NC - 1 - s and stages rows 4w .. 4w + 3 of the
+    // block after (NC - 2 - s) into its buffer, which no wave reads in step s
     f32x4 X[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) X[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     BChainIn cb[2];
+    BStage sg[2];
     bchain_load<AL>(cb[0], NC - 1, A, w, lane);
     bchain_load<AL>(cb[1], max(NC - 2, 0), A, w, lane);
+    bstage_load<AL>(sg[0], max(NC - 2, 0), A, w, lane);
+    bstage_load<AL>(sg[1], max(NC - 3, 0), A, w, lane);
     lds_barrier();
     for (int s = 0; s < NC + 2; ++s) {
         const int c = NC - 1 - s;
         // the chain's inputs are loaded two steps ahead into buffer s & 1
         // (static indices: no register copies)
         if ((s & 1) == 0) {
+            if (c >= 1) bstage_store(sg[0], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             if (c >= 0)
                 bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                                 lane);
             bchain_load<AL>(cb[0], max(c - 2, 0), A, w, lane);
+            bstage_load<AL>(sg[0], max(c - 3, 0), A, w, lane);
         } else {
+            if (c >= 1) bstage_store(sg[1], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             if (c >= 0)
                 bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                                 lane);
             bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
+            bstage_load<AL>(sg[1], max(c - 3, 0), A, w, lane);
         }
         lds_barrier();
     }
