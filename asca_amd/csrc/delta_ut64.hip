@@ -954,11 +954,16 @@ ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
 
 ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int T, int hw, int lane) {
     const int row = 4 * hw + (lane >> 4);
-    const bool live = c * C + row < T;
+    float* dst = sb + row * RP + 4 * (lane & 15);
+    if ((c + 1) * C <= T) {  // a whole block (uniform): the loaded registers go straight out
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-        *reinterpret_cast<float4*>(sb + m * SB_MAT + row * RP + 4 * (lane & 15)) =
-            live ? st.x[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int m = 0; m < 4; ++m) *reinterpret_cast<float4*>(dst + m * SB_MAT) = st.x[m];
+    } else {
+        const bool live = c * C + row < T;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            *reinterpret_cast<float4*>(dst + m * SB_MAT) = live ? st.x[m] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 }
 
 // After the block loop: the gate gradients of every block, block c on wave
@@ -1047,27 +1052,28 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     bstage_load<AL>(sg[0], max(NC - 2, 0), A, w, lane);
     bstage_load<AL>(sg[1], max(NC - 3, 0), A, w, lane);
     lds_barrier();
-    for (int s = 0; s < NC + 2; ++s) {
+    for (int s = 0; s < NC; ++s) {
         const int c = NC - 1 - s;
         // the chain's inputs are loaded two steps ahead into buffer s & 1
-        // (static indices: no register copies)
+        // (static indices: no register copies; X is updated on every path)
         if ((s & 1) == 0) {
             if (c >= 1) bstage_store(sg[0], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
-            if (c >= 0)
-                bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
-                                lane);
+            bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
+                            lane);
             bchain_load<AL>(cb[0], max(c - 2, 0), A, w, lane);
             bstage_load<AL>(sg[0], max(c - 3, 0), A, w, lane);
         } else {
             if (c >= 1) bstage_store(sg[1], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
-            if (c >= 0)
-                bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
-                                lane);
+            bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
+                            lane);
             bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
             bstage_load<AL>(sg[1], max(c - 3, 0), A, w, lane);
         }
         lds_barrier();
     }
+    // the helpers' last two steps (products of block 0, then nothing)
+    lds_barrier();
+    lds_barrier();
     bgate_tail<FUSED>(A, scr, w, lane);
 }
 
