@@ -1023,20 +1023,24 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         bhelp_load<FUSED>(hin[1], NC - 1, A, hw, lane);
         bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, hw, lane);
         lds_barrier();
+        lds_barrier();  // step 0: the chain's first block
+        // steps 1 .. NC: the products of block cp = NC - s on every path (the
+        // carried dq, dk are then never copied), the epilogue of cp + 1 from
+        // step 2 on; step NC + 1: the epilogue of block 0
         auto step = [&](int s, BHelpIn& hb) {
-            const int ce = NC + 1 - s, cp = NC - s;
-            if (ce >= 0 && ce < NC) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + (ce & 1) * EP_SZ, scr, ce, A, hw, lane);
-            if (cp >= 0 && cp < NC)
-                bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF,
-                               lds + B_STG + ((cp + NSB - 1) % NSB) * SB_BUF, lds + B_HO + (cp & 1) * HO_SZ,
-                               lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
-            bhelp_load<FUSED>(hb, min(max(cp - 2, 0), NC - 1), A, hw, lane);
+            const int cp = NC - s;
+            if (s >= 2) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + ((cp + 1) & 1) * EP_SZ, scr, cp + 1, A, hw, lane);
+            bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_STG + ((cp + NSB - 1) % NSB) * SB_BUF,
+                           lds + B_HO + (cp & 1) * HO_SZ, lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
+            bhelp_load<FUSED>(hb, max(cp - 2, 0), A, hw, lane);
             lds_barrier();
         };
-        for (int s = 0; s < NC + 2; s += 2) {
-            step(s, hin[0]);
-            if (s + 1 < NC + 2) step(s + 1, hin[1]);
+        for (int s = 1; s <= NC; s += 2) {
+            step(s, hin[1]);
+            if (s + 1 <= NC) step(s + 1, hin[0]);
         }
+        bhelp_epilogue<FUSED, AL>(cy, lds + B_EP, scr, 0, A, hw, lane);
+        lds_barrier();
         bgate_tail<FUSED>(A, scr, w, lane);
         return;
     }
