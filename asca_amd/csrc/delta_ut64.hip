@@ -627,7 +627,7 @@ struct BHelpIn {
     float4 sk[4];        // checkpoint before block c & ~1: S[16hw + n][16c + 4g ..], value tile c
     float a, b;          // gates of step 16c + n
     float ap;            // alpha of step 16(c - 1) + n (odd c)
-    float qn[4], kn[4];  // norms of rows 16c + 4g + j
+    float qn, kn;        // norms of row 16c + n (1 for the raw gradients)
     float4 gr;           // Gamma of the block (accumulator layout)
 };
 
@@ -642,12 +642,11 @@ ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
     hi.ap = A.alpha[(unsigned)(max((c - 1) * C + n, 0) * A.H)];  // block c - 1 is whole for odd c
     hi.b = A.beta[(unsigned)(t * A.H)];
     if constexpr (FUSED) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int tj = min(c * C + 4 * g + j, A.T - 1);
-            hi.qn[j] = A.qn[(unsigned)(tj * A.H)];
-            hi.kn[j] = A.kn[(unsigned)(tj * A.H)];
-        }
+        hi.qn = A.qn[(unsigned)(t * A.H)];
+        hi.kn = A.kn[(unsigned)(t * A.H)];
+    } else {
+        hi.qn = 1.0f;
+        hi.kn = 1.0f;
     }
     const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
     hi.gr = rq[(R_G >> 2) + lane];
@@ -657,7 +656,7 @@ ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
 struct BCarry {
     f32x4 dq, dk;        // raw dq, dk of rows 4g + j, keys 16hw + n
     float qb[4], kb[4];  // q, k at the same places
-    float qn[4], kn[4];
+    float rq[4], rk[4];  // 1 / |q|, 1 / |k| of rows 4g + j
 };
 
 ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
@@ -670,10 +669,11 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     const float a = live ? hi.a : 1.0f;
     const float bt = live ? hi.b : 0.0f;
     const float gam = prefix_prod<16>(a);
-    float4 vec[4];
+    float4 vec[6];
     {
-        const float x[4] = {gam, bt * gam, suffix_excl_prod(a), bt};
-        rows4x<4>(x, vec, scr + SVO, lane);
+        const float x[6] = {gam, bt * gam, suffix_excl_prod(a), bt, __builtin_amdgcn_rcpf(hi.qn),
+                            __builtin_amdgcn_rcpf(hi.kn)};
+        rows4x<6>(x, vec, scr + SVO, lane);
     }
     const float4 gm = vec[0], bg = vec[1], gc = vec[2], bb = vec[3];
     const float G[4] = {hi.gr.x, hi.gr.y, hi.gr.z, hi.gr.w};
@@ -814,8 +814,8 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     for (int j = 0; j < 4; ++j) {
         cy.qb[j] = qb[j];
         cy.kb[j] = kb[j];
-        cy.qn[j] = hi.qn[j];
-        cy.kn[j] = hi.kn[j];
+        cy.rq[j] = el(vec[4], j);
+        cy.rk[j] = el(vec[5], j);
     }
 }
 
@@ -834,8 +834,8 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            dq[j] = (dq[j] - cy.qb[j] * el(dotq, j)) * __builtin_amdgcn_rcpf(cy.qn[j]);
-            dk[j] = (dk[j] - cy.kb[j] * el(dotk, j)) * __builtin_amdgcn_rcpf(cy.kn[j]);
+            dq[j] = (dq[j] - cy.qb[j] * el(dotq, j)) * cy.rq[j];
+            dk[j] = (dk[j] - cy.kb[j] * el(dotk, j)) * cy.rk[j];
         }
     }
     float4 q4, k4;
