@@ -848,11 +848,15 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
 }
 
 // Gate gradients of block c (dalpha, dbeta and their sigmoid backward), run by
-// one wave from the sums the helpers left in the backward scratch `gs`; lane t
-// of each row is step t.
+// one wave from the sums the helpers left in the backward scratch (loaded with
+// the block's record, one block ahead); lane t of each row is step t.
 struct BGateIn {
     float4 ar, bq, gr;  // K K^T, Q K^T, Gamma of the block (accumulator layout)
     float a, b;         // gates of step 16c + n
+    float4 pm, pl;      // dM, dL (accumulator layout)
+    float rw[3][NW];    // the helpers' row sums q.F, k.Zt, k.D of row n
+    float ds[NW];       // the helpers' <X, S>
+    float yv;           // row sum of Y o V of row n
 };
 
 ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
@@ -863,29 +867,37 @@ ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
     const int t = min(c * C + (lane & 15), A.T - 1);
     gi.a = A.alpha[(unsigned)(t * A.H)];
     gi.b = A.beta[(unsigned)(t * A.H)];
+    const float* gs = A.bsc + (unsigned)(c * D64_BSC);
+    const int n = lane & 15;
+    gi.pm = *reinterpret_cast<const float4*>(gs + GS_DM + 4 * lane);
+    gi.pl = *reinterpret_cast<const float4*>(gs + GS_DL + 4 * lane);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+#pragma unroll
+        for (int e = 0; e < 3; ++e) gi.rw[e][w] = gs[GS_ROW + (w * 3 + e) * 16 + n];
+        gi.ds[w] = gs[GS_DSS + w];
+    }
+    gi.yv = gs[GS_YV + n];
 }
 
 template <bool FUSED>
-ASCA_DEV void bgate(const BGateIn& gin, const float* __restrict__ gs, float* __restrict__ scr, int c, const BArgs& A,
-                    int lane) {
+ASCA_DEV void bgate(const BGateIn& gin, float* __restrict__ scr, int c, const BArgs& A, int lane) {
     const int n = lane & 15, g = lane >> 4;
     BGateIn gi = gin;
     if (c * C + n >= A.T) { gi.a = 1.0f; gi.b = 0.0f; }
     const float gam = prefix_prod<16>(gi.a);
-    const float4 pm = *reinterpret_cast<const float4*>(gs + GS_DM + 4 * lane);
-    const float4 pl = *reinterpret_cast<const float4*>(gs + GS_DL + 4 * lane);
-    const float dM[4] = {pm.x, pm.y, pm.z, pm.w};
-    const float dL[4] = {pl.x, pl.y, pl.z, pl.w};
+    const float dM[4] = {gi.pm.x, gi.pm.y, gi.pm.z, gi.pm.w};
+    const float dL[4] = {gi.pl.x, gi.pl.y, gi.pl.z, gi.pl.w};
     const float G[4] = {gi.gr.x, gi.gr.y, gi.gr.z, gi.gr.w};
     float szk = 0.f, sqf = 0.f, skd = 0.f, dss = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        sqf += gs[GS_ROW + (w * 3 + 0) * 16 + n];
-        szk += gs[GS_ROW + (w * 3 + 1) * 16 + n];
-        skd += gs[GS_ROW + (w * 3 + 2) * 16 + n];
-        dss += gs[GS_DSS + w];
+        sqf += gi.rw[0][w];
+        szk += gi.rw[1][w];
+        skd += gi.rw[2][w];
+        dss += gi.ds[w];
     }
-    const float yv = gs[GS_YV + n];
+    const float yv = gi.yv;
     const float dgam = -gi.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
     float4 vec[2];
     {
@@ -974,10 +986,9 @@ ASCA_DEV void bgate_tail(const BArgs& A, float* __restrict__ scr, int w, int lan
     BGateIn gin;
     if (w < A.NC) bgate_load(gin, w, A, lane);
     for (int c = w; c < A.NC; c += 2 * NW) {
-        const float* gs = A.bsc + (unsigned)(c * D64_BSC);
         BGateIn cur = gin;
         if (c + 2 * NW < A.NC) bgate_load(gin, c + 2 * NW, A, lane);
-        bgate<FUSED>(cur, gs, scr, c, A, lane);
+        bgate<FUSED>(cur, scr, c, A, lane);
     }
 }
 
