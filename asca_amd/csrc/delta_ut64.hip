@@ -652,15 +652,21 @@ ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
     hi.gr = rq[(R_G >> 2) + lane];
 }
 
-// What a helper carries from the products of a block to its epilogue.
-struct BCarry {
-    f32x4 dq, dk;        // raw dq, dk of rows 4g + j, keys 16hw + n
-    float qb[4], kb[4];  // q, k at the same places
-    float rq[4], rk[4];  // 1 / |q|, 1 / |k| of rows 4g + j
-};
-
 ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
 
+// What a helper carries from the products of a block to its epilogue: dq, dk as
+// row pieces (lane (g, n): row n, keys 16hw + 4g .. + 3), ready to store.
+struct BCarry {
+    f32x4 dq, dk;   // raw dq, dk
+    float4 qr, kr;  // qhat, khat at the same places
+    float rq, rk;   // 1 / |q|, 1 / |k| of row n
+};
+
+// The products of block c for the helper's keys 16hw .. 16hw + 15, computed
+// transposed (keys as accumulator rows): lane (g, n) holds row n (step) and keys
+// 16hw + 4g + r, so the per-step gate factors are the lane's own, the row sums
+// over keys are in-register sums plus two lane swaps, and dq, dk leave without a
+// transpose.
 ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restrict__ sb,
                              const float* __restrict__ sbp, const float* __restrict__ ho, float* __restrict__ ep,
                              float* __restrict__ scr, int c, const BArgs& A, int hw, int lane) {
@@ -668,14 +674,15 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     const bool live = c * C + n < A.T;
     const float a = live ? hi.a : 1.0f;
     const float bt = live ? hi.b : 0.0f;
-    const float gam = prefix_prod<16>(a);
-    float4 vec[6];
+    const float gam = prefix_prod<16>(a);       // gamma_n
+    const float gcn = suffix_excl_prod(a);      // Gamma[15][n]
+    float4 bb;                                  // beta of rows 4g .. 4g + 3
     {
-        const float x[6] = {gam, bt * gam, suffix_excl_prod(a), bt, __builtin_amdgcn_rcpf(hi.qn),
-                            __builtin_amdgcn_rcpf(hi.kn)};
-        rows4x<6>(x, vec, scr + SVO, lane);
+        const float x[1] = {bt};
+        float4 v1[1];
+        rows4x<1>(x, v1, scr + SVO, lane);
+        bb = v1[0];
     }
-    const float4 gm = vec[0], bg = vec[1], gc = vec[2], bb = vec[3];
     const float G[4] = {hi.gr.x, hi.gr.y, hi.gr.z, hi.gr.w};
     // The forward stores the state before every other block.  An odd block's
     // state follows from the block before (staged in `sbp`, always whole):
@@ -701,7 +708,7 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
             sk[cc] = make_float4(t4[0], t4[1], t4[2], t4[3]);
         }
     }
-    // dO S^T, Y S^T, U X^T for the helper's keys, over all value columns
+    // (dO S^T)^T, (Y S^T)^T, (U X^T)^T: keys x steps, over all value columns
     f32x4 F = {0.f, 0.f, 0.f, 0.f}, Zt = F, D = F;
     float dss = 0.0f;
 #pragma unroll
@@ -712,9 +719,9 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
         const float4 x4 = *reinterpret_cast<const float4*>(ho + HO_DS + ((hw * 4 + cc) * 64 + lane) * 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            F = mfma4(el(dO4, j), el(sk[cc], j), F);
-            Zt = mfma4(el(y4, j), el(sk[cc], j), Zt);
-            D = mfma4(el(u4, j), el(x4, j), D);
+            F = mfma4(el(sk[cc], j), el(dO4, j), F);
+            Zt = mfma4(el(sk[cc], j), el(y4, j), Zt);
+            D = mfma4(el(x4, j), el(u4, j), D);
             dss += el(x4, j) * el(sk[cc], j);
         }
     }
@@ -737,64 +744,52 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
     float4 gdmt, dat;  // (Gamma o dM)[n][4g ..], dA[n][4g ..]
     tile_t2(GdM, dA, gdmt, dat, scr, lane);
-    float kb[4], qb[4];
+    float kb[4], qb[4];  // K, Q[4g + j][16hw + n]
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         kb[j] = sb[SB_K + (4 * g + j) * RP + 16 * hw + n];
         qb[j] = sb[SB_Q + (4 * g + j) * RP + 16 * hw + n];
     }
+    const float4 qr = *reinterpret_cast<const float4*>(sb + SB_Q + n * RP + 16 * hw + 4 * g);
+    const float4 kr = *reinterpret_cast<const float4*>(sb + SB_K + n * RP + 16 * hw + 4 * g);
+    // dq^T = gamma o F^T + K^T (Gamma o dM)^T,
+    // dk^T = Gamma[15] o D^T - beta gamma o Zt^T + Q^T (Gamma o dM) + K^T (dA + dA^T)
     f32x4 dq, dk;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        dq[j] = el(gm, j) * F[j];
-        dk[j] = el(gc, j) * D[j] - el(bg, j) * Zt[j];
+        dq[j] = gam * F[j];
+        dk[j] = gcn * D[j] - bt * gam * Zt[j];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        dq = mfma4(el(gdmt, j), kb[j], dq);
-        dk = mfma4(GdM[j], qb[j], dk);
-        dk = mfma4(dA[j] + el(dat, j), kb[j], dk);
+        dq = mfma4(kb[j], el(gdmt, j), dq);
+        dk = mfma4(qb[j], GdM[j], dk);
+        dk = mfma4(kb[j], dA[j] + el(dat, j), dk);
     }
-    // row sums over the helper's keys (rows 4g + j) of the 20 products, as one
-    // transposed reduction over the 16 lanes of a row: the lane pairs of lane bit
-    // 3 (row_ror 8) and then of bit 2 (half mirror) each keep half of the values,
-    // the last two levels are plain butterflies
-    float rv[20];
+    // row sums over the helper's keys: in-register, then over the four lanes of
+    // row n (lane bits 4 and 5)
+    float rs[5];
+    rs[EP_RQ] = el(qr, 0) * dq[0];
+    rs[EP_RK] = el(kr, 0) * dk[0];
+    rs[EP_QF] = el(qr, 0) * F[0];
+    rs[EP_ZK] = el(kr, 0) * Zt[0];
+    rs[EP_KD] = el(kr, 0) * D[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        rv[EP_RQ * 4 + j] = qb[j] * dq[j];
-        rv[EP_RK * 4 + j] = kb[j] * dk[j];
-        rv[EP_QF * 4 + j] = qb[j] * F[j];
-        rv[EP_ZK * 4 + j] = kb[j] * Zt[j];
-        rv[EP_KD * 4 + j] = kb[j] * D[j];
-    }
-    const bool b3 = (n & 8) != 0, b2 = (n & 4) != 0;
-    float h10[10];
-#pragma unroll
-    for (int i = 0; i < 10; ++i) {
-        const float keep = b3 ? rv[10 + i] : rv[i];
-        const float send = b3 ? rv[i] : rv[10 + i];
-        h10[i] = keep + dpp<DPP_ROW_ROR8>(send);
-    }
-    float h5[5];
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const float keep = b2 ? h10[5 + i] : h10[i];
-        const float send = b2 ? h10[i] : h10[5 + i];
-        h5[i] = keep + dpp<DPP_HALF_MIRROR>(send);
+    for (int j = 1; j < 4; ++j) {
+        rs[EP_RQ] += el(qr, j) * dq[j];
+        rs[EP_RK] += el(kr, j) * dk[j];
+        rs[EP_QF] += el(qr, j) * F[j];
+        rs[EP_ZK] += el(kr, j) * Zt[j];
+        rs[EP_KD] += el(kr, j) * D[j];
     }
 #pragma unroll
-    for (int i = 0; i < 5; ++i) h5[i] = group_sum<4>(h5[i]);
+    for (int e = 0; e < 5; ++e) rs[e] = add_xor32(add_xor16(rs[e]));
     float* gs = A.bsc + (unsigned)(c * D64_BSC);
-    if ((n & 3) == 0) {
-        const int base = (b3 ? 10 : 0) + (b2 ? 5 : 0);
+    if (lane < 16) {
+        ep[(hw * 2 + EP_RQ) * 16 + n] = rs[EP_RQ];
+        ep[(hw * 2 + EP_RK) * 16 + n] = rs[EP_RK];
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int idx = base + i;   // quantity idx / 4, row 4g + idx % 4
-            const int e = idx >> 2, row = 4 * g + (idx & 3);
-            if (e < EP_QF) ep[(hw * 2 + e) * 16 + row] = h5[i];
-            else gs[GS_ROW + (hw * 3 + e - EP_QF) * 16 + row] = h5[i];
-        }
+        for (int e = EP_QF; e <= EP_KD; ++e) gs[GS_ROW + (hw * 3 + e - EP_QF) * 16 + n] = rs[e];
     }
     dss = wave_sum(dss);
     if (lane == 0) gs[GS_DSS + hw] = dss;
@@ -810,13 +805,10 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
     cy.dq = dq;
     cy.dk = dk;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        cy.qb[j] = qb[j];
-        cy.kb[j] = kb[j];
-        cy.rq[j] = el(vec[4], j);
-        cy.rk[j] = el(vec[5], j);
-    }
+    cy.qr = qr;
+    cy.kr = kr;
+    cy.rq = __builtin_amdgcn_rcpf(hi.qn);
+    cy.rk = __builtin_amdgcn_rcpf(hi.kn);
 }
 
 template <bool FUSED, bool AL>
@@ -825,25 +817,22 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
     const int n = lane & 15, g = lane >> 4;
     f32x4 dq = cy.dq, dk = cy.dk;
     if constexpr (FUSED) {
-        float4 dotq = *reinterpret_cast<const float4*>(ep + EP_RQ * 16 + 4 * g);
-        float4 dotk = *reinterpret_cast<const float4*>(ep + EP_RK * 16 + 4 * g);
+        float dotq = ep[EP_RQ * 16 + n], dotk = ep[EP_RK * 16 + n];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
-            dotq = f4add(dotq, *reinterpret_cast<const float4*>(ep + (w * 2 + EP_RQ) * 16 + 4 * g));
-            dotk = f4add(dotk, *reinterpret_cast<const float4*>(ep + (w * 2 + EP_RK) * 16 + 4 * g));
+            dotq += ep[(w * 2 + EP_RQ) * 16 + n];
+            dotk += ep[(w * 2 + EP_RK) * 16 + n];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            dq[j] = (dq[j] - cy.qb[j] * el(dotq, j)) * cy.rq[j];
-            dk[j] = (dk[j] - cy.kb[j] * el(dotk, j)) * cy.rk[j];
+            dq[j] = (dq[j] - el(cy.qr, j) * dotq) * cy.rq;
+            dk[j] = (dk[j] - el(cy.kr, j) * dotk) * cy.rk;
         }
     }
-    float4 q4, k4;
-    tile_t2(dq, dk, q4, k4, scr, lane);
     if (c * C + n < A.T) {
         const unsigned o = (unsigned)((c * C + n) * A.ldxi + 16 * hw + 4 * g);
-        store4<AL>(A.gq + o, q4);
-        store4<AL>(A.gk + o, k4);
+        store4<AL>(A.gq + o, make_float4(dq[0], dq[1], dq[2], dq[3]));
+        store4<AL>(A.gk + o, make_float4(dk[0], dk[1], dk[2], dk[3]));
     }
 }
 
