@@ -38,8 +38,9 @@ PEAK_HBM = 8.0e12     # MI355X HBM3E, B/s
 HEADLINE = dict(B=32, T=512, H=8, dh=64, seed=1)
 PMC_FILE = ROOT / "profiles" / "delta_b32t512h8d64_traffic.json"
 # the sources of the delta kernels: counters measured on other sources are stale
-KERNEL_SOURCES = ["asca_amd/csrc/delta.hip", "asca_amd/csrc/delta_ut64.hip", "asca_amd/csrc/delta.h",
-                  "asca_amd/csrc/common.h"]
+KERNEL_SOURCES = ["asca_amd/csrc/delta.hip", "asca_amd/csrc/delta_ut64.hip", "asca_amd/csrc/ut64_kernels.h",
+                  "asca_amd/csrc/delta_ut64_b.hip", "asca_amd/csrc/delta.h", "asca_amd/csrc/common.h",
+                  "asca_amd/build.py"]
 
 
 def kernel_sources_sha() -> str:
