@@ -13,14 +13,14 @@ namespace asca {
 //    (the recurrent kernels store S^T, element (a, i) at i*dh + a; the blocked
 //    form its own tile order): slot j is the state before step j*ck for
 //    j < ceil(T/ck), the last slot the state after step T-1;
-//  * part_x / part_g: partial dq, dk and dalpha, dbeta of a column-split backward.
+//  * rec: the blocked form's per-block records.
+// The forward writes it; the backward only reads it (a column-split backward
+// keeps its partial sums in scratch of its own), so several backwards may read
+// one forward's workspace at once.
 struct DeltaWs {
     float* sk;
     float* ckpt;
-    float* part_x;  // column split: partial dq, dk  [2][CS][B*T][H*dh]
-    float* part_g;  // column split: partial dalpha, dbeta  [CS][B*T][2H]
-    float* rec;     // dh = 64 blocked form: per unit and 16-step block, K K^T, Q K^T, T, M, Gamma
-    float* bsc;     // dh = 64 blocked form: the backward's per-block gate sums (scratch)
+    float* rec;     // dh = 64 blocked form: per unit and 16-step block, K K^T, Q K^T, T, M, Gamma, gate vectors
     int ck;
     int nslots;
     int cs;
@@ -71,14 +71,11 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
 // every dh = 64 shape with one block per unit (ws.cs == 1).  Its workspace: the
 // u rows in `sk`, the state before every other D64_BLK-step block (every
 // D64_CK steps) and the final state in `ckpt`, per block a record of D64_REC
-// floats in `rec` (all written by the
-// forward), and per block D64_BSC floats of backward scratch in `bsc` (written
-// and read inside one backward: backwards on one workspace must not overlap).
-// Any pointer alignment.
+// floats in `rec`, all written by the forward and read by the backward.  Any
+// pointer alignment.
 constexpr int D64_BLK = 16;
 constexpr int D64_CK = 2 * D64_BLK;
-constexpr int D64_REC = 1280;
-constexpr int D64_BSC = 768;
+constexpr int D64_REC = 1344;
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st);
 int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, const float* alpha,

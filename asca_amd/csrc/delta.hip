@@ -1113,22 +1113,21 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     w.nslots = (T + w.ck - 1) / w.ck + 1;   // the state before every chunk, then the final state
     const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
-    const size_t px_bytes = w.cs > 1 ? align256((size_t)2 * w.cs * B * T * H * dh * sizeof(float)) : 0;
-    const size_t pg_bytes = w.cs > 1 ? align256((size_t)w.cs * B * T * 2 * H * sizeof(float)) : 0;
     const size_t rec_bytes =
         blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_BLK - 1) / D64_BLK) * D64_REC * sizeof(float)) : 0;
     char* c = reinterpret_cast<char*>(base);
     w.sk = reinterpret_cast<float*>(base);
     w.ckpt = base ? reinterpret_cast<float*>(c + sk_bytes) : nullptr;
-    w.part_x = base && px_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
-    w.part_g = base && pg_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes) : nullptr;
-    const size_t bsc_bytes =
-        blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_BLK - 1) / D64_BLK) * D64_BSC * sizeof(float)) : 0;
-    w.rec = base && rec_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes) : nullptr;
-    w.bsc = base && bsc_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes)
-                              : nullptr;
-    w.bytes = sk_bytes + ck_bytes + px_bytes + pg_bytes + rec_bytes + bsc_bytes;
+    w.rec = base && rec_bytes ? reinterpret_cast<float*>(c + sk_bytes + ck_bytes) : nullptr;
+    w.bytes = sk_bytes + ck_bytes + rec_bytes;
     return w;
+}
+
+// Floats of the column-split backward's partial dq, dk and dalpha, dbeta
+// (stream-ordered scratch of the backward call, never the forward's workspace).
+static size_t part_floats(int cs, int B, int T, int H, int dh) {
+    if (cs <= 1) return 0;
+    return (size_t)2 * cs * B * T * H * dh + (size_t)cs * B * T * 2 * H;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -1196,16 +1195,29 @@ static int launch_bwd_cs(const float* q, const float* k, const float* v, const f
     }
     int rc = pre_launch("delta_bwd");
     if (rc) return rc;
+    // the column halves' partials: scratch of this call on its stream
+    StreamScratch sc;
+    if ((rc = sc.get(part_floats(CS, B, T, H, dh), st))) return rc;
+    float* part_x = sc.ws.p;
+    float* part_g = CS > 1 ? part_x + (size_t)2 * CS * B * T * H * dh : nullptr;
     hipLaunchKernelGGL((delta_bwd_k<DH, CS, EXACT, FUSED>), dim3(B * H * CS), dim3(BS<DH, CS>::NT), lds, st, q, k,
-                       v, alpha, beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, ws.part_x,
-                       ws.part_g, B, T, H, dh, ws.nslots);
-    if ((rc = post_launch("delta_bwd"))) return rc;
-    if (CS == 1) return ASCA_OK;
-    if ((rc = pre_launch("delta_combine"))) return rc;
+                       v, alpha, beta, d_o, ws.sk, ws.ckpt, qn, kn, gq, gk, gv, ldx, ga, gb, ldg, part_x, part_g, B,
+                       T, H, dh, ws.nslots);
+    if ((rc = post_launch("delta_bwd"))) {
+        (void)sc.release(st);
+        return rc;
+    }
+    if (CS == 1) return sc.release(st);
+    if ((rc = pre_launch("delta_combine"))) {
+        (void)sc.release(st);
+        return rc;
+    }
     const long rows = (long)B * T;
-    hipLaunchKernelGGL((delta_combine_k<FUSED>), dim3((unsigned)((rows * H + 3) / 4)), dim3(256), 0, st, ws.part_x,
-                       ws.part_g, q, k, alpha, beta, qn, kn, gq, gk, ldx, ga, gb, ldg, rows, H, dh);
-    return post_launch("delta_combine");
+    hipLaunchKernelGGL((delta_combine_k<FUSED>), dim3((unsigned)((rows * H + 3) / 4)), dim3(256), 0, st, part_x,
+                       part_g, q, k, alpha, beta, qn, kn, gq, gk, ldx, ga, gb, ldg, rows, H, dh);
+    rc = post_launch("delta_combine");
+    const int rr = sc.release(st);
+    return rc ? rc : rr;
 }
 
 template <int DH, bool EXACT, bool FUSED>

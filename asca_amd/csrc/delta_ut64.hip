@@ -18,10 +18,10 @@ int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, 
                     const float* beta, const float* d_o, const DeltaWs& ws, const float* qn, const float* kn,
                     float* gq, float* gk, float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H,
                     hipStream_t st) {
-    if (ws.cs != 1 || !ws.rec || !ws.bsc) return fail(ASCA_ERR_INVALID, "ut_bwd64: workspace layout mismatch");
+    if (ws.cs != 1 || !ws.rec) return fail(ASCA_ERR_INVALID, "ut_bwd64: workspace layout mismatch");
     ut64::BArgs a;
     a.q = q; a.k = k; a.v = v; a.alpha = alpha; a.beta = beta; a.d_o = d_o; a.u = ws.sk; a.ckpt = ws.ckpt;
-    a.rec = ws.rec; a.bsc = ws.bsc; a.qn = qn; a.kn = kn; a.gq = gq; a.gk = gk; a.gv = gv; a.ga = ga; a.gb = gb;
+    a.rec = ws.rec; a.qn = qn; a.kn = kn; a.gq = gq; a.gk = gk; a.gv = gv; a.ga = ga; a.gb = gb;
     a.ldx = ldx; a.ldg = ldg; a.d = (long)H * ut64::DH; a.T = T; a.H = H; a.nslots = ws.nslots;
     a.NC = (T + ut64::C - 1) / ut64::C;
     // per-unit fields are filled in the kernel from blockIdx
@@ -33,8 +33,14 @@ int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, 
         (long)((T + ut64::C - 1) / ut64::C + 1) * ut64::DH2 >= (1L << 31))
         return fail(ASCA_ERR_UNSUPPORTED, "ut_bwd64: one sequence's rows exceed 32-bit offsets");
     a.di = (int)a.d; a.ldxi = (int)ldx; a.ldgi = (int)ldg;
-    if (fused && al) return launch_ut_bwd64_t<true, true>(a, units, st);
-    return launch_ut_bwd64_other(a, units, fused, al, st);
+    // the gate sums: scratch of this call on its stream (the forward's workspace is only read)
+    StreamScratch sc;
+    int rc = sc.get(ut_bwd64_scratch_floats(units, a.NC), st);
+    if (rc) return rc;
+    a.gsc = sc.ws.p;
+    rc = fused && al ? launch_ut_bwd64_t<true, true>(a, units, st) : launch_ut_bwd64_other(a, units, fused, al, st);
+    const int rr = sc.release(st);
+    return rc ? rc : rr;
 }
 
 }  // namespace asca

@@ -39,14 +39,23 @@ struct Ws {
 };
 
 // Scratch for the entry points that take no workspace argument (as the
-// reference's operators take none): get() allocates from the stream-ordered
-// allocator on the call's stream (hipMallocAsync), release() returns it behind
-// the work queued so far (hipFreeAsync).  Calls on different streams never
-// share scratch and nothing waits for the device.
+// reference's operators take none): each stream has one cached device buffer
+// (from the library's stream-ordered pool, grown when a call needs more, the
+// old one freed behind the work queued on that stream), so work on one stream
+// uses it in stream order and calls on different streams never share it.
+// get() holds a library lock until release() (or the destructor), so two host
+// threads enqueueing on one stream do not interleave a grow with a launch.
 struct StreamScratch {
     Ws ws{nullptr, 0};
     int get(size_t floats, hipStream_t st);
     int release(hipStream_t st);
+    ~StreamScratch();
+
+private:
+    bool held_ = false;
 };
+
+// Drops the cached scratch of a stream that is about to be destroyed.
+void stream_scratch_forget(hipStream_t st);
 
 }  // namespace asca

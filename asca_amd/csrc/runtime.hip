@@ -73,21 +73,62 @@ int pre_launch(const char* kernel) {
     return ASCA_OK;
 }
 
+// The stream-ordered pool behind StreamScratch: the library's own (created at
+// asca_init), so that its release threshold (keep what is freed for reuse
+// instead of returning it to the driver at every synchronisation) does not
+// change the device's default pool that other code in the process may use.
+static hipMemPool_t g_scratch_pool = nullptr;
+
+// One cached buffer per stream (a stream-ordered allocation and free per call
+// costs several microseconds of stream time).
+struct ScratchEntry {
+    float* p = nullptr;
+    size_t floats = 0;
+};
+static std::mutex g_scratch_mu;
+static std::unordered_map<hipStream_t, ScratchEntry> g_scratch;
+
 int StreamScratch::get(size_t floats, hipStream_t st) {
     ws = Ws{nullptr, 0};
     if (floats == 0) return ASCA_OK;
-    void* p = nullptr;
-    hipError_t e = hipMallocAsync(&p, floats * sizeof(float), st);
-    if (e != hipSuccess) return fail(ASCA_ERR_OOM, "hipMallocAsync(%zu): %s", floats * sizeof(float), hipGetErrorString(e));
-    ws = Ws{reinterpret_cast<float*>(p), floats};
+    if (!g_scratch_pool) return fail(ASCA_ERR_NOT_INIT, "asca_init has not been called");
+    g_scratch_mu.lock();
+    held_ = true;
+    ScratchEntry& en = g_scratch[st];
+    if (en.floats < floats) {
+        if (en.p) (void)hipFreeAsync(en.p, st);   // behind the queued work that still uses it
+        en = ScratchEntry{};
+        const size_t want = floats + floats / 4;  // headroom for slightly larger calls
+        void* p = nullptr;
+        hipError_t e = hipMallocFromPoolAsync(&p, want * sizeof(float), g_scratch_pool, st);
+        if (e != hipSuccess) {
+            held_ = false;
+            g_scratch_mu.unlock();
+            return fail(ASCA_ERR_OOM, "hipMallocFromPoolAsync(%zu): %s", want * sizeof(float), hipGetErrorString(e));
+        }
+        en = ScratchEntry{reinterpret_cast<float*>(p), want};
+    }
+    ws = Ws{en.p, floats};
     return ASCA_OK;
 }
 
-int StreamScratch::release(hipStream_t st) {
-    if (!ws.p) return ASCA_OK;
-    hipError_t e = hipFreeAsync(ws.p, st);
+int StreamScratch::release(hipStream_t) {
     ws = Ws{nullptr, 0};
-    return e == hipSuccess ? (int)ASCA_OK : fail(ASCA_ERR_HIP, "hipFreeAsync: %s", hipGetErrorString(e));
+    if (held_) {
+        held_ = false;
+        g_scratch_mu.unlock();
+    }
+    return ASCA_OK;
+}
+
+StreamScratch::~StreamScratch() { (void)release(nullptr); }
+
+void stream_scratch_forget(hipStream_t st) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch.find(st);
+    if (it == g_scratch.end()) return;
+    if (it->second.p) (void)hipFreeAsync(it->second.p, st);
+    g_scratch.erase(it);
 }
 
 int post_launch(const char* kernel) {
@@ -129,12 +170,23 @@ int asca_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(ASCA_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", device,
                     prop.gcnArchName);
-    // The stream-ordered allocator behind StreamScratch keeps what is freed for
-    // reuse instead of returning it to the driver at every synchronisation.
-    hipMemPool_t pool = nullptr;
-    if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess && pool) {
+    if (!g_scratch_pool || g_device != device) {
+        hipMemPoolProps props;
+        memset(&props, 0, sizeof props);
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = device;
+        hipMemPool_t pool = nullptr;
+        e = hipMemPoolCreate(&pool, &props);
+        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipMemPoolCreate: %s", hipGetErrorString(e));
         uint64_t keep = UINT64_MAX;
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) {
+            (void)hipMemPoolDestroy(pool);
+            return fail(ASCA_ERR_HIP, "hipMemPoolSetAttribute: %s", hipGetErrorString(e));
+        }
+        g_scratch_pool = pool;   // a pool of an earlier device stays until the process ends
     }
     if (int rc = noalloc_scratch_init(device)) return rc;
     g_device = device;
@@ -195,6 +247,14 @@ int asca_pool_release(void) {
     for (auto& kv : g_pool)
         for (void* p : kv.second) hipFree(p);
     g_pool.clear();
+    {
+        std::lock_guard<std::mutex> lk2(g_scratch_mu);   // the streams' cached scratch too (the device is idle)
+        for (auto& kv : g_scratch)
+            if (kv.second.p) (void)hipFreeAsync(kv.second.p, kv.first);
+        g_scratch.clear();
+    }
+    hipDeviceSynchronize();
+    if (g_scratch_pool) (void)hipMemPoolTrimTo(g_scratch_pool, 0);
     return ASCA_OK;
 }
 
@@ -293,6 +353,7 @@ int asca_stream_create(void** stream) {
 
 int asca_stream_destroy(void* stream) {
     if (!stream) return ASCA_OK;
+    stream_scratch_forget(as_stream(stream));
     hipError_t e = hipStreamDestroy(as_stream(stream));
     if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipStreamDestroy: %s", hipGetErrorString(e));
     return ASCA_OK;

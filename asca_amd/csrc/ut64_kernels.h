@@ -78,10 +78,13 @@ struct PrepIn {
 // Forms block p's matrices from its loads into the slot `ps`.  Steps past the
 // sequence end get alpha = 1, beta = 0: they leave the state, T and the
 // products of the live steps unchanged.  `scr` is the wave's own scratch.
-// Record of a block for the backward (1280 floats): K K^T, Q K^T, T, M and
+// Record of a block for the backward (1344 floats): K K^T, Q K^T, T, M and
 // Gamma (zero above the diagonal) in the accumulator layout, 16 bytes per lane (float4 index 64 m + lane holds
-// matrix m's elements [4 (lane/16) + j][lane % 16], j = 0..3).
-constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_G = 1024, R_SZ = 1280;
+// matrix m's elements [4 (lane/16) + j][lane % 16], j = 0..3), then the per-step gate
+// vectors gamma_t, beta_t gamma_t, Gamma[15][t], beta_t (16 floats each; steps past the
+// sequence end as alpha = 1, beta = 0), so that no wave of the backward forms them again.
+constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_G = 1024, R_V = 1280, R_SZ = 1344;
+constexpr int RV_GAM = R_V, RV_BG = R_V + 16, RV_GC = R_V + 32, RV_BET = R_V + 48;
 static_assert(R_SZ == D64_REC, "record size");
 static_assert(C == D64_BLK && D64_CK == 2 * C, "a checkpoint before every other block");
 
@@ -115,6 +118,7 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
         ps[P_BET + n] = b;
         ps[P_GC + n] = pr;
     }
+    rec[R_V + lane] = g == 0 ? gam : g == 1 ? b * gam : g == 2 ? pr : b;
     const float4 bt = *reinterpret_cast<const float4*>(ps + P_BET + 4 * g);
     float Lv[4];
 #pragma unroll
@@ -433,14 +437,15 @@ constexpr int HO_SZ = 7232;
 // [hw][2][16]) and q.F, k.Zt, k.D (to the gate gradients, in the backward scratch)
 constexpr int EP_RQ = 0, EP_RK = 1, EP_QF = 2, EP_ZK = 3, EP_KD = 4;
 constexpr int EP_SZ = NW * 2 * 16;
-// per unit and block in the workspace's backward scratch (D64_BSC floats): what
-// the gate gradients need, written by the helpers, read after the block loop
+// per unit and block in the backward's scratch (GS_SZ floats): what the gate
+// gradients need, written by the helpers with the block's products, read after
+// the block loop
 constexpr int GS_ROW = 0;                    // [hw][3][16]: q.F, k.Zt, k.D row sums per helper
 constexpr int GS_DSS = 192;                  // [hw]: <X, S> per helper
 constexpr int GS_YV = 196;                   // [16]: row sums of Y o V
 constexpr int GS_DM = 256;                   // dM, accumulator layout [lane][4]
 constexpr int GS_DL = 512;                   // dL
-static_assert(GS_DL + 256 == D64_BSC, "backward scratch");
+constexpr int GS_SZ = 768;
 constexpr int WSCR = 2 * C * OTP + 128;      // per wave: two transpose tiles and a vector area
 constexpr int SVO = 2 * C * OTP;             // the vector area's offset
 constexpr int B_STG = 0;
@@ -526,28 +531,33 @@ ASCA_DEV float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + 
 struct BArgs {
     const float *q, *k, *v, *alpha, *beta, *d_o, *u, *ckpt, *rec, *qn, *kn;
     float *gq, *gk, *gv, *ga, *gb;
-    float* bsc;   // the workspace's backward scratch
+    float* gsc;   // scratch of this call: per block the sums of the gate gradients (GS_SZ floats)
     long ldx, ldg, d, ubase, gbase, rowbase;
     int B, T, H, h, nslots, NC, unit;
     int di, ldxi, ldgi;   // d, ldx, ldg as 32-bit strides (the launcher checks they fit)
 };
 
 struct BChainIn {
-    float a, b;       // gates of step 16c + n
     float4 v;         // V[16c + n][16w + 4g ..]
     float4 tr, mr;    // T and M of the block (accumulator layout)
+    float4 gm, bg, gc;  // gamma, beta gamma, Gamma[15][.] of steps 4g .. 4g + 3
+    float g15, bn;    // gamma_15; beta of step n
 };
 
 template <bool AL>
 ASCA_DEV void bchain_load(BChainIn& ci, int c, const BArgs& A, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const int t = min(c * C + n, A.T - 1);
-    ci.a = A.alpha[(unsigned)(t * A.H)];
-    ci.b = A.beta[(unsigned)(t * A.H)];
     ci.v = ld4<AL>(A.v + (unsigned)(t * A.di + 16 * w + 4 * g));
-    const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
+    const float* rb = A.rec + (unsigned)(c * R_SZ);
+    const float4* rq = reinterpret_cast<const float4*>(rb);
     ci.tr = rq[(R_T >> 2) + lane];
     ci.mr = rq[(R_M >> 2) + lane];
+    ci.gm = rq[(RV_GAM >> 2) + g];
+    ci.bg = rq[(RV_BG >> 2) + g];
+    ci.gc = rq[(RV_GC >> 2) + g];
+    ci.g15 = rb[RV_GAM + 15];
+    ci.bn = rb[RV_BET + n];
 }
 
 template <bool AL>
@@ -555,33 +565,23 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
                           float* __restrict__ scr, int c, const BArgs& A, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const bool live = c * C + n < A.T;
-    const float a = live ? ci.a : 1.0f;
-    const float bt = live ? ci.b : 0.0f;
-    const float gam = prefix_prod<16>(a);
-    const float g15 = readlane_f(gam, 15);
-    float4 vec[3];
-    {
-        const float x[3] = {gam, bt * gam, suffix_excl_prod(a)};
-        rows4x<3>(x, vec, scr + SVO, lane);
-    }
-    const float4 gm = vec[0], bg = vec[1], gc = vec[2];
+    const float bt = ci.bn;
+    const float g15 = ci.g15;
+    const float4 gm = ci.gm, bg = ci.bg, gc = ci.gc;
     float4 kc[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) kc[r] = *reinterpret_cast<const float4*>(sb + SB_K + n * RP + 16 * r + 4 * g);
     float dO[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) dO[j] = sb[SB_DO + (4 * g + j) * RP + 16 * w + n];
-    f32x4 k0 = {0.f, 0.f, 0.f, 0.f}, k1 = k0;
+    f32x4 kx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; r += 2)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            k0 = mfma4(el(kc[r], j), X[r][j], k0);
-            k1 = mfma4(el(kc[r + 1], j), X[r + 1][j], k1);
-        }
+        for (int j = 0; j < 4; ++j) kx = mfma4(el(kc[r], j), X[r][j], kx);
     f32x4 dU;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dU[j] = el(gc, j) * (k0[j] + k1[j]);
+    for (int j = 0; j < 4; ++j) dU[j] = el(gc, j) * kx[j];
 #pragma unroll
     for (int j = 0; j < 4; ++j) dU = mfma4(el(ci.mr, j), dO[j], dU);
     f32x4 Y = {0.f, 0.f, 0.f, 0.f};
@@ -631,8 +631,10 @@ ASCA_DEV void bchain_step(f32x4 (&X)[4], const BChainIn& ci, const float* __rest
 
 struct BHelpIn {
     float4 sk[4];        // checkpoint before block c & ~1: S[16hw + n][16c + 4g ..], value tile c
-    float a, b;          // gates of step 16c + n
-    float ap;            // alpha of step 16(c - 1) + n (odd c)
+    float gam, gcn, bt;  // gamma, Gamma[15][.], beta of step 16c + n
+    float4 bb;           // beta of steps 4g .. 4g + 3
+    float4 gq;           // block c - 1 (odd c): Gamma'[15][4i + g], i = 0..3
+    float g15p;          // block c - 1: gamma'_15
     float qn, kn;        // norms of row 16c + n (1 for the raw gradients)
     float4 gr;           // Gamma of the block (accumulator layout)
 };
@@ -644,9 +646,14 @@ ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = sp[(hw * 4 + cc) * 64 + lane];
     const int t = min(c * C + n, A.T - 1);
-    hi.a = A.alpha[(unsigned)(t * A.H)];
-    hi.ap = A.alpha[(unsigned)(max((c - 1) * C + n, 0) * A.H)];  // block c - 1 is whole for odd c
-    hi.b = A.beta[(unsigned)(t * A.H)];
+    const float* rb = A.rec + (unsigned)(c * R_SZ);
+    hi.gam = rb[RV_GAM + n];
+    hi.gcn = rb[RV_GC + n];
+    hi.bt = rb[RV_BET + n];
+    hi.bb = reinterpret_cast<const float4*>(rb)[(RV_BET >> 2) + g];
+    const float* rp = A.rec + (unsigned)(max(c - 1, 0) * R_SZ);  // block c - 1 is whole for odd c
+    hi.gq = make_float4(rp[RV_GC + g], rp[RV_GC + 4 + g], rp[RV_GC + 8 + g], rp[RV_GC + 12 + g]);
+    hi.g15p = rp[RV_GAM + 15];
     if constexpr (FUSED) {
         hi.qn = A.qn[(unsigned)(t * A.H)];
         hi.kn = A.kn[(unsigned)(t * A.H)];
@@ -677,18 +684,8 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
                              const float* __restrict__ sbp, const float* __restrict__ ho, float* __restrict__ ep,
                              float* __restrict__ scr, int c, const BArgs& A, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const bool live = c * C + n < A.T;
-    const float a = live ? hi.a : 1.0f;
-    const float bt = live ? hi.b : 0.0f;
-    const float gam = prefix_prod<16>(a);       // gamma_n
-    const float gcn = suffix_excl_prod(a);      // Gamma[15][n]
-    float4 bb;                                  // beta of rows 4g .. 4g + 3
-    {
-        const float x[1] = {bt};
-        float4 v1[1];
-        rows4x<1>(x, v1, scr + SVO, lane);
-        bb = v1[0];
-    }
+    const float bt = hi.bt, gam = hi.gam, gcn = hi.gcn;
+    const float4 bb = hi.bb;                    // beta of rows 4g .. 4g + 3
     const float G[4] = {hi.gr.x, hi.gr.y, hi.gr.z, hi.gr.w};
     // The forward stores the state before every other block.  An odd block's
     // state follows from the block before (staged in `sbp`, always whole):
@@ -696,13 +693,8 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     // keys (rows) as the transposed tiles of the checkpoint layout.
     float4 sk[4] = {hi.sk[0], hi.sk[1], hi.sk[2], hi.sk[3]};
     if (c & 1) {
-        const float gcp = suffix_excl_prod(hi.ap);  // lane m: Gamma'[15][m]
-        const float g15 = readlane_f(gcp, 0) * readlane_f(hi.ap, 0);
-        float* sv = scr + SVO + 64;
-        if (lane < 16) sv[(n & 3) * 4 + (n >> 2)] = gcp;
-        wave_sync();
-        const float4 gq = *reinterpret_cast<const float4*>(sv + 4 * g);  // Gamma'[15][4i + g], i = 0..3
-        wave_sync();
+        const float g15 = hi.g15p;
+        const float4 gq = hi.gq;  // Gamma'[15][4i + g], i = 0..3
         float kg[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) kg[i] = el(gq, i) * sbp[SB_K + (4 * i + g) * RP + 16 * hw + n];
@@ -790,7 +782,7 @@ ASCA_DEV void bhelp_products(BCarry& cy, const BHelpIn& hi, const float* __restr
     }
 #pragma unroll
     for (int e = 0; e < 5; ++e) rs[e] = add_xor32(add_xor16(rs[e]));
-    float* gs = A.bsc + (unsigned)(c * D64_BSC);
+    float* gs = A.gsc + (unsigned)(c * GS_SZ);
     if (lane < 16) {
         ep[(hw * 2 + EP_RQ) * 16 + n] = rs[EP_RQ];
         ep[(hw * 2 + EP_RK) * 16 + n] = rs[EP_RK];
@@ -843,11 +835,13 @@ ASCA_DEV void bhelp_epilogue(const BCarry& cy, const float* __restrict__ ep, flo
 }
 
 // Gate gradients of block c (dalpha, dbeta and their sigmoid backward), run by
-// one wave from the sums the helpers left in the backward scratch (loaded with
-// the block's record, one block ahead); lane t of each row is step t.
+// one wave from the sums the helpers left in the scratch (loaded with the
+// block's record, one block ahead); lane t of each row is step t.
 struct BGateIn {
     float4 ar, bq, gr;  // K K^T, Q K^T, Gamma of the block (accumulator layout)
-    float a, b;         // gates of step 16c + n
+    float a, b;         // gates of step 16c + n (as loaded, for the sigmoid backward)
+    float gam, bm;      // gamma, beta of step 16c + n (beta 0 past the sequence end)
+    float4 bb;          // beta of steps 4g .. 4g + 3 (0 past the sequence end)
     float4 pm, pl;      // dM, dL (accumulator layout)
     float rw[3][NW];    // the helpers' row sums q.F, k.Zt, k.D of row n
     float ds[NW];       // the helpers' <X, S>
@@ -862,8 +856,12 @@ ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
     const int t = min(c * C + (lane & 15), A.T - 1);
     gi.a = A.alpha[(unsigned)(t * A.H)];
     gi.b = A.beta[(unsigned)(t * A.H)];
-    const float* gs = A.bsc + (unsigned)(c * D64_BSC);
     const int n = lane & 15;
+    const float* rb = A.rec + (unsigned)(c * R_SZ);
+    gi.gam = rb[RV_GAM + n];
+    gi.bm = rb[RV_BET + n];
+    gi.bb = rq[(RV_BET >> 2) + (lane >> 4)];
+    const float* gs = A.gsc + (unsigned)(c * GS_SZ);
     gi.pm = *reinterpret_cast<const float4*>(gs + GS_DM + 4 * lane);
     gi.pl = *reinterpret_cast<const float4*>(gs + GS_DL + 4 * lane);
 #pragma unroll
@@ -876,11 +874,9 @@ ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
 }
 
 template <bool FUSED>
-ASCA_DEV void bgate(const BGateIn& gin, float* __restrict__ scr, int c, const BArgs& A, int lane) {
+ASCA_DEV void bgate(const BGateIn& gi, float* __restrict__ scr, int c, const BArgs& A, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    BGateIn gi = gin;
-    if (c * C + n >= A.T) { gi.a = 1.0f; gi.b = 0.0f; }
-    const float gam = prefix_prod<16>(gi.a);
+    const float gam = gi.gam;
     const float dM[4] = {gi.pm.x, gi.pm.y, gi.pm.z, gi.pm.w};
     const float dL[4] = {gi.pl.x, gi.pl.y, gi.pl.z, gi.pl.w};
     const float G[4] = {gi.gr.x, gi.gr.y, gi.gr.z, gi.gr.w};
@@ -893,13 +889,13 @@ ASCA_DEV void bgate(const BGateIn& gin, float* __restrict__ scr, int c, const BA
         dss += gi.ds[w];
     }
     const float yv = gi.yv;
-    const float dgam = -gi.b * szk + sqf + (n == C - 1 ? dss : 0.0f);
-    float4 vec[2];
+    const float dgam = -gi.bm * szk + sqf + (n == C - 1 ? dss : 0.0f);
+    float4 vec[1];
     {
-        const float x[2] = {dgam, gi.b};
-        rows4x<2>(x, vec, scr + SVO, lane);
+        const float x[1] = {dgam};
+        rows4x<1>(x, vec, scr + SVO, lane);
     }
-    const float4 dg4 = vec[0], bb = vec[1];
+    const float4 dg4 = vec[0], bb = gi.bb;
     // dGamma (strict lower part), row sums of dL o Gamma o A, and the first term of dalpha
     f32x4 dgs, Gv;
     float t1 = 0.0f, rb[4];
@@ -959,10 +955,12 @@ ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
     st.x[3] = *reinterpret_cast<const float4*>(A.u + off);
 }
 
+// WHOLE: the caller knows block c is whole (every block but the last is).
+template <bool WHOLE>
 ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int T, int hw, int lane) {
     const int row = 4 * hw + (lane >> 4);
     float* dst = sb + row * RP + 4 * (lane & 15);
-    if ((c + 1) * C <= T) {  // a whole block (uniform): the loaded registers go straight out
+    if (WHOLE || (c + 1) * C <= T) {  // a whole block (uniform): the loaded registers go straight out
 #pragma unroll
         for (int m = 0; m < 4; ++m) *reinterpret_cast<float4*>(dst + m * SB_MAT) = st.x[m];
     } else {
@@ -974,7 +972,7 @@ ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int 
 }
 
 // After the block loop: the gate gradients of every block, block c on wave
-// c mod 8, from the helpers' sums in the backward scratch.
+// c mod 8, from the helpers' sums in the scratch.
 template <bool FUSED>
 ASCA_DEV void bgate_tail(const BArgs& A, float* __restrict__ scr, int w, int lane) {
     __syncthreads();   // the scratch writes of every wave are visible
@@ -1003,7 +1001,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         if (A.qn) { A.qn += gbase; A.kn += gbase; }
         A.ckpt += (long)A.unit * A.nslots * DH2;
         A.rec += (long)A.unit * A.NC * R_SZ;
-        A.bsc += (long)A.unit * A.NC * D64_BSC;
+        A.gsc += (long)A.unit * A.NC * GS_SZ;
         A.gq += rowbase * A.ldx + (long)A.h * DH; A.gk += rowbase * A.ldx + (long)A.h * DH;
         A.gv += rowbase * A.ldx + (long)A.h * DH;
         A.ga += rowbase * A.ldg + A.h; A.gb += rowbase * A.ldg + A.h;
@@ -1024,7 +1022,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         {
             BStage st0;
             bstage_load<AL>(st0, NC - 1, A, hw, lane);
-            bstage_store(st0, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
+            bstage_store<false>(st0, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
         }
         bhelp_load<FUSED>(hin[1], NC - 1, A, hw, lane);
         bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, hw, lane);
@@ -1067,13 +1065,15 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         // the chain's inputs are loaded two steps ahead into buffer s & 1
         // (static indices: no register copies; X is updated on every path)
         if ((s & 1) == 0) {
-            if (c >= 1) bstage_store(sg[0], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
+            // block c - 1 < NC - 1 is whole (only the last block can be partial)
+            if (c >= 1) bstage_store<true>(sg[0], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                             lane);
             bchain_load<AL>(cb[0], max(c - 2, 0), A, w, lane);
             bstage_load<AL>(sg[0], max(c - 3, 0), A, w, lane);
         } else {
-            if (c >= 1) bstage_store(sg[1], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
+            // block c - 1 < NC - 1 is whole (only the last block can be partial)
+            if (c >= 1) bstage_store<true>(sg[1], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                             lane);
             bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
@@ -1081,7 +1081,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         }
         lds_barrier();
     }
-    // the helpers' last two steps (products of block 0, then nothing)
+    // the helpers' last two steps (products of block 0, then its epilogue)
     lds_barrier();
     lds_barrier();
     bgate_tail<FUSED>(A, scr, w, lane);
@@ -1109,6 +1109,9 @@ static int launch_ut_fwd64_t(const float* q, const float* k, const float* v, con
                        ws.ckpt, ws.rec, B, T, H, ws.nslots);
     return post_launch("ut_fwd64");
 }
+
+// Floats of the backward's gate-sum scratch (ut64::BArgs::gsc).
+inline size_t ut_bwd64_scratch_floats(int units, int NC) { return (size_t)units * NC * ut64::GS_SZ; }
 
 template <bool FUSED, bool AL>
 static int launch_ut_bwd64_t(const ut64::BArgs& a, int units, hipStream_t st) {

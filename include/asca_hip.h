@@ -132,11 +132,16 @@ ASCA_API void asca_rng_normal(uint64_t* state, float* out, size_t n, float scale
 
 /* --------------------------------------------------- delta rule (recurrent) */
 
-/* Bytes of the workspace a delta forward leaves for its backward: the per-step
- * S^T k vector (B*T*H*dh floats) and state checkpoints every C steps
- * (B*H*ceil(T/C)*dh*dh floats; C depends on dh).  It replaces the full state
- * history DeltaDev.states of rust/src/cuda/mod.rs:1274-1275,1386-1397
- * ((T+1)*dh*dh floats per unit).  dh may be 1..128. */
+/* Bytes of the workspace a delta forward leaves for its backward: one dh-vector
+ * per token-head (B*T*H*dh floats: S_{t-1}^T k_t, or at dh = 64 the u_t rows)
+ * and state checkpoints every C steps plus the final state
+ * (B*H*(ceil(T/C)+1)*dh*dh floats; C depends on dh, 32 at dh = 64); at dh = 64
+ * also a record of 1344 floats per 16-step block and unit
+ * (B*H*ceil(T/16)*1344 floats: the block's Gram products, triangular factors and
+ * gate vectors).  It replaces the full state history DeltaDev.states of
+ * rust/src/cuda/mod.rs:1274-1275,1386-1397 ((T+1)*dh*dh floats per unit).
+ * dh may be 1..128.  The forward writes the workspace and the backwards only
+ * read it, so several backwards may use one forward's workspace at once. */
 ASCA_API int asca_delta_ws_bytes(int B, int T, int H, int dh, size_t* bytes);
 
 /* Forward recurrence of the gated delta rule for all (sequence, head) units,
@@ -148,7 +153,8 @@ ASCA_API int asca_delta_ws_bytes(int B, int T, int H, int dh, size_t* bytes);
  *   q, k, v : (B*T, H*dh), q and k already L2-normalised per head
  *   alpha, beta : (B*T, H)
  *   o : (B*T, H*dh) output
- *   ws : asca_delta_ws_bytes(B,T,H,dh) bytes, kept for asca_delta_bwd_*  */
+ *   ws : asca_delta_ws_bytes(B,T,H,dh) bytes, kept for asca_delta_bwd_* (which
+ *        read it and never write it) */
 ASCA_API int asca_delta_fwd(const float* q, const float* k, const float* v,
                             const float* alpha, const float* beta, float* o, void* ws,
                             int B, int T, int H, int dh, void* stream);

@@ -88,26 +88,25 @@ def test_workspace_bytes_layout():
     _lib.call("asca_delta_ws_bytes", 32, 512, 8, 64, C.byref(out))
     sk = 32 * 512 * 8 * 64 * 4
     # dh = 64 on a block per unit (the blocked form): the u rows, a checkpoint
-    # before every other 16-step block plus the state after the last step, a
-    # 1280-float record per block (K K^T, Q K^T, T, M, Gamma) and 768 floats of
-    # backward scratch per block
+    # before every other 16-step block plus the state after the last step, and a
+    # 1344-float record per block (K K^T, Q K^T, T, M, Gamma, the gate vectors);
+    # the backward writes nothing into it
     ckpt = 32 * 8 * (512 // 32 + 1) * 64 * 64 * 4
-    rec = 32 * 8 * (512 // 16) * (1280 + 768) * 4
+    rec = 32 * 8 * (512 // 16) * 1344 * 4
     assert out.value == sk + ckpt + rec
-    # at most 128 (sequence, head) units: each unit's columns run on two blocks,
-    # and the workspace adds the two blocks' partial dq, dk and dalpha, dbeta
+    # at most 128 (sequence, head) units: each unit's columns run on two blocks;
+    # their partial dq, dk and dalpha, dbeta live in the backward call's own
+    # scratch, not in the forward's workspace
     _lib.call("asca_delta_ws_bytes", 4, 128, 4, 32, C.byref(out))
     base = 4 * 128 * 4 * 32 * 4 + 4 * 4 * (128 // 8 + 1) * 32 * 32 * 4
-    part_x = 2 * 2 * 4 * 128 * 4 * 32 * 4
-    part_g = 2 * 4 * 128 * 2 * 4 * 4
-    assert out.value == base + part_x + part_g
+    assert out.value == base
     # dh = 64 runs a block per unit at any unit count (configs[3]'s 128 units too)
     _lib.call("asca_delta_ws_bytes", 16, 1024, 8, 64, C.byref(out))
     assert out.value == (16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 32 + 1) * 64 * 64 * 4
-                         + 16 * 8 * (1024 // 16) * (1280 + 768) * 4)
+                         + 16 * 8 * (1024 // 16) * 1344 * 4)
     _lib.call("asca_delta_ws_bytes", 1, 40, 2, 64, C.byref(out))
     assert out.value == (256 * ((1 * 40 * 2 * 64 * 4 + 255) // 256) + 2 * (40 // 32 + 2) * 64 * 64 * 4
-                         + 256 * ((2 * 3 * 1280 * 4 + 255) // 256) + 256 * ((2 * 3 * 768 * 4 + 255) // 256))
+                         + 256 * ((2 * 3 * 1344 * 4 + 255) // 256))
     with pytest.raises(_lib.AscaError) as ei:
         _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))
     assert ei.value.code == 3
