@@ -131,13 +131,17 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
     *reinterpret_cast<float4*>(scr + n * 16 + 4 * g) = make_float4(Lv[0], Lv[1], Lv[2], Lv[3]);
     // row n of T = (I + L)^-1 from x^T (I + L) = e_n^T, columns from the last:
     // x_j = [j == n] - sum_{m > j} x_m L[m][j]
+    // Right-looking: once x_m is final it is taken out of every x_j, j < m (the
+    // terms of each x_j in descending m), so x_j is one FMA behind x_{j+1}
+    // instead of at the end of a chain of 15 - j, with 16 live partial sums.
     float x[C];
 #pragma unroll
-    for (int j = C - 1; j >= 0; --j) {
-        float acc = n == j ? 1.f : 0.f;
+    for (int j = 0; j < C; ++j) x[j] = n == j ? 1.f : 0.f;
 #pragma unroll
-        for (int m = j + 1; m < C; ++m) acc -= x[m] * scr[j * 16 + m];
-        x[j] = acc;
+    for (int m = C - 1; m >= 1; --m) {
+#pragma unroll
+        for (int j = 0; j < m; ++j) x[j] -= x[m] * scr[j * 16 + m];
+        __builtin_amdgcn_sched_barrier(0);   // keep the solve's steps in order (bounds the live registers)
     }
     if (g == 0) {
 #pragma unroll
