@@ -51,13 +51,34 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def _run(cmd: list[str], verbose: bool) -> None:
+def _run(cmd: list[str], verbose: bool, quiet_fail: bool = False) -> bool:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
+        if quiet_fail:
+            return False
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed with status {res.returncode}: {cmd[-1]}")
+    return True
+
+
+def _compile(src: Path, obj: str, inc: list[str], verbose: bool) -> None:
+    """Compile one source with the common flags plus its own.  If its own flags
+    make the compiler fail (the iterative-ILP scheduler is an experimental LLVM
+    setting that has crashed its register allocator on some code), compile it
+    again with the common flags alone and say so: the library is then slower
+    but built."""
+    extra = EXTRA_FLAGS.get(src.name, [])
+    cmd = [hipcc(), *HIP_FLAGS, *extra, *inc, "-c", "-o", obj, str(src)]
+    if not extra:
+        _run(cmd, verbose)
+        return
+    if _run(cmd, verbose, quiet_fail=True):
+        return
+    sys.stderr.write(f"asca_amd.build: {src.name} failed to compile with {' '.join(extra)}; "
+                     "compiling it with the common flags only\n")
+    _run([hipcc(), *HIP_FLAGS, *inc, "-c", "-o", obj, str(src)], verbose)
 
 
 def build(verbose: bool = False) -> Path:
@@ -69,14 +90,11 @@ def build(verbose: bool = False) -> Path:
     inc = ["-I", str(HERE.parent / "include")]
     tmp = LIB.with_suffix(".so.tmp")
     with tempfile.TemporaryDirectory(prefix="asca_build_") as td:
-        jobs = []
-        for src in sources():
-            obj = str(Path(td) / (src.stem + ".o"))
-            jobs.append((obj, [hipcc(), *HIP_FLAGS, *EXTRA_FLAGS.get(src.name, []), *inc, "-c", "-o", obj, str(src)]))
+        jobs = [(src, str(Path(td) / (src.stem + ".o"))) for src in sources()]
         workers = max(1, min(len(jobs), os.cpu_count() or 1, 16))
         with ThreadPoolExecutor(max_workers=workers) as ex:
-            list(ex.map(lambda j: _run(j[1], verbose), jobs))
-        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", str(tmp), *[o for o, _ in jobs]], verbose)
+            list(ex.map(lambda j: _compile(j[0], j[1], inc, verbose), jobs))
+        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", str(tmp), *[o for _, o in jobs]], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -1354,12 +1354,16 @@ int gemm_run(int trans_a, int trans_b, int M, int N, int K, float alpha, const f
 }
 
 // Scratch of asca_gemm_noalloc, the entry point for callers that cannot
-// allocate: a static device array of SCRATCH_FLOATS floats (64 MiB), which
-// every device the library runs on holds until the process ends.  In host code
-// `scratch` names a host-side stand-in, never the device memory: its device
-// address comes from hipGetSymbolAddress, once per device at asca_init (with
-// that device current), and only that address is used.
-constexpr size_t SCRATCH_FLOATS = (size_t)16 << 20;
+// allocate: a static device array of SCRATCH_FLOATS floats (32 MiB), which
+// every device the library runs on holds until the process ends.  Its size is
+// the most split-K partials can take on gfx950 (256 CUs): gemm_splits keeps
+// splits * tiles <= 2 * CUs and a tile covers at most GM_BM x GM_BN outputs,
+// so splits * M * N <= 2 * 256 * GM_BM * GM_BN floats; the size check in
+// asca_gemm_noalloc stays as a guard.  In host code `scratch` names a
+// host-side stand-in, never the device memory: its device address comes from
+// hipGetSymbolAddress, once per device at asca_init (with that device
+// current), and only that address is used.
+constexpr size_t SCRATCH_FLOATS = (size_t)2 * 256 * GM_BM * GM_BN;
 static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
 static float* g_scratch_dev[64] = {};
 

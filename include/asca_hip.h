@@ -325,9 +325,11 @@ ASCA_API int asca_gemm_ws_bytes(int trans_a, int trans_b, int M, int N, int K, s
 /* asca_gemm that allocates nothing, for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No reference counterpart.  The split-K partials live in a
- * static 64 MiB device array that every device the library runs on holds
- * until the process ends; a product whose partials need more is refused with
- * ASCA_ERR_INVALID (asca_gemm_ws takes any size).  The partials are written in
+ * static 32 MiB device array that every device the library runs on holds
+ * until the process ends: the most the split-K partials of any product take
+ * on gfx950 (2 * 256 CUs output tiles of 128 x 128 floats), so every product
+ * fits; a larger need would be refused with ASCA_ERR_INVALID (asca_gemm_ws
+ * takes any size).  The partials are written in
  * full before they are read (nothing needs clearing), and the results are the
  * bits of asca_gemm.  All calls on one device share the array: calls that
  * overlap on one device (concurrent streams or threads) race. */

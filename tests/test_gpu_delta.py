@@ -278,3 +278,56 @@ def test_blocked_dh64_unaligned_pointers(orc, g):
     assert errs[0] <= FWD_TOL and max(errs[1:]) <= GRAD_TOL, errs
     for b in [*bufs, al, be, ws, o, *outs]:
         b.free()
+
+
+@pytest.mark.parametrize("shift", ["inputs", "output"])
+def test_blocked_dh64_fused_unaligned(orc, g, shift):
+    # The fused backward (the drop-in for Gpu::delta_bwd_dev, rust/src/cuda/mod.rs:1328-1382)
+    # on rows off a 16-byte boundary: q, k, v, dO one float past it ("inputs"), or
+    # the d_qkv output one float past it ("output").  Either sends the call to the
+    # unaligned fused instantiation, which must give the aligned path's parity.
+    # (d_qkv's row stride is 3*H*dh floats, a multiple of 4 at dh = 64 for every H,
+    # so an unaligned stride cannot reach this path through the C ABI.)
+    import ctypes as C
+    from asca_amd import _lib
+    from asca_amd.gpu import DevBuf, _vp
+
+    B, T, H, dh = 9, 37, 4, 64
+    x = orc.DeltaInputs(43, B, T, H, dh)
+    o_ref, dq, dk, dv, da, db = orc.delta_fwd_bwd(x.q, x.k, x.v, x.alpha, x.beta, x.d_o, B, T, H, dh)
+    d_qkv_ref, d_gate_ref = orc.delta_fuse(x.q, x.k, x.qn, x.kn, x.alpha, x.beta, dq, dk, dv, da, db, H, dh)
+    rows, d = B * T, H * dh
+    off = 1 if shift == "inputs" else 0
+
+    def placed(a, k):
+        buf = DevBuf((a.size + k) * 4)
+        buf.upload(np.concatenate([np.zeros(k, np.float32), a.ravel()]))
+        return buf, buf.ptr + 4 * k
+
+    bufs, ptr = [], {}
+    for name in ("q", "k", "v", "d_o"):
+        bf, p = placed(getattr(x, name), off)
+        bufs.append(bf)
+        ptr[name] = p
+    small = {name: DevBuf.from_host(getattr(x, name)) for name in ("alpha", "beta", "qn", "kn")}
+    wsb = C.c_size_t()
+    _lib.call("asca_delta_ws_bytes", B, T, H, dh, C.byref(wsb))
+    ws = DevBuf(wsb.value)
+    o = DevBuf(rows * d * 4)
+    k_out = 1 if shift == "output" else 0
+    dqkv = DevBuf((rows * 3 * d + k_out) * 4)
+    dgate = DevBuf(rows * 2 * H * 4)
+    _lib.call("asca_delta_fwd", _vp(ptr["q"]), _vp(ptr["k"]), _vp(ptr["v"]), _vp(small["alpha"]),
+              _vp(small["beta"]), _vp(o), _vp(ws), B, T, H, dh, None)
+    _lib.call("asca_delta_bwd_fused", _vp(ptr["q"]), _vp(ptr["k"]), _vp(ptr["v"]), _vp(small["alpha"]),
+              _vp(small["beta"]), _vp(small["qn"]), _vp(small["kn"]), _vp(ptr["d_o"]), _vp(ws),
+              _vp(dqkv.ptr + 4 * k_out), _vp(dgate), B, T, H, dh, None)
+    _lib.call("asca_sync")
+    got_qkv = dqkv.to_host((rows * 3 * d + k_out,))[k_out:].reshape(rows, 3 * d)
+    errs = {"o": orc.rel_err(o.to_host((rows, d)), o_ref),
+            "d_qkv": orc.rel_err(got_qkv, d_qkv_ref),
+            "d_gate": orc.rel_err(dgate.to_host((rows, 2 * H)), d_gate_ref)}
+    print(f"[delta parity] dh64 fused unaligned ({shift}) rel errors {errs}", flush=True)
+    assert errs["o"] <= FWD_TOL and errs["d_qkv"] <= GRAD_TOL and errs["d_gate"] <= GRAD_TOL, errs
+    for b in [*bufs, *small.values(), ws, o, dqkv, dgate]:
+        b.free()

@@ -293,3 +293,44 @@ def test_train_step_failure_leaves_parameters_untouched(where):
         np.testing.assert_array_equal(x, y)
     a.close()
     b.close()
+
+
+def test_device_batch_parity():
+    """rust/tests/batch_parity.rs:20-133 on the device: one training step on a
+    batch of 4 sequences of 12 tokens equals the mean of four single-sequence
+    steps (loss within 1e-5, every gradient within 2e-4 relative, the
+    reference's bars), with Config::tiny (rust/src/model.rs:32-41) and the
+    reference's seeds (Rng(5) for ids and targets below 256, Rng(9) for the
+    parameters)."""
+    import ctypes as C
+    from asca_amd import _lib
+
+    cfg, batch, seq = (256, 64, 4, 2, 8, 128), 4, 12
+    dm, _ = _models(cfg, 9)
+    st = (C.c_uint64 * 2)()
+    lib = _lib.load()
+    lib.asca_rng_seed(5, st)
+    raw = np.empty(2 * batch * seq, np.uint64)
+    lib.asca_rng_u64(st, raw.ctypes.data_as(C.POINTER(C.c_uint64)), raw.size)
+    ids = (raw[:batch * seq] % np.uint64(256)).astype(np.uint32)
+    tgts = (raw[batch * seq:] % np.uint64(256)).astype(np.uint32)
+    loss1, acc = 0.0, None
+    for b in range(batch):
+        s = slice(b * seq, (b + 1) * seq)
+        loss1 += dm.forward_backward(ids[s], tgts[s], 1)
+        gr = [g.astype(np.float64) for g in dm.grads()]
+        acc = gr if acc is None else [a + g for a, g in zip(acc, gr)]
+    loss1 /= batch
+    g1 = [(a / batch).astype(np.float32) for a in acc]
+    lossb = dm.forward_backward(ids, tgts, batch)
+    gb = dm.grads()
+    rel = abs(loss1 - lossb) / max(abs(loss1), abs(lossb), 1e-6)
+    worst = 0.0
+    for name, a, b in zip(mo.tensor_names(cfg[3]), g1, gb):
+        err = np.max(np.abs(a - b)) / max(np.max(np.abs(a)), 1e-9)
+        worst = max(worst, err)
+        assert err <= 2e-4, (name, err)
+    print(f"[model] device batch parity: loss batch=1 {loss1:.6f} batch=4 {lossb:.6f} (rel {rel:.2e}), "
+          f"worst grad rel {worst:.2e}", flush=True)
+    assert rel <= 1e-5
+    dm.close()
