@@ -87,6 +87,19 @@ ASCA_DEV float wave_sum(float x) {
 
 ASCA_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Raw buffer resource over `bytes` bytes at p: buffer stores whose offset is
+// not below `bytes` are dropped by the hardware, so a store to a row past a
+// sequence's end needs no exec-mask branch (which would split the scheduling
+// region of the code around it).  Offsets are 32-bit byte offsets.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int RSRC_WORD3 = 0x00020000;   // raw 32-bit data, gfx9 (CDNA) encoding
+ASCA_DEV Rsrc make_rsrc(const void* p, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, RSRC_WORD3);
+}
+ASCA_DEV void buf_store1(Rsrc r, unsigned off, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)off, 0, 0);
+}
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
 // outstanding global load and store of the wave (s_waitcnt vmcnt(0)), which
 // turns a prefetch issued before it into a stall; kernels whose waves share

@@ -458,6 +458,7 @@ constexpr int B_EP = B_HO + 2 * HO_SZ;
 constexpr int B_SCR = B_EP + 2 * EP_SZ;
 constexpr int B_END = B_SCR + 2 * NW * WSCR;
 constexpr size_t B_LDS = (size_t)B_END * 4;
+static_assert(2 * NW * 4 * WSCR <= B_END, "the gate tail's scratch fits in the loop's LDS");
 static_assert(B_LDS <= 160 * 1024 && B_HO % 4 == 0 && B_EP % 4 == 0 && B_SCR % 4 == 0, "backward LDS");
 
 // Orders the wave's own LDS writes before its reads of other lanes' values.  The
@@ -877,68 +878,100 @@ ASCA_DEV void bgate_load(BGateIn& gi, int c, const BArgs& A, int lane) {
     gi.yv = gs[GS_YV + n];
 }
 
-template <bool FUSED>
-ASCA_DEV void bgate(const BGateIn& gi, float* __restrict__ scr, int c, const BArgs& A, int lane) {
+// The gate gradients of NB blocks at once (block cs[i] from gin[i]): every
+// phase runs over all NB blocks before the next, so their dependency chains
+// interleave and the LDS transposes share their wave syncs.  scr holds NB
+// areas of WSCR floats.  Blocks past the sequence end (clamped loads) store
+// nothing: their rows lie outside the resources' range.
+template <bool FUSED, int NB>
+ASCA_DEV void bgate_batch(const BGateIn (&gin)[NB], const int (&cs)[NB], float* __restrict__ scr,
+                          const BArgs& A, Rsrc rga, Rsrc rgb, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const float gam = gi.gam;
-    const float dM[4] = {gi.pm.x, gi.pm.y, gi.pm.z, gi.pm.w};
-    const float dL[4] = {gi.pl.x, gi.pl.y, gi.pl.z, gi.pl.w};
-    const float G[4] = {gi.gr.x, gi.gr.y, gi.gr.z, gi.gr.w};
-    float szk = 0.f, sqf = 0.f, skd = 0.f, dss = 0.f;
+    float szk[NB], dgam[NB];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        sqf += gi.rw[0][w];
-        szk += gi.rw[1][w];
-        skd += gi.rw[2][w];
-        dss += gi.ds[w];
+    for (int i = 0; i < NB; ++i) {
+        const BGateIn& gi = gin[i];
+        float sqf = 0.f, dss = 0.f;
+        szk[i] = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            sqf += gi.rw[0][w];
+            szk[i] += gi.rw[1][w];
+            dss += gi.ds[w];
+        }
+        dgam[i] = -gi.bm * szk[i] + sqf + (n == C - 1 ? dss : 0.0f);
+        scr[i * WSCR + SVO + 16 * g + n] = dgam[i];   // every lane: row n of copy g
     }
-    const float yv = gi.yv;
-    const float dgam = -gi.bm * szk + sqf + (n == C - 1 ? dss : 0.0f);
-    float4 vec[1];
-    {
-        const float x[1] = {dgam};
-        rows4x<1>(x, vec, scr + SVO, lane);
-    }
-    const float4 dg4 = vec[0], bb = gi.bb;
-    // dGamma (strict lower part), row sums of dL o Gamma o A, and the first term of dalpha
-    f32x4 dgs, Gv;
-    float t1 = 0.0f, rb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int t = 4 * g + j;
-        rb[j] = rowsum16(dL[j] * G[j] * el(gi.ar, j));
-        dgs[j] = n < t ? dM[j] * el(gi.bq, j) + dL[j] * el(bb, j) * el(gi.ar, j) + (t == C - 1 ? skd : 0.0f)
-                       : 0.0f;
-        Gv[j] = G[j];
-        t1 += G[j] * el(dg4, j);
-    }
-    t1 = add_xor32(add_xor16(t1));
-    // second term: R = dGs Gamma'^T with Gamma'[m][i] = Gamma[m-1][i] (the row above,
-    // zero for m = 0) on the matrix cores, then sum_t Gamma[t][m] R[t][m]
-    float4 dgst, gt;
-    tile_t2(dgs, Gv, dgst, gt, scr, lane);   // dGs[n][4g ..], Gamma[n][4g ..]
-    const float gp[4] = {dpp_or<0x111>(0.0f, gt.x), dpp_or<0x111>(0.0f, gt.y), dpp_or<0x111>(0.0f, gt.z),
-                         dpp_or<0x111>(0.0f, gt.w)};   // Gamma[n-1][4g ..]
-    f32x4 R = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) R = mfma4(el(dgst, j), gp[j], R);
-    float t2 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) t2 += G[j] * R[j];
-    t2 = add_xor32(add_xor16(t2));
-    const float gprev = dpp_or<0x111>(1.0f, gam);   // gamma_{n-1}
-    const float dal = gprev * t1 + t2;
-    // dbeta of step n: Y.V - gamma Z'.K + sum_l dL Gamma A
-    float* sv = scr + SVO;
-    if (n == 0) *reinterpret_cast<float4*>(sv + 4 * g) = make_float4(rb[0], rb[1], rb[2], rb[3]);
     wave_sync();
-    const float rbn = sv[n];
+    float4 dg4[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) dg4[i] = *reinterpret_cast<const float4*>(scr + i * WSCR + SVO + 4 * g);
     wave_sync();
-    const float dbe = yv - gam * szk + rbn;
-    if (lane < 16 && c * C + n < A.T) {
-        const unsigned r = (unsigned)((c * C + n) * A.ldgi);
-        A.ga[r] = FUSED ? dal * gi.a * (1.0f - gi.a) : dal;
-        A.gb[r] = FUSED ? dbe * gi.b * (1.0f - gi.b) : dbe;
+    // dGamma (strict lower part), row sums of dL o Gamma o A, the first term of dalpha
+    f32x4 dgs[NB];
+    float t1[NB], rb[NB][4];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const BGateIn& gi = gin[i];
+        float skd = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) skd += gi.rw[2][w];
+        t1[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * g + j;
+            const float dL = el(gi.pl, j), G = el(gi.gr, j);
+            rb[i][j] = rowsum16(dL * G * el(gi.ar, j));
+            dgs[i][j] = n < t ? el(gi.pm, j) * el(gi.bq, j) + dL * el(gi.bb, j) * el(gi.ar, j) +
+                                    (t == C - 1 ? skd : 0.0f)
+                              : 0.0f;
+            t1[i] += G * el(dg4[i], j);
+        }
+        t1[i] = add_xor32(add_xor16(t1[i]));
+    }
+    // R = dGs Gamma'^T with Gamma'[m][i] = Gamma[m-1][i] (the row above, zero for
+    // m = 0) on the matrix cores, then sum_t Gamma[t][m] R[t][m]
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        float* st = scr + i * WSCR;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            st[(4 * g + j) * OTP + n] = dgs[i][j];
+            st[C * OTP + (4 * g + j) * OTP + n] = el(gin[i].gr, j);
+        }
+        *reinterpret_cast<float4*>(st + SVO + 64 + 4 * g) = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+    }
+    wave_sync();
+    float dal[NB], dbe[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const float* st = scr + i * WSCR;
+        const float4 dgst = *reinterpret_cast<const float4*>(st + n * OTP + 4 * g);       // dGs[n][4g ..]
+        const float4 gt = *reinterpret_cast<const float4*>(st + C * OTP + n * OTP + 4 * g);  // Gamma[n][4g ..]
+        const float gp[4] = {dpp_or<0x111>(0.0f, gt.x), dpp_or<0x111>(0.0f, gt.y), dpp_or<0x111>(0.0f, gt.z),
+                             dpp_or<0x111>(0.0f, gt.w)};   // Gamma[n-1][4g ..]
+        f32x4 R = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) R = mfma4(el(dgst, j), gp[j], R);
+        float t2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t2 += el(gin[i].gr, j) * R[j];
+        t2 = add_xor32(add_xor16(t2));
+        const float gprev = dpp_or<0x111>(1.0f, gin[i].gam);   // gamma_{n-1}
+        dal[i] = gprev * t1[i] + t2;
+        // dbeta of step n: Y.V - gamma Z'.K + sum_l dL Gamma A (row n's sum from lane (n/4, .))
+        const float rbn = st[SVO + 64 + n];
+        dbe[i] = gin[i].yv - gin[i].gam * szk[i] + rbn;
+    }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        // every lane stores (the four lanes of row n hold the same values); rows
+        // past the sequence end fall outside the resources and are dropped
+        const unsigned r = 4u * (unsigned)((cs[i] * C + n) * A.ldgi);
+        const float a = gin[i].a, b = gin[i].b;
+        buf_store1(rga, r, FUSED ? dal[i] * a * (1.0f - a) : dal[i]);
+        buf_store1(rgb, r, FUSED ? dbe[i] * b * (1.0f - b) : dbe[i]);
     }
 }
 
@@ -976,16 +1009,25 @@ ASCA_DEV void bstage_store(const BStage& st, int c, float* __restrict__ sb, int 
 }
 
 // After the block loop: the gate gradients of every block, block c on wave
-// c mod 8, from the helpers' sums in the scratch.
+// c mod 8, four blocks of a wave at a time; the loop's LDS is free by then
+// (the block's final barrier) and gives each wave four scratch areas.
 template <bool FUSED>
-ASCA_DEV void bgate_tail(const BArgs& A, float* __restrict__ scr, int w, int lane) {
-    __syncthreads();   // the scratch writes of every wave are visible
-    BGateIn gin;
-    if (w < A.NC) bgate_load(gin, w, A, lane);
-    for (int c = w; c < A.NC; c += 2 * NW) {
-        BGateIn cur = gin;
-        if (c + 2 * NW < A.NC) bgate_load(gin, c + 2 * NW, A, lane);
-        bgate<FUSED>(cur, scr, c, A, lane);
+ASCA_DEV void bgate_tail(const BArgs& A, float* __restrict__ lds, int w, int lane) {
+    constexpr int NB = 4;
+    __syncthreads();   // the scratch writes of every wave are visible, the loop's LDS is free
+    float* scr = lds + w * NB * WSCR;
+    // the unit's rows of dalpha, dbeta: row t at t * ldg
+    const unsigned gbytes = 4u * (unsigned)((A.T - 1) * A.ldgi + 1);
+    const Rsrc rga = make_rsrc(A.ga, gbytes), rgb = make_rsrc(A.gb, gbytes);
+    for (int c0 = w; c0 < A.NC; c0 += 2 * NW * NB) {
+        BGateIn gin[NB];
+        int cs[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            cs[i] = c0 + 2 * NW * i;                 // past NC: rows beyond T, stores dropped
+            bgate_load(gin[i], min(cs[i], A.NC - 1), A, lane);
+        }
+        bgate_batch<FUSED, NB>(gin, cs, scr, A, rga, rgb, lane);
     }
 }
 
@@ -1049,7 +1091,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         }
         bhelp_epilogue<FUSED, AL>(cy, lds + B_EP, scr, 0, A, hw, lane);
         lds_barrier();
-        bgate_tail<FUSED>(A, scr, w, lane);
+        bgate_tail<FUSED>(A, lds, w, lane);
         return;
     }
     // chain: step s runs block NC - 1 - s and stages rows 4w .. 4w + 3 of the
@@ -1088,7 +1130,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     // the helpers' last two steps (products of block 0, then its epilogue)
     lds_barrier();
     lds_barrier();
-    bgate_tail<FUSED>(A, scr, w, lane);
+    bgate_tail<FUSED>(A, lds, w, lane);
 }
 
 }  // namespace ut64
