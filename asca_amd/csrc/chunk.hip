@@ -1853,14 +1853,9 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
     const long us = (long)d.NC * d.DD;
     if (d.dh == SC_D) {
         constexpr size_t lds = (size_t)(SC_D + 64) * SC_LD * sizeof(float);
-        static bool attr[2] = {false, false};
         const void* fn = tr ? reinterpret_cast<const void*>(&ck_scan_k<true>)
                             : reinterpret_cast<const void*>(&ck_scan_k<false>);
-        if (!attr[tr]) {
-            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-            attr[tr] = true;
-        }
+        if (int arc = allow_lds(fn, lds)) return arc;
         int rc = pre_launch("chunk_scan");
         if (rc) return rc;
         if (tr)
@@ -1886,13 +1881,7 @@ static int scan(bool tr, const ChunkDims& d, const float* Gp, const float* R, fl
 // The factorised forward state scan of the fused C = 64, dh = 128 path.
 static int scan2(const ChunkDims& d, const ChunkWs& w, const uint16_t* k, hipStream_t st) {
     constexpr size_t lds = (size_t)S2_LDS_F * sizeof(float);
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_scan2_k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&ck_scan2_k), lds)) return arc;
     int rc = pre_launch("chunk_scan2");
     if (rc) return rc;
     hipLaunchKernelGGL(ck_scan2_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, k, d.T, d.H, w.S, d.NC);
@@ -1953,13 +1942,7 @@ int asca_chunk_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     if (C == FP_C && dh == FP_D) {
         // one fused kernel for every state-independent part of every chunk
         constexpr size_t lds = (size_t)FP_LDS_F * sizeof(float);
-        static bool attr = false;
-        if (!attr) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_fwd_prep_k),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-            attr = true;
-        }
+        if (int arc = allow_lds(reinterpret_cast<const void*>(&ck_fwd_prep_k), lds)) return arc;
         rc = pre_launch("chunk_fwd_prep");
         if (rc) return rc;
         hipLaunchKernelGGL(ck_fwd_prep_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, alpha, beta, T, H,
@@ -2026,26 +2009,14 @@ int asca_chunk_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
         // E, the reverse scan, then one fused kernel for all per-chunk gradients
         {
             constexpr size_t lds = (size_t)S3_LDS_F * sizeof(float);
-            static bool attr = false;
-            if (!attr) {
-                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_scan2_bwd_k),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-                attr = true;
-            }
+            if (int arc = allow_lds(reinterpret_cast<const void*>(&ck_scan2_bwd_k), lds)) return arc;
             if ((rc = pre_launch("chunk_scan2_bwd"))) return rc;
             hipLaunchKernelGGL(ck_scan2_bwd_k, dim3((unsigned)(2 * d.U)), dim3(FP_NT), lds, st, w, k, d_o, T, H,
                                d.NC);
             if ((rc = post_launch("chunk_scan2_bwd"))) return rc;
         }
         constexpr size_t lds = (size_t)FB_LDS_F * sizeof(float);
-        static bool attr = false;
-        if (!attr) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ck_bwd_fused_k),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-            attr = true;
-        }
+        if (int arc = allow_lds(reinterpret_cast<const void*>(&ck_bwd_fused_k), lds)) return arc;
         if ((rc = pre_launch("chunk_bwd_fused"))) return rc;
         hipLaunchKernelGGL(ck_bwd_fused_k, dim3((unsigned)d.N), dim3(FP_NT), lds, st, q, k, v, d_o, T, H, d.NC, w,
                            dq, dk, dv, dalpha, dbeta);

@@ -1185,14 +1185,8 @@ static int launch_bwd_cs(const float* q, const float* k, const float* v, const f
                          const float* d_o, const DeltaWs& ws, const float* qn, const float* kn, float* gq, float* gk,
                          float* gv, long ldx, float* ga, float* gb, long ldg, int B, int T, int H, int dh,
                          hipStream_t st) {
-    static bool attr = false;
     const size_t lds = BS<DH, CS>::LDS;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&delta_bwd_k<DH, CS, EXACT, FUSED>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu): %s", lds, hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&delta_bwd_k<DH, CS, EXACT, FUSED>), lds)) return arc;
     int rc = pre_launch("delta_bwd");
     if (rc) return rc;
     // the column halves' partials: scratch of this call on its stream

@@ -880,13 +880,7 @@ static int launch_gemm_t(const GemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds =
         DMA ? (size_t)DMA_STAGES * dma_stage_bytes<WN>()
             : 2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 16 * TNW * WN>()) * sizeof(float);
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN, TNW, DMA>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&gemm_k<TA, TB, EPI, VEC, WM, WN, TNW, DMA>), lds)) return arc;
     hipLaunchKernelGGL((gemm_k<TA, TB, EPI, VEC, WM, WN, TNW, DMA>), grid, dim3(64 * WM * WN), lds, st, a);
     return ASCA_OK;
 }
@@ -905,13 +899,7 @@ template <bool TA, bool TB, int WM, int WN>
 static int launch_batched_t(const GemmArgs& a, long items, hipStream_t st) {
     constexpr size_t lds =
         2 * (size_t)(tile_floats<!TA, 64 * WM>() + tile_floats<TB, 64 * WN>()) * sizeof(float);
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_batched_k<TA, TB, WM, WN>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&gemm_batched_k<TA, TB, WM, WN>), lds)) return arc;
     // two resident blocks per CU, each walking items with a grid stride
     const long cap = 2L * (cu_count() > 0 ? cu_count() : 256);
     const unsigned grid = (unsigned)(items < cap ? items : cap);

@@ -22,6 +22,11 @@ int pre_launch(const char* kernel);
 // Map the HIP status of the launch just made to an error code.
 int post_launch(const char* kernel);
 
+// Allow kernel `fn` `bytes` of dynamic LDS on the library's device.  Set once
+// per (kernel, device) and remembered under a lock, so concurrent first calls
+// from several host threads and a later asca_init on another device each set it.
+int allow_lds(const void* fn, size_t bytes);
+
 // Convert an opaque stream handle from the C ABI.
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -73,6 +73,24 @@ int pre_launch(const char* kernel) {
     return ASCA_OK;
 }
 
+static std::mutex g_attr_mu;
+static std::unordered_map<const void*, std::vector<size_t>> g_attr;  // per kernel: bytes set, by device
+
+int allow_lds(const void* fn, size_t bytes) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    const int dev = g_device;
+    std::lock_guard<std::mutex> lk(g_attr_mu);
+    std::vector<size_t>& set = g_attr[fn];
+    if ((int)set.size() <= dev) set.resize(dev + 1, 0);
+    if (set[dev] >= bytes) return ASCA_OK;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess)
+        return fail(ASCA_ERR_HIP, "hipFuncSetAttribute(LDS %zu) on device %d: %s", bytes, dev, hipGetErrorString(e));
+    set[dev] = bytes;
+    return ASCA_OK;
+}
+
 // The stream-ordered pool behind StreamScratch: the library's own (created at
 // asca_init), so that its release threshold (keep what is freed for reuse
 // instead of returning it to the driver at every synchronisation) does not

@@ -1142,13 +1142,7 @@ static int launch_ut_fwd64_t(const float* q, const float* k, const float* v, con
                              float* o, const DeltaWs& ws, int B, int T, int H, hipStream_t st) {
     const int units = B * H;
     const size_t lds = ut64::F_LDS;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ut64::ut_fwd64_k<AL>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)ut64::F_LDS);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&ut64::ut_fwd64_k<AL>), ut64::F_LDS)) return arc;
     int rc = pre_launch("ut_fwd64");
     if (rc) return rc;
     hipLaunchKernelGGL(ut64::ut_fwd64_k<AL>, dim3(units), dim3(2 * ut64::NT), lds, st, q, k, v, alpha, beta, o, ws.sk,
@@ -1161,13 +1155,7 @@ inline size_t ut_bwd64_scratch_floats(int units, int NC) { return (size_t)units 
 
 template <bool FUSED, bool AL>
 static int launch_ut_bwd64_t(const ut64::BArgs& a, int units, hipStream_t st) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ut64::ut_bwd64_k<FUSED, AL>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)ut64::B_LDS);
-        if (e != hipSuccess) return fail(ASCA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int arc = allow_lds(reinterpret_cast<const void*>(&ut64::ut_bwd64_k<FUSED, AL>), ut64::B_LDS)) return arc;
     int rc = pre_launch("ut_bwd64");
     if (rc) return rc;
     hipLaunchKernelGGL((ut64::ut_bwd64_k<FUSED, AL>), dim3(units), dim3(2 * ut64::NT), ut64::B_LDS, st, a);
