@@ -762,9 +762,6 @@ ASCA_DEV void st_nt4(float* p, float4 v) {
     __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(p));
 }
 
-// 64 x 128 bf16 rows of one chunk -> LDS f32 [t][f] (stride FP_LK) and, if
-// gdst is set, the unit-major f32 copy; rows past T are zero.  tid counts from
-// 0 over the nthr threads taking part.
 // 4 bf16 of chunk row t at column f, 0 for rows past the sequence (t >=
 // valid, valid >= 1).  The load itself is unconditional (row clamped): a load
 // under a branch is waited for inside the branch, which serialises the loads.
@@ -778,44 +775,27 @@ ASCA_DEV float4 bf4_f32(uint2 r) {
                        __uint_as_float(r.y & 0xffff0000u));
 }
 
-// The chunk's 64 rows x 128 bf16 (rows past the sequence as 0) into LDS as
-// f32 [64][FP_LK], by NTHR threads: all of a thread's loads are issued before
-// the first is used.
-template <int NTHR>
-ASCA_DEV void fp_load_rows(const uint16_t* __restrict__ src, float* lds, long rowbase, long rowstride, int valid_rows,
-                           int tid) {
-    constexpr int NE = FP_C * FP_D / 4, NPER = (NE + NTHR - 1) / NTHR;
-    uint2 r[NPER];
+// A chunk's rows held as bf16 in registers (the zero rows past T included), by
+// all FP_NT threads, so that a tensor needed in LDS twice, or later than it is
+// loaded, is read from HBM once and early.
+struct FpRows {
+    uint2 r[FP_C * FP_D / 4 / FP_NT];
+};
+
+ASCA_DEV void fp_rows_ld(FpRows& x, const uint16_t* __restrict__ src, long rowbase, long rowstride, int valid_rows,
+                         int tid) {
 #pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-        const int e = min(tid + i * NTHR, NE - 1);
-        r[i] = ld_row4(src, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
-    }
-#pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-        const int e = tid + i * NTHR;
-        if (NE % NTHR == 0 || e < NE) *reinterpret_cast<float4*>(lds + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r[i]);
+    for (int i = 0; i < (int)(sizeof(x.r) / sizeof(x.r[0])); ++i) {
+        const int e = tid + i * FP_NT;
+        x.r[i] = ld_row4(src, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
     }
 }
 
-// Two such tensors, with all loads of both in flight together.
-template <int NTHR>
-ASCA_DEV void fp_load_rows2(const uint16_t* __restrict__ s0, float* l0, const uint16_t* __restrict__ s1, float* l1,
-                            long rowbase, long rowstride, int valid_rows, int tid) {
-    constexpr int NE = FP_C * FP_D / 4, NPER = (NE + NTHR - 1) / NTHR;
-    static_assert(NE % NTHR == 0, "whole passes");
-    uint2 r0[NPER], r1[NPER];
+ASCA_DEV void fp_rows_st(const FpRows& x, float* lds, int tid) {
 #pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-        const int e = tid + i * NTHR;
-        r0[i] = ld_row4(s0, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
-        r1[i] = ld_row4(s1, rowbase, rowstride, e >> 5, valid_rows, 4 * (e & 31));
-    }
-#pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-        const int e = tid + i * NTHR;
-        *reinterpret_cast<float4*>(l0 + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r0[i]);
-        *reinterpret_cast<float4*>(l1 + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(r1[i]);
+    for (int i = 0; i < (int)(sizeof(x.r) / sizeof(x.r[0])); ++i) {
+        const int e = tid + i * FP_NT;
+        *reinterpret_cast<float4*>(lds + (e >> 5) * FP_LK + 4 * (e & 31)) = bf4_f32(x.r[i]);
     }
 }
 
@@ -867,8 +847,14 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     const long rowstride = (long)H * FP_D;
     const long cd = n * FP_C * FP_D, cc = n * FP_C * FP_C, dd = n * FP_D * FP_D;
 
-    // gates (padding steps are identities), K and Q
-    fp_load_rows2<FP_NT>(k, Ks, q, X, rowbase, rowstride, valid, tid);
+    // gates (padding steps are identities), K and Q into LDS; Q and V stay in
+    // registers for later (every row load of the kernel is in flight here)
+    FpRows kr, qr, vr;
+    fp_rows_ld(kr, k, rowbase, rowstride, valid, tid);
+    fp_rows_ld(qr, q, rowbase, rowstride, valid, tid);
+    fp_rows_ld(vr, v, rowbase, rowstride, valid, tid);
+    fp_rows_st(kr, Ks, tid);
+    fp_rows_st(qr, X, tid);
     if (tid < FP_C) {
         const bool in = tid < valid;
         const long gi = ((long)b * T + t0 + min(tid, valid - 1)) * H + h;
@@ -951,9 +937,9 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
     __syncthreads();
     // T = (I + L)^-1 into Ts.  First wave: the four 16 x 16 diagonal blocks,
     // lane = (block, column), the column in registers, right-looking forward
-    // substitution.  The other waves zero the blocks above the diagonal and
-    // bring V in where Q was.  (Kt = Gamma[C-1, :] K is not stored: the fused
-    // backward forms it from K and Gamma[C-1, :].)
+    // substitution.  The other waves zero the blocks above the diagonal; then
+    // V (in registers since the start) goes where Q was.  (Kt = Gamma[C-1, :] K
+    // is not stored: the fused backward forms it from K and Gamma[C-1, :].)
     if (wv == 0) {
         const int o = 16 * l4, m = li;
         float d[16];
@@ -972,8 +958,8 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
             const int bj = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
             Ts[(16 * bi + ((e >> 4) & 15)) * FP_LC + 16 * bj + (e & 15)] = 0.0f;
         }
-        fp_load_rows<FP_NT - 64>(v, X, rowbase, rowstride, valid, t2);
     }
+    fp_rows_st(vr, X, tid);   // Q's reads are done (the barrier before this phase)
     __syncthreads();
     // the blocks below the diagonal, one block diagonal at a time
     if (wv < 3) fp_tri_block(Ls, Ts, wv + 1, wv, lane);
@@ -1021,7 +1007,7 @@ __global__ __launch_bounds__(FP_NT) void ck_fwd_prep_k(const uint16_t* __restric
                     Y[t * FP_LK + f] = acc[x][y][r];
                     st_nt(w.W + cd + t * FP_D + f, acc[x][y][r]);
                 }
-        fp_load_rows<FP_NT>(q, X, rowbase, rowstride, valid, tid);
+        fp_rows_st(qr, X, tid);
     }
     __syncthreads();
     // Qp = diag(gamma) Q - M W
