@@ -69,7 +69,8 @@ ASCA_DEV void cross_step_sum(const float (&y)[CK], float* __restrict__ red_ab, i
 
 // dh = 64: the blocked (UT) form on the matrix cores (delta_ut64.hip), used for
 // every dh = 64 shape with one block per unit (ws.cs == 1).  Its workspace: the
-// u rows in `sk`, the state before every other D64_BLK-step block (every
+// u rows in `sk` (per unit and D64_BLK-step block, as the forward's wave tiles,
+// T rounded up to whole blocks), the state before every other block (every
 // D64_CK steps) and the final state in `ckpt`, per block a record of D64_REC
 // floats in `rec`, all written by the forward and read by the backward.  Any
 // pointer alignment.

@@ -1111,7 +1111,9 @@ static DeltaWs ws_layout(int B, int T, int H, int dh, void* base) {
     w.cs = col_split(B, H, dh, dhc);
     w.ck = blocked64(dh, w.cs) ? D64_CK : ck_for(dhc);
     w.nslots = (T + w.ck - 1) / w.ck + 1;   // the state before every chunk, then the final state
-    const size_t sk_bytes = align256((size_t)B * T * H * dh * sizeof(float));
+    // the blocked form keeps the u rows per unit and 16-step block (ut64_kernels.h, U_TILE)
+    const size_t sk_rows = blocked64(dh, w.cs) ? (size_t)(T + D64_BLK - 1) / D64_BLK * D64_BLK : (size_t)T;
+    const size_t sk_bytes = align256((size_t)B * sk_rows * H * dh * sizeof(float));
     const size_t ck_bytes = align256((size_t)B * H * w.nslots * dh * dh * sizeof(float));
     const size_t rec_bytes =
         blocked64(dh, w.cs) ? align256((size_t)B * H * ((T + D64_BLK - 1) / D64_BLK) * D64_REC * sizeof(float)) : 0;

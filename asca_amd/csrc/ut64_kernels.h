@@ -84,6 +84,11 @@ struct PrepIn {
 // vectors gamma_t, beta_t gamma_t, Gamma[15][t], beta_t (16 floats each; steps past the
 // sequence end as alpha = 1, beta = 0), so that no wave of the backward forms them again.
 constexpr int R_A = 0, R_BQ = 256, R_T = 512, R_M = 768, R_G = 1024, R_V = 1280, R_SZ = 1344;
+// U_TILE: the u rows for the backward, per unit and block (U_BLK floats): the
+// four chain waves' 16 x 16 tiles (value columns 16w ..) one after another,
+// each row-major, so a wave writes its block's u as one contiguous 1 KB.
+constexpr int U_BLK = 4 * 256;
+static_assert(U_BLK == D64_BLK * DH, "a block's u rows");
 constexpr int RV_GAM = R_V, RV_BG = R_V + 16, RV_GC = R_V + 32, RV_BET = R_V + 48;
 static_assert(R_SZ == D64_REC, "record size");
 static_assert(C == D64_BLK && D64_CK == 2 * C, "a checkpoint before every other block");
@@ -289,8 +294,9 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
             float* po = o + ubase + t * d + 16 * w + cc;
             if constexpr (AL) *reinterpret_cast<float4*>(po) = o4;
             else { po[0] = o4.x; po[1] = o4.y; po[2] = o4.z; po[3] = o4.w; }
-            *reinterpret_cast<float4*>(ws_u + ubase + t * d + 16 * w + cc) = u4;
         }
+        // u tile: 1 KB contiguous per wave and block (layout at U_TILE)
+        *reinterpret_cast<float4*>(ws_u + (long)c * U_BLK + w * 256 + rr * 16 + cc) = u4;
     }
     float Ut[4];
 #pragma unroll
@@ -377,6 +383,7 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
 
     float* ot = lds + F_OT + w * 3 * C * OTP;
     float* ckb = ckpt + (long)unit * nslots * DH2;
+    ws_u += (long)unit * NC * U_BLK;
     f32x4 S[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) S[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -989,7 +996,11 @@ ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
     st.x[0] = ld4<AL>(A.k + off);
     st.x[1] = ld4<AL>(A.q + off);
     st.x[2] = ld4<AL>(A.d_o + off);
-    st.x[3] = *reinterpret_cast<const float4*>(A.u + off);
+    // u in the forward's tile layout: block t / 16, tile of columns 16 (j / 4),
+    // row t % 16, columns 4 (j % 4) .. (j = lane % 16)
+    const int j = lane & 15;
+    st.x[3] = *reinterpret_cast<const float4*>(A.u + (unsigned)((t >> 4) * U_BLK + (j >> 2) * 256 + (t & 15) * 16 +
+                                                                4 * (j & 3)));
 }
 
 // WHOLE: the caller knows block c is whole (every block but the last is).
@@ -1042,7 +1053,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         const long gbase = (long)b * A.T * A.H + A.h;
         const long rowbase = (long)b * A.T;
         // every pointer rebased on the unit: the per-block offsets are 32-bit
-        A.q += ubase; A.k += ubase; A.v += ubase; A.d_o += ubase; A.u += ubase;
+        A.q += ubase; A.k += ubase; A.v += ubase; A.d_o += ubase; A.u += (long)A.unit * A.NC * U_BLK;
         A.alpha += gbase; A.beta += gbase;
         if (A.qn) { A.qn += gbase; A.kn += gbase; }
         A.ckpt += (long)A.unit * A.nslots * DH2;

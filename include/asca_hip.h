@@ -133,8 +133,8 @@ ASCA_API void asca_rng_normal(uint64_t* state, float* out, size_t n, float scale
 /* --------------------------------------------------- delta rule (recurrent) */
 
 /* Bytes of the workspace a delta forward leaves for its backward: one dh-vector
- * per token-head (B*T*H*dh floats: S_{t-1}^T k_t, or at dh = 64 the u_t rows)
- * and state checkpoints every C steps plus the final state
+ * per token-head (B*T*H*dh floats: S_{t-1}^T k_t; at dh = 64 the u_t rows, with
+ * T rounded up to a multiple of 16) and state checkpoints every C steps plus the final state
  * (B*H*(ceil(T/C)+1)*dh*dh floats; C depends on dh, 32 at dh = 64); at dh = 64
  * also a record of 1344 floats per 16-step block and unit
  * (B*H*ceil(T/16)*1344 floats: the block's Gram products, triangular factors and

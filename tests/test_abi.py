@@ -87,10 +87,11 @@ def test_workspace_bytes_layout():
     out = C.c_size_t()
     _lib.call("asca_delta_ws_bytes", 32, 512, 8, 64, C.byref(out))
     sk = 32 * 512 * 8 * 64 * 4
-    # dh = 64 on a block per unit (the blocked form): the u rows, a checkpoint
-    # before every other 16-step block plus the state after the last step, and a
-    # 1344-float record per block (K K^T, Q K^T, T, M, Gamma, the gate vectors);
-    # the backward writes nothing into it
+    # dh = 64 on a block per unit (the blocked form): the u rows (per unit and
+    # 16-step block, T rounded up to whole blocks), a checkpoint before every
+    # other 16-step block plus the state after the last step, and a 1344-float
+    # record per block (K K^T, Q K^T, T, M, Gamma, the gate vectors); the
+    # backward writes nothing into it
     ckpt = 32 * 8 * (512 // 32 + 1) * 64 * 64 * 4
     rec = 32 * 8 * (512 // 16) * 1344 * 4
     assert out.value == sk + ckpt + rec
@@ -105,7 +106,7 @@ def test_workspace_bytes_layout():
     assert out.value == (16 * 1024 * 8 * 64 * 4 + 16 * 8 * (1024 // 32 + 1) * 64 * 64 * 4
                          + 16 * 8 * (1024 // 16) * 1344 * 4)
     _lib.call("asca_delta_ws_bytes", 1, 40, 2, 64, C.byref(out))
-    assert out.value == (256 * ((1 * 40 * 2 * 64 * 4 + 255) // 256) + 2 * (40 // 32 + 2) * 64 * 64 * 4
+    assert out.value == (256 * ((1 * 48 * 2 * 64 * 4 + 255) // 256) + 2 * (40 // 32 + 2) * 64 * 64 * 4
                          + 256 * ((2 * 3 * 1344 * 4 + 255) // 256))
     with pytest.raises(_lib.AscaError) as ei:
         _lib.call("asca_delta_ws_bytes", 1, 1, 1, 129, C.byref(out))
