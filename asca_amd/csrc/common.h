@@ -99,6 +99,17 @@ ASCA_DEV Rsrc make_rsrc(const void* p, unsigned bytes) {
 ASCA_DEV void buf_store1(Rsrc r, unsigned off, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)off, 0, 0);
 }
+// Buffer loads at byte offset voff + soff (soff uniform: an SGPR, so a loop's
+// per-lane offset is computed once and a block's offset costs no VALU); past
+// the resource's size they return 0.
+ASCA_DEV float buf_load1(Rsrc r, unsigned voff, unsigned soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+ASCA_DEV float4 buf_load4(Rsrc r, unsigned voff, unsigned soff) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+}
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
 // outstanding global load and store of the wave (s_waitcnt vmcnt(0)), which

@@ -29,10 +29,11 @@ int launch_ut_bwd64(bool fused, const float* q, const float* k, const float* v, 
                     ut_aligned16(gk) && ut_aligned16(gv) && (ldx * 4) % 16 == 0;
     const int units = B * H;
     a.B = B; a.unit = 0; a.h = 0; a.ubase = 0; a.gbase = 0; a.rowbase = 0;
-    // element offsets within a unit are 32-bit, and the bounds-checked stores
-    // take 32-bit byte offsets: 4 T ldx and 4 T ldg must fit in 32 bits
+    // element offsets within a unit are 32-bit, and the buffer resources over a
+    // unit's rows, checkpoints and records take 32-bit byte sizes and offsets
     if ((long)T * (ldx > a.d ? ldx : a.d) >= (1L << 30) || (long)T * ldg >= (1L << 30) ||
-        (long)((T + ut64::C - 1) / ut64::C + 1) * ut64::DH2 >= (1L << 31))
+        (long)((T + ut64::C - 1) / ut64::C + 1) * ut64::DH2 >= (1L << 30) ||
+        (long)((T + ut64::C - 1) / ut64::C) * ut64::R_SZ >= (1L << 30))
         return fail(ASCA_ERR_UNSUPPORTED, "ut_bwd64: one sequence's rows exceed 32-bit byte offsets");
     a.di = (int)a.d; a.ldxi = (int)ldx; a.ldgi = (int)ldg;
     // the gate sums: scratch of this call on its stream (the forward's workspace is only read)

@@ -549,6 +549,30 @@ struct BArgs {
     int di, ldxi, ldgi;   // d, ldx, ldg as 32-bit strides (the launcher checks they fit)
 };
 
+// Buffer resources over the unit's part of every array the block loops read,
+// made once per kernel (after the unit rebase): a load's lane offset is then
+// loop-invariant and the block's offset a uniform register.  Rows past the
+// sequence end lie outside the row resources and load as 0.
+struct BRes {
+    Rsrc ck, rec, nq, nk, v, k, q, dO, u;
+};
+
+ASCA_DEV BRes bres_make(const BArgs& A) {
+    BRes r;
+    r.ck = make_rsrc(A.ckpt, 4u * (unsigned)(A.nslots * DH2));
+    r.rec = make_rsrc(A.rec, 4u * (unsigned)(A.NC * R_SZ));
+    const unsigned rows = 4u * (unsigned)((A.T - 1) * A.di + DH);   // the unit's columns of rows t < T
+    r.v = make_rsrc(A.v, rows);
+    r.k = make_rsrc(A.k, rows);
+    r.q = make_rsrc(A.q, rows);
+    r.dO = make_rsrc(A.d_o, rows);
+    r.u = make_rsrc(A.u, 4u * (unsigned)(A.NC * U_BLK));
+    const unsigned nrm = 4u * (unsigned)((A.T - 1) * A.H + 1);
+    r.nq = make_rsrc(A.qn ? A.qn : A.rec, A.qn ? nrm : 0u);
+    r.nk = make_rsrc(A.kn ? A.kn : A.rec, A.kn ? nrm : 0u);
+    return r;
+}
+
 struct BChainIn {
     float4 v;         // V[16c + n][16w + 4g ..]
     float4 tr, mr;    // T and M of the block (accumulator layout)
@@ -557,19 +581,23 @@ struct BChainIn {
 };
 
 template <bool AL>
-ASCA_DEV void bchain_load(BChainIn& ci, int c, const BArgs& A, int w, int lane) {
+ASCA_DEV void bchain_load(BChainIn& ci, int c, const BArgs& A, const BRes& R, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const int t = min(c * C + n, A.T - 1);
-    ci.v = ld4<AL>(A.v + (unsigned)(t * A.di + 16 * w + 4 * g));
-    const float* rb = A.rec + (unsigned)(c * R_SZ);
-    const float4* rq = reinterpret_cast<const float4*>(rb);
-    ci.tr = rq[(R_T >> 2) + lane];
-    ci.mr = rq[(R_M >> 2) + lane];
-    ci.gm = rq[(RV_GAM >> 2) + g];
-    ci.bg = rq[(RV_BG >> 2) + g];
-    ci.gc = rq[(RV_GC >> 2) + g];
-    ci.g15 = rb[RV_GAM + 15];
-    ci.bn = rb[RV_BET + n];
+    if constexpr (AL) {
+        // v of rows past the sequence end: 0 (outside the resource; their dv is not stored)
+        ci.v = buf_load4(R.v, 4u * (unsigned)(n * A.di + 16 * w + 4 * g), 4u * (unsigned)(c * C * A.di));
+    } else {
+        const int t = min(c * C + n, A.T - 1);
+        ci.v = ld4<AL>(A.v + (unsigned)(t * A.di + 16 * w + 4 * g));
+    }
+    const unsigned sb = 4u * (unsigned)(c * R_SZ);
+    ci.tr = buf_load4(R.rec, 16u * ((R_T >> 2) + lane), sb);
+    ci.mr = buf_load4(R.rec, 16u * ((R_M >> 2) + lane), sb);
+    ci.gm = buf_load4(R.rec, 16u * ((RV_GAM >> 2) + g), sb);
+    ci.bg = buf_load4(R.rec, 16u * ((RV_BG >> 2) + g), sb);
+    ci.gc = buf_load4(R.rec, 16u * ((RV_GC >> 2) + g), sb);
+    ci.g15 = buf_load1(R.rec, 4u * (RV_GAM + 15), sb);
+    ci.bn = buf_load1(R.rec, 4u * (RV_BET + n), sb);
 }
 
 template <bool AL>
@@ -652,29 +680,30 @@ struct BHelpIn {
 };
 
 template <bool FUSED>
-ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, int hw, int lane) {
+ASCA_DEV void bhelp_load(BHelpIn& hi, int c, const BArgs& A, const BRes& R, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
-    const float4* sp = reinterpret_cast<const float4*>(A.ckpt + (unsigned)((c >> 1) * DH2));
+    const unsigned sc = 4u * (unsigned)((c >> 1) * DH2);
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = sp[(hw * 4 + cc) * 64 + lane];
-    const int t = min(c * C + n, A.T - 1);
-    const float* rb = A.rec + (unsigned)(c * R_SZ);
-    hi.gam = rb[RV_GAM + n];
-    hi.gcn = rb[RV_GC + n];
-    hi.bt = rb[RV_BET + n];
-    hi.bb = reinterpret_cast<const float4*>(rb)[(RV_BET >> 2) + g];
-    const float* rp = A.rec + (unsigned)(max(c - 1, 0) * R_SZ);  // block c - 1 is whole for odd c
-    hi.gq = make_float4(rp[RV_GC + g], rp[RV_GC + 4 + g], rp[RV_GC + 8 + g], rp[RV_GC + 12 + g]);
-    hi.g15p = rp[RV_GAM + 15];
+    for (int cc = 0; cc < 4; ++cc) hi.sk[cc] = buf_load4(R.ck, 16u * ((hw * 4 + cc) * 64 + lane), sc);
+    const unsigned sb = 4u * (unsigned)(c * R_SZ);
+    hi.gam = buf_load1(R.rec, 4u * (RV_GAM + n), sb);
+    hi.gcn = buf_load1(R.rec, 4u * (RV_GC + n), sb);
+    hi.bt = buf_load1(R.rec, 4u * (RV_BET + n), sb);
+    hi.bb = buf_load4(R.rec, 16u * ((RV_BET >> 2) + g), sb);
+    const unsigned sp = 4u * (unsigned)(max(c - 1, 0) * R_SZ);  // block c - 1 is whole for odd c
+    hi.gq = make_float4(buf_load1(R.rec, 4u * (RV_GC + g), sp), buf_load1(R.rec, 4u * (RV_GC + 4 + g), sp),
+                        buf_load1(R.rec, 4u * (RV_GC + 8 + g), sp), buf_load1(R.rec, 4u * (RV_GC + 12 + g), sp));
+    hi.g15p = buf_load1(R.rec, 4u * (RV_GAM + 15), sp);
     if constexpr (FUSED) {
-        hi.qn = A.qn[(unsigned)(t * A.H)];
-        hi.kn = A.kn[(unsigned)(t * A.H)];
+        // rows past the sequence end read row T - 1 (their norms must stay finite)
+        const unsigned t = (unsigned)min(c * C + n, A.T - 1);
+        hi.qn = buf_load1(R.nq, 4u * t * (unsigned)A.H, 0u);
+        hi.kn = buf_load1(R.nk, 4u * t * (unsigned)A.H, 0u);
     } else {
         hi.qn = 1.0f;
         hi.kn = 1.0f;
     }
-    const float4* rq = reinterpret_cast<const float4*>(A.rec + (unsigned)(c * R_SZ));
-    hi.gr = rq[(R_G >> 2) + lane];
+    hi.gr = buf_load4(R.rec, 16u * ((R_G >> 2) + lane), sb);
 }
 
 ASCA_DEV float rowsum16(float x) { return group_sum<16>(x); }
@@ -990,15 +1019,24 @@ struct BStage {
 };
 
 template <bool AL>
-ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, int hw, int lane) {
-    const int t = min(c * C + 4 * hw + (lane >> 4), A.T - 1);
+ASCA_DEV void bstage_load(BStage& st, int c, const BArgs& A, const BRes& R, int hw, int lane) {
+    const int j = lane & 15, r = 4 * hw + (lane >> 4);   // row c C + r of the block, columns 4 j ..
+    if constexpr (AL) {
+        // rows past the sequence end load as 0 (outside the row resources)
+        const unsigned vo = 4u * (unsigned)(r * A.di + 4 * j), so = 4u * (unsigned)(c * C * A.di);
+        st.x[0] = buf_load4(R.k, vo, so);
+        st.x[1] = buf_load4(R.q, vo, so);
+        st.x[2] = buf_load4(R.dO, vo, so);
+        // u in the forward's tile layout: tile of columns 16 (j / 4), row r, columns 4 (j % 4) ..
+        st.x[3] = buf_load4(R.u, 4u * (unsigned)((j >> 2) * 256 + r * 16 + 4 * (j & 3)), 4u * (unsigned)(c * U_BLK));
+        return;
+    }
+    const int t = min(c * C + r, A.T - 1);
     const unsigned off = (unsigned)(t * A.di + 4 * (lane & 15));
     st.x[0] = ld4<AL>(A.k + off);
     st.x[1] = ld4<AL>(A.q + off);
     st.x[2] = ld4<AL>(A.d_o + off);
-    // u in the forward's tile layout: block t / 16, tile of columns 16 (j / 4),
-    // row t % 16, columns 4 (j % 4) .. (j = lane % 16)
-    const int j = lane & 15;
+    // u (the workspace: aligned) as above, from row t % 16 of block t / 16
     st.x[3] = *reinterpret_cast<const float4*>(A.u + (unsigned)((t >> 4) * U_BLK + (j >> 2) * 256 + (t & 15) * 16 +
                                                                 4 * (j & 3)));
 }
@@ -1066,6 +1104,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     }
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int NC = A.NC;
+    const BRes R = bres_make(A);
     float* scr = lds + B_SCR + w * WSCR;
     if (w >= NW) {
         // helper: step s runs the epilogue of block NC + 1 - s and the products
@@ -1078,11 +1117,11 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         BCarry cy;
         {
             BStage st0;
-            bstage_load<AL>(st0, NC - 1, A, hw, lane);
+            bstage_load<AL>(st0, NC - 1, A, R, hw, lane);
             bstage_store<false>(st0, NC - 1, lds + B_STG + ((NC - 1) % NSB) * SB_BUF, A.T, hw, lane);
         }
-        bhelp_load<FUSED>(hin[1], NC - 1, A, hw, lane);
-        bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, hw, lane);
+        bhelp_load<FUSED>(hin[1], NC - 1, A, R, hw, lane);
+        bhelp_load<FUSED>(hin[0], max(NC - 2, 0), A, R, hw, lane);
         lds_barrier();
         lds_barrier();  // step 0: the chain's first block
         // steps 1 .. NC: the products of block cp = NC - s on every path (the
@@ -1093,7 +1132,7 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
             if (s >= 2) bhelp_epilogue<FUSED, AL>(cy, lds + B_EP + ((cp + 1) & 1) * EP_SZ, scr, cp + 1, A, hw, lane);
             bhelp_products(cy, hb, lds + B_STG + (cp % NSB) * SB_BUF, lds + B_STG + ((cp + NSB - 1) % NSB) * SB_BUF,
                            lds + B_HO + (cp & 1) * HO_SZ, lds + B_EP + (cp & 1) * EP_SZ, scr, cp, A, hw, lane);
-            bhelp_load<FUSED>(hb, max(cp - 2, 0), A, hw, lane);
+            bhelp_load<FUSED>(hb, max(cp - 2, 0), A, R, hw, lane);
             lds_barrier();
         };
         for (int s = 1; s <= NC; s += 2) {
@@ -1112,10 +1151,10 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
     for (int r = 0; r < 4; ++r) X[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     BChainIn cb[2];
     BStage sg[2];
-    bchain_load<AL>(cb[0], NC - 1, A, w, lane);
-    bchain_load<AL>(cb[1], max(NC - 2, 0), A, w, lane);
-    bstage_load<AL>(sg[0], max(NC - 2, 0), A, w, lane);
-    bstage_load<AL>(sg[1], max(NC - 3, 0), A, w, lane);
+    bchain_load<AL>(cb[0], NC - 1, A, R, w, lane);
+    bchain_load<AL>(cb[1], max(NC - 2, 0), A, R, w, lane);
+    bstage_load<AL>(sg[0], max(NC - 2, 0), A, R, w, lane);
+    bstage_load<AL>(sg[1], max(NC - 3, 0), A, R, w, lane);
     lds_barrier();
     for (int s = 0; s < NC; ++s) {
         const int c = NC - 1 - s;
@@ -1126,15 +1165,15 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
             if (c >= 1) bstage_store<true>(sg[0], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             bchain_step<AL>(X, cb[0], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                             lane);
-            bchain_load<AL>(cb[0], max(c - 2, 0), A, w, lane);
-            bstage_load<AL>(sg[0], max(c - 3, 0), A, w, lane);
+            bchain_load<AL>(cb[0], max(c - 2, 0), A, R, w, lane);
+            bstage_load<AL>(sg[0], max(c - 3, 0), A, R, w, lane);
         } else {
             // block c - 1 < NC - 1 is whole (only the last block can be partial)
             if (c >= 1) bstage_store<true>(sg[1], c - 1, lds + B_STG + ((c - 1) % NSB) * SB_BUF, A.T, w, lane);
             bchain_step<AL>(X, cb[1], lds + B_STG + (c % NSB) * SB_BUF, lds + B_HO + (c & 1) * HO_SZ, scr, c, A, w,
                             lane);
-            bchain_load<AL>(cb[1], max(c - 2, 0), A, w, lane);
-            bstage_load<AL>(sg[1], max(c - 3, 0), A, w, lane);
+            bchain_load<AL>(cb[1], max(c - 2, 0), A, R, w, lane);
+            bstage_load<AL>(sg[1], max(c - 3, 0), A, R, w, lane);
         }
         lds_barrier();
     }
