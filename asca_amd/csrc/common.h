@@ -96,8 +96,14 @@ constexpr int RSRC_WORD3 = 0x00020000;   // raw 32-bit data, gfx9 (CDNA) encodin
 ASCA_DEV Rsrc make_rsrc(const void* p, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, RSRC_WORD3);
 }
-ASCA_DEV void buf_store1(Rsrc r, unsigned off, float x) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)off, 0, 0);
+ASCA_DEV void buf_store1(Rsrc r, unsigned off, float x, unsigned soff = 0) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)off, (int)soff, 0);
+}
+// 16 bytes at byte offset off + soff (the whole store is dropped past the resource's size)
+ASCA_DEV void buf_store4(Rsrc r, unsigned off, float4 x, unsigned soff = 0) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, (int)soff, 0);
 }
 // Buffer loads at byte offset voff + soff (soff uniform: an SGPR, so a loop's
 // per-lane offset is computed once and a block's offset costs no VALU); past

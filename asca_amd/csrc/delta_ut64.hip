@@ -9,6 +9,12 @@ namespace asca {
 int launch_ut_fwd64(const float* q, const float* k, const float* v, const float* alpha, const float* beta, float* o,
                     const DeltaWs& ws, int B, int T, int H, hipStream_t st) {
     if (ws.ck != D64_CK || ws.cs != 1) return fail(ASCA_ERR_INVALID, "ut_fwd64: workspace layout mismatch");
+    // the buffer resources over a unit's rows, gates, u tiles, checkpoints and
+    // records take 32-bit byte sizes and offsets
+    const long NC = (T + ut64::C - 1) / ut64::C;
+    if ((long)T * H * ut64::DH >= (1L << 30) || (long)T * H >= (1L << 30) || (NC + 1) * ut64::DH2 >= (1L << 30) ||
+        NC * ut64::R_SZ >= (1L << 30))
+        return fail(ASCA_ERR_UNSUPPORTED, "ut_fwd64: one sequence's rows exceed 32-bit byte offsets");
     return ut_aligned16(q) && ut_aligned16(k) && ut_aligned16(v) && ut_aligned16(o)
                ? launch_ut_fwd64_t<true>(q, k, v, alpha, beta, o, ws, B, T, H, st)
                : launch_ut_fwd64_t<false>(q, k, v, alpha, beta, o, ws, B, T, H, st);

@@ -70,6 +70,15 @@ constexpr int NSLOT = 8;    // two groups of four blocks
 constexpr int F_SCR = NSLOT * P_SZ;      // per wave: L^T scratch [16][16]
 constexpr int F_FLOATS = F_SCR + NW * 256;
 
+// Buffer resources over the unit's part of every array the forward reads or
+// writes, made once per kernel: a load's or store's lane offset is then
+// loop-invariant and the block's offset a uniform register.  Rows past the
+// sequence end lie outside the row resources: they load as 0 (their gates make
+// such steps inert) and their stores are dropped.
+struct FRes {
+    Rsrc q, k, v, o, al, be, u, ck, rec;
+};
+
 struct PrepIn {
     float4 kr[4], qr[4];  // K, Q rows n = lane % 16: columns 16r + 4(lane/16) .. +3
     float a, b;           // alpha, beta of step n (as loaded)
@@ -94,7 +103,8 @@ static_assert(R_SZ == D64_REC, "record size");
 static_assert(C == D64_BLK && D64_CK == 2 * C, "a checkpoint before every other block");
 
 ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ ps, float* __restrict__ scr,
-                           float* __restrict__ rec, int lane) {
+                           Rsrc rrec, int lane) {
+    const unsigned srec = 4u * (unsigned)(p * R_SZ);   // the block's record
     const int n = lane & 15, g = lane >> 4;
     const bool live = p * C + n < T;
     const float a = live ? pi.a : 1.0f;
@@ -123,7 +133,7 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
         ps[P_BET + n] = b;
         ps[P_GC + n] = pr;
     }
-    rec[R_V + lane] = g == 0 ? gam : g == 1 ? b * gam : g == 2 ? pr : b;
+    buf_store1(rrec, 4u * (R_V + lane), g == 0 ? gam : g == 1 ? b * gam : g == 2 ? pr : b, srec);
     const float4 bt = *reinterpret_cast<const float4*>(ps + P_BET + 4 * g);
     float Lv[4];
 #pragma unroll
@@ -154,15 +164,16 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
             *reinterpret_cast<float4*>(ps + P_T + n * 16 + 4 * q4) =
                 make_float4(x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]);
     }
-    float4* rq = reinterpret_cast<float4*>(rec);
-    rq[(R_A >> 2) + lane] = make_float4(A[0], A[1], A[2], A[3]);
-    rq[(R_BQ >> 2) + lane] = make_float4(Bq[0], Bq[1], Bq[2], Bq[3]);
+    buf_store4(rrec, 16u * ((R_A >> 2) + lane), make_float4(A[0], A[1], A[2], A[3]), srec);
+    buf_store4(rrec, 16u * ((R_BQ >> 2) + lane), make_float4(Bq[0], Bq[1], Bq[2], Bq[3]), srec);
     const float* tp = ps + P_T + 64 * g + n;
-    rq[(R_T >> 2) + lane] = make_float4(tp[0], tp[16], tp[32], tp[48]);
+    buf_store4(rrec, 16u * ((R_T >> 2) + lane), make_float4(tp[0], tp[16], tp[32], tp[48]), srec);
     const float* mp = ps + P_M + 64 * g + n;
-    rq[(R_M >> 2) + lane] = make_float4(mp[0], mp[16], mp[32], mp[48]);
-    rq[(R_G >> 2) + lane] = make_float4(n <= 4 * g ? G[0] : 0.f, n <= 4 * g + 1 ? G[1] : 0.f,
-                                        n <= 4 * g + 2 ? G[2] : 0.f, n <= 4 * g + 3 ? G[3] : 0.f);
+    buf_store4(rrec, 16u * ((R_M >> 2) + lane), make_float4(mp[0], mp[16], mp[32], mp[48]), srec);
+    buf_store4(rrec, 16u * ((R_G >> 2) + lane),
+               make_float4(n <= 4 * g ? G[0] : 0.f, n <= 4 * g + 1 ? G[1] : 0.f, n <= 4 * g + 2 ? G[2] : 0.f,
+                           n <= 4 * g + 3 ? G[3] : 0.f),
+               srec);
 }
 
 // Staging of a group's k, q, v rows in LDS: buffer of 4 blocks x 16 rows, row
@@ -188,7 +199,18 @@ struct Stage {
 
 template <bool AL>
 ASCA_DEV void stage_load(Stage& st, int c, const float* __restrict__ q, const float* __restrict__ k,
-                         const float* __restrict__ v, long ubase, long d, int T, int lane) {
+                         const float* __restrict__ v, const FRes& R, long ubase, long d, int T, int lane) {
+    if constexpr (AL) {
+        const unsigned so = 4u * (unsigned)(c * C * d);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const unsigned vo = 4u * (unsigned)(((lane >> 4) + 4 * s4) * d + 4 * (lane & 15));
+            st.x[0][s4] = buf_load4(R.k, vo, so);
+            st.x[1][s4] = buf_load4(R.q, vo, so);
+            st.x[2][s4] = buf_load4(R.v, vo, so);
+        }
+        return;
+    }
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
         const long t = min(c * C + (lane >> 4) + 4 * s4, T - 1);
@@ -215,14 +237,14 @@ ASCA_DEV void stage_store(const Stage& st, float* __restrict__ buf, int w, int l
 // (key tile r, value tile c).  The forward's wave w holds value tile c = w with
 // keys and values swapped within each 16 x 16 tile, so every tile is transposed
 // through the wave's LDS scratch `st` on its way out.
-ASCA_DEV void ck_store(float* __restrict__ slot, const f32x4 (&S)[4], float* __restrict__ st, int w, int lane) {
+ASCA_DEV void ck_store(const FRes& R, int slot, const f32x4 (&S)[4], float* __restrict__ st, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[(4 * g + i) * OTP + n] = S[r][i];
         const float4 t4 = *reinterpret_cast<const float4*>(st + n * OTP + 4 * g);
-        *reinterpret_cast<float4*>(slot + ((r * 4 + w) * 64 + lane) * 4) = t4;
+        buf_store4(R.ck, 16u * ((r * 4 + w) * 64 + lane), t4, 4u * (unsigned)(slot * DH2));
     }
 }
 
@@ -232,8 +254,8 @@ ASCA_DEV void ck_store(float* __restrict__ slot, const f32x4 (&S)[4], float* __r
 // (q and v rows follow at S_MAT and 2 S_MAT).
 template <bool FULL, bool AL>
 ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const float* __restrict__ ps,
-                         float* __restrict__ ot, int c, float* __restrict__ o, float* __restrict__ ws_u,
-                         float* __restrict__ ckb, bool ckw, long ubase, long d, int T, int w, int lane) {
+                         float* __restrict__ ot, int c, float* __restrict__ o, const FRes& res, bool ckw, long ubase,
+                         long d, int T, int w, int lane) {
     const int n = lane & 15, g = lane >> 4;
     const float* qb = kb + S_MAT;
     const float* vb = kb + 2 * S_MAT;
@@ -277,7 +299,7 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
     for (int i = 0; i < 4; ++i) O[i] = el(gm, i) * (qa[i] + qb2[i]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) O = mfma4(el(mr, i), U[i], O);
-    if (ckw) ck_store(ckb + (long)(c >> 1) * DH2, S, ot + 2 * C * OTP, w, lane);
+    if (ckw) ck_store(res, c >> 1, S, ot + 2 * C * OTP, w, lane);
     // o and u rows leave as 16-byte stores: the 16 x 16 tiles go through the
     // wave's LDS scratch (lane: row lane / 4, columns 4 (lane % 4) .. +3)
 #pragma unroll
@@ -289,14 +311,18 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
         const int rr = lane >> 2, cc = 4 * (lane & 3);
         const float4 o4 = *reinterpret_cast<const float4*>(ot + rr * OTP + cc);
         const float4 u4 = *reinterpret_cast<const float4*>(ot + C * OTP + rr * OTP + cc);
-        const long t = (long)c * C + rr;
-        if (FULL || t < T) {
-            float* po = o + ubase + t * d + 16 * w + cc;
-            if constexpr (AL) *reinterpret_cast<float4*>(po) = o4;
-            else { po[0] = o4.x; po[1] = o4.y; po[2] = o4.z; po[3] = o4.w; }
+        if constexpr (AL) {
+            // rows past the sequence end fall outside the resource: dropped
+            buf_store4(res.o, 4u * (unsigned)(rr * d + 16 * w + cc), o4, 4u * (unsigned)(c * C * d));
+        } else {
+            const long t = (long)c * C + rr;
+            if (FULL || t < T) {
+                float* po = o + ubase + t * d + 16 * w + cc;
+                po[0] = o4.x; po[1] = o4.y; po[2] = o4.z; po[3] = o4.w;
+            }
         }
         // u tile: 1 KB contiguous per wave and block (layout at U_TILE)
-        *reinterpret_cast<float4*>(ws_u + (long)c * U_BLK + w * 256 + rr * 16 + cc) = u4;
+        buf_store4(res.u, 4u * (unsigned)(w * 256 + rr * 16 + cc), u4, 4u * (unsigned)(c * U_BLK));
     }
     float Ut[4];
 #pragma unroll
@@ -310,16 +336,16 @@ ASCA_DEV void chain_step(f32x4 (&S)[4], const float* __restrict__ kb, const floa
 }
 
 // A helper wave's gate loads: lane l holds alpha, beta of step 16 c + (l % 16).
-ASCA_DEV void gate_load(float& a, float& b, int c, const float* __restrict__ alpha, const float* __restrict__ beta,
-                        long gbase, int T, int H, int lane) {
-    const long t = min(c * C + (lane & 15), T - 1);
-    a = alpha[gbase + t * H];
-    b = beta[gbase + t * H];
+// Steps past the sequence end load 0 (prep_compute makes them alpha = 1, beta = 0).
+ASCA_DEV void gate_load(float& a, float& b, int c, const FRes& R, int H, int lane) {
+    const unsigned vo = 4u * (unsigned)((lane & 15) * H), so = 4u * (unsigned)(c * C * H);
+    a = buf_load1(R.al, vo, so);
+    b = buf_load1(R.be, vo, so);
 }
 
 // The helper wave's prep of block p from its staged rows (rows 16 hw .. of `buf`).
 ASCA_DEV void helper_prep(int p, const float* __restrict__ buf, float a, float b, float* __restrict__ ps,
-                          float* __restrict__ scr, float* __restrict__ rec, int T, int hw, int lane) {
+                          float* __restrict__ scr, Rsrc rrec, int T, int hw, int lane) {
     const int n = lane & 15, g = lane >> 4;
     PrepIn pi;
 #pragma unroll
@@ -329,7 +355,7 @@ ASCA_DEV void helper_prep(int p, const float* __restrict__ buf, float a, float b
     }
     pi.a = a;
     pi.b = b;
-    prep_compute(pi, p, T, ps, scr, rec + (long)p * R_SZ, lane);
+    prep_compute(pi, p, T, ps, scr, rrec, lane);
 }
 
 // Block of 2 NW waves.  Waves 0 .. NW-1 (one per SIMD) run the chain: wave w owns
@@ -349,41 +375,54 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
     extern __shared__ float lds[];
     const int unit = blockIdx.x;  // h*B + b
     const int h = unit / B, b = unit - h * B;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index, uniform in a scalar register (so are the block indices and
+    // buffer offsets derived from it)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const long d = (long)H * DH;
     const long ubase = (long)b * T * d + (long)h * DH;
     const int NC = (T + C - 1) / C;
+    FRes R;
+    {
+        const unsigned rows = 4u * (unsigned)((T - 1) * d + DH);   // the unit's columns of rows t < T
+        R.q = make_rsrc(q + ubase, rows);
+        R.k = make_rsrc(k + ubase, rows);
+        R.v = make_rsrc(v + ubase, rows);
+        R.o = make_rsrc(o + ubase, rows);
+        const long gbase = (long)b * T * H + h;
+        const unsigned grow = 4u * (unsigned)((T - 1) * H + 1);
+        R.al = make_rsrc(alpha + gbase, grow);
+        R.be = make_rsrc(beta + gbase, grow);
+        R.u = make_rsrc(ws_u + (long)unit * NC * U_BLK, 4u * (unsigned)(NC * U_BLK));
+        R.ck = make_rsrc(ckpt + (long)unit * nslots * DH2, 4u * (unsigned)(nslots * DH2));
+        R.rec = make_rsrc(rec + (long)unit * NC * R_SZ, 4u * (unsigned)(NC * R_SZ));
+    }
 
     if (w >= NW) {
         const int hw = w - NW;
-        const long gbase = (long)b * T * H + h;
         float* scr = lds + F_SCR + hw * 256;
-        float* recb = rec + (long)unit * NC * R_SZ;
         Stage stg;
         float ga, gb;
-        stage_load<AL>(stg, min(hw, NC - 1), q, k, v, ubase, d, T, lane);
-        gate_load(ga, gb, min(hw, NC - 1), alpha, beta, gbase, T, H, lane);
+        stage_load<AL>(stg, min(hw, NC - 1), q, k, v, R, ubase, d, T, lane);
+        gate_load(ga, gb, min(hw, NC - 1), R, H, lane);
         stage_store(stg, lds + F_STG, hw, lane);
-        if (hw < NC) helper_prep(hw, lds + F_STG, ga, gb, lds + hw * P_SZ, scr, recb, T, hw, lane);
-        stage_load<AL>(stg, min(NW + hw, NC - 1), q, k, v, ubase, d, T, lane);
-        gate_load(ga, gb, min(NW + hw, NC - 1), alpha, beta, gbase, T, H, lane);
+        if (hw < NC) helper_prep(hw, lds + F_STG, ga, gb, lds + hw * P_SZ, scr, R.rec, T, hw, lane);
+        stage_load<AL>(stg, min(NW + hw, NC - 1), q, k, v, R, ubase, d, T, lane);
+        gate_load(ga, gb, min(NW + hw, NC - 1), R, H, lane);
         lds_barrier();
         for (int c0 = 0; c0 < NC; c0 += NW) {
             const int pn = c0 + NW + hw;
             float* nbuf = lds + F_STG + (((c0 / NW) + 1) & 1) * S_BUF;
             stage_store(stg, nbuf, hw, lane);
             const float a = ga, bb = gb;
-            stage_load<AL>(stg, min(pn + NW, NC - 1), q, k, v, ubase, d, T, lane);
-            gate_load(ga, gb, min(pn + NW, NC - 1), alpha, beta, gbase, T, H, lane);
-            if (pn < NC) helper_prep(pn, nbuf, a, bb, lds + (pn % NSLOT) * P_SZ, scr, recb, T, hw, lane);
+            stage_load<AL>(stg, min(pn + NW, NC - 1), q, k, v, R, ubase, d, T, lane);
+            gate_load(ga, gb, min(pn + NW, NC - 1), R, H, lane);
+            if (pn < NC) helper_prep(pn, nbuf, a, bb, lds + (pn % NSLOT) * P_SZ, scr, R.rec, T, hw, lane);
             lds_barrier();
         }
         return;
     }
 
     float* ot = lds + F_OT + w * 3 * C * OTP;
-    float* ckb = ckpt + (long)unit * nslots * DH2;
-    ws_u += (long)unit * NC * U_BLK;
     f32x4 S[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) S[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -394,17 +433,16 @@ __global__ __launch_bounds__(2 * NT) void ut_fwd64_k(const float* __restrict__ q
         if (c0 + NW <= NCF) {
 #pragma unroll
             for (int j = 0; j < NW; ++j)
-                chain_step<true, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, ws_u, ckb,
-                                     (j & 1) == 0,
-                                     ubase, d, T, w, lane);
+                chain_step<true, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, R,
+                                     (j & 1) == 0, ubase, d, T, w, lane);
         } else {
             for (int j = 0; j < NW && c0 + j < NC; ++j)
-                chain_step<false, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, ws_u,
-                                      ckb, ((c0 + j) & 1) == 0, ubase, d, T, w, lane);
+                chain_step<false, AL>(S, buf + j * C * RP, lds + ((c0 + j) % NSLOT) * P_SZ, ot, c0 + j, o, R,
+                                      ((c0 + j) & 1) == 0, ubase, d, T, w, lane);
         }
         lds_barrier();
     }
-    ck_store(ckb + (long)((NC + 1) >> 1) * DH2, S, ot + 2 * C * OTP, w, lane);
+    ck_store(R, (NC + 1) >> 1, S, ot + 2 * C * OTP, w, lane);
 }
 
 // ================================================================= backward
@@ -1102,7 +1140,9 @@ __global__ __launch_bounds__(2 * NT) void ut_bwd64_k(BArgs A) {
         A.ga += rowbase * A.ldg + A.h; A.gb += rowbase * A.ldg + A.h;
         A.ubase = 0; A.gbase = 0; A.rowbase = 0;
     }
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index, uniform in a scalar register (so are the block indices and
+    // buffer offsets derived from it)
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int NC = A.NC;
     const BRes R = bres_make(A);
     float* scr = lds + B_SCR + w * WSCR;
