@@ -326,9 +326,11 @@ ASCA_DEV void dma_mainloop(f32x4 (&acc)[4][4], const float* A, const float* B, c
     const unsigned ca = lds_b + (unsigned)(APW * wu) * 1024u, cb = lds_b + (unsigned)(8 + 2 * wu) * 1024u;
     // tile t into stage S (compile-time)
     const long t_tail = (K_hi - K_lo) / DMA_BK;  // first k-tile not wholly inside the K range
-    auto issue = [&](long t, auto S) {
+    // TL (compile-time): tile t may reach past K_hi (only then are the lanes'
+    // k checked against it)
+    auto issue = [&](long t, auto S, auto TL) {
         constexpr unsigned so = (unsigned)decltype(S)::value * STAGE_B;
-        const bool tail = t >= t_tail;
+        const bool tail = decltype(TL)::value && t >= t_tail;
 #pragma unroll
         for (int j = 0; j < APW; ++j)
             dma_issue<A_KC>(sa[j], t, A, p.lda, p.a_rows, a_off, K_lo, K_hi, tail, ca + 1024u * j + so);
@@ -365,45 +367,62 @@ ASCA_DEV void dma_mainloop(f32x4 (&acc)[4][4], const float* A, const float* B, c
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     const long nk = (K_hi - K_lo + DMA_BK - 1) / DMA_BK;  // > 0
-    issue(0, I0{});
-    if (nk > 1) issue(1, I1{});
+    using Tail = std::true_type;
+    using NoTail = std::false_type;
+    issue(0, I0{}, Tail{});
+    if (nk > 1) issue(1, I1{}, Tail{});
     dma_wait_all();
     __syncthreads();
     rd(I0{}, I0{});
     // Step t at phase P = t % 6: tile t in buffer P % 2 and stage P % 3.
-    auto step = [&](long t, auto P) {
+    // The scheduling barriers keep the fragment reads for the next step ahead
+    // of the products and the next step's wait and barrier behind them (left
+    // alone, the compiler moved the reads down to the barrier, whose wait then
+    // fell on them).
+    auto step = [&](long t, auto P, auto TL) {
         constexpr int ph = decltype(P)::value;
         dma_wait_all();
         __syncthreads();
-        if (t + 2 < nk) issue(t + 2, std::integral_constant<int, (ph + 2) % 3>{});
+        if (t + 2 < nk) issue(t + 2, std::integral_constant<int, (ph + 2) % 3>{}, TL);
         rd(std::integral_constant<int, (ph + 1) % 3>{}, std::integral_constant<int, (ph + 1) % 2>{});
+        __builtin_amdgcn_sched_barrier(0);
         mfma_4xn<4>(acc, fa[ph % 2], fb[ph % 2]);
+        __builtin_amdgcn_sched_barrier(0);
     };
     using P3 = std::integral_constant<int, 3>;
     using P4 = std::integral_constant<int, 4>;
     using P5 = std::integral_constant<int, 5>;
     long t = 0;
+    // steps whose issued tile t + 2 lies wholly inside the K range (t + 2 < t_tail)
+    for (; t + 6 < nk && t + 7 < t_tail; t += 6) {
+        step(t, I0{}, NoTail{});
+        step(t + 1, I1{}, NoTail{});
+        step(t + 2, I2{}, NoTail{});
+        step(t + 3, P3{}, NoTail{});
+        step(t + 4, P4{}, NoTail{});
+        step(t + 5, P5{}, NoTail{});
+    }
     for (; t + 6 < nk; t += 6) {
-        step(t, I0{});
-        step(t + 1, I1{});
-        step(t + 2, I2{});
-        step(t + 3, P3{});
-        step(t + 4, P4{});
-        step(t + 5, P5{});
+        step(t, I0{}, Tail{});
+        step(t + 1, I1{}, Tail{});
+        step(t + 2, I2{}, Tail{});
+        step(t + 3, P3{}, Tail{});
+        step(t + 4, P4{}, Tail{});
+        step(t + 5, P5{}, Tail{});
     }
     // the last 1..6 steps (the fragments read past the last tile are unused)
     do {
-        step(t, I0{});
+        step(t, I0{}, Tail{});
         if (t + 1 >= nk) break;
-        step(t + 1, I1{});
+        step(t + 1, I1{}, Tail{});
         if (t + 2 >= nk) break;
-        step(t + 2, I2{});
+        step(t + 2, I2{}, Tail{});
         if (t + 3 >= nk) break;
-        step(t + 3, P3{});
+        step(t + 3, P3{}, Tail{});
         if (t + 4 >= nk) break;
-        step(t + 4, P4{});
+        step(t + 4, P4{}, Tail{});
         if (t + 5 >= nk) break;
-        step(t + 5, P5{});
+        step(t + 5, P5{}, Tail{});
     } while (false);
     dma_wait_all();
 }
@@ -947,26 +966,29 @@ int gemm_launch(int ta, int tb, int epi, GemmArgs a, long m_total, hipStream_t s
         round_fill(count(64), per_cu64) * (per_cu64 >= 3 ? 0.95 : 0.8) > round_fill(count(128), 2);
     // Direct-to-LDS 128 x 256 tiles (one 8-wave block per CU) where every
     // operand float4 is whole (k-contiguous operands need K in multiples of 4,
-    // mn-contiguous ones M or N) and the grid fills whole rounds of the CUs.
-    // Measured against the 128 x 128 register-staged tile: 5-9% faster on
-    // plain products with full rounds (16384 x {1536, 512} x 512 NN and NT,
-    // 4096^3) and on the grouped-K expert weight gradients; slower with a
-    // partly empty last round and on the grouped-row products.
+    // mn-contiguous ones M or N) and the grid (tiles x K splits) fills whole
+    // rounds of the CUs.  Measured against the 128 x 128 register-staged tile:
+    // 5-9% faster on plain products with full rounds (16384 x {1536, 512} x 512
+    // NN and NT, 4096^3) and on the grouped-K expert weight gradients, and on
+    // the split-K weight gradients (512x1536x16384 TN, ten splits: 272 -> 243
+    // us; the configs[3] training step 21.55 -> 20.83 ms); slower with a partly
+    // empty last round and on the grouped-row products.
     const bool kc_any = !ta || tb;
     const bool dma_ops = vec && (!kc_any || a.K % 4 == 0) && (!ta || a.M % 4 == 0) && (tb || a.N % 4 == 0) &&
                          a.N >= 4 && (!ta || a.M >= 4);
-    const bool dma_ok = dma_ops && ((a.gmode == 0 && a.k_per_split <= 0) || a.gmode == 2);
+    const bool dma_ok = dma_ops && (a.gmode == 0 || a.gmode == 2);
     auto count_dma = [&]() -> long {
         const long tn = (a.N + 255) / 256, tm = (a.M + 127) / 128;
-        return a.gmode == 2 ? (long)a.ngroups * tm * tn : tm * tn;
+        const long sp = a.gmode == 0 && a.k_per_split > 0 ? (a.K + a.k_per_split - 1) / a.k_per_split : 1;
+        return a.gmode == 2 ? (long)a.ngroups * tm * tn : tm * tn * sp;
     };
     const bool dma = dma_ok && wm == 2 && round_fill(count_dma(), 1) >= 0.9;
     // otherwise the same loads on a 128 x 128 tile (4 waves, two blocks per CU)
-    // for the grouped-row expert products and plain products without split-K
+    // for the grouped-row expert products and the other plain products
     // (measured: MoE forward 466 -> 439 us, backward 903 -> 840 us, the
-    // 16384x256x512 head 52 -> 48 us; the split-K weight gradients stay on the
-    // register path, 312 against 337 us)
-    const bool dma128 = !dma && dma_ops && wm == 2 && (a.gmode == 1 || (a.gmode == 0 && a.k_per_split <= 0));
+    // 16384x256x512 head 52 -> 48 us, 512x1536x16384 TN split ten ways on
+    // this tile 272 -> 258 us)
+    const bool dma128 = !dma && dma_ops && wm == 2 && (a.gmode == 1 || a.gmode == 0);
     const int bn = dma ? 256 : dma128 ? 128 : narrow ? 64 : 128;
     a.tiles_n = (a.N + bn - 1) / bn;
     a.tiles_m = (a.M + 64 * wm - 1) / (64 * wm);

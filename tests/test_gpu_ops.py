@@ -93,6 +93,25 @@ def test_gemm_split_k_projection_weight_grad(orc, g):
     np.testing.assert_array_equal(got, g.gemm(x, d, trans_a=True))
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_split_k_direct_to_lds_with_edges(orc, g, ta, tb):
+    # 500 x 1532 output, K = 16380: ten K splits of 1664 (the last 1404, a
+    # k-tail of 12) over 4 x 6 tiles of 128 x 256 fill the CUs, so the split
+    # products run on the direct-to-LDS tile, with partial last row and column
+    # tiles, then the split-K reduction with alpha, beta, C and the bias
+    M, N, K = 500, 1532, 16380
+    rng = np.random.default_rng(60 + 2 * ta + tb)
+    a = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    c = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    print(f"[gemm] split-K direct-to-LDS ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    got = g.gemm(a, b, trans_a=bool(ta), trans_b=bool(tb), alpha=0.5, beta=1.0, c=c, bias=bias)
+    assert orc.rel_err(got, _ref_gemm(a, b, ta, tb, 0.5, 1.0, c, bias)) <= FWD_TOL
+    np.testing.assert_array_equal(got, g.gemm(a, b, trans_a=bool(ta), trans_b=bool(tb), alpha=0.5, beta=1.0,
+                                              c=c, bias=bias))
+
+
 def _dev(a):
     from asca_amd.gpu import DevBuf
 
