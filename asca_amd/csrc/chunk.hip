@@ -724,10 +724,10 @@ template <int TM, int TN, bool AK, bool AB, bool BK, bool BB, bool SA = false, b
 ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const void* A, int lda, const float* sa,
                       const void* B, int ldb, const float* sb, int m0, int n0, int lane) {
     const int li = lane & 15, kq = lane >> 4;
-#pragma unroll 2
-    for (int kb = k_lo; kb < k_hi; kb += 16) {
-        const int k = kb + 4 * kq;
-        f32x4 a[TM], b[TN];
+    // fragments of the 16-k block at kb (clamped into the range: a block read
+    // past the end is never multiplied)
+    auto frag = [&](int kb, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
+        const int k = min(kb, k_hi - 16) + 4 * kq;
 #pragma unroll
         for (int x = 0; x < TM; ++x) {
             a[x] = lds_frag<AK, AB>(A, lda, m0 + 16 * x + li, k);
@@ -738,6 +738,8 @@ ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const void* A, i
             b[y] = lds_frag<BK, BB>(B, ldb, n0 + 16 * y + li, k);
             if (SB) b[y] *= *reinterpret_cast<const f32x4*>(sb + k);
         }
+    };
+    auto mm = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN]) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -745,7 +747,25 @@ ASCA_DEV void wave_mm(f32x4 (&acc)[TM][TN], int k_lo, int k_hi, const void* A, i
 #pragma unroll
                 for (int y = 0; y < TN; ++y)
                     acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[x][s], b[y][s], acc[x][y], 0, 0, 0);
+    };
+    if (k_hi <= k_lo) return;
+    // Software-pipelined: the fragments of the next 16-k block are read before
+    // the products of the current one, which hide the reads' latency (the
+    // scheduling barriers keep the compiler from sinking the reads to their use).
+    f32x4 a0[TM], b0[TN], a1[TM], b1[TN];
+    frag(k_lo, a0, b0);
+    int kb = k_lo;
+    for (; kb + 32 <= k_hi; kb += 32) {
+        frag(kb + 16, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mm(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        frag(kb + 32, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mm(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (kb < k_hi) mm(a0, b0);   // an odd last block
 }
 
 template <int TM, int TN>
