@@ -142,8 +142,9 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
         Lv[i] = n < t ? el(bt, i) * G[i] * A[i] : 0.f;
         ps[P_M + t * 16 + n] = n <= t ? G[i] * Bq[i] : 0.f;
     }
-    // scr holds L^T row-major: scr[j*16 + m] = L[m][j]
-    *reinterpret_cast<float4*>(scr + n * 16 + 4 * g) = make_float4(Lv[0], Lv[1], Lv[2], Lv[3]);
+    // scr holds L row-major: scr[m*16 + j] = L[m][j]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) scr[(4 * g + i) * 16 + n] = Lv[i];
     // row n of T = (I + L)^-1 from x^T (I + L) = e_n^T, columns from the last:
     // x_j = [j == n] - sum_{m > j} x_m L[m][j]
     // Right-looking: once x_m is final it is taken out of every x_j, j < m (the
@@ -152,10 +153,19 @@ ASCA_DEV void prep_compute(const PrepIn& pi, int p, int T, float* __restrict__ p
     float x[C];
 #pragma unroll
     for (int j = 0; j < C; ++j) x[j] = n == j ? 1.f : 0.f;
+    float4 rw[2][4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) rw[C & 1][q4] = *reinterpret_cast<const float4*>(scr + (C - 1) * 16 + 4 * q4);
 #pragma unroll
     for (int m = C - 1; m >= 1; --m) {
+        // row m - 1 read one step ahead (broadcast: every lane the same address)
+        if (m > 1) {
 #pragma unroll
-        for (int j = 0; j < m; ++j) x[j] -= x[m] * scr[j * 16 + m];
+            for (int q4 = 0; q4 < 4; ++q4)
+                if (4 * q4 < m - 1) rw[m & 1][q4] = *reinterpret_cast<const float4*>(scr + (m - 1) * 16 + 4 * q4);
+        }
+#pragma unroll
+        for (int j = 0; j < m; ++j) x[j] -= x[m] * el(rw[(m + 1) & 1][j >> 2], j & 3);
         __builtin_amdgcn_sched_barrier(0);   // keep the solve's steps in order (bounds the live registers)
     }
     if (g == 0) {
