@@ -118,6 +118,34 @@ def _dev(a):
     return DevBuf.from_host(np.ascontiguousarray(a, dtype=np.float32))
 
 
+@pytest.mark.parametrize("rows,cols", [(16384, 512), (16384, 1536), (70001, 1024), (1000, 37), (3, 3),
+                                       (5, 2048), (33, 12)])
+def test_colsum_against_float64(orc, g, rows, cols):
+    # asca_colsum (the bias gradients, colsum_raw of rust/src/cuda/mod.rs:642-669)
+    # over wide, ragged and tiny shapes; with accumulate the sums are added to what
+    # out holds; reruns give the same bits
+    from asca_amd import _lib
+    from asca_amd.gpu import DevBuf, _vp
+
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    base = rng.standard_normal(cols).astype(np.float32)
+    print(f"[colsum] {rows}x{cols}", flush=True)
+    bx = _dev(x)
+    s1, s2, s3 = DevBuf(cols * 4), DevBuf.from_host(base), DevBuf(cols * 4)
+    _lib.call("asca_colsum", _vp(bx), rows, cols, _vp(s1), 0, None)
+    _lib.call("asca_colsum", _vp(bx), rows, cols, _vp(s2), 1, None)
+    _lib.call("asca_colsum", _vp(bx), rows, cols, _vp(s3), 0, None)
+    _lib.call("asca_sync")
+    ref = x.astype(np.float64).sum(axis=0)
+    got = s1.to_host((cols,))
+    assert orc.rel_err(got, ref) <= FWD_TOL
+    assert orc.rel_err(s2.to_host((cols,)), ref + base.astype(np.float64)) <= FWD_TOL
+    np.testing.assert_array_equal(got, s3.to_host((cols,)))
+    for b in (bx, s1, s2, s3):
+        b.free()
+
+
 def test_gemm_and_colsum_workspace_variants_bit_identical(g):
     # asca_gemm_ws / asca_colsum_ws (caller workspace) give the bits of
     # asca_gemm / asca_colsum (stream-ordered scratch), split and unsplit
